@@ -1,0 +1,125 @@
+/*
+ * q3hip.h -- C ABI of libq3hip.so, the MI355X (gfx950) kernels behind the Qwen3 decoder
+ * operator set.
+ *
+ * Every entry point:
+ *   - takes plain device pointers, element counts/shapes as int64_t, and the hipStream_t to
+ *     launch on (the caller's current stream; NULL = legacy default stream);
+ *   - never allocates device memory: outputs and workspaces are owned by the caller, and a
+ *     `*_workspace_bytes` query states the size of any workspace;
+ *   - returns 0 on success, a hipError_t value if a launch failed, or Q3_ERR_INVALID if the
+ *     arguments were rejected before any launch (see q3_error_string).
+ * Tensors are dense row-major unless a stride argument says otherwise.  `dtype` is one of
+ * Q3_F32 / Q3_F16 / Q3_BF16 and applies to every floating tensor of the call unless noted.
+ *
+ * "Replaces" comments cite the reference entry (wuyii8941/qwen3-triton, file:line) whose
+ * Triton launch(es) the function stands in for.
+ */
+#ifndef Q3HIP_H
+#define Q3HIP_H
+
+#include <hip/hip_runtime_api.h>
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define Q3_OK 0
+#define Q3_ERR_INVALID 100000 /* arguments rejected before launch */
+
+enum { Q3_F32 = 0, Q3_F16 = 1, Q3_BF16 = 2 };
+
+/* Human-readable text for a return code. */
+const char* q3_error_string(int code);
+/* ABI version of this header; bumped on any signature change. */
+int q3_abi_version(void);
+
+/* ------------------------------------------------------------------ RMSNorm
+ * y[r,:] = x[r,:] * rsqrt(mean(x[r,:]^2) + eps) * w, fp32 internally, one rounding.
+ * Replaces: qwen3_triton/kernels/norm.py:7-13 (_forward), kernels/math_precision.py:15-37,
+ *           ops/triton/rms_norm.py:11-31,62-88; inference/kernels.py:176-185 (rms_norm). */
+int q3_rmsnorm_fwd(int dtype, const void* x, const void* w, void* y, int64_t rows, int64_t h, float eps,
+                   hipStream_t stream);
+/* dx = (g*w - x*inv^2*mean(g*w*x))*inv ; dw = sum_rows g*x*inv (deterministic two-level sum).
+ * Replaces: kernels/norm.py:16-37,53-63 (_backward + _reduce_rows), ops/triton/rms_norm.py:33-59,90-116. */
+size_t q3_rmsnorm_bwd_workspace_bytes(int64_t rows, int64_t h);
+int q3_rmsnorm_bwd(int dtype, const void* x, const void* w, const void* dy, void* dx, void* dw, void* workspace,
+                   int64_t rows, int64_t h, float eps, hipStream_t stream);
+
+/* ------------------------------------------------------------------ fused per-head RMSNorm + RoPE
+ * x: [tokens, heads, d] (rows = tokens*heads); cos/sin: [tokens, d]; w: [d].
+ * y = rope(rmsnorm(x)) with split-half rotation.
+ * Replaces: kernels/norm_rope.py:12-28,53-71 (_norm_rope_forward), kernels/math_precision.py:39-64,
+ *           ops/triton/fused_qk_norm_rope.py:11-66 (per tensor), inference/kernels.py:188-194. */
+int q3_norm_rope_fwd(int dtype, const void* x, const void* w, const void* cos, const void* sin, void* y,
+                     int64_t tokens, int64_t heads, int64_t d, float eps, hipStream_t stream);
+/* Backward: inverse rotation, then RMSNorm backward; dw reduced deterministically.
+ * Replaces: kernels/norm_rope.py:30-50,62-69, ops/triton/fused_qk_norm_rope.py:111-235. */
+size_t q3_norm_rope_bwd_workspace_bytes(int64_t tokens, int64_t heads, int64_t d);
+int q3_norm_rope_bwd(int dtype, const void* x, const void* w, const void* cos, const void* sin, const void* dy,
+                     void* dx, void* dw, void* workspace, int64_t tokens, int64_t heads, int64_t d, float eps,
+                     hipStream_t stream);
+
+/* ------------------------------------------------------------------ RoPE
+ * cos/sin[t, j] = cos/sin(fp32(pos[t]) * inv_freq[j mod d/2]) for j < d, stored in `dtype`.
+ * Replaces: kernels/rotary.py:12-17,36-45 (_tables / rotary_tables). */
+int q3_rope_tables(int dtype, const void* pos, int pos_is_int64, const float* inv_freq, void* cos, void* sin,
+                   int64_t n_pos, int64_t d, hipStream_t stream);
+/* y = x*cos + rotate_half(x)*sin (backward=0) or its transpose (backward=1).
+ * layout 0: x is [B,S,H,D] (kernels/rotary.py:19-34,47-66); layout 1: x is [B,H,S,D]
+ * (ops/triton/rope.py:11-148).  cos/sin: [B,S,D]. */
+int q3_rope_apply(int dtype, const void* x, const void* cos, const void* sin, void* y, int64_t batch, int64_t seq,
+                  int64_t heads, int64_t d, int layout, int backward, hipStream_t stream);
+
+/* ------------------------------------------------------------------ SwiGLU
+ * y = silu(g)*u ; backward dg = dy*u*s*(1+g*(1-s)), du = dy*silu(g), s = sigmoid(g).
+ * Replaces: kernels/activation.py:6-36, kernels/math_precision.py:66-96, ops/triton/silu_and_mul.py:20-121. */
+int q3_swiglu_fwd(int dtype, const void* g, const void* u, void* y, int64_t n, hipStream_t stream);
+int q3_swiglu_bwd(int dtype, const void* g, const void* u, const void* dy, void* dg, void* du, int64_t n,
+                  hipStream_t stream);
+
+/* ------------------------------------------------------------------ elementwise / data movement */
+/* c = a + b (fp32 add).  Replaces kernels/residual.py:6-30. */
+int q3_add(int dtype, const void* a, const void* b, void* c, int64_t n, hipStream_t stream);
+/* y = convert(x).  Replaces kernels/attention.py:11-20 (cast_tensor). */
+int q3_cast(int src_dtype, int dst_dtype, const void* x, void* y, int64_t n, hipStream_t stream);
+/* x[:] = value (a kernel, never a memset, so it is safe inside captured graphs). */
+int q3_fill(int dtype, void* x, float value, int64_t n, hipStream_t stream);
+/* out[b, s] = start + s.  Replaces _model.py:29-32 (_positions), inference/kernels.py:12-21. */
+int q3_positions(int64_t* out, int64_t batch, int64_t seq, int64_t start, hipStream_t stream);
+/* y[b][c][r] = x[b][r][c] for 16-bit or 32-bit elements (a layout change, not arithmetic). */
+int q3_transpose(int dtype, const void* x, void* y, int64_t batch, int64_t rows, int64_t cols, hipStream_t stream);
+
+/* ------------------------------------------------------------------ embedding
+ * y[i,:] = w[ids[i],:].  Out-of-range ids produce zero rows and set *bad_ids (device int) to 1.
+ * Replaces: kernels/embedding.py:12-26,49-64. */
+int q3_embedding_fwd(int dtype, const void* ids, int ids_is_int64, const void* w, void* y, int* bad_ids,
+                     int64_t n_ids, int64_t vocab, int64_t h, hipStream_t stream);
+/* dw = scatter-sum of dy rows by id, deterministic (fixed summation order per token, no atomics).
+ * dw is fully written (rows of unused tokens are zero).  Replaces kernels/embedding.py:29-46,66-77. */
+size_t q3_embedding_bwd_workspace_bytes(int64_t n_ids);
+int q3_embedding_bwd(int dtype, const void* ids, int ids_is_int64, const void* dy, void* dw, void* workspace,
+                     int64_t n_ids, int64_t vocab, int64_t h, hipStream_t stream);
+
+
+/* ------------------------------------------------------------------ GEMM
+ * C[M,N] = alpha * A[M,K] . B[N,K]^T (+ C when accumulate != 0); A, B bf16/fp16 with K-contiguous
+ * rows (strides lda, ldb elements; K, lda, ldb multiples of 8; 16-byte aligned bases); C in
+ * out_dtype with row stride ldc; fp32 accumulation on the matrix cores.
+ * Replaces: kernels/linear.py:13-42,45-77 (_gemm / matmul), kernels/gemm_experiments.py:12-101,
+ *           ops/triton/gate_up_swiglu.py:151-176 (_matmul_kernel). */
+int q3_gemm_nt(int in_dtype, int out_dtype, const void* A, int64_t lda, const void* B, int64_t ldb, void* C,
+               int64_t ldc, int64_t M, int64_t N, int64_t K, float alpha, int accumulate, hipStream_t stream);
+/* Same product for arbitrary element strides: A(m,k) = A[m*sam + k*sak], B(k,n) = B[k*sbk + n*sbn];
+ * any dtype (fp32 included).  SIMT path for shapes the matrix-core kernel does not take.
+ * Replaces: kernels/linear.py:13-42 (_gemm with arbitrary strides). */
+int q3_gemm_strided(int in_dtype, int out_dtype, const void* A, int64_t sam, int64_t sak, const void* B, int64_t sbk,
+                    int64_t sbn, void* C, int64_t ldc, int64_t M, int64_t N, int64_t K, float alpha, int accumulate,
+                    hipStream_t stream);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* Q3HIP_H */

@@ -1,0 +1,462 @@
+// Streaming kernels: RoPE tables/apply, SwiGLU fwd/bwd, residual add, cast, fill, positions,
+// transpose, embedding gather and its deterministic scatter-sum.
+//
+// All are HBM-bound: each thread moves whole 16-byte vectors (8 x 16-bit / 4 x fp32) with a
+// grid-stride loop sized to fill the 256 CUs, and falls back to scalar code only for tails or
+// shapes that break 16-byte alignment.
+#include "common.h"
+
+namespace {
+
+constexpr int kBlock = 256;
+
+Q3_DEV float fast_exp(float x) { return __builtin_amdgcn_exp2f(x * 1.4426950408889634f); }
+Q3_DEV float sigmoid(float g) { return __builtin_amdgcn_rcpf(1.f + fast_exp(-g)); }
+
+template <typename T> bool aligned16(const void* p) { return ((uintptr_t)p & 15) == 0; }
+
+// ---------------------------------------------------------------- SwiGLU
+template <typename T>
+__global__ __launch_bounds__(kBlock) void swiglu_fwd_kernel(const typename T::storage* __restrict__ g,
+                                                            const typename T::storage* __restrict__ u,
+                                                            typename T::storage* __restrict__ y, int64_t n,
+                                                            int vec_ok) {
+  constexpr int V = T::vec;
+  const int64_t nv = vec_ok ? n / V : 0;
+  const int64_t stride = (int64_t)gridDim.x * kBlock;
+  for (int64_t i = (int64_t)blockIdx.x * kBlock + threadIdx.x; i < nv; i += stride) {
+    Vec<T> gv = load_vec<T>(g + i * V), uv = load_vec<T>(u + i * V), o;
+#pragma unroll
+    for (int e = 0; e < V; ++e) o.v[e] = gv.v[e] * sigmoid(gv.v[e]) * uv.v[e];
+    store_vec<T>(y + i * V, o);
+  }
+  for (int64_t i = nv * V + (int64_t)blockIdx.x * kBlock + threadIdx.x; i < n; i += stride) {
+    const float gg = to_f32<T>(g[i]);
+    y[i] = from_f32<T>(gg * sigmoid(gg) * to_f32<T>(u[i]));
+  }
+}
+
+template <typename T>
+__global__ __launch_bounds__(kBlock) void swiglu_bwd_kernel(const typename T::storage* __restrict__ g,
+                                                            const typename T::storage* __restrict__ u,
+                                                            const typename T::storage* __restrict__ dy,
+                                                            typename T::storage* __restrict__ dg,
+                                                            typename T::storage* __restrict__ du, int64_t n,
+                                                            int vec_ok) {
+  constexpr int V = T::vec;
+  const int64_t nv = vec_ok ? n / V : 0;
+  const int64_t stride = (int64_t)gridDim.x * kBlock;
+  for (int64_t i = (int64_t)blockIdx.x * kBlock + threadIdx.x; i < nv; i += stride) {
+    Vec<T> gv = load_vec<T>(g + i * V), uv = load_vec<T>(u + i * V), dv = load_vec<T>(dy + i * V), og, ou;
+#pragma unroll
+    for (int e = 0; e < V; ++e) {
+      const float s = sigmoid(gv.v[e]);
+      og.v[e] = dv.v[e] * uv.v[e] * s * (1.f + gv.v[e] * (1.f - s));
+      ou.v[e] = dv.v[e] * gv.v[e] * s;
+    }
+    store_vec<T>(dg + i * V, og);
+    store_vec<T>(du + i * V, ou);
+  }
+  for (int64_t i = nv * V + (int64_t)blockIdx.x * kBlock + threadIdx.x; i < n; i += stride) {
+    const float gg = to_f32<T>(g[i]), uu = to_f32<T>(u[i]), d = to_f32<T>(dy[i]);
+    const float s = sigmoid(gg);
+    dg[i] = from_f32<T>(d * uu * s * (1.f + gg * (1.f - s)));
+    du[i] = from_f32<T>(d * gg * s);
+  }
+}
+
+// ---------------------------------------------------------------- add / cast / fill
+template <typename T>
+__global__ __launch_bounds__(kBlock) void add_kernel(const typename T::storage* __restrict__ a,
+                                                     const typename T::storage* __restrict__ b,
+                                                     typename T::storage* __restrict__ c, int64_t n, int vec_ok) {
+  constexpr int V = T::vec;
+  const int64_t nv = vec_ok ? n / V : 0;
+  const int64_t stride = (int64_t)gridDim.x * kBlock;
+  for (int64_t i = (int64_t)blockIdx.x * kBlock + threadIdx.x; i < nv; i += stride) {
+    Vec<T> av = load_vec<T>(a + i * V), bv = load_vec<T>(b + i * V), o;
+#pragma unroll
+    for (int e = 0; e < V; ++e) o.v[e] = av.v[e] + bv.v[e];
+    store_vec<T>(c + i * V, o);
+  }
+  for (int64_t i = nv * V + (int64_t)blockIdx.x * kBlock + threadIdx.x; i < n; i += stride)
+    c[i] = from_f32<T>(to_f32<T>(a[i]) + to_f32<T>(b[i]));
+}
+
+template <typename S, typename D>
+__global__ __launch_bounds__(kBlock) void cast_kernel(const typename S::storage* __restrict__ x,
+                                                      typename D::storage* __restrict__ y, int64_t n) {
+  const int64_t stride = (int64_t)gridDim.x * kBlock;
+  for (int64_t i = (int64_t)blockIdx.x * kBlock + threadIdx.x; i < n; i += stride)
+    y[i] = from_f32<D>(to_f32<S>(x[i]));
+}
+
+template <typename T>
+__global__ __launch_bounds__(kBlock) void fill_kernel(typename T::storage* __restrict__ x, float value, int64_t n) {
+  const typename T::storage v = from_f32<T>(value);
+  const int64_t stride = (int64_t)gridDim.x * kBlock;
+  for (int64_t i = (int64_t)blockIdx.x * kBlock + threadIdx.x; i < n; i += stride) x[i] = v;
+}
+
+__global__ __launch_bounds__(kBlock) void positions_kernel(int64_t* __restrict__ out, int64_t n, int64_t seq,
+                                                           int64_t start) {
+  const int64_t stride = (int64_t)gridDim.x * kBlock;
+  for (int64_t i = (int64_t)blockIdx.x * kBlock + threadIdx.x; i < n; i += stride) out[i] = start + i % seq;
+}
+
+// ---------------------------------------------------------------- RoPE
+// cos/sin tables: one thread per (position, j < d/2); writes columns j and j + d/2.
+template <typename T>
+__global__ __launch_bounds__(kBlock) void rope_tables_kernel(const void* __restrict__ pos, int pos64,
+                                                             const float* __restrict__ inv_freq,
+                                                             typename T::storage* __restrict__ cs,
+                                                             typename T::storage* __restrict__ sn, int64_t npos,
+                                                             int half) {
+  const int64_t n = npos * half;
+  const int64_t stride = (int64_t)gridDim.x * kBlock;
+  for (int64_t i = (int64_t)blockIdx.x * kBlock + threadIdx.x; i < n; i += stride) {
+    const int64_t t = i / half;
+    const int j = (int)(i % half);
+    const float p = pos64 ? (float)((const int64_t*)pos)[t] : (float)((const int*)pos)[t];
+    const float ang = p * inv_freq[j];
+    float s, c;
+    sincosf(ang, &s, &c);
+    const int64_t o = t * 2 * half + j;
+    cs[o] = from_f32<T>(c);
+    cs[o + half] = from_f32<T>(c);
+    sn[o] = from_f32<T>(s);
+    sn[o + half] = from_f32<T>(s);
+  }
+}
+
+// Token index of a row for the two layouts: 0 = [B,S,H,D] (row = (b*S+s)*H+h),
+// 1 = [B,H,S,D] (row = (b*H+h)*S+s).  cos/sin are [B*S, D].
+Q3_DEV int64_t rope_token(int64_t row, int64_t seq, int64_t heads, int layout) {
+  if (layout == 0) return row / heads;
+  return (row / (heads * seq)) * seq + row % seq;
+}
+
+// One thread per (row, vector j of the first half): handles the element pairs (d, d + D/2).
+template <typename T>
+__global__ __launch_bounds__(kBlock) void rope_apply_vec_kernel(const typename T::storage* __restrict__ x,
+                                                                const typename T::storage* __restrict__ cs,
+                                                                const typename T::storage* __restrict__ sn,
+                                                                typename T::storage* __restrict__ y, int64_t rows,
+                                                                int64_t seq, int64_t heads, int d, int layout,
+                                                                int backward) {
+  constexpr int V = T::vec;
+  const int half = d / 2, hv = half / V;
+  const int64_t n = rows * hv;
+  const int64_t stride = (int64_t)gridDim.x * kBlock;
+  for (int64_t i = (int64_t)blockIdx.x * kBlock + threadIdx.x; i < n; i += stride) {
+    const int64_t row = i / hv;
+    const int j = (int)(i % hv) * V;
+    const int64_t tok = rope_token(row, seq, heads, layout);
+    const typename T::storage* xr = x + row * d;
+    const Vec<T> a = load_vec<T>(xr + j), b = load_vec<T>(xr + half + j);
+    const Vec<T> ca = load_vec<T>(cs + tok * d + j), cb = load_vec<T>(cs + tok * d + half + j);
+    const Vec<T> sa = load_vec<T>(sn + tok * d + j), sb = load_vec<T>(sn + tok * d + half + j);
+    Vec<T> oa, ob;
+#pragma unroll
+    for (int e = 0; e < V; ++e) {
+      if (!backward) {
+        oa.v[e] = a.v[e] * ca.v[e] - b.v[e] * sa.v[e];
+        ob.v[e] = b.v[e] * cb.v[e] + a.v[e] * sb.v[e];
+      } else {
+        oa.v[e] = a.v[e] * ca.v[e] + b.v[e] * sb.v[e];
+        ob.v[e] = b.v[e] * cb.v[e] - a.v[e] * sa.v[e];
+      }
+    }
+    store_vec<T>(y + row * d + j, oa);
+    store_vec<T>(y + row * d + half + j, ob);
+  }
+}
+
+template <typename T>
+__global__ __launch_bounds__(kBlock) void rope_apply_scalar_kernel(const typename T::storage* __restrict__ x,
+                                                                   const typename T::storage* __restrict__ cs,
+                                                                   const typename T::storage* __restrict__ sn,
+                                                                   typename T::storage* __restrict__ y, int64_t rows,
+                                                                   int64_t seq, int64_t heads, int d, int layout,
+                                                                   int backward) {
+  const int half = d / 2;
+  const int64_t n = rows * half;
+  const int64_t stride = (int64_t)gridDim.x * kBlock;
+  for (int64_t i = (int64_t)blockIdx.x * kBlock + threadIdx.x; i < n; i += stride) {
+    const int64_t row = i / half;
+    const int j = (int)(i % half);
+    const int64_t tok = rope_token(row, seq, heads, layout);
+    const float a = to_f32<T>(x[row * d + j]), b = to_f32<T>(x[row * d + half + j]);
+    const float ca = to_f32<T>(cs[tok * d + j]), cb = to_f32<T>(cs[tok * d + half + j]);
+    const float sa = to_f32<T>(sn[tok * d + j]), sb = to_f32<T>(sn[tok * d + half + j]);
+    float oa, ob;
+    if (!backward) {
+      oa = a * ca - b * sa;
+      ob = b * cb + a * sb;
+    } else {
+      oa = a * ca + b * sb;
+      ob = b * cb - a * sa;
+    }
+    y[row * d + j] = from_f32<T>(oa);
+    y[row * d + half + j] = from_f32<T>(ob);
+  }
+}
+
+// ---------------------------------------------------------------- transpose
+// y[b][c][r] = x[b][r][c] through a 64x64 LDS tile (row padded to 66 elements: the column reads
+// of the store phase hit distinct banks).  Elements are moved as raw 16- or 32-bit words.
+template <typename W>
+__global__ __launch_bounds__(kBlock) void transpose_kernel(const W* __restrict__ x, W* __restrict__ y, int64_t rows,
+                                                           int64_t cols) {
+  __shared__ W tile[64][66];
+  const int64_t b = blockIdx.z;
+  const int64_t r0 = (int64_t)blockIdx.y * 64, c0 = (int64_t)blockIdx.x * 64;
+  const W* xb = x + b * rows * cols;
+  W* yb = y + b * rows * cols;
+  const int tx = threadIdx.x & 63, ty = threadIdx.x >> 6;
+  for (int r = ty; r < 64; r += 4) {
+    const int64_t gr = r0 + r, gc = c0 + tx;
+    if (gr < rows && gc < cols) tile[r][tx] = xb[gr * cols + gc];
+  }
+  __syncthreads();
+  for (int c = ty; c < 64; c += 4) {
+    const int64_t gc = c0 + c, gr = r0 + tx;
+    if (gc < cols && gr < rows) yb[gc * rows + gr] = tile[tx][c];
+  }
+}
+
+// ---------------------------------------------------------------- embedding
+template <typename T>
+__global__ __launch_bounds__(kBlock) void embedding_fwd_kernel(const void* __restrict__ ids, int ids64,
+                                                               const typename T::storage* __restrict__ w,
+                                                               typename T::storage* __restrict__ y, int* bad,
+                                                               int64_t n, int64_t vocab, int64_t h, int vec_ok) {
+  constexpr int V = T::vec;
+  const int64_t per = vec_ok ? h / V : h;
+  const int64_t total = n * per;
+  const int64_t stride = (int64_t)gridDim.x * kBlock;
+  for (int64_t i = (int64_t)blockIdx.x * kBlock + threadIdx.x; i < total; i += stride) {
+    const int64_t r = i / per, c = i % per;
+    const int64_t id = ids64 ? ((const int64_t*)ids)[r] : (int64_t)((const int*)ids)[r];
+    const bool ok = id >= 0 && id < vocab;
+    if (!ok && c == 0 && bad) *bad = 1;
+    if (vec_ok) {
+      Vec<T> v;
+      if (ok) {
+        v = load_vec<T>(w + id * h + c * V);
+      } else {
+#pragma unroll
+        for (int e = 0; e < V; ++e) v.v[e] = 0.f;
+      }
+      store_vec<T>(y + r * h + c * V, v);
+    } else {
+      y[r * h + c] = ok ? w[id * h + c] : from_f32<T>(0.f);
+    }
+  }
+}
+
+Q3_DEV int64_t load_id(const void* ids, int ids64, int64_t i) {
+  return ids64 ? ((const int64_t*)ids)[i] : (int64_t)((const int*)ids)[i];
+}
+
+// Stable counting rank: order[rank(i)] = i with positions sorted by (id, position).
+__global__ __launch_bounds__(kBlock) void embedding_rank_kernel(const void* __restrict__ ids, int ids64,
+                                                                int* __restrict__ order, int64_t n) {
+  __shared__ int64_t chunk[kBlock];
+  const int64_t i = (int64_t)blockIdx.x * kBlock + threadIdx.x;
+  const int64_t mine = i < n ? load_id(ids, ids64, i) : 0;
+  int64_t rank = 0;
+  for (int64_t base = 0; base < n; base += kBlock) {
+    __syncthreads();
+    if (base + threadIdx.x < n) chunk[threadIdx.x] = load_id(ids, ids64, base + threadIdx.x);
+    __syncthreads();
+    const int64_t lim = n - base < kBlock ? n - base : kBlock;
+    for (int64_t j = 0; j < lim; ++j) {
+      const int64_t o = chunk[j];
+      rank += (o < mine) || (o == mine && base + j < i);
+    }
+  }
+  if (i < n) order[rank] = (int)i;
+}
+
+// One workgroup per sorted slot that starts a run of equal ids: sums the run's gradient rows in
+// position order and writes the token's row of dw.
+template <typename T>
+__global__ __launch_bounds__(kBlock) void embedding_sum_kernel(const void* __restrict__ ids, int ids64,
+                                                               const int* __restrict__ order,
+                                                               const typename T::storage* __restrict__ dy,
+                                                               typename T::storage* __restrict__ dw, int64_t n,
+                                                               int64_t vocab, int64_t h) {
+  const int64_t s = blockIdx.x;
+  const int64_t id = load_id(ids, ids64, order[s]);
+  if (id < 0 || id >= vocab) return;
+  if (s > 0 && load_id(ids, ids64, order[s - 1]) == id) return;
+  int64_t e = s + 1;
+  while (e < n && load_id(ids, ids64, order[e]) == id) ++e;
+  for (int64_t c = (int64_t)blockIdx.y * kBlock + threadIdx.x; c < h; c += (int64_t)gridDim.y * kBlock) {
+    float acc = 0.f;
+    for (int64_t k = s; k < e; ++k) acc += to_f32<T>(dy[(int64_t)order[k] * h + c]);
+    dw[id * h + c] = from_f32<T>(acc);
+  }
+}
+
+bool dtype_ok(int dt) { return dt == Q3_F32 || dt == Q3_F16 || dt == Q3_BF16; }
+
+template <typename T> int swiglu_fwd_t(const void* g, const void* u, void* y, int64_t n, hipStream_t s) {
+  typedef typename T::storage S;
+  const int vec = aligned16<T>(g) && aligned16<T>(u) && aligned16<T>(y);
+  swiglu_fwd_kernel<T><<<q3_grid_for(n / T::vec + 1, kBlock), kBlock, 0, s>>>((const S*)g, (const S*)u, (S*)y, n,
+                                                                                vec);
+  return (int)hipGetLastError();
+}
+template <typename T>
+int swiglu_bwd_t(const void* g, const void* u, const void* dy, void* dg, void* du, int64_t n, hipStream_t s) {
+  typedef typename T::storage S;
+  const int vec = aligned16<T>(g) && aligned16<T>(u) && aligned16<T>(dy) && aligned16<T>(dg) && aligned16<T>(du);
+  swiglu_bwd_kernel<T><<<q3_grid_for(n / T::vec + 1, kBlock), kBlock, 0, s>>>((const S*)g, (const S*)u,
+                                                                                (const S*)dy, (S*)dg, (S*)du, n, vec);
+  return (int)hipGetLastError();
+}
+template <typename T> int add_t(const void* a, const void* b, void* c, int64_t n, hipStream_t s) {
+  typedef typename T::storage S;
+  const int vec = aligned16<T>(a) && aligned16<T>(b) && aligned16<T>(c);
+  add_kernel<T><<<q3_grid_for(n / T::vec + 1, kBlock), kBlock, 0, s>>>((const S*)a, (const S*)b, (S*)c, n, vec);
+  return (int)hipGetLastError();
+}
+template <typename T> int fill_t(void* x, float v, int64_t n, hipStream_t s) {
+  fill_kernel<T><<<q3_grid_for(n, kBlock), kBlock, 0, s>>>((typename T::storage*)x, v, n);
+  return (int)hipGetLastError();
+}
+template <typename S, typename D> int cast_t2(const void* x, void* y, int64_t n, hipStream_t s) {
+  cast_kernel<S, D><<<q3_grid_for(n, kBlock), kBlock, 0, s>>>((const typename S::storage*)x,
+                                                               (typename D::storage*)y, n);
+  return (int)hipGetLastError();
+}
+template <typename S> int cast_t(int dst, const void* x, void* y, int64_t n, hipStream_t s) {
+  if (dst == Q3_BF16) return cast_t2<S, BF16>(x, y, n, s);
+  if (dst == Q3_F16) return cast_t2<S, F16>(x, y, n, s);
+  return cast_t2<S, F32>(x, y, n, s);
+}
+template <typename T>
+int tables_t(const void* pos, int pos64, const float* f, void* c, void* sn, int64_t npos, int64_t d, hipStream_t s) {
+  rope_tables_kernel<T><<<q3_grid_for(npos * (d / 2), kBlock), kBlock, 0, s>>>(
+      pos, pos64, f, (typename T::storage*)c, (typename T::storage*)sn, npos, (int)(d / 2));
+  return (int)hipGetLastError();
+}
+template <typename T>
+int rope_t(const void* x, const void* c, const void* sn, void* y, int64_t b, int64_t seq, int64_t heads, int64_t d,
+           int layout, int bwd, hipStream_t s) {
+  typedef typename T::storage S;
+  const int64_t rows = b * seq * heads;
+  const bool vec = (d / 2) % T::vec == 0 && aligned16<T>(x) && aligned16<T>(c) && aligned16<T>(sn) &&
+                   aligned16<T>(y);
+  if (vec)
+    rope_apply_vec_kernel<T><<<q3_grid_for(rows * (d / 2 / T::vec), kBlock), kBlock, 0, s>>>(
+        (const S*)x, (const S*)c, (const S*)sn, (S*)y, rows, seq, heads, (int)d, layout, bwd);
+  else
+    rope_apply_scalar_kernel<T><<<q3_grid_for(rows * (d / 2), kBlock), kBlock, 0, s>>>(
+        (const S*)x, (const S*)c, (const S*)sn, (S*)y, rows, seq, heads, (int)d, layout, bwd);
+  return (int)hipGetLastError();
+}
+template <typename T>
+int emb_fwd_t(const void* ids, int ids64, const void* w, void* y, int* bad, int64_t n, int64_t vocab, int64_t h,
+              hipStream_t s) {
+  typedef typename T::storage S;
+  const int vec = h % T::vec == 0 && aligned16<T>(w) && aligned16<T>(y);
+  const int64_t per = vec ? h / T::vec : h;
+  embedding_fwd_kernel<T><<<q3_grid_for(n * per, kBlock), kBlock, 0, s>>>(ids, ids64, (const S*)w, (S*)y, bad, n,
+                                                                           vocab, h, vec);
+  return (int)hipGetLastError();
+}
+template <typename T>
+int emb_bwd_t(const void* ids, int ids64, const void* dy, void* dw, int* order, int64_t n, int64_t vocab, int64_t h,
+              hipStream_t s) {
+  typedef typename T::storage S;
+  fill_kernel<T><<<q3_grid_for(vocab * h, kBlock), kBlock, 0, s>>>((S*)dw, 0.f, vocab * h);
+  embedding_rank_kernel<<<(unsigned)((n + kBlock - 1) / kBlock), kBlock, 0, s>>>(ids, ids64, order, n);
+  int64_t gy = (h + kBlock - 1) / kBlock;
+  if (gy > 16) gy = 16;
+  embedding_sum_kernel<T><<<dim3((unsigned)n, (unsigned)gy), kBlock, 0, s>>>(ids, ids64, order, (const S*)dy, (S*)dw,
+                                                                             n, vocab, h);
+  return (int)hipGetLastError();
+}
+
+}  // namespace
+
+#define Q3_DISPATCH(dt, FN, ...) \
+  ((dt) == Q3_BF16 ? FN<BF16>(__VA_ARGS__) : (dt) == Q3_F16 ? FN<F16>(__VA_ARGS__) : FN<F32>(__VA_ARGS__))
+
+extern "C" {
+
+int q3_swiglu_fwd(int dtype, const void* g, const void* u, void* y, int64_t n, hipStream_t stream) {
+  Q3_REQUIRE(dtype_ok(dtype) && g && u && y && n > 0);
+  return Q3_DISPATCH(dtype, swiglu_fwd_t, g, u, y, n, stream);
+}
+
+int q3_swiglu_bwd(int dtype, const void* g, const void* u, const void* dy, void* dg, void* du, int64_t n,
+                  hipStream_t stream) {
+  Q3_REQUIRE(dtype_ok(dtype) && g && u && dy && dg && du && n > 0);
+  return Q3_DISPATCH(dtype, swiglu_bwd_t, g, u, dy, dg, du, n, stream);
+}
+
+int q3_add(int dtype, const void* a, const void* b, void* c, int64_t n, hipStream_t stream) {
+  Q3_REQUIRE(dtype_ok(dtype) && a && b && c && n > 0);
+  return Q3_DISPATCH(dtype, add_t, a, b, c, n, stream);
+}
+
+int q3_cast(int src, int dst, const void* x, void* y, int64_t n, hipStream_t stream) {
+  Q3_REQUIRE(dtype_ok(src) && dtype_ok(dst) && x && y && n > 0);
+  return Q3_DISPATCH(src, cast_t, dst, x, y, n, stream);
+}
+
+int q3_fill(int dtype, void* x, float value, int64_t n, hipStream_t stream) {
+  Q3_REQUIRE(dtype_ok(dtype) && x && n > 0);
+  return Q3_DISPATCH(dtype, fill_t, x, value, n, stream);
+}
+
+int q3_positions(int64_t* out, int64_t batch, int64_t seq, int64_t start, hipStream_t stream) {
+  Q3_REQUIRE(out && batch > 0 && seq > 0 && start >= 0);
+  positions_kernel<<<q3_grid_for(batch * seq, kBlock), kBlock, 0, stream>>>(out, batch * seq, seq, start);
+  return (int)hipGetLastError();
+}
+
+int q3_transpose(int dtype, const void* x, void* y, int64_t batch, int64_t rows, int64_t cols, hipStream_t stream) {
+  Q3_REQUIRE(dtype_ok(dtype) && x && y && batch > 0 && rows > 0 && cols > 0 && batch < 65536);
+  Q3_REQUIRE((rows + 63) / 64 < 65536);
+  dim3 grid((unsigned)((cols + 63) / 64), (unsigned)((rows + 63) / 64), (unsigned)batch);
+  if (dtype == Q3_F32)
+    transpose_kernel<uint32_t><<<grid, kBlock, 0, stream>>>((const uint32_t*)x, (uint32_t*)y, rows, cols);
+  else
+    transpose_kernel<u16><<<grid, kBlock, 0, stream>>>((const u16*)x, (u16*)y, rows, cols);
+  return (int)hipGetLastError();
+}
+
+int q3_rope_tables(int dtype, const void* pos, int pos_is_int64, const float* inv_freq, void* cos, void* sin,
+                   int64_t n_pos, int64_t d, hipStream_t stream) {
+  Q3_REQUIRE(dtype_ok(dtype) && pos && inv_freq && cos && sin && n_pos > 0 && d > 0 && d % 2 == 0);
+  return Q3_DISPATCH(dtype, tables_t, pos, pos_is_int64, inv_freq, cos, sin, n_pos, d, stream);
+}
+
+int q3_rope_apply(int dtype, const void* x, const void* cos, const void* sin, void* y, int64_t batch, int64_t seq,
+                  int64_t heads, int64_t d, int layout, int backward, hipStream_t stream) {
+  Q3_REQUIRE(dtype_ok(dtype) && x && cos && sin && y && batch > 0 && seq > 0 && heads > 0 && d > 0 && d % 2 == 0 &&
+             (layout == 0 || layout == 1));
+  return Q3_DISPATCH(dtype, rope_t, x, cos, sin, y, batch, seq, heads, d, layout, backward ? 1 : 0, stream);
+}
+
+int q3_embedding_fwd(int dtype, const void* ids, int ids_is_int64, const void* w, void* y, int* bad_ids,
+                     int64_t n_ids, int64_t vocab, int64_t h, hipStream_t stream) {
+  Q3_REQUIRE(dtype_ok(dtype) && ids && w && y && n_ids > 0 && vocab > 0 && h > 0);
+  return Q3_DISPATCH(dtype, emb_fwd_t, ids, ids_is_int64, w, y, bad_ids, n_ids, vocab, h, stream);
+}
+
+size_t q3_embedding_bwd_workspace_bytes(int64_t n_ids) { return (size_t)(n_ids > 0 ? n_ids : 1) * sizeof(int); }
+
+int q3_embedding_bwd(int dtype, const void* ids, int ids_is_int64, const void* dy, void* dw, void* workspace,
+                     int64_t n_ids, int64_t vocab, int64_t h, hipStream_t stream) {
+  Q3_REQUIRE(dtype_ok(dtype) && ids && dy && dw && workspace && n_ids > 0 && n_ids < (1ll << 31) && vocab > 0 &&
+             h > 0 && n_ids < 65536ll * 32768ll);
+  return Q3_DISPATCH(dtype, emb_bwd_t, ids, ids_is_int64, dy, dw, (int*)workspace, n_ids, vocab, h, stream);
+}
+
+}  // extern "C"

@@ -1,0 +1,580 @@
+// RMSNorm and fused per-head RMSNorm + split-half RoPE, forward and backward.
+//
+// Mapping: a "row" (one token of the hidden state, or one (token, head) of Q/K) is owned by an
+// aligned group of TPR lanes; lane t of the group holds the 16-byte vectors t, t+TPR, ... of the
+// row in registers, so x is read from HBM exactly once per pass and every row reduction is a
+// DPP/swizzle butterfly inside the group (TPR <= 64) or wave butterflies + LDS (TPR = 256).
+// Weight gradients are accumulated per lane across the rows a workgroup visits, folded across the
+// workgroup in a fixed order, written as one fp32 partial row per workgroup, and summed over
+// workgroups by a fixed-shape column-sum tree: the result is bitwise deterministic.
+#include "common.h"
+
+namespace {
+
+constexpr int kBlock = 256;
+
+template <int TPR> Q3_DEV float row_sum(float x, float* red) {
+  if constexpr (TPR <= 64) {
+    return group_sum<TPR>(x);
+  } else {
+    x = group_sum<64>(x);
+    const int w = threadIdx.x >> 6;
+    __syncthreads();
+    if (lane_id() == 0) red[w] = x;
+    __syncthreads();
+    float s = 0.f;
+#pragma unroll
+    for (int i = 0; i < TPR / 64; ++i) s += red[i];
+    return s;
+  }
+}
+
+// ---------------------------------------------------------------- RMSNorm forward
+template <typename T, int TPR, int MAXV>
+__global__ __launch_bounds__(kBlock) void rmsnorm_fwd_kernel(const typename T::storage* __restrict__ x,
+                                                             const typename T::storage* __restrict__ w,
+                                                             typename T::storage* __restrict__ y, int64_t rows,
+                                                             int h, float eps) {
+  constexpr int V = T::vec;
+  constexpr int RPB = kBlock / TPR;
+  __shared__ float red[kBlock / 64];
+  const int nvec = h / V;
+  const int t = threadIdx.x % TPR, g = threadIdx.x / TPR;
+  const float inv_h = 1.f / (float)h;
+  for (int64_t base = (int64_t)blockIdx.x * RPB; base < rows; base += (int64_t)gridDim.x * RPB) {
+    const int64_t row = base + g;
+    const bool valid = row < rows;
+    Vec<T> xv[MAXV];
+    float ss = 0.f;
+#pragma unroll
+    for (int j = 0; j < MAXV; ++j) {
+      const int vi = j * TPR + t;
+      if (valid && vi < nvec) {
+        xv[j] = load_vec<T>(x + row * h + (int64_t)vi * V);
+#pragma unroll
+        for (int e = 0; e < V; ++e) ss += xv[j].v[e] * xv[j].v[e];
+      }
+    }
+    const float inv = rsqrtf(row_sum<TPR>(ss, red) * inv_h + eps);
+#pragma unroll
+    for (int j = 0; j < MAXV; ++j) {
+      const int vi = j * TPR + t;
+      if (valid && vi < nvec) {
+        Vec<T> wv = load_vec<T>(w + (int64_t)vi * V), o;
+#pragma unroll
+        for (int e = 0; e < V; ++e) o.v[e] = xv[j].v[e] * inv * wv.v[e];
+        store_vec<T>(y + row * h + (int64_t)vi * V, o);
+      }
+    }
+  }
+}
+
+// ---------------------------------------------------------------- RMSNorm backward (dx + dw partials)
+template <typename T, int TPR, int MAXV>
+__global__ __launch_bounds__(kBlock) void rmsnorm_bwd_kernel(const typename T::storage* __restrict__ x,
+                                                             const typename T::storage* __restrict__ w,
+                                                             const typename T::storage* __restrict__ dy,
+                                                             typename T::storage* __restrict__ dx,
+                                                             float* __restrict__ partial, int64_t rows, int h,
+                                                             float eps) {
+  constexpr int V = T::vec;
+  constexpr int RPB = kBlock / TPR;
+  extern __shared__ float fold[];  // h floats
+  __shared__ float red[kBlock / 64];
+  const int nvec = h / V;
+  const int t = threadIdx.x % TPR, g = threadIdx.x / TPR;
+  const float inv_h = 1.f / (float)h;
+  float acc[MAXV][V];
+  Vec<T> wv[MAXV];
+#pragma unroll
+  for (int j = 0; j < MAXV; ++j) {
+    const int vi = j * TPR + t;
+    if (vi < nvec) wv[j] = load_vec<T>(w + (int64_t)vi * V);
+#pragma unroll
+    for (int e = 0; e < V; ++e) acc[j][e] = 0.f;
+  }
+  for (int64_t base = (int64_t)blockIdx.x * RPB; base < rows; base += (int64_t)gridDim.x * RPB) {
+    const int64_t row = base + g;
+    const bool valid = row < rows;
+    Vec<T> xv[MAXV], gv[MAXV];
+    float ss = 0.f, dot = 0.f;
+#pragma unroll
+    for (int j = 0; j < MAXV; ++j) {
+      const int vi = j * TPR + t;
+      if (valid && vi < nvec) {
+        xv[j] = load_vec<T>(x + row * h + (int64_t)vi * V);
+        gv[j] = load_vec<T>(dy + row * h + (int64_t)vi * V);
+#pragma unroll
+        for (int e = 0; e < V; ++e) {
+          ss += xv[j].v[e] * xv[j].v[e];
+          dot += gv[j].v[e] * wv[j].v[e] * xv[j].v[e];
+        }
+      }
+    }
+    ss = row_sum<TPR>(ss, red);
+    dot = row_sum<TPR>(dot, red);
+    const float inv = rsqrtf(ss * inv_h + eps);
+    const float c = inv * inv * inv * dot * inv_h;  // inv * (inv^2 * mean(g*w*x))
+#pragma unroll
+    for (int j = 0; j < MAXV; ++j) {
+      const int vi = j * TPR + t;
+      if (valid && vi < nvec) {
+        Vec<T> o;
+#pragma unroll
+        for (int e = 0; e < V; ++e) {
+          o.v[e] = gv[j].v[e] * wv[j].v[e] * inv - xv[j].v[e] * c;
+          acc[j][e] += gv[j].v[e] * xv[j].v[e] * inv;
+        }
+        store_vec<T>(dx + row * h + (int64_t)vi * V, o);
+      }
+    }
+  }
+  // Fold the RPB row groups of this workgroup in a fixed order, then write one partial row.
+  for (int gi = 0; gi < RPB; ++gi) {
+    if (g == gi) {
+#pragma unroll
+      for (int j = 0; j < MAXV; ++j) {
+        const int vi = j * TPR + t;
+        if (vi < nvec) {
+#pragma unroll
+          for (int e = 0; e < V; ++e) {
+            const int c = vi * V + e;
+            fold[c] = (gi == 0) ? acc[j][e] : fold[c] + acc[j][e];
+          }
+        }
+      }
+    }
+    __syncthreads();
+  }
+  for (int c = threadIdx.x; c < h; c += kBlock) partial[(int64_t)blockIdx.x * h + c] = fold[c];
+}
+
+// Column sums of an fp32 [R][h] partial matrix as a fixed-shape tree: a workgroup reduces a
+// 64-row x 64-column block (4 row groups of 16 rows, folded in order through LDS) into one row of
+// the next level.  Two levels cover R <= 4096.  Same inputs -> same summation order -> bitwise
+// reproducible results.
+template <typename O>
+__global__ __launch_bounds__(kBlock) void colsum_level_kernel(const float* __restrict__ in,
+                                                              typename O::storage* __restrict__ out, int rows, int h) {
+  __shared__ float fold[4][64];
+  const int c = blockIdx.x * 64 + (threadIdx.x & 63), grp = threadIdx.x >> 6;
+  const int r0 = blockIdx.y * 64 + grp * 16;
+  float s = 0.f;
+  if (c < h) {
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+      const int r = r0 + i;
+      if (r < rows) s += in[(int64_t)r * h + c];
+    }
+  }
+  fold[grp][threadIdx.x & 63] = s;
+  __syncthreads();
+  if (grp == 0 && c < h) {
+    const int l = threadIdx.x & 63;
+    out[(int64_t)blockIdx.y * h + c] = from_f32<O>(((fold[0][l] + fold[1][l]) + fold[2][l]) + fold[3][l]);
+  }
+}
+
+// dw[c] = sum over the nb partial rows in `part`; `part` must have room for nb + ceil(nb/64) rows.
+template <typename T> void colsum(float* part, typename T::storage* dw, int nb, int h, hipStream_t s) {
+  const unsigned gx = (unsigned)((h + 63) / 64);
+  if (nb <= 64) {
+    colsum_level_kernel<T><<<dim3(gx, 1), kBlock, 0, s>>>(part, dw, nb, h);
+    return;
+  }
+  const int r2 = (nb + 63) / 64;
+  float* level2 = part + (int64_t)nb * h;
+  colsum_level_kernel<F32><<<dim3(gx, (unsigned)r2), kBlock, 0, s>>>(part, level2, nb, h);
+  colsum_level_kernel<T><<<dim3(gx, 1), kBlock, 0, s>>>(level2, dw, r2, h);
+}
+
+// ---------------------------------------------------------------- generic (scalar) row kernels
+// One wave per row, scalar element loop: any h (rmsnorm) or any even d (norm+rope).
+// `heads` > 0 enables the rotation (cos/sin indexed by row / heads).
+template <typename T>
+__global__ __launch_bounds__(kBlock) void rownorm_generic_fwd(const typename T::storage* __restrict__ x,
+                                                              const typename T::storage* __restrict__ w,
+                                                              const typename T::storage* __restrict__ cs,
+                                                              const typename T::storage* __restrict__ sn,
+                                                              typename T::storage* __restrict__ y, int64_t rows,
+                                                              int h, int heads, float eps) {
+  const int64_t row = (int64_t)blockIdx.x * (kBlock / 64) + (threadIdx.x >> 6);
+  if (row >= rows) return;  // whole wave exits together
+  const int l = lane_id();
+  const typename T::storage* xr = x + row * h;
+  float ss = 0.f;
+  for (int e = l; e < h; e += 64) {
+    const float v = to_f32<T>(xr[e]);
+    ss += v * v;
+  }
+  const float inv = rsqrtf(group_sum<64>(ss) / (float)h + eps);
+  const int half = h / 2;
+  const int64_t tok = heads > 0 ? row / heads : 0;
+  for (int e = l; e < h; e += 64) {
+    const float n = to_f32<T>(xr[e]) * inv * to_f32<T>(w[e]);
+    float o = n;
+    if (heads > 0) {
+      const int p = e < half ? e + half : e - half;
+      const float np = to_f32<T>(xr[p]) * inv * to_f32<T>(w[p]);
+      const float s = e < half ? -1.f : 1.f;
+      o = n * to_f32<T>(cs[tok * h + e]) + s * np * to_f32<T>(sn[tok * h + e]);
+    }
+    y[row * h + e] = from_f32<T>(o);
+  }
+}
+
+template <typename T>
+__global__ __launch_bounds__(kBlock) void rownorm_generic_bwd(const typename T::storage* __restrict__ x,
+                                                              const typename T::storage* __restrict__ w,
+                                                              const typename T::storage* __restrict__ cs,
+                                                              const typename T::storage* __restrict__ sn,
+                                                              const typename T::storage* __restrict__ dy,
+                                                              typename T::storage* __restrict__ dx,
+                                                              float* __restrict__ partial, int64_t rows, int h,
+                                                              int heads, float eps) {
+  // Each workgroup owns a contiguous slab of rows; its 4 waves take rows round-robin and each wave
+  // accumulates its weight-gradient row in its own partial row of global memory (L2 resident), so
+  // the fixed-order column sum over all partial rows is deterministic.
+  const int wv = threadIdx.x >> 6, l = lane_id();
+  const int64_t per = (rows + gridDim.x - 1) / gridDim.x;
+  const int64_t r0 = (int64_t)blockIdx.x * per, r1 = r0 + per < rows ? r0 + per : rows;
+  const int half = h / 2;
+  float* mine = partial + ((int64_t)blockIdx.x * 4 + wv) * h;
+  for (int e = l; e < h; e += 64) mine[e] = 0.f;
+  for (int64_t row = r0 + wv; row < r1; row += 4) {
+    const int64_t tok = heads > 0 ? row / heads : 0;
+    float ss = 0.f, dot = 0.f;
+    for (int e = l; e < h; e += 64) {
+      const float xv = to_f32<T>(x[row * h + e]);
+      float g = to_f32<T>(dy[row * h + e]);
+      if (heads > 0) {
+        const int p = e < half ? e + half : e - half;
+        const float s = e < half ? 1.f : -1.f;
+        g = g * to_f32<T>(cs[tok * h + e]) + s * to_f32<T>(dy[row * h + p]) * to_f32<T>(sn[tok * h + p]);
+      }
+      ss += xv * xv;
+      dot += g * to_f32<T>(w[e]) * xv;
+    }
+    ss = group_sum<64>(ss);
+    dot = group_sum<64>(dot);
+    const float inv = rsqrtf(ss / (float)h + eps);
+    const float c = inv * inv * inv * dot / (float)h;
+    for (int e = l; e < h; e += 64) {
+      const float xv = to_f32<T>(x[row * h + e]);
+      float g = to_f32<T>(dy[row * h + e]);
+      if (heads > 0) {
+        const int p = e < half ? e + half : e - half;
+        const float s = e < half ? 1.f : -1.f;
+        g = g * to_f32<T>(cs[tok * h + e]) + s * to_f32<T>(dy[row * h + p]) * to_f32<T>(sn[tok * h + p]);
+      }
+      dx[row * h + e] = from_f32<T>(g * to_f32<T>(w[e]) * inv - xv * c);
+      mine[e] += g * xv * inv;
+    }
+  }
+}
+
+// ---------------------------------------------------------------- fused norm + rope (vector path)
+// TPR = d / VEC lanes per (token, head) row, one 16-byte vector per lane; the rotation partner of
+// lane t is lane t ^ (TPR/2) (requires (d/2) % VEC == 0 and TPR a power of two <= 64).
+template <int TPR> Q3_DEV float partner(float v) {
+  if constexpr (TPR == 16) {
+    // row_ror:8 inside a 16-lane DPP row == xor 8.
+    return __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, v), 0x128, 0xF, 0xF, true));
+  } else {
+    return __shfl_xor(v, TPR / 2, 64);
+  }
+}
+
+template <typename T, int TPR>
+__global__ __launch_bounds__(kBlock) void norm_rope_fwd_kernel(const typename T::storage* __restrict__ x,
+                                                               const typename T::storage* __restrict__ w,
+                                                               const typename T::storage* __restrict__ cs,
+                                                               const typename T::storage* __restrict__ sn,
+                                                               typename T::storage* __restrict__ y, int64_t rows,
+                                                               int heads, float eps) {
+  constexpr int V = T::vec, D = TPR * V, RPB = kBlock / TPR;
+  const int t = threadIdx.x % TPR, g = threadIdx.x / TPR;
+  const float sign = (t < TPR / 2) ? -1.f : 1.f;
+  const Vec<T> wv = load_vec<T>(w + t * V);
+  for (int64_t base = (int64_t)blockIdx.x * RPB; base < rows; base += (int64_t)gridDim.x * RPB) {
+    const int64_t row = base + g;
+    const bool valid = row < rows;
+    const int64_t tok = row / heads;
+    Vec<T> xv, cv, sv;
+    float ss = 0.f;
+    if (valid) {
+      xv = load_vec<T>(x + row * D + t * V);
+      cv = load_vec<T>(cs + tok * D + t * V);
+      sv = load_vec<T>(sn + tok * D + t * V);
+#pragma unroll
+      for (int e = 0; e < V; ++e) ss += xv.v[e] * xv.v[e];
+    }
+    const float inv = rsqrtf(group_sum<TPR>(ss) * (1.f / D) + eps);
+    Vec<T> o;
+#pragma unroll
+    for (int e = 0; e < V; ++e) {
+      const float n = xv.v[e] * inv * wv.v[e];
+      const float np = partner<TPR>(n);
+      o.v[e] = n * cv.v[e] + sign * np * sv.v[e];
+    }
+    if (valid) store_vec<T>(y + row * D + t * V, o);
+  }
+}
+
+template <typename T, int TPR>
+__global__ __launch_bounds__(kBlock) void norm_rope_bwd_kernel(const typename T::storage* __restrict__ x,
+                                                               const typename T::storage* __restrict__ w,
+                                                               const typename T::storage* __restrict__ cs,
+                                                               const typename T::storage* __restrict__ sn,
+                                                               const typename T::storage* __restrict__ dy,
+                                                               typename T::storage* __restrict__ dx,
+                                                               float* __restrict__ partial, int64_t rows, int heads,
+                                                               float eps) {
+  constexpr int V = T::vec, D = TPR * V, RPB = kBlock / TPR;
+  __shared__ float fold[D];
+  const int t = threadIdx.x % TPR, g = threadIdx.x / TPR;
+  const float sign = (t < TPR / 2) ? 1.f : -1.f;
+  const Vec<T> wv = load_vec<T>(w + t * V);
+  float acc[V];
+#pragma unroll
+  for (int e = 0; e < V; ++e) acc[e] = 0.f;
+  for (int64_t base = (int64_t)blockIdx.x * RPB; base < rows; base += (int64_t)gridDim.x * RPB) {
+    const int64_t row = base + g;
+    const bool valid = row < rows;
+    const int64_t tok = row / heads;
+    Vec<T> xv, gv, cv, sv;
+    if (valid) {
+      xv = load_vec<T>(x + row * D + t * V);
+      gv = load_vec<T>(dy + row * D + t * V);
+      cv = load_vec<T>(cs + tok * D + t * V);
+      sv = load_vec<T>(sn + tok * D + t * V);
+    } else {
+#pragma unroll
+      for (int e = 0; e < V; ++e) xv.v[e] = gv.v[e] = cv.v[e] = sv.v[e] = 0.f;
+    }
+    float ss = 0.f, dot = 0.f;
+    float ng[V];
+#pragma unroll
+    for (int e = 0; e < V; ++e) {
+      const float gs_p = partner<TPR>(gv.v[e] * sv.v[e]);  // dy[p] * sin[p]
+      ng[e] = gv.v[e] * cv.v[e] + sign * gs_p;
+      ss += xv.v[e] * xv.v[e];
+      dot += ng[e] * wv.v[e] * xv.v[e];
+    }
+    ss = group_sum<TPR>(ss);
+    dot = group_sum<TPR>(dot);
+    const float inv = rsqrtf(ss * (1.f / D) + eps);
+    const float c = inv * inv * inv * dot * (1.f / D);
+    Vec<T> o;
+#pragma unroll
+    for (int e = 0; e < V; ++e) {
+      o.v[e] = ng[e] * wv.v[e] * inv - xv.v[e] * c;
+      acc[e] += ng[e] * xv.v[e] * inv;
+    }
+    if (valid) store_vec<T>(dx + row * D + t * V, o);
+  }
+  for (int gi = 0; gi < RPB; ++gi) {
+    if (g == gi) {
+#pragma unroll
+      for (int e = 0; e < V; ++e) fold[t * V + e] = (gi == 0) ? acc[e] : fold[t * V + e] + acc[e];
+    }
+    __syncthreads();
+  }
+  for (int c = threadIdx.x; c < D; c += kBlock) partial[(int64_t)blockIdx.x * D + c] = fold[c];
+}
+
+// ---------------------------------------------------------------- host-side planning
+int64_t bwd_blocks(int64_t rows, int64_t h) {
+  const int64_t cap = h <= 256 ? 1024 : 512;
+  return rows < cap ? (rows < 4 ? 4 : rows) : cap;  // >= 4: the scalar path writes 4 rows per workgroup
+}
+
+// The scalar backward writes 4 partial rows per workgroup: a quarter of the workgroups keeps the
+// workspace (bwd_blocks rows) the same for both paths.
+int64_t generic_blocks(int64_t rows, int64_t h) {
+  const int64_t nb = bwd_blocks(rows, h) / 4;
+  return nb < 1 ? 1 : nb;
+}
+
+template <typename T, int TPR, int MAXV>
+int launch_fwd(const void* x, const void* w, void* y, int64_t rows, int64_t h, float eps, hipStream_t s) {
+  constexpr int RPB = kBlock / TPR;
+  int64_t g = (rows + RPB - 1) / RPB;
+  if (g > 256 * 16) g = 256 * 16;
+  typedef typename T::storage S;
+  rmsnorm_fwd_kernel<T, TPR, MAXV><<<(unsigned)g, kBlock, 0, s>>>((const S*)x, (const S*)w, (S*)y, rows, (int)h, eps);
+  return (int)hipGetLastError();
+}
+
+template <typename T, int TPR, int MAXV>
+int launch_bwd(const void* x, const void* w, const void* dy, void* dx, void* dw, float* part, int64_t rows,
+               int64_t h, float eps, hipStream_t s) {
+  typedef typename T::storage S;
+  const int64_t nb = bwd_blocks(rows, h);
+  rmsnorm_bwd_kernel<T, TPR, MAXV><<<(unsigned)nb, kBlock, h * sizeof(float), s>>>(
+      (const S*)x, (const S*)w, (const S*)dy, (S*)dx, part, rows, (int)h, eps);
+  colsum<T>(part, (S*)dw, (int)nb, (int)h, s);
+  return (int)hipGetLastError();
+}
+
+template <typename T>
+int rms_fwd_dispatch(const void* x, const void* w, void* y, int64_t rows, int64_t h, float eps, hipStream_t s) {
+  constexpr int V = T::vec;
+  typedef typename T::storage S;
+  const int64_t nvec = h / V;
+  if (h % V == 0) {
+    if (nvec <= 8) return launch_fwd<T, 8, 1>(x, w, y, rows, h, eps, s);
+    if (nvec <= 16) return launch_fwd<T, 16, 1>(x, w, y, rows, h, eps, s);
+    if (nvec <= 32) return launch_fwd<T, 32, 1>(x, w, y, rows, h, eps, s);
+    if (nvec <= 64) return launch_fwd<T, 64, 1>(x, w, y, rows, h, eps, s);
+    if (nvec <= 64 * 4) return launch_fwd<T, 64, 4>(x, w, y, rows, h, eps, s);
+    if (nvec <= 64 * 8) return launch_fwd<T, 64, 8>(x, w, y, rows, h, eps, s);
+    if (nvec <= 256 * 8) return launch_fwd<T, 256, 8>(x, w, y, rows, h, eps, s);
+  }
+  const int64_t g = (rows + 3) / 4;
+  rownorm_generic_fwd<T><<<(unsigned)g, kBlock, 0, s>>>((const S*)x, (const S*)w, nullptr, nullptr, (S*)y, rows,
+                                                        (int)h, 0, eps);
+  return (int)hipGetLastError();
+}
+
+template <typename T>
+int rms_bwd_dispatch(const void* x, const void* w, const void* dy, void* dx, void* dw, float* part, int64_t rows,
+                     int64_t h, float eps, hipStream_t s) {
+  constexpr int V = T::vec;
+  typedef typename T::storage S;
+  const int64_t nvec = h / V;
+  if (h % V == 0) {
+    if (nvec <= 8) return launch_bwd<T, 8, 1>(x, w, dy, dx, dw, part, rows, h, eps, s);
+    if (nvec <= 16) return launch_bwd<T, 16, 1>(x, w, dy, dx, dw, part, rows, h, eps, s);
+    if (nvec <= 32) return launch_bwd<T, 32, 1>(x, w, dy, dx, dw, part, rows, h, eps, s);
+    if (nvec <= 64) return launch_bwd<T, 64, 1>(x, w, dy, dx, dw, part, rows, h, eps, s);
+    if (nvec <= 64 * 4) return launch_bwd<T, 64, 4>(x, w, dy, dx, dw, part, rows, h, eps, s);
+    if (nvec <= 64 * 8) return launch_bwd<T, 64, 8>(x, w, dy, dx, dw, part, rows, h, eps, s);
+    if (nvec <= 256 * 4) return launch_bwd<T, 256, 4>(x, w, dy, dx, dw, part, rows, h, eps, s);
+  }
+  const int64_t gb = generic_blocks(rows, h);
+  rownorm_generic_bwd<T><<<(unsigned)gb, kBlock, 0, s>>>((const S*)x, (const S*)w, nullptr, nullptr, (const S*)dy,
+                                                         (S*)dx, part, rows, (int)h, 0, eps);
+  colsum<T>(part, (S*)dw, (int)(4 * gb), (int)h, s);
+  return (int)hipGetLastError();
+}
+
+template <typename T>
+int nr_fwd_dispatch(const void* x, const void* w, const void* cs, const void* sn, void* y, int64_t rows,
+                    int64_t heads, int64_t d, float eps, hipStream_t s) {
+  constexpr int V = T::vec;
+  typedef typename T::storage S;
+  const int64_t tpr = d / V;
+  auto grid = [&](int t) {
+    int64_t g = (rows + kBlock / t - 1) / (kBlock / t);
+    return (unsigned)(g > 256 * 16 ? 256 * 16 : g);
+  };
+  if (d % V == 0 && (d / 2) % V == 0) {
+    if (tpr == 8) {
+      norm_rope_fwd_kernel<T, 8><<<grid(8), kBlock, 0, s>>>((const S*)x, (const S*)w, (const S*)cs, (const S*)sn,
+                                                             (S*)y, rows, (int)heads, eps);
+      return (int)hipGetLastError();
+    }
+    if (tpr == 16) {
+      norm_rope_fwd_kernel<T, 16><<<grid(16), kBlock, 0, s>>>((const S*)x, (const S*)w, (const S*)cs,
+                                                               (const S*)sn, (S*)y, rows, (int)heads, eps);
+      return (int)hipGetLastError();
+    }
+    if (tpr == 32) {
+      norm_rope_fwd_kernel<T, 32><<<grid(32), kBlock, 0, s>>>((const S*)x, (const S*)w, (const S*)cs,
+                                                               (const S*)sn, (S*)y, rows, (int)heads, eps);
+      return (int)hipGetLastError();
+    }
+  }
+  rownorm_generic_fwd<T><<<(unsigned)((rows + 3) / 4), kBlock, 0, s>>>((const S*)x, (const S*)w, (const S*)cs,
+                                                                       (const S*)sn, (S*)y, rows, (int)d,
+                                                                       (int)heads, eps);
+  return (int)hipGetLastError();
+}
+
+template <typename T>
+int nr_bwd_dispatch(const void* x, const void* w, const void* cs, const void* sn, const void* dy, void* dx, void* dw,
+                    float* part, int64_t rows, int64_t heads, int64_t d, float eps, hipStream_t s) {
+  constexpr int V = T::vec;
+  typedef typename T::storage S;
+  const int64_t tpr = d / V;
+  int64_t nb = bwd_blocks(rows, d);
+  bool done = false;
+  if (d % V == 0 && (d / 2) % V == 0) {
+    if (tpr == 8) {
+      norm_rope_bwd_kernel<T, 8><<<(unsigned)nb, kBlock, 0, s>>>((const S*)x, (const S*)w, (const S*)cs,
+                                                                  (const S*)sn, (const S*)dy, (S*)dx, part, rows,
+                                                                  (int)heads, eps);
+      done = true;
+    } else if (tpr == 16) {
+      norm_rope_bwd_kernel<T, 16><<<(unsigned)nb, kBlock, 0, s>>>((const S*)x, (const S*)w, (const S*)cs,
+                                                                   (const S*)sn, (const S*)dy, (S*)dx, part, rows,
+                                                                   (int)heads, eps);
+      done = true;
+    } else if (tpr == 32) {
+      norm_rope_bwd_kernel<T, 32><<<(unsigned)nb, kBlock, 0, s>>>((const S*)x, (const S*)w, (const S*)cs,
+                                                                   (const S*)sn, (const S*)dy, (S*)dx, part, rows,
+                                                                   (int)heads, eps);
+      done = true;
+    }
+  }
+  if (!done) {
+    const int64_t gb = generic_blocks(rows, d);
+    rownorm_generic_bwd<T><<<(unsigned)gb, kBlock, 0, s>>>((const S*)x, (const S*)w, (const S*)cs, (const S*)sn,
+                                                           (const S*)dy, (S*)dx, part, rows, (int)d, (int)heads, eps);
+    nb = 4 * gb;
+  }
+  colsum<T>(part, (S*)dw, (int)nb, (int)d, s);
+  return (int)hipGetLastError();
+}
+
+bool dtype_ok(int dt) { return dt == Q3_F32 || dt == Q3_F16 || dt == Q3_BF16; }
+
+}  // namespace
+
+#define Q3_DISPATCH(dt, FN, ...)                                 \
+  ((dt) == Q3_BF16 ? FN<BF16>(__VA_ARGS__)                       \
+                   : (dt) == Q3_F16 ? FN<F16>(__VA_ARGS__) : FN<F32>(__VA_ARGS__))
+
+extern "C" {
+
+int q3_rmsnorm_fwd(int dtype, const void* x, const void* w, void* y, int64_t rows, int64_t h, float eps,
+                   hipStream_t stream) {
+  Q3_REQUIRE(dtype_ok(dtype) && x && w && y && rows > 0 && h > 0 && h <= (1 << 20) && eps > 0.f);
+  return Q3_DISPATCH(dtype, rms_fwd_dispatch, x, w, y, rows, h, eps, stream);
+}
+
+size_t q3_rmsnorm_bwd_workspace_bytes(int64_t rows, int64_t h) {
+  const int64_t nb = bwd_blocks(rows, h);
+  return (size_t)(nb + (nb + 63) / 64) * (size_t)h * sizeof(float);
+}
+
+int q3_rmsnorm_bwd(int dtype, const void* x, const void* w, const void* dy, void* dx, void* dw, void* workspace,
+                   int64_t rows, int64_t h, float eps, hipStream_t stream) {
+  Q3_REQUIRE(dtype_ok(dtype) && x && w && dy && dx && dw && workspace && rows > 0 && h > 0 && eps > 0.f);
+  Q3_REQUIRE(h <= 16384);  // LDS fold buffer of the vector path: h floats
+  return Q3_DISPATCH(dtype, rms_bwd_dispatch, x, w, dy, dx, dw, (float*)workspace, rows, h, eps, stream);
+}
+
+int q3_norm_rope_fwd(int dtype, const void* x, const void* w, const void* cos, const void* sin, void* y,
+                     int64_t tokens, int64_t heads, int64_t d, float eps, hipStream_t stream) {
+  Q3_REQUIRE(dtype_ok(dtype) && x && w && cos && sin && y && tokens > 0 && heads > 0 && d > 0 && d % 2 == 0 &&
+             d <= 4096 && eps > 0.f);
+  return Q3_DISPATCH(dtype, nr_fwd_dispatch, x, w, cos, sin, y, tokens * heads, heads, d, eps, stream);
+}
+
+size_t q3_norm_rope_bwd_workspace_bytes(int64_t tokens, int64_t heads, int64_t d) {
+  const int64_t nb = bwd_blocks(tokens * heads, d);
+  return (size_t)(nb + (nb + 63) / 64) * (size_t)d * sizeof(float);
+}
+
+int q3_norm_rope_bwd(int dtype, const void* x, const void* w, const void* cos, const void* sin, const void* dy,
+                     void* dx, void* dw, void* workspace, int64_t tokens, int64_t heads, int64_t d, float eps,
+                     hipStream_t stream) {
+  Q3_REQUIRE(dtype_ok(dtype) && x && w && cos && sin && dy && dx && dw && workspace && tokens > 0 && heads > 0 &&
+             d > 0 && d % 2 == 0 && d <= 4096 && eps > 0.f);
+  return Q3_DISPATCH(dtype, nr_bwd_dispatch, x, w, cos, sin, dy, dx, dw, (float*)workspace, tokens * heads, heads, d,
+                     eps, stream);
+}
+
+}  // extern "C"

@@ -1,0 +1,100 @@
+"""Bias-free Linear with matrix-core forward, dX and dW GEMMs.
+
+Mirrors ``qwen3_triton/kernels/linear.py:45-105``: ``matmul(a, b, *, optimized, output_dtype)``
+computes A[M,K] @ B[K,N] for strided matrices into a contiguous result with fp32 accumulation,
+and ``linear(x, weight)`` is Y = X W^T with dX = dY W and dW = dY^T X.
+
+Dispatch: bf16/fp16 operands go to ``q3_gemm_nt`` (MFMA), which wants both operands with K
+contiguous; an operand that is K-major only as a transposed view is first re-laid out by
+``q3_transpose`` (a bandwidth-bound copy).  fp32 or oddly strided operands use the SIMT
+``q3_gemm_strided`` kernel.  ``optimized`` is accepted for signature compatibility; the tile
+plan is fixed for gfx950.
+"""
+import torch
+
+from .. import _hip as H
+from . import _ops
+
+
+def _k_major_rows(t):
+    """Return (tensor, row_stride) with t's rows (dim 0) K-contiguous, or None if impossible."""
+    if t.stride(1) == 1 and t.stride(0) >= t.shape[1]:
+        return t, t.stride(0)
+    if t.stride(0) == 1 and t.stride(1) >= t.shape[0]:
+        # t is the transpose of a row-major [K, rows] matrix: re-lay it out.
+        src = t.t()
+        if not src.is_contiguous():
+            src = src.contiguous()
+        tt = _ops.transpose_last2(src)
+        return tt, tt.stride(0)
+    return None
+
+
+def _aligned(t, ld):
+    return t.data_ptr() % 16 == 0 and ld % 8 == 0
+
+
+def gemm_nt_into(a, lda, bnk, ldb, out, m, n, k, *, alpha=1.0, accumulate=False):
+    """out[m,n] (+)= alpha * a[m,k] . bnk[n,k]^T on the matrix cores (a, bnk K-contiguous rows)."""
+    H.call("q3_gemm_nt", H.code(a.dtype), H.code(out.dtype), a.data_ptr(), lda, bnk.data_ptr(), ldb,
+           out.data_ptr(), out.stride(0), m, n, k, float(alpha), int(accumulate), H.stream())
+
+
+def matmul_into(a, b, out, *, alpha=1.0, accumulate=False):
+    m, k = a.shape
+    n = b.shape[1]
+    if a.dtype in (torch.bfloat16, torch.float16) and k % 8 == 0:
+        ar = _k_major_rows(a)
+        br = _k_major_rows(b.t())
+        if ar is not None and br is not None and _aligned(*ar) and _aligned(*br):
+            gemm_nt_into(ar[0], ar[1], br[0], br[1], out, m, n, k, alpha=alpha, accumulate=accumulate)
+            return out
+    H.call("q3_gemm_strided", H.code(a.dtype), H.code(out.dtype), a.data_ptr(), a.stride(0), a.stride(1),
+           b.data_ptr(), b.stride(0), b.stride(1), out.data_ptr(), out.stride(0), m, n, k, float(alpha),
+           int(accumulate), H.stream())
+    return out
+
+
+def matmul(a, b, *, optimized=False, output_dtype=None):
+    """A[M,K] @ B[K,N]; strided matrices, contiguous result, FP32 accumulation."""
+    if not (a.is_cuda and b.is_cuda) or a.device != b.device:
+        raise ValueError('Same-device ROCm matrices required; no fallback')
+    if a.ndim != 2 or b.ndim != 2 or a.shape[1] != b.shape[0]:
+        raise ValueError('Expected [M,K] and [K,N]')
+    if a.dtype != b.dtype or a.dtype not in (torch.bfloat16, torch.float16, torch.float32):
+        raise TypeError('Matching BF16/FP16/FP32 matrices required')
+    if min(*a.shape, *b.shape) < 1 or min(*a.stride(), *b.stride()) < 1:
+        raise ValueError('Nonempty, positive-stride matrices required')
+    dtype = output_dtype or a.dtype
+    if dtype not in (torch.bfloat16, torch.float16, torch.float32):
+        raise TypeError('Floating point output required')
+    out = torch.empty((a.shape[0], b.shape[1]), device=a.device, dtype=dtype)
+    return matmul_into(a, b, out)
+
+
+class _Linear(torch.autograd.Function):
+    @staticmethod
+    def forward(ctx, x, weight, optimized):
+        if x.ndim < 2 or weight.ndim != 2 or x.shape[-1] != weight.shape[1]:
+            raise ValueError('Expected X[...,K] and weight[N,K]')
+        if not x.is_contiguous():
+            raise ValueError('Linear input must be contiguous; no hidden layout copy')
+        flat = x.view(-1, x.shape[-1])
+        y = matmul(flat, weight.t(), optimized=optimized)
+        ctx.save_for_backward(flat, weight)
+        ctx.shape = x.shape
+        ctx.optimized = optimized
+        return y.view(*x.shape[:-1], weight.shape[0])
+
+    @staticmethod
+    def backward(ctx, dy):
+        x, w = ctx.saved_tensors
+        dy = dy.contiguous().view(-1, w.shape[0])
+        dx = matmul(dy, w, optimized=ctx.optimized).view(ctx.shape) if ctx.needs_input_grad[0] else None
+        dw = matmul(dy.t(), x, optimized=ctx.optimized) if ctx.needs_input_grad[1] else None
+        return dx, dw, None
+
+
+def linear(x, weight, *, optimized=False):
+    """``kernels/linear.py:104``."""
+    return _Linear.apply(x, weight, optimized)

@@ -1,0 +1,37 @@
+"""RMSNorm with a deterministic weight-gradient reduction.
+
+Mirrors ``qwen3_triton/kernels/norm.py:39-66`` (``_RMSNorm`` / ``rms_norm``): same signature,
+same validation, fp32 internals; the forward is ``q3_rmsnorm_fwd`` and the backward
+``q3_rmsnorm_bwd`` (dx plus a fixed-order two-level dW sum, no float atomics).
+"""
+import torch
+
+from . import _ops
+
+
+class _RMSNorm(torch.autograd.Function):
+    @staticmethod
+    def forward(ctx, x, weight, eps, optimized):
+        if not x.is_cuda or x.device != weight.device or x.dtype != weight.dtype:
+            raise ValueError('Same-device/dtype ROCm input and weight required; no fallback')
+        if x.dtype not in (torch.float32, torch.bfloat16, torch.float16):
+            raise TypeError('Floating point required')
+        if weight.ndim != 1 or not x.is_contiguous() or not weight.is_contiguous() or \
+                x.shape[-1] != weight.numel() or x.numel() < 1:
+            raise ValueError('Contiguous [...,H] input and [H] weight required')
+        if eps <= 0:
+            raise ValueError('Positive epsilon required')
+        ctx.save_for_backward(x, weight)
+        ctx.eps = eps
+        return _ops.rmsnorm_fwd(x, weight, eps)
+
+    @staticmethod
+    def backward(ctx, dy):
+        x, w = ctx.saved_tensors
+        dx, dw = _ops.rmsnorm_bwd(x, w, dy.contiguous(), ctx.eps)
+        return dx, dw, None, None
+
+
+def rms_norm(x, weight, eps=1e-6, *, optimized=False):
+    """``kernels/norm.py:65``."""
+    return _RMSNorm.apply(x, weight, eps, optimized)

@@ -1,0 +1,77 @@
+"""Matrix-core GEMM (q3_gemm_nt) and the strided fallback vs fp64 torch.matmul on the host."""
+import pytest
+import torch
+
+from _util import cosine, max_rel, randn, seeded
+
+from qwen3_triton.kernels.linear import gemm_nt_into, linear, matmul, matmul_into
+
+pytestmark = pytest.mark.gpu
+
+
+def ref(a, b):
+    return (a.double() @ b.double())
+
+
+@pytest.mark.parametrize("m,n,k", [(32, 32, 16), (256, 128, 64), (300, 200, 8), (1, 4096, 4096), (8, 1024, 4096),
+                                   (513, 687, 688), (2048, 1024, 4096), (64, 151936 // 16, 256)])
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+def test_gemm_nt_shapes(m, n, k, dtype):
+    print(f"gemm_nt {m}x{n}x{k} {dtype}", flush=True)
+    gen = seeded(m * 7 + n + k)
+    a = randn(m, k, gen=gen, dtype=dtype)
+    w = randn(n, k, gen=gen, dtype=dtype)
+    out = torch.empty(m, n, device="cuda", dtype=torch.float32)
+    gemm_nt_into(a.cuda(), k, w.cuda(), k, out, m, n, k)
+    e = ref(a, w.t())
+    r = max_rel(out, e)
+    assert r < 1e-5, r  # fp32 accumulation of exact bf16 products
+    y = matmul(a.cuda(), w.cuda().t())
+    assert y.dtype == dtype
+    assert max_rel(y, e) < (8e-3 if dtype == torch.bfloat16 else 1e-3)
+
+
+def test_gemm_alpha_accumulate_and_ldc():
+    gen = seeded(9)
+    a = randn(70, 64, gen=gen, dtype=torch.bfloat16)
+    b = randn(90, 64, gen=gen, dtype=torch.bfloat16)
+    c0 = randn(70, 100, gen=gen)
+    out = c0.clone().cuda()
+    gemm_nt_into(a.cuda(), 64, b.cuda(), 64, out, 70, 90, 64, alpha=0.5, accumulate=True)
+    e = c0.double().clone()
+    e[:, :90] += 0.5 * ref(a, b.t())
+    assert max_rel(out, e) < 1e-5
+    assert torch.equal(out[:, 90:].cpu(), c0[:, 90:])  # columns beyond N untouched
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
+def test_matmul_layouts(dtype):
+    """NT direct, NN and TN (operands re-laid out by the transpose kernel), and fp32 (SIMT path)."""
+    gen = seeded(10)
+    x = randn(200, 96, gen=gen, dtype=dtype)
+    w = randn(136, 96, gen=gen, dtype=dtype)
+    dy = randn(200, 136, gen=gen, dtype=dtype)
+    tol = 8e-3 if dtype == torch.bfloat16 else 1e-5
+    xd, wd, dyd = x.cuda(), w.cuda(), dy.cuda()
+    assert max_rel(matmul(xd, wd.t()), ref(x, w.t())) < tol
+    assert max_rel(matmul(dyd, wd), ref(dy, w)) < tol
+    assert max_rel(matmul(dyd.t(), xd), ref(dy.t(), x)) < tol
+    assert max_rel(matmul(xd[:, ::2], wd[:, ::2].t()), ref(x[:, ::2], w[:, ::2].t())) < tol
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
+def test_linear_autograd(dtype):
+    gen = seeded(11)
+    x = randn(4, 33, 64, gen=gen, dtype=dtype)
+    w = randn(80, 64, gen=gen, dtype=dtype, scale=0.1)
+    dy = randn(4, 33, 80, gen=gen, dtype=dtype)
+    xd, wd = x.cuda().requires_grad_(), w.cuda().requires_grad_()
+    y = linear(xd, wd)
+    dx, dw = torch.autograd.grad(y, (xd, wd), dy.cuda())
+    xr, wr = x.double().requires_grad_(), w.double().requires_grad_()
+    yr = xr @ wr.t()
+    ex, ew = torch.autograd.grad(yr, (xr, wr), dy.double())
+    tol = 2e-2 if dtype == torch.bfloat16 else 1e-5
+    for a, e in ((y, yr), (dx, ex), (dw, ew)):
+        assert max_rel(a, e) < tol
+        assert cosine(a, e) > 0.999

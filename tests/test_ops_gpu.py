@@ -1,0 +1,184 @@
+"""HIP bandwidth-bound ops vs the CPU oracle (bf16/fp16 forward: max-rel <= 2e-2 / 3e-3; gradients:
+cosine >= 0.999 and max-rel <= the same bounds; fp32: 1e-5)."""
+import pytest
+import torch
+
+import oracle as O
+from _util import cosine, max_rel, randn, seeded, tol_for
+
+from qwen3_triton.kernels import _ops
+from qwen3_triton.kernels.norm import rms_norm
+from qwen3_triton.kernels.norm_rope import norm_rope
+from qwen3_triton.kernels.rotary import apply_rotary, rotary_tables
+from qwen3_triton.kernels.activation import swiglu
+from qwen3_triton.kernels.residual import residual_add
+from qwen3_triton.kernels.embedding import embedding
+from ops.triton.rms_norm import rms_norm_triton
+from ops.triton.rope import apply_rope_triton
+from ops.triton.fused_qk_norm_rope import fused_qk_norm_rope_triton
+from ops.triton.silu_and_mul import silu_and_mul_triton
+
+pytestmark = pytest.mark.gpu
+DTYPES = [torch.bfloat16, torch.float16, torch.float32]
+
+
+def _grads(out, inputs, up):
+    return torch.autograd.grad(out, inputs, up)
+
+
+def check(actual, expected, dtype, what):
+    tol = tol_for(dtype) * (2 if dtype == torch.float32 else 1)
+    r = max_rel(actual, expected)
+    assert r <= tol, f"{what}: max-rel {r:.3e} > {tol}"
+    if expected.numel() > 1 and expected.double().abs().max() > 0:
+        c = cosine(actual, expected)
+        assert c >= 0.999, f"{what}: cosine {c:.6f}"
+
+
+@pytest.mark.parametrize("dtype", DTYPES)
+@pytest.mark.parametrize("shape", [(2, 7, 128), (1, 17, 2048), (3, 4096), (5, 24), (2, 3, 5120), (2, 8192),
+                                   (1, 1, 128), (64, 256)])
+def test_rmsnorm_fwd_bwd(shape, dtype):
+    print(f"rmsnorm {shape} {dtype}", flush=True)
+    gen = seeded(1)
+    h = shape[-1]
+    x = randn(*shape, gen=gen, dtype=dtype)
+    w = randn(h, gen=gen, dtype=dtype, scale=0.1, shift=1.0)
+    dy = randn(*shape, gen=gen, dtype=dtype)
+    xd, wd = x.cuda().requires_grad_(), w.cuda().requires_grad_()
+    y = rms_norm(xd, wd, 1e-6)
+    dx, dw = _grads(y, (xd, wd), dy.cuda())
+    check(y, O.rms_norm_reference(x, w, 1e-6), dtype, "y")
+    ex, ew = O.rms_norm_backward_reference(x, w, dy, 1e-6)
+    check(dx, ex, dtype, "dx")
+    check(dw, ew, dtype, "dw")
+    # deterministic: same inputs, bitwise-equal weight gradient
+    _, dw2 = _grads(rms_norm(xd, wd, 1e-6), (xd, wd), dy.cuda())
+    assert torch.equal(dw, dw2)
+
+
+@pytest.mark.parametrize("dtype", DTYPES)
+@pytest.mark.parametrize("b,s,hq,hk,d", [(2, 5, 4, 2, 128), (1, 17, 32, 8, 128), (2, 3, 4, 2, 64),
+                                         (1, 4, 2, 1, 24), (1, 3, 2, 2, 256)])
+def test_norm_rope_fwd_bwd(b, s, hq, hk, d, dtype):
+    print(f"norm_rope {b} {s} {hq} {hk} {d} {dtype}", flush=True)
+    gen = seeded(2)
+    q = randn(b, s, hq, d, gen=gen, dtype=dtype)
+    k = randn(b, s, hk, d, gen=gen, dtype=dtype)
+    qw = randn(d, gen=gen, dtype=dtype, scale=0.1, shift=1.0)
+    kw = randn(d, gen=gen, dtype=dtype, scale=0.1, shift=1.0)
+    # independent random tables (not real angles) exercise the general transpose
+    c = randn(b, s, d, gen=gen, dtype=dtype)
+    sn = randn(b, s, d, gen=gen, dtype=dtype)
+    gq = randn(b, s, hq, d, gen=gen, dtype=dtype)
+    gk = randn(b, s, hk, d, gen=gen, dtype=dtype)
+    dev = [t.cuda() for t in (q, k, qw, kw)]
+    for t in dev:
+        t.requires_grad_()
+    yq, yk = fused_qk_norm_rope_triton(*dev, c.cuda(), sn.cuda(), 1e-6)
+    grads = _grads((yq, yk), dev, (gq.cuda(), gk.cuda()))
+    eq, ek = O.fused_qk_norm_rope_reference(q, k, qw, kw, c, sn, 1e-6)
+    check(yq, eq, dtype, "yq")
+    check(yk, ek, dtype, "yk")
+    e = O.fused_qk_norm_rope_backward_reference(q, k, qw, kw, c, sn, gq, gk, 1e-6)
+    for a, x, n in zip(grads, e, ("dq", "dk", "dqw", "dkw")):
+        check(a, x, dtype, n)
+    # the single-tensor module API (kernels/norm_rope.py) agrees with the pair API
+    y1 = norm_rope(dev[0].detach(), dev[2].detach(), c.cuda(), sn.cuda(), 1e-6)
+    assert torch.equal(y1, yq.detach())
+
+
+@pytest.mark.parametrize("dtype", DTYPES)
+@pytest.mark.parametrize("b,s,h,d", [(2, 7, 4, 16), (1, 129, 2, 128), (2, 3, 3, 6)])
+def test_rope_both_layouts(b, s, h, d, dtype):
+    print(f"rope {b} {s} {h} {d} {dtype}", flush=True)
+    gen = seeded(3)
+    x = randn(b, s, h, d, gen=gen, dtype=dtype)
+    c = randn(b, s, d, gen=gen, dtype=dtype)
+    sn = randn(b, s, d, gen=gen, dtype=dtype)
+    gy = randn(b, s, h, d, gen=gen, dtype=dtype)
+    xd = x.cuda().requires_grad_()
+    y = apply_rotary(xd, c.cuda(), sn.cuda())
+    (dx,) = _grads(y, (xd,), gy.cuda())
+    e, _ = O.apply_rope_reference(x.transpose(1, 2), x.transpose(1, 2), c, sn)
+    check(y, e.transpose(1, 2), dtype, "y")
+    eg, _ = O.apply_rope_backward_reference(gy.transpose(1, 2), gy.transpose(1, 2), c, sn)
+    check(dx, eg.transpose(1, 2), dtype, "dx")
+    # [B,H,S,D] layout through ops.triton
+    xh = x.transpose(1, 2).contiguous().cuda().requires_grad_()
+    yq, yk = apply_rope_triton(xh, xh, c.cuda(), sn.cuda())
+    check(yq, e, dtype, "yq[BHSD]")
+    (dxh,) = _grads(yq, (xh,), gy.transpose(1, 2).contiguous().cuda())
+    check(dxh, eg, dtype, "dx[BHSD]")
+
+
+@pytest.mark.parametrize("dtype", DTYPES)
+def test_rope_tables_against_oracle(dtype):
+    pos = torch.arange(2048).repeat(2).view(2, 2048)
+    inv = O.rope_inv_freq(1e6, 128)
+    c, s = rotary_tables(pos.cuda(), inv.cuda(), dtype)
+    ec, es = O.rotary_tables_reference(pos, inv)
+    tol = {torch.float32: 2e-6, torch.float16: 1e-3, torch.bfloat16: 8e-3}[dtype]
+    assert (c.float().cpu() - ec).abs().max() <= tol
+    assert (s.float().cpu() - es).abs().max() <= tol
+    c32, _ = rotary_tables(pos.int().cuda(), inv.cuda(), dtype)
+    assert torch.equal(c32, c)
+
+
+@pytest.mark.parametrize("dtype", DTYPES)
+@pytest.mark.parametrize("shape", [(1, 1), (2, 17), (1, 129, 257), (3, 6144), (4099,)])
+def test_swiglu_fwd_bwd(shape, dtype):
+    print(f"swiglu {shape} {dtype}", flush=True)
+    gen = seeded(4)
+    gt = randn(*shape, gen=gen, dtype=dtype)
+    ut = randn(*shape, gen=gen, dtype=dtype)
+    dy = randn(*shape, gen=gen, dtype=dtype)
+    gd, ud = gt.cuda().requires_grad_(), ut.cuda().requires_grad_()
+    y = silu_and_mul_triton(gd, ud)
+    dg, du = _grads(y, (gd, ud), dy.cuda())
+    check(y, O.swiglu_reference(gt, ut), dtype, "y")
+    eg, eu = O.swiglu_backward_reference(gt, ut, dy)
+    check(dg, eg, dtype, "dg")
+    check(du, eu, dtype, "du")
+    assert torch.equal(swiglu(gd.detach(), ud.detach()), y.detach())
+
+
+@pytest.mark.parametrize("dtype", DTYPES)
+def test_residual_cast_fill_transpose(dtype):
+    gen = seeded(5)
+    a = randn(3, 1000, gen=gen, dtype=dtype)
+    b = randn(3, 1000, gen=gen, dtype=dtype)
+    c = residual_add(a.cuda(), b.cuda())
+    assert torch.equal(c.cpu(), (a.float() + b.float()).to(dtype))
+    x = randn(2, 67, 130, gen=gen, dtype=dtype)
+    assert torch.equal(_ops.transpose_last2(x.cuda()).cpu(), x.transpose(1, 2).contiguous())
+    y = _ops.cast(x.cuda(), torch.float32)
+    assert torch.equal(y.cpu(), x.float())
+    z = _ops.fill_(torch.empty(1001, device="cuda", dtype=dtype), 1.5)
+    assert bool((z == 1.5).all())
+    p = _ops.positions(2, 5, 7, "cuda")
+    assert p.cpu().tolist() == [[7, 8, 9, 10, 11]] * 2
+
+
+@pytest.mark.parametrize("dtype", DTYPES)
+@pytest.mark.parametrize("h", [64, 4096, 12])
+def test_embedding_fwd_bwd_deterministic(h, dtype):
+    gen = seeded(6)
+    v = 50
+    w = randn(v, h, gen=gen, dtype=dtype)
+    ids = torch.randint(0, v, (3, 40), generator=gen)
+    ids[0, :5] = 7  # repeated ids
+    dy = randn(3, 40, h, gen=gen, dtype=dtype)
+    wd = w.cuda().requires_grad_()
+    y = embedding(ids.cuda(), wd)
+    assert torch.equal(y.detach().cpu(), w[ids])
+    (dw,) = _grads(y, (wd,), dy.cuda())
+    check(dw, O.embedding_backward_reference(ids, dy, v), dtype, "dw")
+    (dw2,) = _grads(embedding(ids.int().cuda(), wd), (wd,), dy.cuda())
+    assert torch.equal(dw, dw2)
+
+
+def test_embedding_out_of_range_raises():
+    w = torch.randn(10, 8, device="cuda")
+    with pytest.raises(ValueError):
+        embedding(torch.tensor([[1, 10]], device="cuda"), w)
