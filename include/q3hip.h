@@ -89,8 +89,10 @@ int q3_cast(int src_dtype, int dst_dtype, const void* x, void* y, int64_t n, hip
 int q3_fill(int dtype, void* x, float value, int64_t n, hipStream_t stream);
 /* out[b, s] = start + s.  Replaces _model.py:29-32 (_positions), inference/kernels.py:12-21. */
 int q3_positions(int64_t* out, int64_t batch, int64_t seq, int64_t start, hipStream_t stream);
-/* y[b][c][r] = x[b][r][c] for 16-bit or 32-bit elements (a layout change, not arithmetic). */
-int q3_transpose(int dtype, const void* x, void* y, int64_t batch, int64_t rows, int64_t cols, hipStream_t stream);
+/* y[b][c][r] = x[b][r][c] for 16-bit or 32-bit elements (a layout change, not arithmetic); output rows
+ * have stride ldy >= rows and the pad [rows, ldy) is zero-filled. */
+int q3_transpose(int dtype, const void* x, void* y, int64_t batch, int64_t rows, int64_t cols, int64_t ldy,
+                 hipStream_t stream);
 
 /* ------------------------------------------------------------------ embedding
  * y[i,:] = w[ids[i],:].  Out-of-range ids produce zero rows and set *bad_ids (device int) to 1.
@@ -118,6 +120,50 @@ int q3_gemm_nt(int in_dtype, int out_dtype, const void* A, int64_t lda, const vo
 int q3_gemm_strided(int in_dtype, int out_dtype, const void* A, int64_t sam, int64_t sak, const void* B, int64_t sbk,
                     int64_t sbn, void* C, int64_t ldc, int64_t M, int64_t N, int64_t K, float alpha, int accumulate,
                     hipStream_t stream);
+
+/* ------------------------------------------------------------------ causal GQA flash attention
+ * Q/O [B,Hq,Lq,D], K/V [B,Hkv,Lk,D], Lk >= Lq, query i attends keys j <= i + (Lk - Lq); query head h
+ * uses KV head h/(Hq/Hkv).  LSE [B,Hq,Lq] fp32 (natural log).  On the matrix-core path
+ * (q3_attention_mfma_supported) the caller passes sequence-contiguous transposed copies of the
+ * operands contracted over the sequence: vt = V^T [B,Hkv,D,ldvt] (forward), qt = Q^T [B,Hq,D,ldqt],
+ * kt = K^T [B,Hkv,D,ldkt], dot = dO^T [B,Hq,D,ldqt] (backward), with ld* >= L, ld* % 8 == 0 and the
+ * pad zero-filled (q3_transpose does this).  Other dtypes/head sizes run a SIMT path that ignores
+ * them.  delta [B,Hq,Lq] fp32 is backward scratch (rowsum(O*dO)).
+ * Replaces: kernels/attention.py:20-50 + attention_kernels.py:9-253 (_attention_forward_kernel,
+ *           _attention_delta_kernel, _attention_dq_kernel, _attention_dkdv_fused_kernel,
+ *           _attention_kv_head_reduce_kernel), kernels/attention_precision.py:14-182,
+ *           ops/triton/attention.py:29-292, ops/triton/attention_backward.py:21-236. */
+int q3_attention_mfma_supported(int dtype, int64_t d);
+int q3_attention_fwd(int dtype, const void* q, const void* k, const void* v, const void* vt, int64_t ldvt, void* o,
+                     float* lse, int64_t B, int64_t Hq, int64_t Hkv, int64_t Lq, int64_t Lk, int64_t D, float scale,
+                     hipStream_t stream);
+int q3_attention_bwd(int dtype, const void* q, const void* k, const void* v, const void* o, const void* dout,
+                     const float* lse, const void* qt, int64_t ldqt, const void* kt, int64_t ldkt, const void* dot,
+                     float* delta, void* dq, void* dk, void* dv, int64_t B, int64_t Hq, int64_t Hkv, int64_t Lq,
+                     int64_t Lk, int64_t D, float scale, hipStream_t stream);
+
+/* ------------------------------------------------------------------ causal cross-entropy
+ * Rows r = b*S + s of logits z (row stride ld).  tgt[r] = labels[b, s+1] for s < S-1, else
+ * ignore_index (q3_ce_shift_labels).  For a vocabulary chunk z[:, 0:n] holding columns
+ * [col0, col0+n) of the full logits, q3_ce_chunk_stats writes the row max m and sum exp(z - m) and,
+ * where the target lies in the chunk, its logit into pick.  q3_ce_finish merges nchunks chunk-major
+ * partials ([nchunks][rows]) into lse[r], per-row loss lse - z_target (0 when ignored), and
+ * loss = sum / count over valid rows (fixed summation order); *bad is set to 1 for a target outside
+ * [0, vocab) that is not ignore_index.  q3_ce_chunk_grad writes
+ * dz = (exp(z - lse) - onehot(target - col0)) * (*up) / (*count) (0 for ignored rows) in out_dtype.
+ * Replaces: kernels/loss.py:6-44,46-71 (_partials, _rows, _mean, _backward, _CausalCE); together with
+ * q3_gemm_nt it is the fused LM-head + CE (no reference function; composes kernels/linear.py and
+ * kernels/loss.py). */
+int q3_ce_shift_labels(const int64_t* labels, int64_t* tgt, int64_t batch, int64_t seq, int64_t ignore_index,
+                       hipStream_t stream);
+int q3_ce_chunk_stats(int dtype, const void* z, int64_t ld, int64_t n, int64_t col0, const int64_t* tgt,
+                      float* m_out, float* s_out, float* pick, int64_t rows, hipStream_t stream);
+int q3_ce_finish(const float* m_part, const float* s_part, int nchunks, const float* pick, const int64_t* tgt,
+                 float* lse, float* loss_rows, int* bad, float* loss, float* count, int64_t rows, int64_t vocab,
+                 int64_t ignore_index, hipStream_t stream);
+int q3_ce_chunk_grad(int dtype, int out_dtype, const void* z, int64_t ld, int64_t n, int64_t col0, const int64_t* tgt,
+                     const float* lse, const float* count, const float* up, void* dz, int64_t ldo, int64_t rows,
+                     int64_t vocab, int64_t ignore_index, hipStream_t stream);
 
 #ifdef __cplusplus
 }

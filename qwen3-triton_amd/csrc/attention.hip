@@ -1,0 +1,712 @@
+// Causal GQA flash attention, forward and backward.
+//
+// Layouts: Q/O/dO/dQ [B,Hq,Lq,D], K/V/dK/dV [B,Hkv,Lk,D] (row-major, D contiguous); query head h
+// reads KV head h / (Hq/Hkv).  Causal with a suffix offset: query i sees keys j <= i + (Lk - Lq).
+// LSE [B,Hq,Lq] is the natural-log row logsumexp of the scaled scores; softmax runs in base 2 on
+// scores pre-multiplied by scale*log2(e).
+//
+// Matrix-core path (bf16/fp16, D in {32, 64, 128}): every contraction is a v_mfma_f32_32x32x16.
+// An MFMA operand must have its contraction index contiguous per lane, so operands contracted
+// over the sequence axis (V in P.V; K in dS.K; Q, dO in dK/dV) are supplied by the host as
+// sequence-contiguous transposed copies (Vt, Kt, Qt, dOt: [.., D, Lpad], Lpad = L rounded up to 8,
+// zero padded), made by the transpose kernel.  Score tiles are computed transposed
+// (S^T = K Q^T), so a lane owns one query and holds 32 key scores in registers: the softmax max/sum
+// is an in-lane reduction plus one cross-half swizzle, and the probabilities are already laid out
+// as the B operand of the next MFMA (with a fixed permutation of the 16 keys of each k-step that
+// the A operand reads mirror).
+//
+// SIMT path: one wave per query (forward, dQ) or per key (dK/dV) with fp32 math; used for fp32
+// and other head sizes.
+#include "common.h"
+
+namespace {
+
+constexpr int kThreads = 256;
+constexpr float kLog2e = 1.4426950408889634f;
+constexpr float kLn2 = 0.6931471805599453f;
+
+template <typename T> Q3_DEV f32x16 mma(bf16x8_t a, bf16x8_t b, f32x16 c);
+template <> Q3_DEV f32x16 mma<BF16>(bf16x8_t a, bf16x8_t b, f32x16 c) {
+  return __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, c, 0, 0, 0);
+}
+template <> Q3_DEV f32x16 mma<F16>(bf16x8_t a, bf16x8_t b, f32x16 c) {
+  return __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(f16x8_t, a), __builtin_bit_cast(f16x8_t, b), c, 0,
+                                                 0, 0);
+}
+
+Q3_DEV f32x16 zero16() {
+  f32x16 z;
+#pragma unroll
+  for (int i = 0; i < 16; ++i) z[i] = 0.f;
+  return z;
+}
+Q3_DEV i32x4 ld16(const u16* p) { return *reinterpret_cast<const i32x4*>(p); }
+Q3_DEV void st16(u16* p, i32x4 v) { *reinterpret_cast<i32x4*>(p) = v; }
+Q3_DEV bf16x8_t as_frag(i32x4 v) { return __builtin_bit_cast(bf16x8_t, v); }
+
+// A-operand fragment whose 8 k-slots are the keys {c16 + 4g .. +3} and {c16 + 8 + 4g .. +3} of a
+// sequence-contiguous row (g = lane / 32): the permutation produced by the accumulator layout.
+Q3_DEV bf16x8_t perm_frag(const u16* row, int c16, int g) {
+  typedef __attribute__((__vector_size__(2 * sizeof(int)))) int i32x2;
+  const i32x2 lo = *reinterpret_cast<const i32x2*>(row + c16 + 4 * g);
+  const i32x2 hi = *reinterpret_cast<const i32x2*>(row + c16 + 8 + 4 * g);
+  i32x4 v = {lo[0], lo[1], hi[0], hi[1]};
+  return as_frag(v);
+}
+
+// Pack 8 accumulator values (v0..v0+7 of one 32x32 tile) into a B-operand fragment.
+template <typename T> Q3_DEV bf16x8_t pack8(const f32x16& a, int v0) {
+  i32x4 r;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const uint32_t lo = from_f32<T>(a[v0 + 2 * i]), hi = from_f32<T>(a[v0 + 2 * i + 1]);
+    r[i] = (int)(lo | (hi << 16));
+  }
+  return as_frag(r);
+}
+
+// Row (key/query) index inside a 32x32 accumulator tile for element v of lane `lane`.
+Q3_DEV int acc_row(int v, int lane) { return 8 * (v >> 2) + 4 * (lane >> 5) + (v & 3); }
+
+// ============================================================================ forward (MFMA)
+// Workgroup: 4 waves x 32 queries of one (b, h); key tiles of 64 double-buffered in LDS.
+template <typename T, int D>
+__global__ __launch_bounds__(kThreads) void attn_fwd_mfma(const u16* __restrict__ Q, const u16* __restrict__ K,
+                                                          const u16* __restrict__ Vt, u16* __restrict__ O,
+                                                          float* __restrict__ LSE, int Hq, int Hkv, int Lq, int Lk,
+                                                          int ldvt, float scale2) {
+  constexpr int BN = 64, KP = D + 8, VP = BN + 8, KS = D / 16, DT = D / 32;
+  constexpr int KCH = BN * D / 8 / kThreads, VCH = D * BN / 8 / kThreads;
+  static_assert(KCH >= 1 && VCH >= 1, "tile too small");
+  __shared__ __attribute__((aligned(16))) u16 lk[2][BN * KP];
+  __shared__ __attribute__((aligned(16))) u16 lv[2][D * VP];
+
+  const int nqt = (Lq + 127) / 128;
+  const int qt = nqt - 1 - (int)blockIdx.x;  // the longest (latest) query tiles start first
+  const int bh = blockIdx.y, b = bh / Hq, h = bh % Hq, hk = h / (Hq / Hkv);
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, g = lane >> 5;
+  const int off = Lk - Lq;
+  const int q0 = qt * 128 + wave * 32;
+  const int qi = q0 + (lane & 31);
+  const u16* Qb = Q + (int64_t)bh * Lq * D;
+  const u16* Kb = K + (int64_t)(b * Hkv + hk) * Lk * D;
+  const u16* Vb = Vt + (int64_t)(b * Hkv + hk) * D * ldvt;
+
+  bf16x8_t qf[KS];
+#pragma unroll
+  for (int ks = 0; ks < KS; ++ks)
+    qf[ks] = qi < Lq ? as_frag(ld16(Qb + (int64_t)qi * D + ks * 16 + g * 8)) : as_frag(i32x4{0, 0, 0, 0});
+
+  const int qlast_blk = min(qt * 128 + 127, Lq - 1) + off;
+  const int kend = min(Lk, qlast_blk + 1);
+  const int ntiles = (kend + BN - 1) / BN;
+  const int qlast_wave = min(q0 + 31, Lq - 1) + off;
+  const int qpos = qi + off;
+
+  i32x4 rk[KCH], rv[VCH];
+  auto gload = [&](int t) {
+    const int k0 = t * BN;
+#pragma unroll
+    for (int i = 0; i < KCH; ++i) {
+      const int c = tid + i * kThreads, row = c / (D / 8), col = (c % (D / 8)) * 8, key = k0 + row;
+      rk[i] = key < Lk ? ld16(Kb + (int64_t)key * D + col) : i32x4{0, 0, 0, 0};
+    }
+#pragma unroll
+    for (int i = 0; i < VCH; ++i) {
+      const int c = tid + i * kThreads, d = c / (BN / 8), kc = k0 + (c % (BN / 8)) * 8;
+      rv[i] = kc < ldvt ? ld16(Vb + (int64_t)d * ldvt + kc) : i32x4{0, 0, 0, 0};
+    }
+  };
+  auto swrite = [&](int buf) {
+#pragma unroll
+    for (int i = 0; i < KCH; ++i) {
+      const int c = tid + i * kThreads;
+      st16(&lk[buf][(c / (D / 8)) * KP + (c % (D / 8)) * 8], rk[i]);
+    }
+#pragma unroll
+    for (int i = 0; i < VCH; ++i) {
+      const int c = tid + i * kThreads;
+      st16(&lv[buf][(c / (BN / 8)) * VP + (c % (BN / 8)) * 8], rv[i]);
+    }
+  };
+
+  float m = -INFINITY, l = 0.f;
+  f32x16 oacc[DT];
+#pragma unroll
+  for (int i = 0; i < DT; ++i) oacc[i] = zero16();
+
+  if (ntiles > 0) {
+    gload(0);
+    swrite(0);
+  }
+  __syncthreads();
+  for (int t = 0; t < ntiles; ++t) {
+    const int cur = t & 1;
+    if (t + 1 < ntiles) gload(t + 1);
+    const int k0 = t * BN;
+    if (k0 <= qlast_wave) {
+      f32x16 sacc[2] = {zero16(), zero16()};
+      const u16* kl = &lk[cur][(lane & 31) * KP + g * 8];
+#pragma unroll
+      for (int ks = 0; ks < KS; ++ks)
+#pragma unroll
+        for (int tt = 0; tt < 2; ++tt)
+          sacc[tt] = mma<T>(as_frag(ld16(kl + tt * 32 * KP + ks * 16)), qf[ks], sacc[tt]);
+      float mx = -INFINITY;
+#pragma unroll
+      for (int tt = 0; tt < 2; ++tt)
+#pragma unroll
+        for (int v = 0; v < 16; ++v) {
+          const int key = k0 + tt * 32 + acc_row(v, lane);
+          const float s = key <= qpos ? sacc[tt][v] * scale2 : -INFINITY;
+          sacc[tt][v] = s;
+          mx = fmaxf(mx, s);
+        }
+      mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
+      const float mnew = fmaxf(m, mx);
+      const float muse = mnew == -INFINITY ? 0.f : mnew;
+      const float alpha = __builtin_amdgcn_exp2f(m - muse);
+      float ps = 0.f;
+#pragma unroll
+      for (int tt = 0; tt < 2; ++tt)
+#pragma unroll
+        for (int v = 0; v < 16; ++v) {
+          const float p = __builtin_amdgcn_exp2f(sacc[tt][v] - muse);
+          sacc[tt][v] = p;
+          ps += p;
+        }
+      ps += __shfl_xor(ps, 32, 64);
+      l = l * alpha + ps;
+      m = mnew;
+#pragma unroll
+      for (int dt = 0; dt < DT; ++dt)
+#pragma unroll
+        for (int v = 0; v < 16; ++v) oacc[dt][v] *= alpha;
+#pragma unroll
+      for (int c = 0; c < BN / 16; ++c) {
+        const bf16x8_t pb = pack8<T>(sacc[c >> 1], (c & 1) * 8);
+#pragma unroll
+        for (int dt = 0; dt < DT; ++dt)
+          oacc[dt] = mma<T>(perm_frag(&lv[cur][(dt * 32 + (lane & 31)) * VP], c * 16, g), pb, oacc[dt]);
+      }
+    }
+    if (t + 1 < ntiles) swrite(cur ^ 1);
+    __syncthreads();
+  }
+
+  if (qi < Lq) {
+    const float inv = 1.f / l;
+    u16* orow = O + ((int64_t)bh * Lq + qi) * D;
+#pragma unroll
+    for (int dt = 0; dt < DT; ++dt)
+#pragma unroll
+      for (int vg = 0; vg < 4; ++vg) {
+        const int d = dt * 32 + 8 * vg + 4 * g;
+        typedef __attribute__((__vector_size__(2 * sizeof(int)))) int i32x2;
+        i32x2 w;
+        w[0] = (int)(from_f32<T>(oacc[dt][4 * vg] * inv) | ((uint32_t)from_f32<T>(oacc[dt][4 * vg + 1] * inv) << 16));
+        w[1] = (int)(from_f32<T>(oacc[dt][4 * vg + 2] * inv) | ((uint32_t)from_f32<T>(oacc[dt][4 * vg + 3] * inv) << 16));
+        *reinterpret_cast<i32x2*>(orow + d) = w;
+      }
+    if (g == 0) LSE[(int64_t)bh * Lq + qi] = (m + __log2f(l)) * kLn2;
+  }
+}
+
+// ============================================================================ backward: delta
+// delta[r] = sum_d O[r,d] * dO[r,d] (fp32), one wave per row.
+template <typename T>
+__global__ __launch_bounds__(kThreads) void attn_delta_kernel(const typename T::storage* __restrict__ O,
+                                                              const typename T::storage* __restrict__ dO,
+                                                              float* __restrict__ delta, int64_t rows, int D) {
+  const int64_t row = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (row >= rows) return;
+  float s = 0.f;
+  for (int d = lane_id(); d < D; d += 64) s += to_f32<T>(O[row * D + d]) * to_f32<T>(dO[row * D + d]);
+  s = group_sum<64>(s);
+  if (lane_id() == 0) delta[row] = s;
+}
+
+// ============================================================================ backward: dQ (MFMA)
+// Workgroup: 4 waves x 32 queries of one (b, h).  Per key tile: S^T = K Q^T, dP^T = V dO^T,
+// dS = P (dP - delta), dQ^T += Kt dS^T.
+template <typename T, int D>
+__global__ __launch_bounds__(kThreads) void attn_bwd_dq_mfma(const u16* __restrict__ Q, const u16* __restrict__ K,
+                                                             const u16* __restrict__ V, const u16* __restrict__ Kt,
+                                                             const u16* __restrict__ dO,
+                                                             const float* __restrict__ LSE,
+                                                             const float* __restrict__ Delta, u16* __restrict__ dQ,
+                                                             int Hq, int Hkv, int Lq, int Lk, int ldkt, float scale,
+                                                             float scale2) {
+  constexpr int BN = 64, KP = D + 8, VP = BN + 8, KS = D / 16, DT = D / 32;
+  constexpr int KCH = BN * D / 8 / kThreads;
+  __shared__ __attribute__((aligned(16))) u16 lk[BN * KP];
+  __shared__ __attribute__((aligned(16))) u16 lvv[BN * KP];
+  __shared__ __attribute__((aligned(16))) u16 lkt[D * VP];
+
+  const int nqt = (Lq + 127) / 128;
+  const int qt = nqt - 1 - (int)blockIdx.x;
+  const int bh = blockIdx.y, b = bh / Hq, h = bh % Hq, hk = h / (Hq / Hkv);
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, g = lane >> 5;
+  const int off = Lk - Lq;
+  const int q0 = qt * 128 + wave * 32;
+  const int qi = q0 + (lane & 31);
+  const int64_t kvbase = (int64_t)(b * Hkv + hk);
+  const u16* Kb = K + kvbase * Lk * D;
+  const u16* Vb = V + kvbase * Lk * D;
+  const u16* Ktb = Kt + kvbase * D * ldkt;
+
+  bf16x8_t qf[KS], dof[KS];
+#pragma unroll
+  for (int ks = 0; ks < KS; ++ks) {
+    const bool ok = qi < Lq;
+    qf[ks] = ok ? as_frag(ld16(Q + ((int64_t)bh * Lq + qi) * D + ks * 16 + g * 8)) : as_frag(i32x4{0, 0, 0, 0});
+    dof[ks] = ok ? as_frag(ld16(dO + ((int64_t)bh * Lq + qi) * D + ks * 16 + g * 8)) : as_frag(i32x4{0, 0, 0, 0});
+  }
+  const float lse2 = qi < Lq ? LSE[(int64_t)bh * Lq + qi] * kLog2e : 0.f;
+  const float dlt = qi < Lq ? Delta[(int64_t)bh * Lq + qi] : 0.f;
+  const int qpos = qi + off;
+  const int qlast_blk = min(qt * 128 + 127, Lq - 1) + off;
+  const int ntiles = (min(Lk, qlast_blk + 1) + BN - 1) / BN;
+  const int qlast_wave = min(q0 + 31, Lq - 1) + off;
+
+  f32x16 dq[DT];
+#pragma unroll
+  for (int i = 0; i < DT; ++i) dq[i] = zero16();
+
+  for (int t = 0; t < ntiles; ++t) {
+    const int k0 = t * BN;
+    __syncthreads();
+#pragma unroll
+    for (int i = 0; i < KCH; ++i) {
+      const int c = tid + i * kThreads, row = c / (D / 8), col = (c % (D / 8)) * 8, key = k0 + row;
+      const bool ok = key < Lk;
+      st16(&lk[row * KP + col], ok ? ld16(Kb + (int64_t)key * D + col) : i32x4{0, 0, 0, 0});
+      st16(&lvv[row * KP + col], ok ? ld16(Vb + (int64_t)key * D + col) : i32x4{0, 0, 0, 0});
+      const int d = c / (BN / 8), kc = k0 + (c % (BN / 8)) * 8;
+      st16(&lkt[d * VP + (c % (BN / 8)) * 8], kc < ldkt ? ld16(Ktb + (int64_t)d * ldkt + kc) : i32x4{0, 0, 0, 0});
+    }
+    __syncthreads();
+    if (k0 > qlast_wave) continue;
+    f32x16 s[2] = {zero16(), zero16()}, dp[2] = {zero16(), zero16()};
+    const u16* kl = &lk[(lane & 31) * KP + g * 8];
+    const u16* vl = &lvv[(lane & 31) * KP + g * 8];
+#pragma unroll
+    for (int ks = 0; ks < KS; ++ks)
+#pragma unroll
+      for (int tt = 0; tt < 2; ++tt) {
+        s[tt] = mma<T>(as_frag(ld16(kl + tt * 32 * KP + ks * 16)), qf[ks], s[tt]);
+        dp[tt] = mma<T>(as_frag(ld16(vl + tt * 32 * KP + ks * 16)), dof[ks], dp[tt]);
+      }
+#pragma unroll
+    for (int tt = 0; tt < 2; ++tt)
+#pragma unroll
+      for (int v = 0; v < 16; ++v) {
+        const int key = k0 + tt * 32 + acc_row(v, lane);
+        const float p = key <= qpos ? __builtin_amdgcn_exp2f(s[tt][v] * scale2 - lse2) : 0.f;
+        s[tt][v] = p * (dp[tt][v] - dlt);
+      }
+#pragma unroll
+    for (int c = 0; c < BN / 16; ++c) {
+      const bf16x8_t db = pack8<T>(s[c >> 1], (c & 1) * 8);
+#pragma unroll
+      for (int dt = 0; dt < DT; ++dt) dq[dt] = mma<T>(perm_frag(&lkt[(dt * 32 + (lane & 31)) * VP], c * 16, g), db, dq[dt]);
+    }
+  }
+  if (qi < Lq) {
+    u16* row = dQ + ((int64_t)bh * Lq + qi) * D;
+#pragma unroll
+    for (int dt = 0; dt < DT; ++dt)
+#pragma unroll
+      for (int v = 0; v < 16; ++v) row[dt * 32 + acc_row(v, lane)] = from_f32<T>(dq[dt][v] * scale);
+  }
+}
+
+// ============================================================================ backward: dK, dV (MFMA)
+// Workgroup: 4 waves x 32 keys of one (b, kv head); loops over the Hq/Hkv query heads of the group
+// and over 32-query tiles at or after the diagonal.  Per tile: S = Q K^T, dP = dO V^T (lane = key),
+// P, dS; dV^T += dOt P, dK^T += Qt dS.  The group's query heads accumulate into the same
+// registers: no partial buffers, no atomics.
+template <typename T, int D>
+__global__ __launch_bounds__(kThreads) void attn_bwd_dkdv_mfma(const u16* __restrict__ Q, const u16* __restrict__ K,
+                                                               const u16* __restrict__ V, const u16* __restrict__ Qt,
+                                                               const u16* __restrict__ dO,
+                                                               const u16* __restrict__ dOt,
+                                                               const float* __restrict__ LSE,
+                                                               const float* __restrict__ Delta, u16* __restrict__ dK,
+                                                               u16* __restrict__ dV, int Hq, int Hkv, int Lq, int Lk,
+                                                               int ldqt, float scale, float scale2) {
+  constexpr int BM = 32, KP = D + 8, QP = BM + 8, KS = D / 16, DT = D / 32;
+  constexpr int RCH = BM * D / 8;  // 16-byte chunks of one [BM][D] tile
+  __shared__ __attribute__((aligned(16))) u16 lq[BM * KP];
+  __shared__ __attribute__((aligned(16))) u16 ldo[BM * KP];
+  __shared__ __attribute__((aligned(16))) u16 lqt[D * QP];
+  __shared__ __attribute__((aligned(16))) u16 ldot[D * QP];
+  __shared__ float llse[BM], ldel[BM];
+
+  const int nkt = (Lk + 127) / 128;
+  const int kt = (int)blockIdx.x;
+  const int bk = blockIdx.y, b = bk / Hkv, hk = bk % Hkv, ratio = Hq / Hkv;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, g = lane >> 5;
+  const int off = Lk - Lq;
+  const int k0w = kt * 128 + wave * 32;
+  const int kj = k0w + (lane & 31);
+  const u16* Kb = K + (int64_t)bk * Lk * D;
+  const u16* Vb = V + (int64_t)bk * Lk * D;
+  (void)nkt;
+
+  bf16x8_t kf[KS], vf[KS];
+#pragma unroll
+  for (int ks = 0; ks < KS; ++ks) {
+    const bool ok = kj < Lk;
+    kf[ks] = ok ? as_frag(ld16(Kb + (int64_t)kj * D + ks * 16 + g * 8)) : as_frag(i32x4{0, 0, 0, 0});
+    vf[ks] = ok ? as_frag(ld16(Vb + (int64_t)kj * D + ks * 16 + g * 8)) : as_frag(i32x4{0, 0, 0, 0});
+  }
+  f32x16 dk[DT], dv[DT];
+#pragma unroll
+  for (int i = 0; i < DT; ++i) dk[i] = dv[i] = zero16();
+
+  // First query index that can see this workgroup's first key: q + off >= kt*128.
+  const int qstart_blk = max(0, kt * 128 - off) / BM * BM;
+  const int kfirst_wave = k0w;  // wave skips query tiles that end before its first key
+  for (int hh = 0; hh < ratio; ++hh) {
+    const int h = hk * ratio + hh;
+    const int64_t bh = (int64_t)b * Hq + h;
+    const u16* Qb = Q + bh * Lq * D;
+    const u16* dOb = dO + bh * Lq * D;
+    const u16* Qtb = Qt + bh * D * ldqt;
+    const u16* dOtb = dOt + bh * D * ldqt;
+    for (int q0 = qstart_blk; q0 < Lq; q0 += BM) {
+      __syncthreads();
+      for (int c = tid; c < RCH; c += kThreads) {
+        const int row = c / (D / 8), col = (c % (D / 8)) * 8, qq = q0 + row;
+        const bool ok = qq < Lq;
+        st16(&lq[row * KP + col], ok ? ld16(Qb + (int64_t)qq * D + col) : i32x4{0, 0, 0, 0});
+        st16(&ldo[row * KP + col], ok ? ld16(dOb + (int64_t)qq * D + col) : i32x4{0, 0, 0, 0});
+        const int d = c / (BM / 8), qc = q0 + (c % (BM / 8)) * 8;
+        const bool okt = qc < ldqt;
+        st16(&lqt[d * QP + (c % (BM / 8)) * 8], okt ? ld16(Qtb + (int64_t)d * ldqt + qc) : i32x4{0, 0, 0, 0});
+        st16(&ldot[d * QP + (c % (BM / 8)) * 8], okt ? ld16(dOtb + (int64_t)d * ldqt + qc) : i32x4{0, 0, 0, 0});
+      }
+      if (tid < BM) {
+        const int qq = q0 + tid;
+        llse[tid] = qq < Lq ? LSE[bh * Lq + qq] * kLog2e : 0.f;
+        ldel[tid] = qq < Lq ? Delta[bh * Lq + qq] : 0.f;
+      }
+      __syncthreads();
+      // the last query of this tile must reach the wave's first key
+      if (min(q0 + BM - 1, Lq - 1) + off < kfirst_wave) continue;
+      f32x16 s = zero16(), dp = zero16();
+      const u16* ql = &lq[(lane & 31) * KP + g * 8];
+      const u16* dl = &ldo[(lane & 31) * KP + g * 8];
+#pragma unroll
+      for (int ks = 0; ks < KS; ++ks) {
+        s = mma<T>(as_frag(ld16(ql + ks * 16)), kf[ks], s);
+        dp = mma<T>(as_frag(ld16(dl + ks * 16)), vf[ks], dp);
+      }
+      // element v: query q0 + acc_row(v), key kj (= lane's column)
+      f32x16 ds;
+#pragma unroll
+      for (int v = 0; v < 16; ++v) {
+        const int r = acc_row(v, lane), qq = q0 + r;
+        const float p = (qq < Lq && kj <= qq + off) ? __builtin_amdgcn_exp2f(s[v] * scale2 - llse[r]) : 0.f;
+        s[v] = p;
+        ds[v] = p * (dp[v] - ldel[r]);
+      }
+#pragma unroll
+      for (int c = 0; c < BM / 16; ++c) {
+        const bf16x8_t pb = pack8<T>(s, c * 8);
+        const bf16x8_t db = pack8<T>(ds, c * 8);
+#pragma unroll
+        for (int dt = 0; dt < DT; ++dt) {
+          dv[dt] = mma<T>(perm_frag(&ldot[(dt * 32 + (lane & 31)) * QP], c * 16, g), pb, dv[dt]);
+          dk[dt] = mma<T>(perm_frag(&lqt[(dt * 32 + (lane & 31)) * QP], c * 16, g), db, dk[dt]);
+        }
+      }
+    }
+  }
+  if (kj < Lk) {
+    u16* krow = dK + ((int64_t)bk * Lk + kj) * D;
+    u16* vrow = dV + ((int64_t)bk * Lk + kj) * D;
+#pragma unroll
+    for (int dt = 0; dt < DT; ++dt)
+#pragma unroll
+      for (int v = 0; v < 16; ++v) {
+        const int d = dt * 32 + acc_row(v, lane);
+        krow[d] = from_f32<T>(dk[dt][v] * scale);
+        vrow[d] = from_f32<T>(dv[dt][v]);
+      }
+  }
+}
+
+// ============================================================================ SIMT path
+// One wave per (b, h, query).  D <= 256: lane holds d = lane + 64*i.
+template <typename T>
+__global__ __launch_bounds__(kThreads) void attn_fwd_simt(const typename T::storage* __restrict__ Q,
+                                                          const typename T::storage* __restrict__ K,
+                                                          const typename T::storage* __restrict__ V,
+                                                          typename T::storage* __restrict__ O,
+                                                          float* __restrict__ LSE, int Hq, int Hkv, int Lq, int Lk,
+                                                          int D, float scale) {
+  const int64_t row = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+  const int b = blockIdx.z;
+  if (row >= (int64_t)Hq * Lq) return;
+  const int h = (int)(row / Lq), qi = (int)(row % Lq), hk = h / (Hq / Hkv), l = lane_id();
+  const int64_t bh = (int64_t)b * Hq + h;
+  const typename T::storage* q = Q + (bh * Lq + qi) * D;
+  const typename T::storage* kb = K + ((int64_t)b * Hkv + hk) * Lk * D;
+  const typename T::storage* vb = V + ((int64_t)b * Hkv + hk) * Lk * D;
+  float qv[4], acc[4] = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+  for (int i = 0; i < 4; ++i) qv[i] = (l + 64 * i < D) ? to_f32<T>(q[l + 64 * i]) : 0.f;
+  float m = -INFINITY, den = 0.f;
+  const int kend = min(Lk, qi + (Lk - Lq) + 1);
+  for (int j = 0; j < kend; ++j) {
+    float s = 0.f;
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+      if (l + 64 * i < D) s += qv[i] * to_f32<T>(kb[(int64_t)j * D + l + 64 * i]);
+    s = group_sum<64>(s) * scale;
+    const float mn = fmaxf(m, s), a = __expf(m - mn), p = __expf(s - mn);
+    den = den * a + p;
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+      if (l + 64 * i < D) acc[i] = acc[i] * a + p * to_f32<T>(vb[(int64_t)j * D + l + 64 * i]);
+    m = mn;
+  }
+#pragma unroll
+  for (int i = 0; i < 4; ++i)
+    if (l + 64 * i < D) O[(bh * Lq + qi) * D + l + 64 * i] = from_f32<T>(acc[i] / den);
+  if (l == 0) LSE[bh * Lq + qi] = m + __logf(den);
+}
+
+template <typename T>
+__global__ __launch_bounds__(kThreads) void attn_bwd_dq_simt(const typename T::storage* __restrict__ Q,
+                                                             const typename T::storage* __restrict__ K,
+                                                             const typename T::storage* __restrict__ V,
+                                                             const typename T::storage* __restrict__ dO,
+                                                             const float* __restrict__ LSE,
+                                                             const float* __restrict__ Delta,
+                                                             typename T::storage* __restrict__ dQ, int Hq, int Hkv,
+                                                             int Lq, int Lk, int D, float scale) {
+  const int64_t row = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+  const int b = blockIdx.z;
+  if (row >= (int64_t)Hq * Lq) return;
+  const int h = (int)(row / Lq), qi = (int)(row % Lq), hk = h / (Hq / Hkv), l = lane_id();
+  const int64_t bh = (int64_t)b * Hq + h;
+  const typename T::storage* kb = K + ((int64_t)b * Hkv + hk) * Lk * D;
+  const typename T::storage* vb = V + ((int64_t)b * Hkv + hk) * Lk * D;
+  float qv[4], dov[4], acc[4] = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const bool ok = l + 64 * i < D;
+    qv[i] = ok ? to_f32<T>(Q[(bh * Lq + qi) * D + l + 64 * i]) : 0.f;
+    dov[i] = ok ? to_f32<T>(dO[(bh * Lq + qi) * D + l + 64 * i]) : 0.f;
+  }
+  const float lse = LSE[bh * Lq + qi], dl = Delta[bh * Lq + qi];
+  const int kend = min(Lk, qi + (Lk - Lq) + 1);
+  for (int j = 0; j < kend; ++j) {
+    float s = 0.f, dp = 0.f;
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+      if (l + 64 * i < D) {
+        s += qv[i] * to_f32<T>(kb[(int64_t)j * D + l + 64 * i]);
+        dp += dov[i] * to_f32<T>(vb[(int64_t)j * D + l + 64 * i]);
+      }
+    s = group_sum<64>(s);
+    dp = group_sum<64>(dp);
+    const float p = __expf(s * scale - lse), ds = p * (dp - dl);
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+      if (l + 64 * i < D) acc[i] += ds * to_f32<T>(kb[(int64_t)j * D + l + 64 * i]);
+  }
+#pragma unroll
+  for (int i = 0; i < 4; ++i)
+    if (l + 64 * i < D) dQ[(bh * Lq + qi) * D + l + 64 * i] = from_f32<T>(acc[i] * scale);
+}
+
+template <typename T>
+__global__ __launch_bounds__(kThreads) void attn_bwd_dkdv_simt(const typename T::storage* __restrict__ Q,
+                                                               const typename T::storage* __restrict__ K,
+                                                               const typename T::storage* __restrict__ V,
+                                                               const typename T::storage* __restrict__ dO,
+                                                               const float* __restrict__ LSE,
+                                                               const float* __restrict__ Delta,
+                                                               typename T::storage* __restrict__ dK,
+                                                               typename T::storage* __restrict__ dV, int Hq, int Hkv,
+                                                               int Lq, int Lk, int D, float scale) {
+  const int64_t row = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+  const int b = blockIdx.z;
+  if (row >= (int64_t)Hkv * Lk) return;
+  const int hk = (int)(row / Lk), kj = (int)(row % Lk), ratio = Hq / Hkv, l = lane_id();
+  const int64_t bk = (int64_t)b * Hkv + hk;
+  float kv[4], vv[4], ak[4] = {0.f, 0.f, 0.f, 0.f}, av[4] = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const bool ok = l + 64 * i < D;
+    kv[i] = ok ? to_f32<T>(K[(bk * Lk + kj) * D + l + 64 * i]) : 0.f;
+    vv[i] = ok ? to_f32<T>(V[(bk * Lk + kj) * D + l + 64 * i]) : 0.f;
+  }
+  const int off = Lk - Lq;
+  for (int hh = 0; hh < ratio; ++hh) {
+    const int64_t bh = (int64_t)b * Hq + hk * ratio + hh;
+    for (int qi = max(0, kj - off); qi < Lq; ++qi) {
+      const typename T::storage* q = Q + (bh * Lq + qi) * D;
+      const typename T::storage* d = dO + (bh * Lq + qi) * D;
+      float s = 0.f, dp = 0.f;
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+        if (l + 64 * i < D) {
+          s += kv[i] * to_f32<T>(q[l + 64 * i]);
+          dp += vv[i] * to_f32<T>(d[l + 64 * i]);
+        }
+      s = group_sum<64>(s);
+      dp = group_sum<64>(dp);
+      const float p = __expf(s * scale - LSE[bh * Lq + qi]), ds = p * (dp - Delta[bh * Lq + qi]);
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+        if (l + 64 * i < D) {
+          av[i] += p * to_f32<T>(d[l + 64 * i]);
+          ak[i] += ds * to_f32<T>(q[l + 64 * i]);
+        }
+    }
+  }
+#pragma unroll
+  for (int i = 0; i < 4; ++i)
+    if (l + 64 * i < D) {
+      dK[(bk * Lk + kj) * D + l + 64 * i] = from_f32<T>(ak[i] * scale);
+      dV[(bk * Lk + kj) * D + l + 64 * i] = from_f32<T>(av[i]);
+    }
+}
+
+// ============================================================================ host dispatch
+bool dtype_ok(int dt) { return dt == Q3_F32 || dt == Q3_F16 || dt == Q3_BF16; }
+
+template <typename T, int D>
+int fwd_mfma(const void* q, const void* k, const void* vt, void* o, float* lse, int B, int Hq, int Hkv, int Lq,
+             int Lk, int ldvt, float scale, hipStream_t s) {
+  dim3 grid((unsigned)((Lq + 127) / 128), (unsigned)(B * Hq));
+  attn_fwd_mfma<T, D><<<grid, kThreads, 0, s>>>((const u16*)q, (const u16*)k, (const u16*)vt, (u16*)o, lse, Hq, Hkv,
+                                                 Lq, Lk, ldvt, scale * kLog2e);
+  return (int)hipGetLastError();
+}
+
+template <typename T, int D>
+int bwd_mfma(const void* q, const void* k, const void* v, const void* qt, const void* kt, const void* dout,
+             const void* dot, const float* lse, const float* delta, void* dq, void* dk, void* dv, int B, int Hq,
+             int Hkv, int Lq, int Lk, int ldqt, int ldkt, float scale, hipStream_t s) {
+  dim3 g1((unsigned)((Lq + 127) / 128), (unsigned)(B * Hq));
+  attn_bwd_dq_mfma<T, D><<<g1, kThreads, 0, s>>>((const u16*)q, (const u16*)k, (const u16*)v, (const u16*)kt,
+                                                  (const u16*)dout, lse, delta, (u16*)dq, Hq, Hkv, Lq, Lk, ldkt, scale,
+                                                  scale * kLog2e);
+  dim3 g2((unsigned)((Lk + 127) / 128), (unsigned)(B * Hkv));
+  attn_bwd_dkdv_mfma<T, D><<<g2, kThreads, 0, s>>>((const u16*)q, (const u16*)k, (const u16*)v, (const u16*)qt,
+                                                    (const u16*)dout, (const u16*)dot, lse, delta, (u16*)dk, (u16*)dv,
+                                                    Hq, Hkv, Lq, Lk, ldqt, scale, scale * kLog2e);
+  return (int)hipGetLastError();
+}
+
+template <typename T>
+int fwd_simt(const void* q, const void* k, const void* v, void* o, float* lse, int B, int Hq, int Hkv, int Lq, int Lk,
+             int D, float scale, hipStream_t s) {
+  typedef typename T::storage S;
+  dim3 grid((unsigned)(((int64_t)Hq * Lq + 3) / 4), 1, (unsigned)B);
+  attn_fwd_simt<T><<<grid, kThreads, 0, s>>>((const S*)q, (const S*)k, (const S*)v, (S*)o, lse, Hq, Hkv, Lq, Lk, D,
+                                             scale);
+  return (int)hipGetLastError();
+}
+
+template <typename T>
+int bwd_simt(const void* q, const void* k, const void* v, const void* dout, const float* lse, const float* delta,
+             void* dq, void* dk, void* dv, int B, int Hq, int Hkv, int Lq, int Lk, int D, float scale, hipStream_t s) {
+  typedef typename T::storage S;
+  dim3 g1((unsigned)(((int64_t)Hq * Lq + 3) / 4), 1, (unsigned)B);
+  attn_bwd_dq_simt<T><<<g1, kThreads, 0, s>>>((const S*)q, (const S*)k, (const S*)v, (const S*)dout, lse, delta,
+                                              (S*)dq, Hq, Hkv, Lq, Lk, D, scale);
+  dim3 g2((unsigned)(((int64_t)Hkv * Lk + 3) / 4), 1, (unsigned)B);
+  attn_bwd_dkdv_simt<T><<<g2, kThreads, 0, s>>>((const S*)q, (const S*)k, (const S*)v, (const S*)dout, lse, delta,
+                                                (S*)dk, (S*)dv, Hq, Hkv, Lq, Lk, D, scale);
+  return (int)hipGetLastError();
+}
+
+template <typename T>
+int delta_t(const void* o, const void* dout, float* delta, int64_t rows, int D, hipStream_t s) {
+  typedef typename T::storage S;
+  attn_delta_kernel<T><<<(unsigned)((rows + 3) / 4), kThreads, 0, s>>>((const S*)o, (const S*)dout, delta, rows, D);
+  return (int)hipGetLastError();
+}
+
+bool shapes_ok(int64_t B, int64_t Hq, int64_t Hkv, int64_t Lq, int64_t Lk, int64_t D) {
+  return B > 0 && Hq > 0 && Hkv > 0 && Hq % Hkv == 0 && Lq > 0 && Lk >= Lq && D > 0 && D <= 256 &&
+         B * Hq < 65536 && Lk < (1 << 30);
+}
+
+}  // namespace
+
+extern "C" {
+
+int q3_attention_mfma_supported(int dtype, int64_t d) {
+  return (dtype == Q3_BF16 || dtype == Q3_F16) && (d == 32 || d == 64 || d == 128);
+}
+
+int q3_attention_fwd(int dtype, const void* q, const void* k, const void* v, const void* vt, int64_t ldvt, void* o,
+                     float* lse, int64_t B, int64_t Hq, int64_t Hkv, int64_t Lq, int64_t Lk, int64_t D, float scale,
+                     hipStream_t stream) {
+  Q3_REQUIRE(dtype_ok(dtype) && q && k && o && lse && shapes_ok(B, Hq, Hkv, Lq, Lk, D));
+  if (q3_attention_mfma_supported(dtype, D)) {
+    Q3_REQUIRE(vt && ldvt >= Lk && ldvt % 8 == 0);
+    const int b = (int)B, hq = (int)Hq, hkv = (int)Hkv, lq = (int)Lq, lk = (int)Lk, ld = (int)ldvt;
+    if (dtype == Q3_BF16) {
+      if (D == 128) return fwd_mfma<BF16, 128>(q, k, vt, o, lse, b, hq, hkv, lq, lk, ld, scale, stream);
+      if (D == 64) return fwd_mfma<BF16, 64>(q, k, vt, o, lse, b, hq, hkv, lq, lk, ld, scale, stream);
+      return fwd_mfma<BF16, 32>(q, k, vt, o, lse, b, hq, hkv, lq, lk, ld, scale, stream);
+    }
+    if (D == 128) return fwd_mfma<F16, 128>(q, k, vt, o, lse, b, hq, hkv, lq, lk, ld, scale, stream);
+    if (D == 64) return fwd_mfma<F16, 64>(q, k, vt, o, lse, b, hq, hkv, lq, lk, ld, scale, stream);
+    return fwd_mfma<F16, 32>(q, k, vt, o, lse, b, hq, hkv, lq, lk, ld, scale, stream);
+  }
+  Q3_REQUIRE(v);
+  if (dtype == Q3_BF16) return fwd_simt<BF16>(q, k, v, o, lse, B, Hq, Hkv, Lq, Lk, D, scale, stream);
+  if (dtype == Q3_F16) return fwd_simt<F16>(q, k, v, o, lse, B, Hq, Hkv, Lq, Lk, D, scale, stream);
+  return fwd_simt<F32>(q, k, v, o, lse, B, Hq, Hkv, Lq, Lk, D, scale, stream);
+}
+
+int q3_attention_bwd(int dtype, const void* q, const void* k, const void* v, const void* o, const void* dout,
+                     const float* lse, const void* qt, int64_t ldqt, const void* kt, int64_t ldkt, const void* dot,
+                     float* delta, void* dq, void* dk, void* dv, int64_t B, int64_t Hq, int64_t Hkv, int64_t Lq,
+                     int64_t Lk, int64_t D, float scale, hipStream_t stream) {
+  Q3_REQUIRE(dtype_ok(dtype) && q && k && v && o && dout && lse && delta && dq && dk && dv &&
+             shapes_ok(B, Hq, Hkv, Lq, Lk, D));
+  int rc;
+  if (dtype == Q3_BF16) rc = delta_t<BF16>(o, dout, delta, B * Hq * Lq, (int)D, stream);
+  else if (dtype == Q3_F16) rc = delta_t<F16>(o, dout, delta, B * Hq * Lq, (int)D, stream);
+  else rc = delta_t<F32>(o, dout, delta, B * Hq * Lq, (int)D, stream);
+  if (rc) return rc;
+  const int b = (int)B, hq = (int)Hq, hkv = (int)Hkv, lq = (int)Lq, lk = (int)Lk, d = (int)D;
+  if (q3_attention_mfma_supported(dtype, D)) {
+    Q3_REQUIRE(qt && kt && dot && ldqt >= Lq && ldkt >= Lk && ldqt % 8 == 0 && ldkt % 8 == 0);
+    const int lq8 = (int)ldqt, lk8 = (int)ldkt;
+    if (dtype == Q3_BF16) {
+      if (D == 128)
+        return bwd_mfma<BF16, 128>(q, k, v, qt, kt, dout, dot, lse, delta, dq, dk, dv, b, hq, hkv, lq, lk, lq8, lk8,
+                                   scale, stream);
+      if (D == 64)
+        return bwd_mfma<BF16, 64>(q, k, v, qt, kt, dout, dot, lse, delta, dq, dk, dv, b, hq, hkv, lq, lk, lq8, lk8,
+                                  scale, stream);
+      return bwd_mfma<BF16, 32>(q, k, v, qt, kt, dout, dot, lse, delta, dq, dk, dv, b, hq, hkv, lq, lk, lq8, lk8,
+                                scale, stream);
+    }
+    if (D == 128)
+      return bwd_mfma<F16, 128>(q, k, v, qt, kt, dout, dot, lse, delta, dq, dk, dv, b, hq, hkv, lq, lk, lq8, lk8, scale,
+                                stream);
+    if (D == 64)
+      return bwd_mfma<F16, 64>(q, k, v, qt, kt, dout, dot, lse, delta, dq, dk, dv, b, hq, hkv, lq, lk, lq8, lk8, scale,
+                               stream);
+    return bwd_mfma<F16, 32>(q, k, v, qt, kt, dout, dot, lse, delta, dq, dk, dv, b, hq, hkv, lq, lk, lq8, lk8, scale,
+                             stream);
+  }
+  if (dtype == Q3_BF16) return bwd_simt<BF16>(q, k, v, dout, lse, delta, dq, dk, dv, b, hq, hkv, lq, lk, d, scale, stream);
+  if (dtype == Q3_F16) return bwd_simt<F16>(q, k, v, dout, lse, delta, dq, dk, dv, b, hq, hkv, lq, lk, d, scale, stream);
+  return bwd_simt<F32>(q, k, v, dout, lse, delta, dq, dk, dv, b, hq, hkv, lq, lk, d, scale, stream);
+}
+
+}  // extern "C"

@@ -1,0 +1,226 @@
+// Causal cross-entropy pieces: label shift, per-row online log-sum-exp over (a chunk of) the
+// vocabulary, chunk merge + per-row loss, deterministic token mean, and the logits gradient.
+//
+// The same kernels serve the reference's CE on materialised [B,S,V] logits (one chunk = whole
+// vocabulary) and the fused LM-head CE, where the logits of one vocabulary chunk at a time come
+// from the matrix-core GEMM and are never materialised for the full vocabulary.
+//
+// Row r = (b, s) uses target tgt[r] = labels[b, s+1] for s < S-1 and ignore_index for s = S-1
+// (the causal shift of kernels/loss.py:16-24); ignored rows contribute neither loss nor count.
+#include "common.h"
+
+namespace {
+
+constexpr int kThreads = 256;
+
+// (max, sum-exp) pair combine in base e.
+Q3_DEV void lse_combine(float& m, float& s, float m2, float s2) {
+  const float mn = fmaxf(m, m2);
+  if (mn == -INFINITY) return;
+  s = s * __expf(m - mn) + s2 * __expf(m2 - mn);
+  m = mn;
+}
+
+__global__ __launch_bounds__(kThreads) void shift_labels_kernel(const int64_t* __restrict__ labels,
+                                                                int64_t* __restrict__ tgt, int64_t rows, int64_t seq,
+                                                                int64_t ignore) {
+  const int64_t stride = (int64_t)gridDim.x * kThreads;
+  for (int64_t r = (int64_t)blockIdx.x * kThreads + threadIdx.x; r < rows; r += stride)
+    tgt[r] = (r % seq) < seq - 1 ? labels[r + 1] : ignore;
+}
+
+// One workgroup per row: m/s over z[r, 0:n] (row stride ld); picks z[r, tgt - col0] when the target
+// falls inside [col0, col0 + n).
+template <typename T>
+__global__ __launch_bounds__(kThreads) void ce_stats_kernel(const typename T::storage* __restrict__ z, int64_t ld,
+                                                            int64_t n, int64_t col0,
+                                                            const int64_t* __restrict__ tgt,
+                                                            float* __restrict__ m_out, float* __restrict__ s_out,
+                                                            float* __restrict__ pick, int vec_ok) {
+  constexpr int V = T::vec;
+  __shared__ float rm[kThreads / 64], rs[kThreads / 64];
+  const int64_t r = blockIdx.x;
+  const typename T::storage* row = z + r * ld;
+  float m = -INFINITY, s = 0.f;
+  const int64_t nv = vec_ok ? n / V : 0;
+  for (int64_t i = threadIdx.x; i < nv; i += kThreads) {
+    const Vec<T> x = load_vec<T>(row + i * V);
+    float vm = x.v[0];
+#pragma unroll
+    for (int e = 1; e < V; ++e) vm = fmaxf(vm, x.v[e]);
+    float vs = 0.f;
+#pragma unroll
+    for (int e = 0; e < V; ++e) vs += __expf(x.v[e] - vm);
+    lse_combine(m, s, vm, vs);
+  }
+  for (int64_t i = nv * V + threadIdx.x; i < n; i += kThreads) lse_combine(m, s, to_f32<T>(row[i]), 1.f);
+#pragma unroll
+  for (int o = 1; o < 64; o <<= 1) {
+    const float m2 = __shfl_xor(m, o, 64), s2 = __shfl_xor(s, o, 64);
+    lse_combine(m, s, m2, s2);
+  }
+  const int w = threadIdx.x >> 6;
+  if (lane_id() == 0) {
+    rm[w] = m;
+    rs[w] = s;
+  }
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    float M = rm[0], S = rs[0];
+    for (int i = 1; i < kThreads / 64; ++i) lse_combine(M, S, rm[i], rs[i]);
+    m_out[r] = M;
+    s_out[r] = S;
+    const int64_t t = tgt[r];
+    if (t >= col0 && t < col0 + n) pick[r] = to_f32<T>(row[t - col0]);
+  }
+}
+
+// Merge the per-chunk (m, s) of each row (chunk-major arrays [nchunks][rows]), write lse and the
+// per-row loss; flag targets outside [0, vocab) that are not ignore_index.
+__global__ __launch_bounds__(kThreads) void ce_finish_kernel(const float* __restrict__ m_part,
+                                                             const float* __restrict__ s_part, int nchunks,
+                                                             const float* __restrict__ pick,
+                                                             const int64_t* __restrict__ tgt,
+                                                             float* __restrict__ lse, float* __restrict__ loss_rows,
+                                                             int* __restrict__ bad, int64_t rows, int64_t vocab,
+                                                             int64_t ignore) {
+  const int64_t r = (int64_t)blockIdx.x * kThreads + threadIdx.x;
+  if (r >= rows) return;
+  float m = -INFINITY, s = 0.f;
+  for (int c = 0; c < nchunks; ++c) lse_combine(m, s, m_part[(int64_t)c * rows + r], s_part[(int64_t)c * rows + r]);
+  const float l = m + __logf(s);
+  lse[r] = l;
+  const int64_t t = tgt[r];
+  const bool valid = t != ignore && t >= 0 && t < vocab;
+  if (t != ignore && !valid && bad) *bad = 1;
+  loss_rows[r] = valid ? l - pick[r] : 0.f;
+}
+
+// loss = sum(loss_rows) / count(valid); one workgroup, fixed-order strided sums + fixed tree.
+__global__ __launch_bounds__(kThreads) void ce_mean_kernel(const float* __restrict__ loss_rows,
+                                                           const int64_t* __restrict__ tgt, int64_t rows,
+                                                           int64_t vocab, int64_t ignore, float* __restrict__ loss,
+                                                           float* __restrict__ count) {
+  __shared__ float sl[kThreads], sc[kThreads];
+  float a = 0.f, c = 0.f;
+  for (int64_t r = threadIdx.x; r < rows; r += kThreads) {
+    a += loss_rows[r];
+    const int64_t t = tgt[r];
+    c += (t != ignore && t >= 0 && t < vocab) ? 1.f : 0.f;
+  }
+  sl[threadIdx.x] = a;
+  sc[threadIdx.x] = c;
+  __syncthreads();
+  for (int o = kThreads / 2; o > 0; o >>= 1) {
+    if ((int)threadIdx.x < o) {
+      sl[threadIdx.x] += sl[threadIdx.x + o];
+      sc[threadIdx.x] += sc[threadIdx.x + o];
+    }
+    __syncthreads();
+  }
+  if (threadIdx.x == 0) {
+    *loss = sl[0] / sc[0];
+    *count = sc[0];
+  }
+}
+
+// dz[r, c] = (exp(z[r, c] - lse[r]) - [c + col0 == tgt[r]]) * up / count for valid rows, else 0.
+template <typename T, typename O>
+__global__ __launch_bounds__(kThreads) void ce_grad_kernel(const typename T::storage* __restrict__ z, int64_t ld,
+                                                           int64_t n, int64_t col0, const int64_t* __restrict__ tgt,
+                                                           const float* __restrict__ lse,
+                                                           const float* __restrict__ count,
+                                                           const float* __restrict__ up,
+                                                           typename O::storage* __restrict__ dz, int64_t ldo,
+                                                           int64_t rows, int64_t vocab, int64_t ignore) {
+  const int64_t r = blockIdx.x;
+  const int64_t t = tgt[r];
+  const bool valid = t != ignore && t >= 0 && t < vocab;
+  const float scale = valid ? (up ? *up : 1.f) / *count : 0.f;
+  const float l = lse[r];
+  const typename T::storage* row = z + r * ld;
+  typename O::storage* out = dz + r * ldo;
+  for (int64_t c = (int64_t)blockIdx.y * kThreads + threadIdx.x; c < n; c += (int64_t)gridDim.y * kThreads) {
+    const float p = valid ? __expf(to_f32<T>(row[c]) - l) - ((c + col0 == t) ? 1.f : 0.f) : 0.f;
+    out[c] = from_f32<O>(p * scale);
+  }
+}
+
+bool dtype_ok(int dt) { return dt == Q3_F32 || dt == Q3_F16 || dt == Q3_BF16; }
+
+template <typename T>
+int stats_t(const void* z, int64_t ld, int64_t n, int64_t col0, const int64_t* tgt, float* m, float* s, float* pick,
+            int64_t rows, hipStream_t st) {
+  typedef typename T::storage S;
+  const int vec = ((uintptr_t)z % 16 == 0) && (ld % T::vec == 0);
+  ce_stats_kernel<T><<<(unsigned)rows, kThreads, 0, st>>>((const S*)z, ld, n, col0, tgt, m, s, pick, vec);
+  return (int)hipGetLastError();
+}
+
+template <typename T, typename O>
+int grad_t2(const void* z, int64_t ld, int64_t n, int64_t col0, const int64_t* tgt, const float* lse,
+            const float* count, const float* up, void* dz, int64_t ldo, int64_t rows, int64_t vocab, int64_t ignore,
+            hipStream_t st) {
+  int64_t gx = (n + kThreads - 1) / kThreads;
+  if (gx > 64) gx = 64;
+  ce_grad_kernel<T, O><<<dim3((unsigned)rows, (unsigned)gx), kThreads, 0, st>>>(
+      (const typename T::storage*)z, ld, n, col0, tgt, lse, count, up, (typename O::storage*)dz, ldo, rows, vocab,
+      ignore);
+  return (int)hipGetLastError();
+}
+
+template <typename T>
+int grad_t(int out_dtype, const void* z, int64_t ld, int64_t n, int64_t col0, const int64_t* tgt, const float* lse,
+           const float* count, const float* up, void* dz, int64_t ldo, int64_t rows, int64_t vocab, int64_t ignore,
+           hipStream_t st) {
+  if (out_dtype == Q3_BF16)
+    return grad_t2<T, BF16>(z, ld, n, col0, tgt, lse, count, up, dz, ldo, rows, vocab, ignore, st);
+  if (out_dtype == Q3_F16)
+    return grad_t2<T, F16>(z, ld, n, col0, tgt, lse, count, up, dz, ldo, rows, vocab, ignore, st);
+  return grad_t2<T, F32>(z, ld, n, col0, tgt, lse, count, up, dz, ldo, rows, vocab, ignore, st);
+}
+
+}  // namespace
+
+extern "C" {
+
+int q3_ce_shift_labels(const int64_t* labels, int64_t* tgt, int64_t batch, int64_t seq, int64_t ignore_index,
+                       hipStream_t stream) {
+  Q3_REQUIRE(labels && tgt && batch > 0 && seq > 0);
+  shift_labels_kernel<<<q3_grid_for(batch * seq, kThreads), kThreads, 0, stream>>>(labels, tgt, batch * seq, seq,
+                                                                                   ignore_index);
+  return (int)hipGetLastError();
+}
+
+int q3_ce_chunk_stats(int dtype, const void* z, int64_t ld, int64_t n, int64_t col0, const int64_t* tgt,
+                      float* m_out, float* s_out, float* pick, int64_t rows, hipStream_t stream) {
+  Q3_REQUIRE(dtype_ok(dtype) && z && tgt && m_out && s_out && pick && n > 0 && rows > 0 && ld >= n &&
+             rows < (1ll << 31));
+  if (dtype == Q3_BF16) return stats_t<BF16>(z, ld, n, col0, tgt, m_out, s_out, pick, rows, stream);
+  if (dtype == Q3_F16) return stats_t<F16>(z, ld, n, col0, tgt, m_out, s_out, pick, rows, stream);
+  return stats_t<F32>(z, ld, n, col0, tgt, m_out, s_out, pick, rows, stream);
+}
+
+int q3_ce_finish(const float* m_part, const float* s_part, int nchunks, const float* pick, const int64_t* tgt,
+                 float* lse, float* loss_rows, int* bad, float* loss, float* count, int64_t rows, int64_t vocab,
+                 int64_t ignore_index, hipStream_t stream) {
+  Q3_REQUIRE(m_part && s_part && nchunks > 0 && pick && tgt && lse && loss_rows && loss && count && rows > 0);
+  ce_finish_kernel<<<(unsigned)((rows + kThreads - 1) / kThreads), kThreads, 0, stream>>>(
+      m_part, s_part, nchunks, pick, tgt, lse, loss_rows, bad, rows, vocab, ignore_index);
+  ce_mean_kernel<<<1, kThreads, 0, stream>>>(loss_rows, tgt, rows, vocab, ignore_index, loss, count);
+  return (int)hipGetLastError();
+}
+
+int q3_ce_chunk_grad(int dtype, int out_dtype, const void* z, int64_t ld, int64_t n, int64_t col0, const int64_t* tgt,
+                     const float* lse, const float* count, const float* up, void* dz, int64_t ldo, int64_t rows,
+                     int64_t vocab, int64_t ignore_index, hipStream_t stream) {
+  Q3_REQUIRE(dtype_ok(dtype) && dtype_ok(out_dtype) && z && tgt && lse && count && dz && n > 0 && rows > 0 &&
+             rows < (1ll << 31) && ld >= n && ldo >= n);
+  if (dtype == Q3_BF16)
+    return grad_t<BF16>(out_dtype, z, ld, n, col0, tgt, lse, count, up, dz, ldo, rows, vocab, ignore_index, stream);
+  if (dtype == Q3_F16)
+    return grad_t<F16>(out_dtype, z, ld, n, col0, tgt, lse, count, up, dz, ldo, rows, vocab, ignore_index, stream);
+  return grad_t<F32>(out_dtype, z, ld, n, col0, tgt, lse, count, up, dz, ldo, rows, vocab, ignore_index, stream);
+}
+
+}  // extern "C"

@@ -204,15 +204,16 @@ __global__ __launch_bounds__(kBlock) void rope_apply_scalar_kernel(const typenam
 
 // ---------------------------------------------------------------- transpose
 // y[b][c][r] = x[b][r][c] through a 64x64 LDS tile (row padded to 66 elements: the column reads
-// of the store phase hit distinct banks).  Elements are moved as raw 16- or 32-bit words.
+// of the store phase hit distinct banks).  Elements are moved as raw 16- or 32-bit words.  Output
+// rows have stride ldy >= rows; the pad columns [rows, ldy) are written with zeros.
 template <typename W>
 __global__ __launch_bounds__(kBlock) void transpose_kernel(const W* __restrict__ x, W* __restrict__ y, int64_t rows,
-                                                           int64_t cols) {
+                                                           int64_t cols, int64_t ldy) {
   __shared__ W tile[64][66];
   const int64_t b = blockIdx.z;
   const int64_t r0 = (int64_t)blockIdx.y * 64, c0 = (int64_t)blockIdx.x * 64;
   const W* xb = x + b * rows * cols;
-  W* yb = y + b * rows * cols;
+  W* yb = y + b * cols * ldy;
   const int tx = threadIdx.x & 63, ty = threadIdx.x >> 6;
   for (int r = ty; r < 64; r += 4) {
     const int64_t gr = r0 + r, gc = c0 + tx;
@@ -221,7 +222,7 @@ __global__ __launch_bounds__(kBlock) void transpose_kernel(const W* __restrict__
   __syncthreads();
   for (int c = ty; c < 64; c += 4) {
     const int64_t gc = c0 + c, gr = r0 + tx;
-    if (gc < cols && gr < rows) yb[gc * rows + gr] = tile[tx][c];
+    if (gc < cols && gr < ldy) yb[gc * ldy + gr] = gr < rows ? tile[tx][c] : (W)0;
   }
 }
 
@@ -420,14 +421,15 @@ int q3_positions(int64_t* out, int64_t batch, int64_t seq, int64_t start, hipStr
   return (int)hipGetLastError();
 }
 
-int q3_transpose(int dtype, const void* x, void* y, int64_t batch, int64_t rows, int64_t cols, hipStream_t stream) {
-  Q3_REQUIRE(dtype_ok(dtype) && x && y && batch > 0 && rows > 0 && cols > 0 && batch < 65536);
-  Q3_REQUIRE((rows + 63) / 64 < 65536);
-  dim3 grid((unsigned)((cols + 63) / 64), (unsigned)((rows + 63) / 64), (unsigned)batch);
+int q3_transpose(int dtype, const void* x, void* y, int64_t batch, int64_t rows, int64_t cols, int64_t ldy,
+                 hipStream_t stream) {
+  Q3_REQUIRE(dtype_ok(dtype) && x && y && batch > 0 && rows > 0 && cols > 0 && batch < 65536 && ldy >= rows);
+  Q3_REQUIRE((ldy + 63) / 64 < 65536);
+  dim3 grid((unsigned)((cols + 63) / 64), (unsigned)((ldy + 63) / 64), (unsigned)batch);
   if (dtype == Q3_F32)
-    transpose_kernel<uint32_t><<<grid, kBlock, 0, stream>>>((const uint32_t*)x, (uint32_t*)y, rows, cols);
+    transpose_kernel<uint32_t><<<grid, kBlock, 0, stream>>>((const uint32_t*)x, (uint32_t*)y, rows, cols, ldy);
   else
-    transpose_kernel<u16><<<grid, kBlock, 0, stream>>>((const u16*)x, (u16*)y, rows, cols);
+    transpose_kernel<u16><<<grid, kBlock, 0, stream>>>((const u16*)x, (u16*)y, rows, cols, ldy);
   return (int)hipGetLastError();
 }
 

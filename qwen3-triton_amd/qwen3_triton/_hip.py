@@ -41,11 +41,19 @@ SIGNATURES: dict[str, tuple] = {
     "q3_cast": (_i32, [_i32, _i32, _p, _p, _i64, _p]),
     "q3_fill": (_i32, [_i32, _p, _f32, _i64, _p]),
     "q3_positions": (_i32, [_p, _i64, _i64, _i64, _p]),
-    "q3_transpose": (_i32, [_i32, _p, _p, _i64, _i64, _i64, _p]),
+    "q3_transpose": (_i32, [_i32, _p, _p, _i64, _i64, _i64, _i64, _p]),
     "q3_embedding_fwd": (_i32, [_i32, _p, _i32, _p, _p, _p, _i64, _i64, _i64, _p]),
     "q3_embedding_bwd_workspace_bytes": (_sz, [_i64]),
     "q3_embedding_bwd": (_i32, [_i32, _p, _i32, _p, _p, _p, _i64, _i64, _i64, _p]),
     "q3_gemm_nt": (_i32, [_i32, _i32, _p, _i64, _p, _i64, _p, _i64, _i64, _i64, _i64, _f32, _i32, _p]),
+    "q3_attention_mfma_supported": (_i32, [_i32, _i64]),
+    "q3_attention_fwd": (_i32, [_i32, _p, _p, _p, _p, _i64, _p, _p, _i64, _i64, _i64, _i64, _i64, _i64, _f32, _p]),
+    "q3_attention_bwd": (_i32, [_i32, _p, _p, _p, _p, _p, _p, _p, _i64, _p, _i64, _p, _p, _p, _p, _p, _i64, _i64,
+                                 _i64, _i64, _i64, _i64, _f32, _p]),
+    "q3_ce_shift_labels": (_i32, [_p, _p, _i64, _i64, _i64, _p]),
+    "q3_ce_chunk_stats": (_i32, [_i32, _p, _i64, _i64, _i64, _p, _p, _p, _p, _i64, _p]),
+    "q3_ce_finish": (_i32, [_p, _p, _i32, _p, _p, _p, _p, _p, _p, _p, _i64, _i64, _i64, _p]),
+    "q3_ce_chunk_grad": (_i32, [_i32, _i32, _p, _i64, _i64, _i64, _p, _p, _p, _p, _p, _i64, _i64, _i64, _i64, _p]),
     "q3_gemm_strided": (_i32, [_i32, _i32, _p, _i64, _i64, _p, _i64, _i64, _p, _i64, _i64, _i64, _i64, _f32, _i32,
                                 _p]),
 }

@@ -118,13 +118,15 @@ def positions(batch, seq, start, device):
     return out
 
 
-def transpose_last2(x):
-    """[..., R, C] -> contiguous [..., C, R] (a layout change done by a HIP kernel)."""
+def transpose_last2(x, pad_to=1):
+    """[..., R, C] -> contiguous [..., C, Rp] with Rp = R rounded up to ``pad_to`` (pad zero-filled);
+    a layout change done by a HIP kernel."""
     r, c = x.shape[-2], x.shape[-1]
+    rp = -(-r // pad_to) * pad_to
     batch = x.numel() // (r * c) if x.numel() else 0
-    y = torch.empty((*x.shape[:-2], c, r), device=x.device, dtype=x.dtype)
+    y = torch.empty((*x.shape[:-2], c, rp), device=x.device, dtype=x.dtype)
     if batch:
-        H.call("q3_transpose", H.code(x.dtype), x.data_ptr(), y.data_ptr(), batch, r, c, H.stream())
+        H.call("q3_transpose", H.code(x.dtype), x.data_ptr(), y.data_ptr(), batch, r, c, rp, H.stream())
     return y
 
 
@@ -144,3 +146,85 @@ def embedding_bwd(ids, dy, vocab, dtype):
     H.call("q3_embedding_bwd", H.code(dtype), ids.data_ptr(), int(ids.dtype == torch.int64), dy.data_ptr(),
            dw.data_ptr(), ws.data_ptr(), ids.numel(), vocab, h, H.stream())
     return dw
+
+
+# ---------------------------------------------------------------- attention
+def attention_mfma(dtype, d):
+    return bool(H.query("q3_attention_mfma_supported", H.code(dtype), d))
+
+
+def attention_fwd(q, k, v, scale):
+    """Causal GQA attention: q [B,Hq,Lq,D], k/v [B,Hkv,Lk,D] contiguous -> (o, lse [B,Hq,Lq] fp32)."""
+    b, hq, lq, d = q.shape
+    hkv, lk = k.shape[1], k.shape[2]
+    o = torch.empty_like(q)
+    lse = torch.empty((b, hq, lq), device=q.device, dtype=torch.float32)
+    vt, ldvt = None, 0
+    if attention_mfma(q.dtype, d):
+        vt = transpose_last2(v, pad_to=8)
+        ldvt = vt.shape[-1]
+    H.call("q3_attention_fwd", H.code(q.dtype), q.data_ptr(), k.data_ptr(), v.data_ptr(),
+           0 if vt is None else vt.data_ptr(), ldvt, o.data_ptr(), lse.data_ptr(), b, hq, hkv, lq, lk, d,
+           float(scale), H.stream())
+    return o, lse
+
+
+def attention_bwd(q, k, v, o, lse, do, scale):
+    b, hq, lq, d = q.shape
+    hkv, lk = k.shape[1], k.shape[2]
+    dq, dk, dv = torch.empty_like(q), torch.empty_like(k), torch.empty_like(v)
+    delta = torch.empty((b, hq, lq), device=q.device, dtype=torch.float32)
+    qt = kt = dot = None
+    ldq = ldk = 0
+    if attention_mfma(q.dtype, d):
+        qt, kt, dot = (transpose_last2(t, pad_to=8) for t in (q, k, do))
+        ldq, ldk = qt.shape[-1], kt.shape[-1]
+    p = (lambda t: 0 if t is None else t.data_ptr())
+    H.call("q3_attention_bwd", H.code(q.dtype), q.data_ptr(), k.data_ptr(), v.data_ptr(), o.data_ptr(),
+           do.data_ptr(), lse.data_ptr(), p(qt), ldq, p(kt), ldk, p(dot), delta.data_ptr(), dq.data_ptr(),
+           dk.data_ptr(), dv.data_ptr(), b, hq, hkv, lq, lk, d, float(scale), H.stream())
+    return dq, dk, dv
+
+
+# ---------------------------------------------------------------- cross-entropy
+def ce_shift_labels(labels, ignore_index):
+    b, s = labels.shape
+    tgt = torch.empty(b * s, device=labels.device, dtype=torch.int64)
+    H.call("q3_ce_shift_labels", labels.data_ptr(), tgt.data_ptr(), b, s, int(ignore_index), H.stream())
+    return tgt
+
+
+class CEState:
+    """Per-row partial statistics of a chunked causal CE (chunk-major [nchunks][rows])."""
+
+    def __init__(self, rows, nchunks, device):
+        f = dict(device=device, dtype=torch.float32)
+        self.rows, self.nchunks = rows, nchunks
+        self.m = torch.empty((nchunks, rows), **f)
+        self.s = torch.empty((nchunks, rows), **f)
+        self.pick = torch.empty(rows, **f)
+        self.lse = torch.empty(rows, **f)
+        self.loss_rows = torch.empty(rows, **f)
+        self.loss = torch.empty((), **f)
+        self.count = torch.empty((), **f)
+
+    def stats(self, chunk, z, ld, n, col0, tgt):
+        H.call("q3_ce_chunk_stats", H.code(z.dtype), z.data_ptr(), ld, n, col0, tgt.data_ptr(),
+               self.m[chunk].data_ptr(), self.s[chunk].data_ptr(), self.pick.data_ptr(), self.rows, H.stream())
+
+    def finish(self, tgt, vocab, ignore_index, check=True):
+        capturing = torch.cuda.is_current_stream_capturing()
+        bad = None if (capturing or not check) else torch.zeros((), device=tgt.device, dtype=torch.int32)
+        H.call("q3_ce_finish", self.m.data_ptr(), self.s.data_ptr(), self.nchunks, self.pick.data_ptr(),
+               tgt.data_ptr(), self.lse.data_ptr(), self.loss_rows.data_ptr(), 0 if bad is None else bad.data_ptr(),
+               self.loss.data_ptr(), self.count.data_ptr(), self.rows, vocab, int(ignore_index), H.stream())
+        if bad is not None and bool(bad.item()):
+            raise ValueError('CE label out of range')
+        return self.loss
+
+
+def ce_grad(z, ld, n, col0, tgt, lse, count, up, dz, ldo, vocab, ignore_index):
+    rows = tgt.numel()
+    H.call("q3_ce_chunk_grad", H.code(z.dtype), H.code(dz.dtype), z.data_ptr(), ld, n, col0, tgt.data_ptr(),
+           lse.data_ptr(), count.data_ptr(), 0 if up is None else up.data_ptr(), dz.data_ptr(), ldo, rows, vocab,
+           int(ignore_index), H.stream())

@@ -1,0 +1,93 @@
+"""Fused LM head + causal cross-entropy without materialising the full logits.
+
+New in this build (the reference materialises [B,S,V] logits: ``qwen3_triton/_model.py:131-132``
+``lm_head`` then ``kernels/loss.py:46-71``).  The vocabulary is processed in chunks of ``chunk``
+columns: each chunk's fp32 logits come from the matrix-core GEMM (h . W_c^T) into one reusable
+[T, chunk] buffer and are folded into per-row (max, sum-exp) partials plus the target logit; a
+final merge gives lse and the token-mean loss.  Backward recomputes each chunk's logits, turns them
+into dz = (softmax - onehot) * up / count (bf16), accumulates dH += dz . W_c in fp32 and writes
+dW_c = dz^T . h.  The same math as ``linear`` followed by ``causal_cross_entropy``.
+"""
+import torch
+
+from . import _ops
+from .linear import gemm_nt_into, matmul_into
+
+DEFAULT_CHUNK = 16384
+
+
+def _mfma_ok(x, w):
+    return x.dtype in (torch.bfloat16, torch.float16) and x.shape[-1] % 8 == 0 and w.shape[0] % 8 == 0
+
+
+def _chunk_logits(x, w, c0, n, zbuf):
+    """zbuf[:, :n] = x . w[c0:c0+n]^T in fp32."""
+    t, h = x.shape
+    if _mfma_ok(x, w):
+        gemm_nt_into(x, h, w[c0:c0 + n], h, zbuf, t, n, h)
+    else:
+        matmul_into(x, w[c0:c0 + n].t(), zbuf[:, :n])
+
+
+class _LMHeadCE(torch.autograd.Function):
+    @staticmethod
+    def forward(ctx, hidden, weight, labels, ignore_index, chunk):
+        if not hidden.is_cuda or hidden.ndim != 3 or weight.ndim != 2 or weight.shape[1] != hidden.shape[-1]:
+            raise ValueError('ROCm hidden [B,S,H] and weight [V,H] required')
+        if labels.shape != hidden.shape[:2] or labels.dtype != torch.int64 or labels.device != hidden.device:
+            raise ValueError('int64 [B,S] labels on the hidden device required')
+        if hidden.dtype != weight.dtype or not hidden.is_contiguous() or not weight.is_contiguous():
+            raise ValueError('Contiguous hidden/weight of one dtype required')
+        b, s, h = hidden.shape
+        v = weight.shape[0]
+        if s < 2:
+            raise ValueError('At least 2 tokens required')
+        x = hidden.view(b * s, h)
+        tgt = _ops.ce_shift_labels(labels, ignore_index)
+        chunk = min(chunk, v)
+        nch = -(-v // chunk)
+        st = _ops.CEState(b * s, nch, hidden.device)
+        zbuf = torch.empty((b * s, chunk), device=hidden.device, dtype=torch.float32)
+        for c in range(nch):
+            c0 = c * chunk
+            n = min(chunk, v - c0)
+            _chunk_logits(x, weight, c0, n, zbuf)
+            st.stats(c, zbuf, chunk, n, c0, tgt)
+        loss = st.finish(tgt, v, ignore_index)
+        ctx.save_for_backward(hidden, weight, tgt, st.lse, st.count)
+        ctx.ignore, ctx.chunk = ignore_index, chunk
+        return loss.clone()
+
+    @staticmethod
+    def backward(ctx, dy):
+        hidden, weight, tgt, lse, count = ctx.saved_tensors
+        b, s, h = hidden.shape
+        v, t, chunk = weight.shape[0], b * s, ctx.chunk
+        x = hidden.view(t, h)
+        up = dy.float().contiguous()
+        zbuf = torch.empty((t, chunk), device=x.device, dtype=torch.float32)
+        dz = torch.empty((t, chunk), device=x.device, dtype=x.dtype)
+        dx = torch.empty((t, h), device=x.device, dtype=torch.float32)
+        dw = torch.empty_like(weight)
+        mfma = _mfma_ok(x, weight) and t % 8 == 0
+        if mfma:
+            wt = _ops.transpose_last2(weight, pad_to=8)   # [H, Vp]
+            xt = _ops.transpose_last2(x)                  # [H, T]
+        for c in range(-(-v // chunk)):
+            c0 = c * chunk
+            n = min(chunk, v - c0)
+            _chunk_logits(x, weight, c0, n, zbuf)
+            _ops.ce_grad(zbuf, chunk, n, c0, tgt, lse, count, up, dz, chunk, v, ctx.ignore)
+            if mfma:
+                gemm_nt_into(dz, chunk, wt[:, c0:], wt.shape[1], dx, t, h, n, accumulate=c > 0)
+                dzt = _ops.transpose_last2(dz)            # [chunk, T]
+                gemm_nt_into(dzt, t, xt, t, dw[c0:c0 + n], n, h, t)
+            else:
+                matmul_into(dz[:, :n], weight[c0:c0 + n], dx, accumulate=c > 0)
+                matmul_into(dz[:, :n].t(), x, dw[c0:c0 + n])
+        return _ops.cast(dx, x.dtype).view(b, s, h), dw, None, None, None
+
+
+def lm_head_cross_entropy(hidden, weight, labels, *, ignore_index=-100, chunk=DEFAULT_CHUNK):
+    """Causal token-mean CE of ``hidden @ weight.T`` against ``labels`` (shift inside), fused."""
+    return _LMHeadCE.apply(hidden, weight, labels, ignore_index, chunk)

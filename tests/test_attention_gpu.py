@@ -1,0 +1,113 @@
+"""Causal GQA flash attention (matrix-core and SIMT paths) vs the CPU oracle and, at the benchmark
+shapes, vs torch SDPA in fp32 on the GPU.  Gates: forward max-rel <= 2e-2 (bf16) / 3e-3 (fp16) /
+1e-4 (fp32); LSE abs <= 3e-3; gradients cosine >= 0.999 and max-rel <= 4e-2 (bf16)."""
+import math
+
+import pytest
+import torch
+import torch.nn.functional as F
+
+import oracle as O
+from _util import cosine, max_rel, randn, seeded
+
+from qwen3_triton.kernels import _ops
+from qwen3_triton.kernels.attention import causal_attention
+from ops.triton.attention import attention_triton, attention_triton_autograd, attention_triton_qwen_prefill
+from ops.triton.attention_backward import attention_backward_triton
+
+pytestmark = pytest.mark.gpu
+
+FWD_TOL = {torch.bfloat16: 2e-2, torch.float16: 3e-3, torch.float32: 1e-4}
+GRAD_TOL = {torch.bfloat16: 4e-2, torch.float16: 8e-3, torch.float32: 1e-4}
+
+
+def make(b, hq, hk, lq, lk, d, dtype, seed):
+    gen = seeded(seed)
+    q = randn(b, hq, lq, d, gen=gen, dtype=dtype)
+    k = randn(b, hk, lk, d, gen=gen, dtype=dtype)
+    v = randn(b, hk, lk, d, gen=gen, dtype=dtype)
+    do = randn(b, hq, lq, d, gen=gen, dtype=dtype)
+    return q, k, v, do
+
+
+CASES = [(2, 4, 2, 17, 32), (1, 4, 2, 128, 128), (1, 16, 8, 129, 128), (2, 8, 2, 200, 64), (1, 32, 8, 300, 128),
+         (1, 2, 2, 1, 128), (2, 4, 1, 65, 32), (1, 4, 2, 33, 48)]
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16, torch.float32])
+@pytest.mark.parametrize("b,hq,hk,s,d", CASES)
+def test_attention_fwd_bwd_vs_oracle(b, hq, hk, s, d, dtype):
+    print(f"attention {b} {hq} {hk} {s} {d} {dtype}", flush=True)
+    q, k, v, do = make(b, hq, hk, s, s, d, dtype, seed=b * 100 + s + d)
+    qd, kd, vd = (t.cuda().requires_grad_() for t in (q, k, v))
+    o = causal_attention(qd, kd, vd)
+    dq, dk, dv = torch.autograd.grad(o, (qd, kd, vd), do.cuda())
+    eo = O.scaled_dot_product_attention_reference(q, k, v)
+    assert max_rel(o, eo) <= FWD_TOL[dtype]
+    _, lse = _ops.attention_fwd(qd.detach(), kd.detach(), vd.detach(), 1 / math.sqrt(d))
+    assert (lse.cpu() - O.attention_lse_reference(q, k)).abs().max() <= 3e-3
+    e = O.scaled_dot_product_attention_backward_reference(q, k, v, do)
+    for a, x, n in zip((dq, dk, dv), e, "qkv"):
+        assert cosine(a, x) >= 0.999, f"d{n} cosine"
+        assert max_rel(a, x) <= GRAD_TOL[dtype], f"d{n} max-rel {max_rel(a, x)}"
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
+@pytest.mark.parametrize("lq,lk", [(1, 1), (1, 300), (7, 129), (64, 1000), (129, 129)])
+def test_attention_query_suffix_offset(lq, lk, dtype):
+    """Prefill/chunked attention against a longer KV prefix (query i sees keys <= i + lk - lq)."""
+    q, k, v, _ = make(2, 8, 2, lq, lk, 128, dtype, seed=lq + lk)
+    o, lse = _ops.attention_fwd(q.cuda(), k.cuda(), v.cuda(), 128 ** -0.5)
+    assert max_rel(o, O.scaled_dot_product_attention_reference(q, k, v)) <= FWD_TOL[dtype]
+    assert (lse.cpu() - O.attention_lse_reference(q, k)).abs().max() <= 3e-3
+
+
+def test_reference_entry_points_agree():
+    q, k, v, do = make(1, 4, 2, 128, 128, 128, torch.bfloat16, seed=11)
+    qd, kd, vd = q.cuda(), k.cuda(), v.cuda()
+    o1 = attention_triton(qd, kd, vd)
+    o2, lse = attention_triton(qd, kd, vd, return_lse=True)
+    o3 = attention_triton_qwen_prefill(qd, kd, vd)
+    assert torch.equal(o1, o2) and torch.equal(o1, o3)
+    g1 = attention_backward_triton(qd, kd, vd, do.cuda(), lse=lse)
+    a = [t.requires_grad_() for t in (qd.clone(), kd.clone(), vd.clone())]
+    g2 = torch.autograd.grad(attention_triton_autograd(*a), a, do.cuda())
+    for x, y in zip(g1, g2):
+        assert torch.equal(x, y)
+    with pytest.raises(NotImplementedError):
+        attention_triton(qd, kd, vd, is_causal=False)
+
+
+def test_attention_invariants_full_shape():
+    """V constant -> O constant; row 0 -> V[0] (B4 S2048 Hq32 Hkv8 D128)."""
+    gen = seeded(2)
+    q = randn(4, 32, 2048, 128, gen=gen, dtype=torch.bfloat16).cuda()
+    k = randn(4, 8, 2048, 128, gen=gen, dtype=torch.bfloat16).cuda()
+    v = torch.full((4, 8, 2048, 128), 0.75, dtype=torch.bfloat16, device="cuda")
+    o, _ = _ops.attention_fwd(q, k, v, 128 ** -0.5)
+    assert bool((o == 0.75).all())
+    v = randn(4, 8, 2048, 128, gen=gen, dtype=torch.bfloat16).cuda()
+    o, _ = _ops.attention_fwd(q, k, v, 128 ** -0.5)
+    assert torch.equal(o[:, :, 0], v.repeat_interleave(4, 1)[:, :, 0])
+
+
+@pytest.mark.parametrize("b,s", [(4, 2048), (1, 8192)])
+def test_attention_benchmark_shapes_vs_sdpa_fp32(b, s):
+    """Config #3 shapes against torch SDPA in fp32 on the GPU (a library routine as the checker)."""
+    print(f"attention full {b}x{s}", flush=True)
+    gen = seeded(2)
+    q = randn(b, 32, s, 128, gen=gen, dtype=torch.bfloat16).cuda()
+    k = randn(b, 8, s, 128, gen=gen, dtype=torch.bfloat16).cuda()
+    v = randn(b, 8, s, 128, gen=gen, dtype=torch.bfloat16).cuda()
+    do = randn(b, 32, s, 128, gen=gen, dtype=torch.bfloat16).cuda()
+    qd, kd, vd = (t.clone().requires_grad_() for t in (q, k, v))
+    o = causal_attention(qd, kd, vd)
+    dq, dk, dv = torch.autograd.grad(o, (qd, kd, vd), do)
+    qf, kf, vf = (t.float().requires_grad_() for t in (q, k, v))
+    with torch.nn.attention.sdpa_kernel(torch.nn.attention.SDPBackend.MATH):
+        eo = F.scaled_dot_product_attention(qf, kf, vf, is_causal=True, enable_gqa=True)
+    e = torch.autograd.grad(eo, (qf, kf, vf), do.float())
+    assert max_rel(o, eo) <= 2e-2
+    for a, x in zip((dq, dk, dv), e):
+        assert cosine(a, x) >= 0.999
+        assert max_rel(a, x) <= 4e-2
