@@ -122,25 +122,31 @@ int q3_gemm_strided(int in_dtype, int out_dtype, const void* A, int64_t sam, int
                     hipStream_t stream);
 
 /* ------------------------------------------------------------------ causal GQA flash attention
- * Q/O [B,Hq,Lq,D], K/V [B,Hkv,Lk,D], Lk >= Lq, query i attends keys j <= i + (Lk - Lq); query head h
- * uses KV head h/(Hq/Hkv).  LSE [B,Hq,Lq] fp32 (natural log).  On the matrix-core path
- * (q3_attention_mfma_supported) the caller passes sequence-contiguous transposed copies of the
- * operands contracted over the sequence: vt = V^T [B,Hkv,D,ldvt] (forward), qt = Q^T [B,Hq,D,ldqt],
- * kt = K^T [B,Hkv,D,ldkt], dot = dO^T [B,Hq,D,ldqt] (backward), with ld* >= L, ld* % 8 == 0 and the
- * pad zero-filled (q3_transpose does this).  Other dtypes/head sizes run a SIMT path that ignores
- * them.  delta [B,Hq,Lq] fp32 is backward scratch (rowsum(O*dO)).
+ * Q/O/dO/dQ are [B,Hq,Lq,D] and K/V/dK/dV [B,Hkv,Lk,D] with D contiguous and element strides
+ * (qsb, qsh, qss) resp. (ksb, ksh, kss) for batch, head and position (so [B,S,H,D] and cache
+ * layouts are taken in place).  Lk >= Lq; query i attends keys j <= i + (Lk - Lq); query head h
+ * uses KV head h/(Hq/Hkv).  LSE and delta are [B,Hq,Lq] fp32 (natural-log LSE; delta =
+ * rowsum(O*dO) is backward scratch).  On the matrix-core path (q3_attention_mfma_supported) the
+ * caller also passes sequence-contiguous copies [B,H,D,ld] (ld >= L, ld % 8 == 0, zero pad) made by
+ * q3_attention_seq_major: vt of V (forward), qt of Q, kt of K and dot of dO (backward), and every
+ * row must be 16-byte aligned.  Other dtypes/head sizes run a SIMT path that ignores them.
  * Replaces: kernels/attention.py:20-50 + attention_kernels.py:9-253 (_attention_forward_kernel,
  *           _attention_delta_kernel, _attention_dq_kernel, _attention_dkdv_fused_kernel,
  *           _attention_kv_head_reduce_kernel), kernels/attention_precision.py:14-182,
- *           ops/triton/attention.py:29-292, ops/triton/attention_backward.py:21-236. */
+ *           ops/triton/attention.py:29-292, ops/triton/attention_backward.py:21-236,
+ *           inference/kernels.py:38-68 (_inference_cached_attention, prefill against the cache). */
 int q3_attention_mfma_supported(int dtype, int64_t d);
-int q3_attention_fwd(int dtype, const void* q, const void* k, const void* v, const void* vt, int64_t ldvt, void* o,
-                     float* lse, int64_t B, int64_t Hq, int64_t Hkv, int64_t Lq, int64_t Lk, int64_t D, float scale,
+int q3_attention_seq_major(int dtype, const void* x, int64_t sb, int64_t sh, int64_t ss, void* y, int64_t ldy,
+                           int64_t B, int64_t H, int64_t L, int64_t D, hipStream_t stream);
+int q3_attention_fwd(int dtype, const void* q, int64_t qsb, int64_t qsh, int64_t qss, const void* k, const void* v,
+                     int64_t ksb, int64_t ksh, int64_t kss, const void* vt, int64_t ldvt, void* o, float* lse,
+                     int64_t B, int64_t Hq, int64_t Hkv, int64_t Lq, int64_t Lk, int64_t D, float scale,
                      hipStream_t stream);
-int q3_attention_bwd(int dtype, const void* q, const void* k, const void* v, const void* o, const void* dout,
-                     const float* lse, const void* qt, int64_t ldqt, const void* kt, int64_t ldkt, const void* dot,
-                     float* delta, void* dq, void* dk, void* dv, int64_t B, int64_t Hq, int64_t Hkv, int64_t Lq,
-                     int64_t Lk, int64_t D, float scale, hipStream_t stream);
+int q3_attention_bwd(int dtype, const void* q, int64_t qsb, int64_t qsh, int64_t qss, const void* k, const void* v,
+                     int64_t ksb, int64_t ksh, int64_t kss, const void* o, const void* dout, const float* lse,
+                     const void* qt, int64_t ldqt, const void* kt, int64_t ldkt, const void* dot, float* delta,
+                     void* dq, void* dk, void* dv, int64_t B, int64_t Hq, int64_t Hkv, int64_t Lq, int64_t Lk,
+                     int64_t D, float scale, hipStream_t stream);
 
 /* ------------------------------------------------------------------ causal cross-entropy
  * Rows r = b*S + s of logits z (row stride ld).  tgt[r] = labels[b, s+1] for s < S-1, else
@@ -164,6 +170,32 @@ int q3_ce_finish(const float* m_part, const float* s_part, int nchunks, const fl
 int q3_ce_chunk_grad(int dtype, int out_dtype, const void* z, int64_t ld, int64_t n, int64_t col0, const int64_t* tgt,
                      const float* lse, const float* count, const float* up, void* dz, int64_t ldo, int64_t rows,
                      int64_t vocab, int64_t ignore_index, hipStream_t stream);
+
+/* ------------------------------------------------------------------ greedy decode
+ * y[m, n] = sum_k x[m, k] * W[n, k] for m < M <= 8 (x rows at stride ldx, y rows at stride ldy),
+ * fp32 accumulation, weights streamed once.  Replaces: inference/kernels.py:116-146 (_inference_gemv
+ * / linear for M <= 8), inference/accumulation.py:13-84. */
+int q3_gemv(int dtype, const void* x, int64_t ldx, const void* w, void* y, int64_t ldy, int64_t m, int64_t n,
+            int64_t k, hipStream_t stream);
+/* cache_{k,v}[b, h, start + s, :] = {k,v}[b, s, h, :]; caches are [B,H,capacity,D].
+ * Replaces: inference/kernels.py:24-35 (_inference_cache_append / append). */
+int q3_kv_append(int dtype, const void* k, const void* v, void* cache_k, void* cache_v, int64_t B, int64_t S,
+                 int64_t H, int64_t D, int64_t capacity, int64_t start, hipStream_t stream);
+/* One query per (b, head) against the first T_len cached positions (D = 128): split-KV partials of
+ * 128 keys, then a fixed-order merge.  q/out element strides (batch, head); cache strides
+ * (ksb, ksh) with position stride D.  Replaces: inference/kernels.py:71-113 (_inference_decode_partial,
+ * _inference_decode_merge, attention with s == 1). */
+size_t q3_decode_attention_workspace_bytes(int64_t B, int64_t Hq, int64_t T_len);
+int q3_decode_attention(int dtype, const void* q, int64_t qsb, int64_t qsh, const void* cache_k, const void* cache_v,
+                        int64_t ksb, int64_t ksh, void* out, int64_t osb, int64_t osh, void* workspace, int64_t B,
+                        int64_t Hq, int64_t Hkv, int64_t T_len, int64_t D, float scale, hipStream_t stream);
+/* Greedy step: token[b] = argmax logits[b, :vocab] (lowest index on ties), pad if done[b]; writes
+ * ids[b, pos] (ids may be NULL), next[b], done[b] |= token in eos[0:n_eos].
+ * Replaces: inference/kernels.py:149-173 (_inference_argmax_parts, _inference_select, select). */
+size_t q3_greedy_select_workspace_bytes(int64_t batch);
+int q3_greedy_select(int dtype, const void* logits, int64_t ld, int64_t batch, int64_t vocab, void* workspace,
+                     int64_t* ids, int64_t ld_ids, int64_t pos, int64_t* next, uint8_t* done, const int64_t* eos,
+                     int n_eos, int64_t pad, hipStream_t stream);
 
 #ifdef __cplusplus
 }

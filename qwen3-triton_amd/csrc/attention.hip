@@ -68,11 +68,16 @@ template <typename T> Q3_DEV bf16x8_t pack8(const f32x16& a, int v0) {
 // Row (key/query) index inside a 32x32 accumulator tile for element v of lane `lane`.
 Q3_DEV int acc_row(int v, int lane) { return 8 * (v >> 2) + 4 * (lane >> 5) + (v & 3); }
 
+// Element strides (batch, head, position) of a [B, H, L, D] operand whose D axis is contiguous.
+struct Lay {
+  int64_t b, h, s;
+};
+
 // ============================================================================ forward (MFMA)
 // Workgroup: 4 waves x 32 queries of one (b, h); key tiles of 64 double-buffered in LDS.
 template <typename T, int D>
-__global__ __launch_bounds__(kThreads) void attn_fwd_mfma(const u16* __restrict__ Q, const u16* __restrict__ K,
-                                                          const u16* __restrict__ Vt, u16* __restrict__ O,
+__global__ __launch_bounds__(kThreads) void attn_fwd_mfma(const u16* __restrict__ Q, Lay ql, const u16* __restrict__ K,
+                                                          Lay kl, const u16* __restrict__ Vt, u16* __restrict__ O,
                                                           float* __restrict__ LSE, int Hq, int Hkv, int Lq, int Lk,
                                                           int ldvt, float scale2) {
   constexpr int BN = 64, KP = D + 8, VP = BN + 8, KS = D / 16, DT = D / 32;
@@ -88,14 +93,14 @@ __global__ __launch_bounds__(kThreads) void attn_fwd_mfma(const u16* __restrict_
   const int off = Lk - Lq;
   const int q0 = qt * 128 + wave * 32;
   const int qi = q0 + (lane & 31);
-  const u16* Qb = Q + (int64_t)bh * Lq * D;
-  const u16* Kb = K + (int64_t)(b * Hkv + hk) * Lk * D;
+  const u16* Qb = Q + b * ql.b + h * ql.h;
+  const u16* Kb = K + b * kl.b + hk * kl.h;
   const u16* Vb = Vt + (int64_t)(b * Hkv + hk) * D * ldvt;
 
   bf16x8_t qf[KS];
 #pragma unroll
   for (int ks = 0; ks < KS; ++ks)
-    qf[ks] = qi < Lq ? as_frag(ld16(Qb + (int64_t)qi * D + ks * 16 + g * 8)) : as_frag(i32x4{0, 0, 0, 0});
+    qf[ks] = qi < Lq ? as_frag(ld16(Qb + qi * ql.s + ks * 16 + g * 8)) : as_frag(i32x4{0, 0, 0, 0});
 
   const int qlast_blk = min(qt * 128 + 127, Lq - 1) + off;
   const int kend = min(Lk, qlast_blk + 1);
@@ -109,7 +114,7 @@ __global__ __launch_bounds__(kThreads) void attn_fwd_mfma(const u16* __restrict_
 #pragma unroll
     for (int i = 0; i < KCH; ++i) {
       const int c = tid + i * kThreads, row = c / (D / 8), col = (c % (D / 8)) * 8, key = k0 + row;
-      rk[i] = key < Lk ? ld16(Kb + (int64_t)key * D + col) : i32x4{0, 0, 0, 0};
+      rk[i] = key < Lk ? ld16(Kb + key * kl.s + col) : i32x4{0, 0, 0, 0};
     }
 #pragma unroll
     for (int i = 0; i < VCH; ++i) {
@@ -196,7 +201,7 @@ __global__ __launch_bounds__(kThreads) void attn_fwd_mfma(const u16* __restrict_
 
   if (qi < Lq) {
     const float inv = 1.f / l;
-    u16* orow = O + ((int64_t)bh * Lq + qi) * D;
+    u16* orow = O + b * ql.b + h * ql.h + qi * ql.s;
 #pragma unroll
     for (int dt = 0; dt < DT; ++dt)
 #pragma unroll
@@ -216,12 +221,15 @@ __global__ __launch_bounds__(kThreads) void attn_fwd_mfma(const u16* __restrict_
 // delta[r] = sum_d O[r,d] * dO[r,d] (fp32), one wave per row.
 template <typename T>
 __global__ __launch_bounds__(kThreads) void attn_delta_kernel(const typename T::storage* __restrict__ O,
-                                                              const typename T::storage* __restrict__ dO,
-                                                              float* __restrict__ delta, int64_t rows, int D) {
+                                                              const typename T::storage* __restrict__ dO, Lay ql,
+                                                              float* __restrict__ delta, int64_t rows, int H, int L,
+                                                              int D) {
   const int64_t row = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
   if (row >= rows) return;
+  const int64_t b = row / ((int64_t)H * L), h = (row / L) % H, q = row % L;
+  const int64_t base = b * ql.b + h * ql.h + q * ql.s;
   float s = 0.f;
-  for (int d = lane_id(); d < D; d += 64) s += to_f32<T>(O[row * D + d]) * to_f32<T>(dO[row * D + d]);
+  for (int d = lane_id(); d < D; d += 64) s += to_f32<T>(O[base + d]) * to_f32<T>(dO[base + d]);
   s = group_sum<64>(s);
   if (lane_id() == 0) delta[row] = s;
 }
@@ -230,8 +238,9 @@ __global__ __launch_bounds__(kThreads) void attn_delta_kernel(const typename T::
 // Workgroup: 4 waves x 32 queries of one (b, h).  Per key tile: S^T = K Q^T, dP^T = V dO^T,
 // dS = P (dP - delta), dQ^T += Kt dS^T.
 template <typename T, int D>
-__global__ __launch_bounds__(kThreads) void attn_bwd_dq_mfma(const u16* __restrict__ Q, const u16* __restrict__ K,
-                                                             const u16* __restrict__ V, const u16* __restrict__ Kt,
+__global__ __launch_bounds__(kThreads) void attn_bwd_dq_mfma(const u16* __restrict__ Q, Lay ql,
+                                                             const u16* __restrict__ K, const u16* __restrict__ V,
+                                                             Lay kl, const u16* __restrict__ Kt,
                                                              const u16* __restrict__ dO,
                                                              const float* __restrict__ LSE,
                                                              const float* __restrict__ Delta, u16* __restrict__ dQ,
@@ -251,16 +260,17 @@ __global__ __launch_bounds__(kThreads) void attn_bwd_dq_mfma(const u16* __restri
   const int q0 = qt * 128 + wave * 32;
   const int qi = q0 + (lane & 31);
   const int64_t kvbase = (int64_t)(b * Hkv + hk);
-  const u16* Kb = K + kvbase * Lk * D;
-  const u16* Vb = V + kvbase * Lk * D;
+  const u16* Kb = K + b * kl.b + hk * kl.h;
+  const u16* Vb = V + b * kl.b + hk * kl.h;
   const u16* Ktb = Kt + kvbase * D * ldkt;
+  const int64_t qrow = b * ql.b + h * ql.h + (int64_t)qi * ql.s;
 
   bf16x8_t qf[KS], dof[KS];
 #pragma unroll
   for (int ks = 0; ks < KS; ++ks) {
     const bool ok = qi < Lq;
-    qf[ks] = ok ? as_frag(ld16(Q + ((int64_t)bh * Lq + qi) * D + ks * 16 + g * 8)) : as_frag(i32x4{0, 0, 0, 0});
-    dof[ks] = ok ? as_frag(ld16(dO + ((int64_t)bh * Lq + qi) * D + ks * 16 + g * 8)) : as_frag(i32x4{0, 0, 0, 0});
+    qf[ks] = ok ? as_frag(ld16(Q + qrow + ks * 16 + g * 8)) : as_frag(i32x4{0, 0, 0, 0});
+    dof[ks] = ok ? as_frag(ld16(dO + qrow + ks * 16 + g * 8)) : as_frag(i32x4{0, 0, 0, 0});
   }
   const float lse2 = qi < Lq ? LSE[(int64_t)bh * Lq + qi] * kLog2e : 0.f;
   const float dlt = qi < Lq ? Delta[(int64_t)bh * Lq + qi] : 0.f;
@@ -280,8 +290,8 @@ __global__ __launch_bounds__(kThreads) void attn_bwd_dq_mfma(const u16* __restri
     for (int i = 0; i < KCH; ++i) {
       const int c = tid + i * kThreads, row = c / (D / 8), col = (c % (D / 8)) * 8, key = k0 + row;
       const bool ok = key < Lk;
-      st16(&lk[row * KP + col], ok ? ld16(Kb + (int64_t)key * D + col) : i32x4{0, 0, 0, 0});
-      st16(&lvv[row * KP + col], ok ? ld16(Vb + (int64_t)key * D + col) : i32x4{0, 0, 0, 0});
+      st16(&lk[row * KP + col], ok ? ld16(Kb + key * kl.s + col) : i32x4{0, 0, 0, 0});
+      st16(&lvv[row * KP + col], ok ? ld16(Vb + key * kl.s + col) : i32x4{0, 0, 0, 0});
       const int d = c / (BN / 8), kc = k0 + (c % (BN / 8)) * 8;
       st16(&lkt[d * VP + (c % (BN / 8)) * 8], kc < ldkt ? ld16(Ktb + (int64_t)d * ldkt + kc) : i32x4{0, 0, 0, 0});
     }
@@ -313,7 +323,7 @@ __global__ __launch_bounds__(kThreads) void attn_bwd_dq_mfma(const u16* __restri
     }
   }
   if (qi < Lq) {
-    u16* row = dQ + ((int64_t)bh * Lq + qi) * D;
+    u16* row = dQ + qrow;
 #pragma unroll
     for (int dt = 0; dt < DT; ++dt)
 #pragma unroll
@@ -327,8 +337,9 @@ __global__ __launch_bounds__(kThreads) void attn_bwd_dq_mfma(const u16* __restri
 // P, dS; dV^T += dOt P, dK^T += Qt dS.  The group's query heads accumulate into the same
 // registers: no partial buffers, no atomics.
 template <typename T, int D>
-__global__ __launch_bounds__(kThreads) void attn_bwd_dkdv_mfma(const u16* __restrict__ Q, const u16* __restrict__ K,
-                                                               const u16* __restrict__ V, const u16* __restrict__ Qt,
+__global__ __launch_bounds__(kThreads) void attn_bwd_dkdv_mfma(const u16* __restrict__ Q, Lay ql,
+                                                               const u16* __restrict__ K, const u16* __restrict__ V,
+                                                               Lay kl, const u16* __restrict__ Qt,
                                                                const u16* __restrict__ dO,
                                                                const u16* __restrict__ dOt,
                                                                const float* __restrict__ LSE,
@@ -350,16 +361,16 @@ __global__ __launch_bounds__(kThreads) void attn_bwd_dkdv_mfma(const u16* __rest
   const int off = Lk - Lq;
   const int k0w = kt * 128 + wave * 32;
   const int kj = k0w + (lane & 31);
-  const u16* Kb = K + (int64_t)bk * Lk * D;
-  const u16* Vb = V + (int64_t)bk * Lk * D;
+  const u16* Kb = K + b * kl.b + hk * kl.h;
+  const u16* Vb = V + b * kl.b + hk * kl.h;
   (void)nkt;
 
   bf16x8_t kf[KS], vf[KS];
 #pragma unroll
   for (int ks = 0; ks < KS; ++ks) {
     const bool ok = kj < Lk;
-    kf[ks] = ok ? as_frag(ld16(Kb + (int64_t)kj * D + ks * 16 + g * 8)) : as_frag(i32x4{0, 0, 0, 0});
-    vf[ks] = ok ? as_frag(ld16(Vb + (int64_t)kj * D + ks * 16 + g * 8)) : as_frag(i32x4{0, 0, 0, 0});
+    kf[ks] = ok ? as_frag(ld16(Kb + kj * kl.s + ks * 16 + g * 8)) : as_frag(i32x4{0, 0, 0, 0});
+    vf[ks] = ok ? as_frag(ld16(Vb + kj * kl.s + ks * 16 + g * 8)) : as_frag(i32x4{0, 0, 0, 0});
   }
   f32x16 dk[DT], dv[DT];
 #pragma unroll
@@ -371,8 +382,8 @@ __global__ __launch_bounds__(kThreads) void attn_bwd_dkdv_mfma(const u16* __rest
   for (int hh = 0; hh < ratio; ++hh) {
     const int h = hk * ratio + hh;
     const int64_t bh = (int64_t)b * Hq + h;
-    const u16* Qb = Q + bh * Lq * D;
-    const u16* dOb = dO + bh * Lq * D;
+    const u16* Qb = Q + b * ql.b + h * ql.h;
+    const u16* dOb = dO + b * ql.b + h * ql.h;
     const u16* Qtb = Qt + bh * D * ldqt;
     const u16* dOtb = dOt + bh * D * ldqt;
     for (int q0 = qstart_blk; q0 < Lq; q0 += BM) {
@@ -380,8 +391,8 @@ __global__ __launch_bounds__(kThreads) void attn_bwd_dkdv_mfma(const u16* __rest
       for (int c = tid; c < RCH; c += kThreads) {
         const int row = c / (D / 8), col = (c % (D / 8)) * 8, qq = q0 + row;
         const bool ok = qq < Lq;
-        st16(&lq[row * KP + col], ok ? ld16(Qb + (int64_t)qq * D + col) : i32x4{0, 0, 0, 0});
-        st16(&ldo[row * KP + col], ok ? ld16(dOb + (int64_t)qq * D + col) : i32x4{0, 0, 0, 0});
+        st16(&lq[row * KP + col], ok ? ld16(Qb + qq * ql.s + col) : i32x4{0, 0, 0, 0});
+        st16(&ldo[row * KP + col], ok ? ld16(dOb + qq * ql.s + col) : i32x4{0, 0, 0, 0});
         const int d = c / (BM / 8), qc = q0 + (c % (BM / 8)) * 8;
         const bool okt = qc < ldqt;
         st16(&lqt[d * QP + (c % (BM / 8)) * 8], okt ? ld16(Qtb + (int64_t)d * ldqt + qc) : i32x4{0, 0, 0, 0});
@@ -425,8 +436,8 @@ __global__ __launch_bounds__(kThreads) void attn_bwd_dkdv_mfma(const u16* __rest
     }
   }
   if (kj < Lk) {
-    u16* krow = dK + ((int64_t)bk * Lk + kj) * D;
-    u16* vrow = dV + ((int64_t)bk * Lk + kj) * D;
+    u16* krow = dK + b * kl.b + hk * kl.h + kj * kl.s;
+    u16* vrow = dV + b * kl.b + hk * kl.h + kj * kl.s;
 #pragma unroll
     for (int dt = 0; dt < DT; ++dt)
 #pragma unroll
@@ -439,11 +450,11 @@ __global__ __launch_bounds__(kThreads) void attn_bwd_dkdv_mfma(const u16* __rest
 }
 
 // ============================================================================ SIMT path
-// One wave per (b, h, query).  D <= 256: lane holds d = lane + 64*i.
+// One wave per (b, h, query) or (b, kv head, key); D <= 256 with lane holding d = lane + 64*i.
 template <typename T>
-__global__ __launch_bounds__(kThreads) void attn_fwd_simt(const typename T::storage* __restrict__ Q,
+__global__ __launch_bounds__(kThreads) void attn_fwd_simt(const typename T::storage* __restrict__ Q, Lay ql,
                                                           const typename T::storage* __restrict__ K,
-                                                          const typename T::storage* __restrict__ V,
+                                                          const typename T::storage* __restrict__ V, Lay kl,
                                                           typename T::storage* __restrict__ O,
                                                           float* __restrict__ LSE, int Hq, int Hkv, int Lq, int Lk,
                                                           int D, float scale) {
@@ -452,37 +463,37 @@ __global__ __launch_bounds__(kThreads) void attn_fwd_simt(const typename T::stor
   if (row >= (int64_t)Hq * Lq) return;
   const int h = (int)(row / Lq), qi = (int)(row % Lq), hk = h / (Hq / Hkv), l = lane_id();
   const int64_t bh = (int64_t)b * Hq + h;
-  const typename T::storage* q = Q + (bh * Lq + qi) * D;
-  const typename T::storage* kb = K + ((int64_t)b * Hkv + hk) * Lk * D;
-  const typename T::storage* vb = V + ((int64_t)b * Hkv + hk) * Lk * D;
+  const int64_t qrow = b * ql.b + h * ql.h + qi * ql.s;
+  const typename T::storage* kb = K + b * kl.b + hk * kl.h;
+  const typename T::storage* vb = V + b * kl.b + hk * kl.h;
   float qv[4], acc[4] = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-  for (int i = 0; i < 4; ++i) qv[i] = (l + 64 * i < D) ? to_f32<T>(q[l + 64 * i]) : 0.f;
+  for (int i = 0; i < 4; ++i) qv[i] = (l + 64 * i < D) ? to_f32<T>(Q[qrow + l + 64 * i]) : 0.f;
   float m = -INFINITY, den = 0.f;
   const int kend = min(Lk, qi + (Lk - Lq) + 1);
   for (int j = 0; j < kend; ++j) {
     float s = 0.f;
 #pragma unroll
     for (int i = 0; i < 4; ++i)
-      if (l + 64 * i < D) s += qv[i] * to_f32<T>(kb[(int64_t)j * D + l + 64 * i]);
+      if (l + 64 * i < D) s += qv[i] * to_f32<T>(kb[j * kl.s + l + 64 * i]);
     s = group_sum<64>(s) * scale;
     const float mn = fmaxf(m, s), a = __expf(m - mn), p = __expf(s - mn);
     den = den * a + p;
 #pragma unroll
     for (int i = 0; i < 4; ++i)
-      if (l + 64 * i < D) acc[i] = acc[i] * a + p * to_f32<T>(vb[(int64_t)j * D + l + 64 * i]);
+      if (l + 64 * i < D) acc[i] = acc[i] * a + p * to_f32<T>(vb[j * kl.s + l + 64 * i]);
     m = mn;
   }
 #pragma unroll
   for (int i = 0; i < 4; ++i)
-    if (l + 64 * i < D) O[(bh * Lq + qi) * D + l + 64 * i] = from_f32<T>(acc[i] / den);
+    if (l + 64 * i < D) O[qrow + l + 64 * i] = from_f32<T>(acc[i] / den);
   if (l == 0) LSE[bh * Lq + qi] = m + __logf(den);
 }
 
 template <typename T>
-__global__ __launch_bounds__(kThreads) void attn_bwd_dq_simt(const typename T::storage* __restrict__ Q,
+__global__ __launch_bounds__(kThreads) void attn_bwd_dq_simt(const typename T::storage* __restrict__ Q, Lay ql,
                                                              const typename T::storage* __restrict__ K,
-                                                             const typename T::storage* __restrict__ V,
+                                                             const typename T::storage* __restrict__ V, Lay kl,
                                                              const typename T::storage* __restrict__ dO,
                                                              const float* __restrict__ LSE,
                                                              const float* __restrict__ Delta,
@@ -493,14 +504,15 @@ __global__ __launch_bounds__(kThreads) void attn_bwd_dq_simt(const typename T::s
   if (row >= (int64_t)Hq * Lq) return;
   const int h = (int)(row / Lq), qi = (int)(row % Lq), hk = h / (Hq / Hkv), l = lane_id();
   const int64_t bh = (int64_t)b * Hq + h;
-  const typename T::storage* kb = K + ((int64_t)b * Hkv + hk) * Lk * D;
-  const typename T::storage* vb = V + ((int64_t)b * Hkv + hk) * Lk * D;
+  const int64_t qrow = b * ql.b + h * ql.h + qi * ql.s;
+  const typename T::storage* kb = K + b * kl.b + hk * kl.h;
+  const typename T::storage* vb = V + b * kl.b + hk * kl.h;
   float qv[4], dov[4], acc[4] = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
     const bool ok = l + 64 * i < D;
-    qv[i] = ok ? to_f32<T>(Q[(bh * Lq + qi) * D + l + 64 * i]) : 0.f;
-    dov[i] = ok ? to_f32<T>(dO[(bh * Lq + qi) * D + l + 64 * i]) : 0.f;
+    qv[i] = ok ? to_f32<T>(Q[qrow + l + 64 * i]) : 0.f;
+    dov[i] = ok ? to_f32<T>(dO[qrow + l + 64 * i]) : 0.f;
   }
   const float lse = LSE[bh * Lq + qi], dl = Delta[bh * Lq + qi];
   const int kend = min(Lk, qi + (Lk - Lq) + 1);
@@ -509,25 +521,25 @@ __global__ __launch_bounds__(kThreads) void attn_bwd_dq_simt(const typename T::s
 #pragma unroll
     for (int i = 0; i < 4; ++i)
       if (l + 64 * i < D) {
-        s += qv[i] * to_f32<T>(kb[(int64_t)j * D + l + 64 * i]);
-        dp += dov[i] * to_f32<T>(vb[(int64_t)j * D + l + 64 * i]);
+        s += qv[i] * to_f32<T>(kb[j * kl.s + l + 64 * i]);
+        dp += dov[i] * to_f32<T>(vb[j * kl.s + l + 64 * i]);
       }
     s = group_sum<64>(s);
     dp = group_sum<64>(dp);
     const float p = __expf(s * scale - lse), ds = p * (dp - dl);
 #pragma unroll
     for (int i = 0; i < 4; ++i)
-      if (l + 64 * i < D) acc[i] += ds * to_f32<T>(kb[(int64_t)j * D + l + 64 * i]);
+      if (l + 64 * i < D) acc[i] += ds * to_f32<T>(kb[j * kl.s + l + 64 * i]);
   }
 #pragma unroll
   for (int i = 0; i < 4; ++i)
-    if (l + 64 * i < D) dQ[(bh * Lq + qi) * D + l + 64 * i] = from_f32<T>(acc[i] * scale);
+    if (l + 64 * i < D) dQ[qrow + l + 64 * i] = from_f32<T>(acc[i] * scale);
 }
 
 template <typename T>
-__global__ __launch_bounds__(kThreads) void attn_bwd_dkdv_simt(const typename T::storage* __restrict__ Q,
+__global__ __launch_bounds__(kThreads) void attn_bwd_dkdv_simt(const typename T::storage* __restrict__ Q, Lay ql,
                                                                const typename T::storage* __restrict__ K,
-                                                               const typename T::storage* __restrict__ V,
+                                                               const typename T::storage* __restrict__ V, Lay kl,
                                                                const typename T::storage* __restrict__ dO,
                                                                const float* __restrict__ LSE,
                                                                const float* __restrict__ Delta,
@@ -538,20 +550,21 @@ __global__ __launch_bounds__(kThreads) void attn_bwd_dkdv_simt(const typename T:
   const int b = blockIdx.z;
   if (row >= (int64_t)Hkv * Lk) return;
   const int hk = (int)(row / Lk), kj = (int)(row % Lk), ratio = Hq / Hkv, l = lane_id();
-  const int64_t bk = (int64_t)b * Hkv + hk;
+  const int64_t krow = b * kl.b + hk * kl.h + kj * kl.s;
   float kv[4], vv[4], ak[4] = {0.f, 0.f, 0.f, 0.f}, av[4] = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
     const bool ok = l + 64 * i < D;
-    kv[i] = ok ? to_f32<T>(K[(bk * Lk + kj) * D + l + 64 * i]) : 0.f;
-    vv[i] = ok ? to_f32<T>(V[(bk * Lk + kj) * D + l + 64 * i]) : 0.f;
+    kv[i] = ok ? to_f32<T>(K[krow + l + 64 * i]) : 0.f;
+    vv[i] = ok ? to_f32<T>(V[krow + l + 64 * i]) : 0.f;
   }
   const int off = Lk - Lq;
   for (int hh = 0; hh < ratio; ++hh) {
-    const int64_t bh = (int64_t)b * Hq + hk * ratio + hh;
+    const int h = hk * ratio + hh;
+    const int64_t bh = (int64_t)b * Hq + h;
     for (int qi = max(0, kj - off); qi < Lq; ++qi) {
-      const typename T::storage* q = Q + (bh * Lq + qi) * D;
-      const typename T::storage* d = dO + (bh * Lq + qi) * D;
+      const typename T::storage* q = Q + b * ql.b + h * ql.h + qi * ql.s;
+      const typename T::storage* d = dO + b * ql.b + h * ql.h + qi * ql.s;
       float s = 0.f, dp = 0.f;
 #pragma unroll
       for (int i = 0; i < 4; ++i)
@@ -573,65 +586,89 @@ __global__ __launch_bounds__(kThreads) void attn_bwd_dkdv_simt(const typename T:
 #pragma unroll
   for (int i = 0; i < 4; ++i)
     if (l + 64 * i < D) {
-      dK[(bk * Lk + kj) * D + l + 64 * i] = from_f32<T>(ak[i] * scale);
-      dV[(bk * Lk + kj) * D + l + 64 * i] = from_f32<T>(av[i]);
+      dK[krow + l + 64 * i] = from_f32<T>(ak[i] * scale);
+      dV[krow + l + 64 * i] = from_f32<T>(av[i]);
     }
+}
+
+// ============================================================================ sequence-major copy
+// y[(b*H + h)*D + d][s] = x[b*sb + h*sh + s*ss + d] for s < L, 0 for L <= s < ldy: the
+// sequence-contiguous operand copies of the matrix-core path.  64 x 64 (position x d) LDS tiles.
+__global__ __launch_bounds__(kThreads) void seq_major_kernel(const u16* __restrict__ x, Lay xl, u16* __restrict__ y,
+                                                             int64_t ldy, int H, int L, int D) {
+  __shared__ u16 tile[64][66];
+  const int bh = blockIdx.z, b = bh / H, h = bh % H;
+  const int s0 = blockIdx.x * 64, d0 = blockIdx.y * 64;
+  const int tx = threadIdx.x & 63, ty = threadIdx.x >> 6;
+  const u16* xb = x + b * xl.b + h * xl.h;
+  for (int r = ty; r < 64; r += 4) {
+    const int s = s0 + r, d = d0 + tx;
+    tile[r][tx] = (s < L && d < D) ? xb[s * xl.s + d] : (u16)0;
+  }
+  __syncthreads();
+  u16* yb = y + (int64_t)bh * D * ldy;
+  for (int c = ty; c < 64; c += 4) {
+    const int d = d0 + c, s = s0 + tx;
+    if (d < D && s < ldy) yb[(int64_t)d * ldy + s] = tile[tx][c];
+  }
 }
 
 // ============================================================================ host dispatch
 bool dtype_ok(int dt) { return dt == Q3_F32 || dt == Q3_F16 || dt == Q3_BF16; }
 
 template <typename T, int D>
-int fwd_mfma(const void* q, const void* k, const void* vt, void* o, float* lse, int B, int Hq, int Hkv, int Lq,
-             int Lk, int ldvt, float scale, hipStream_t s) {
+int fwd_mfma(const void* q, Lay ql, const void* k, Lay kl, const void* vt, void* o, float* lse, int B, int Hq,
+             int Hkv, int Lq, int Lk, int ldvt, float scale, hipStream_t s) {
   dim3 grid((unsigned)((Lq + 127) / 128), (unsigned)(B * Hq));
-  attn_fwd_mfma<T, D><<<grid, kThreads, 0, s>>>((const u16*)q, (const u16*)k, (const u16*)vt, (u16*)o, lse, Hq, Hkv,
-                                                 Lq, Lk, ldvt, scale * kLog2e);
+  attn_fwd_mfma<T, D><<<grid, kThreads, 0, s>>>((const u16*)q, ql, (const u16*)k, kl, (const u16*)vt, (u16*)o, lse,
+                                                 Hq, Hkv, Lq, Lk, ldvt, scale * kLog2e);
   return (int)hipGetLastError();
 }
 
 template <typename T, int D>
-int bwd_mfma(const void* q, const void* k, const void* v, const void* qt, const void* kt, const void* dout,
-             const void* dot, const float* lse, const float* delta, void* dq, void* dk, void* dv, int B, int Hq,
-             int Hkv, int Lq, int Lk, int ldqt, int ldkt, float scale, hipStream_t s) {
+int bwd_mfma(const void* q, Lay ql, const void* k, const void* v, Lay kl, const void* qt, const void* kt,
+             const void* dout, const void* dot, const float* lse, const float* delta, void* dq, void* dk, void* dv,
+             int B, int Hq, int Hkv, int Lq, int Lk, int ldqt, int ldkt, float scale, hipStream_t s) {
   dim3 g1((unsigned)((Lq + 127) / 128), (unsigned)(B * Hq));
-  attn_bwd_dq_mfma<T, D><<<g1, kThreads, 0, s>>>((const u16*)q, (const u16*)k, (const u16*)v, (const u16*)kt,
-                                                  (const u16*)dout, lse, delta, (u16*)dq, Hq, Hkv, Lq, Lk, ldkt, scale,
-                                                  scale * kLog2e);
+  attn_bwd_dq_mfma<T, D><<<g1, kThreads, 0, s>>>((const u16*)q, ql, (const u16*)k, (const u16*)v, kl,
+                                                  (const u16*)kt, (const u16*)dout, lse, delta, (u16*)dq, Hq, Hkv, Lq,
+                                                  Lk, ldkt, scale, scale * kLog2e);
   dim3 g2((unsigned)((Lk + 127) / 128), (unsigned)(B * Hkv));
-  attn_bwd_dkdv_mfma<T, D><<<g2, kThreads, 0, s>>>((const u16*)q, (const u16*)k, (const u16*)v, (const u16*)qt,
-                                                    (const u16*)dout, (const u16*)dot, lse, delta, (u16*)dk, (u16*)dv,
-                                                    Hq, Hkv, Lq, Lk, ldqt, scale, scale * kLog2e);
+  attn_bwd_dkdv_mfma<T, D><<<g2, kThreads, 0, s>>>((const u16*)q, ql, (const u16*)k, (const u16*)v, kl,
+                                                    (const u16*)qt, (const u16*)dout, (const u16*)dot, lse, delta,
+                                                    (u16*)dk, (u16*)dv, Hq, Hkv, Lq, Lk, ldqt, scale, scale * kLog2e);
   return (int)hipGetLastError();
 }
 
 template <typename T>
-int fwd_simt(const void* q, const void* k, const void* v, void* o, float* lse, int B, int Hq, int Hkv, int Lq, int Lk,
-             int D, float scale, hipStream_t s) {
+int fwd_simt(const void* q, Lay ql, const void* k, const void* v, Lay kl, void* o, float* lse, int B, int Hq, int Hkv,
+             int Lq, int Lk, int D, float scale, hipStream_t s) {
   typedef typename T::storage S;
   dim3 grid((unsigned)(((int64_t)Hq * Lq + 3) / 4), 1, (unsigned)B);
-  attn_fwd_simt<T><<<grid, kThreads, 0, s>>>((const S*)q, (const S*)k, (const S*)v, (S*)o, lse, Hq, Hkv, Lq, Lk, D,
-                                             scale);
+  attn_fwd_simt<T><<<grid, kThreads, 0, s>>>((const S*)q, ql, (const S*)k, (const S*)v, kl, (S*)o, lse, Hq, Hkv, Lq,
+                                             Lk, D, scale);
   return (int)hipGetLastError();
 }
 
 template <typename T>
-int bwd_simt(const void* q, const void* k, const void* v, const void* dout, const float* lse, const float* delta,
-             void* dq, void* dk, void* dv, int B, int Hq, int Hkv, int Lq, int Lk, int D, float scale, hipStream_t s) {
+int bwd_simt(const void* q, Lay ql, const void* k, const void* v, Lay kl, const void* dout, const float* lse,
+             const float* delta, void* dq, void* dk, void* dv, int B, int Hq, int Hkv, int Lq, int Lk, int D,
+             float scale, hipStream_t s) {
   typedef typename T::storage S;
   dim3 g1((unsigned)(((int64_t)Hq * Lq + 3) / 4), 1, (unsigned)B);
-  attn_bwd_dq_simt<T><<<g1, kThreads, 0, s>>>((const S*)q, (const S*)k, (const S*)v, (const S*)dout, lse, delta,
-                                              (S*)dq, Hq, Hkv, Lq, Lk, D, scale);
+  attn_bwd_dq_simt<T><<<g1, kThreads, 0, s>>>((const S*)q, ql, (const S*)k, (const S*)v, kl, (const S*)dout, lse,
+                                              delta, (S*)dq, Hq, Hkv, Lq, Lk, D, scale);
   dim3 g2((unsigned)(((int64_t)Hkv * Lk + 3) / 4), 1, (unsigned)B);
-  attn_bwd_dkdv_simt<T><<<g2, kThreads, 0, s>>>((const S*)q, (const S*)k, (const S*)v, (const S*)dout, lse, delta,
-                                                (S*)dk, (S*)dv, Hq, Hkv, Lq, Lk, D, scale);
+  attn_bwd_dkdv_simt<T><<<g2, kThreads, 0, s>>>((const S*)q, ql, (const S*)k, (const S*)v, kl, (const S*)dout, lse,
+                                                delta, (S*)dk, (S*)dv, Hq, Hkv, Lq, Lk, D, scale);
   return (int)hipGetLastError();
 }
 
 template <typename T>
-int delta_t(const void* o, const void* dout, float* delta, int64_t rows, int D, hipStream_t s) {
+int delta_t(const void* o, const void* dout, Lay ql, float* delta, int64_t rows, int H, int L, int D, hipStream_t s) {
   typedef typename T::storage S;
-  attn_delta_kernel<T><<<(unsigned)((rows + 3) / 4), kThreads, 0, s>>>((const S*)o, (const S*)dout, delta, rows, D);
+  attn_delta_kernel<T><<<(unsigned)((rows + 3) / 4), kThreads, 0, s>>>((const S*)o, (const S*)dout, ql, delta, rows, H,
+                                                                       L, D);
   return (int)hipGetLastError();
 }
 
@@ -639,6 +676,12 @@ bool shapes_ok(int64_t B, int64_t Hq, int64_t Hkv, int64_t Lq, int64_t Lk, int64
   return B > 0 && Hq > 0 && Hkv > 0 && Hq % Hkv == 0 && Lq > 0 && Lk >= Lq && D > 0 && D <= 256 &&
          B * Hq < 65536 && Lk < (1 << 30);
 }
+bool al16(const void* p) { return ((uintptr_t)p & 15) == 0; }
+// The matrix-core kernels move 16-byte vectors along D: rows must be 16-byte aligned.
+bool lay_ok(const void* p, Lay l) { return al16(p) && l.b % 8 == 0 && l.h % 8 == 0 && l.s % 8 == 0; }
+
+#define Q3_ATTN_D(T, FN, ...)                                        \
+  (D == 128 ? FN<T, 128>(__VA_ARGS__) : D == 64 ? FN<T, 64>(__VA_ARGS__) : FN<T, 32>(__VA_ARGS__))
 
 }  // namespace
 
@@ -648,65 +691,65 @@ int q3_attention_mfma_supported(int dtype, int64_t d) {
   return (dtype == Q3_BF16 || dtype == Q3_F16) && (d == 32 || d == 64 || d == 128);
 }
 
-int q3_attention_fwd(int dtype, const void* q, const void* k, const void* v, const void* vt, int64_t ldvt, void* o,
-                     float* lse, int64_t B, int64_t Hq, int64_t Hkv, int64_t Lq, int64_t Lk, int64_t D, float scale,
-                     hipStream_t stream) {
-  Q3_REQUIRE(dtype_ok(dtype) && q && k && o && lse && shapes_ok(B, Hq, Hkv, Lq, Lk, D));
-  if (q3_attention_mfma_supported(dtype, D)) {
-    Q3_REQUIRE(vt && ldvt >= Lk && ldvt % 8 == 0);
-    const int b = (int)B, hq = (int)Hq, hkv = (int)Hkv, lq = (int)Lq, lk = (int)Lk, ld = (int)ldvt;
-    if (dtype == Q3_BF16) {
-      if (D == 128) return fwd_mfma<BF16, 128>(q, k, vt, o, lse, b, hq, hkv, lq, lk, ld, scale, stream);
-      if (D == 64) return fwd_mfma<BF16, 64>(q, k, vt, o, lse, b, hq, hkv, lq, lk, ld, scale, stream);
-      return fwd_mfma<BF16, 32>(q, k, vt, o, lse, b, hq, hkv, lq, lk, ld, scale, stream);
-    }
-    if (D == 128) return fwd_mfma<F16, 128>(q, k, vt, o, lse, b, hq, hkv, lq, lk, ld, scale, stream);
-    if (D == 64) return fwd_mfma<F16, 64>(q, k, vt, o, lse, b, hq, hkv, lq, lk, ld, scale, stream);
-    return fwd_mfma<F16, 32>(q, k, vt, o, lse, b, hq, hkv, lq, lk, ld, scale, stream);
-  }
-  Q3_REQUIRE(v);
-  if (dtype == Q3_BF16) return fwd_simt<BF16>(q, k, v, o, lse, B, Hq, Hkv, Lq, Lk, D, scale, stream);
-  if (dtype == Q3_F16) return fwd_simt<F16>(q, k, v, o, lse, B, Hq, Hkv, Lq, Lk, D, scale, stream);
-  return fwd_simt<F32>(q, k, v, o, lse, B, Hq, Hkv, Lq, Lk, D, scale, stream);
+int q3_attention_seq_major(int dtype, const void* x, int64_t sb, int64_t sh, int64_t ss, void* y, int64_t ldy,
+                           int64_t B, int64_t H, int64_t L, int64_t D, hipStream_t stream) {
+  Q3_REQUIRE((dtype == Q3_BF16 || dtype == Q3_F16) && x && y && B > 0 && H > 0 && L > 0 && D > 0 && ldy >= L &&
+             B * H < 65536 && (D + 63) / 64 < 65536);
+  dim3 grid((unsigned)((ldy + 63) / 64), (unsigned)((D + 63) / 64), (unsigned)(B * H));
+  seq_major_kernel<<<grid, kThreads, 0, stream>>>((const u16*)x, Lay{sb, sh, ss}, (u16*)y, ldy, (int)H, (int)L,
+                                                  (int)D);
+  return (int)hipGetLastError();
 }
 
-int q3_attention_bwd(int dtype, const void* q, const void* k, const void* v, const void* o, const void* dout,
-                     const float* lse, const void* qt, int64_t ldqt, const void* kt, int64_t ldkt, const void* dot,
-                     float* delta, void* dq, void* dk, void* dv, int64_t B, int64_t Hq, int64_t Hkv, int64_t Lq,
-                     int64_t Lk, int64_t D, float scale, hipStream_t stream) {
+int q3_attention_fwd(int dtype, const void* q, int64_t qsb, int64_t qsh, int64_t qss, const void* k, const void* v,
+                     int64_t ksb, int64_t ksh, int64_t kss, const void* vt, int64_t ldvt, void* o, float* lse,
+                     int64_t B, int64_t Hq, int64_t Hkv, int64_t Lq, int64_t Lk, int64_t D, float scale,
+                     hipStream_t stream) {
+  Q3_REQUIRE(dtype_ok(dtype) && q && k && o && lse && shapes_ok(B, Hq, Hkv, Lq, Lk, D));
+  const Lay ql{qsb, qsh, qss}, kl{ksb, ksh, kss};
+  const int b = (int)B, hq = (int)Hq, hkv = (int)Hkv, lq = (int)Lq, lk = (int)Lk;
+  if (q3_attention_mfma_supported(dtype, D)) {
+    Q3_REQUIRE(vt && ldvt >= Lk && ldvt % 8 == 0 && lay_ok(q, ql) && lay_ok(k, kl) && lay_ok(o, ql) && al16(vt));
+    const int ld = (int)ldvt;
+    if (dtype == Q3_BF16) return Q3_ATTN_D(BF16, fwd_mfma, q, ql, k, kl, vt, o, lse, b, hq, hkv, lq, lk, ld, scale, stream);
+    return Q3_ATTN_D(F16, fwd_mfma, q, ql, k, kl, vt, o, lse, b, hq, hkv, lq, lk, ld, scale, stream);
+  }
+  Q3_REQUIRE(v);
+  if (dtype == Q3_BF16) return fwd_simt<BF16>(q, ql, k, v, kl, o, lse, b, hq, hkv, lq, lk, (int)D, scale, stream);
+  if (dtype == Q3_F16) return fwd_simt<F16>(q, ql, k, v, kl, o, lse, b, hq, hkv, lq, lk, (int)D, scale, stream);
+  return fwd_simt<F32>(q, ql, k, v, kl, o, lse, b, hq, hkv, lq, lk, (int)D, scale, stream);
+}
+
+int q3_attention_bwd(int dtype, const void* q, int64_t qsb, int64_t qsh, int64_t qss, const void* k, const void* v,
+                     int64_t ksb, int64_t ksh, int64_t kss, const void* o, const void* dout, const float* lse,
+                     const void* qt, int64_t ldqt, const void* kt, int64_t ldkt, const void* dot, float* delta,
+                     void* dq, void* dk, void* dv, int64_t B, int64_t Hq, int64_t Hkv, int64_t Lq, int64_t Lk,
+                     int64_t D, float scale, hipStream_t stream) {
   Q3_REQUIRE(dtype_ok(dtype) && q && k && v && o && dout && lse && delta && dq && dk && dv &&
              shapes_ok(B, Hq, Hkv, Lq, Lk, D));
-  int rc;
-  if (dtype == Q3_BF16) rc = delta_t<BF16>(o, dout, delta, B * Hq * Lq, (int)D, stream);
-  else if (dtype == Q3_F16) rc = delta_t<F16>(o, dout, delta, B * Hq * Lq, (int)D, stream);
-  else rc = delta_t<F32>(o, dout, delta, B * Hq * Lq, (int)D, stream);
-  if (rc) return rc;
+  const Lay ql{qsb, qsh, qss}, kl{ksb, ksh, kss};
   const int b = (int)B, hq = (int)Hq, hkv = (int)Hkv, lq = (int)Lq, lk = (int)Lk, d = (int)D;
+  int rc;
+  if (dtype == Q3_BF16) rc = delta_t<BF16>(o, dout, ql, delta, B * Hq * Lq, hq, lq, d, stream);
+  else if (dtype == Q3_F16) rc = delta_t<F16>(o, dout, ql, delta, B * Hq * Lq, hq, lq, d, stream);
+  else rc = delta_t<F32>(o, dout, ql, delta, B * Hq * Lq, hq, lq, d, stream);
+  if (rc) return rc;
   if (q3_attention_mfma_supported(dtype, D)) {
-    Q3_REQUIRE(qt && kt && dot && ldqt >= Lq && ldkt >= Lk && ldqt % 8 == 0 && ldkt % 8 == 0);
+    Q3_REQUIRE(qt && kt && dot && ldqt >= Lq && ldkt >= Lk && ldqt % 8 == 0 && ldkt % 8 == 0 && lay_ok(q, ql) &&
+               lay_ok(dout, ql) && lay_ok(dq, ql) && lay_ok(k, kl) && lay_ok(v, kl) && lay_ok(dk, kl) &&
+               lay_ok(dv, kl) && al16(qt) && al16(kt) && al16(dot));
     const int lq8 = (int)ldqt, lk8 = (int)ldkt;
-    if (dtype == Q3_BF16) {
-      if (D == 128)
-        return bwd_mfma<BF16, 128>(q, k, v, qt, kt, dout, dot, lse, delta, dq, dk, dv, b, hq, hkv, lq, lk, lq8, lk8,
-                                   scale, stream);
-      if (D == 64)
-        return bwd_mfma<BF16, 64>(q, k, v, qt, kt, dout, dot, lse, delta, dq, dk, dv, b, hq, hkv, lq, lk, lq8, lk8,
-                                  scale, stream);
-      return bwd_mfma<BF16, 32>(q, k, v, qt, kt, dout, dot, lse, delta, dq, dk, dv, b, hq, hkv, lq, lk, lq8, lk8,
-                                scale, stream);
-    }
-    if (D == 128)
-      return bwd_mfma<F16, 128>(q, k, v, qt, kt, dout, dot, lse, delta, dq, dk, dv, b, hq, hkv, lq, lk, lq8, lk8, scale,
-                                stream);
-    if (D == 64)
-      return bwd_mfma<F16, 64>(q, k, v, qt, kt, dout, dot, lse, delta, dq, dk, dv, b, hq, hkv, lq, lk, lq8, lk8, scale,
-                               stream);
-    return bwd_mfma<F16, 32>(q, k, v, qt, kt, dout, dot, lse, delta, dq, dk, dv, b, hq, hkv, lq, lk, lq8, lk8, scale,
-                             stream);
+    if (dtype == Q3_BF16)
+      return Q3_ATTN_D(BF16, bwd_mfma, q, ql, k, v, kl, qt, kt, dout, dot, lse, delta, dq, dk, dv, b, hq, hkv, lq, lk,
+                       lq8, lk8, scale, stream);
+    return Q3_ATTN_D(F16, bwd_mfma, q, ql, k, v, kl, qt, kt, dout, dot, lse, delta, dq, dk, dv, b, hq, hkv, lq, lk,
+                     lq8, lk8, scale, stream);
   }
-  if (dtype == Q3_BF16) return bwd_simt<BF16>(q, k, v, dout, lse, delta, dq, dk, dv, b, hq, hkv, lq, lk, d, scale, stream);
-  if (dtype == Q3_F16) return bwd_simt<F16>(q, k, v, dout, lse, delta, dq, dk, dv, b, hq, hkv, lq, lk, d, scale, stream);
-  return bwd_simt<F32>(q, k, v, dout, lse, delta, dq, dk, dv, b, hq, hkv, lq, lk, d, scale, stream);
+  if (dtype == Q3_BF16)
+    return bwd_simt<BF16>(q, ql, k, v, kl, dout, lse, delta, dq, dk, dv, b, hq, hkv, lq, lk, d, scale, stream);
+  if (dtype == Q3_F16)
+    return bwd_simt<F16>(q, ql, k, v, kl, dout, lse, delta, dq, dk, dv, b, hq, hkv, lq, lk, d, scale, stream);
+  return bwd_simt<F32>(q, ql, k, v, kl, dout, lse, delta, dq, dk, dv, b, hq, hkv, lq, lk, d, scale, stream);
 }
 
 }  // extern "C"

@@ -153,36 +153,72 @@ def attention_mfma(dtype, d):
     return bool(H.query("q3_attention_mfma_supported", H.code(dtype), d))
 
 
+def _bhsd_strides(t):
+    if t.stride(3) != 1:
+        raise ValueError("attention operands need a contiguous head dimension")
+    return t.stride(0), t.stride(1), t.stride(2)
+
+
+def seq_major(x, pad_to=8):
+    """[B,H,L,D]-indexed view (any b/h/s strides) -> contiguous [B,H,D,Lp], Lp = L rounded up to
+    ``pad_to``, zero pad (the sequence-contiguous operand copy of the matrix-core attention)."""
+    b, h, l, d = x.shape
+    lp = -(-l // pad_to) * pad_to
+    y = torch.empty((b, h, d, lp), device=x.device, dtype=x.dtype)
+    H.call("q3_attention_seq_major", H.code(x.dtype), x.data_ptr(), *_bhsd_strides(x), y.data_ptr(), lp, b, h, l, d,
+           H.stream())
+    return y
+
+
 def attention_fwd(q, k, v, scale):
-    """Causal GQA attention: q [B,Hq,Lq,D], k/v [B,Hkv,Lk,D] contiguous -> (o, lse [B,Hq,Lq] fp32)."""
+    """Causal GQA attention on [B,H,L,D]-indexed views (D contiguous; batch/head/position strides free,
+    k and v sharing theirs) -> (o laid out like q, lse [B,Hq,Lq] fp32)."""
     b, hq, lq, d = q.shape
     hkv, lk = k.shape[1], k.shape[2]
+    if v.stride() != k.stride():
+        raise ValueError("k and v must share strides")
     o = torch.empty_like(q)
+    if o.stride() != q.stride():
+        o = torch.empty_strided(q.shape, q.stride(), device=q.device, dtype=q.dtype)
     lse = torch.empty((b, hq, lq), device=q.device, dtype=torch.float32)
     vt, ldvt = None, 0
     if attention_mfma(q.dtype, d):
-        vt = transpose_last2(v, pad_to=8)
+        vt = seq_major(v)
         ldvt = vt.shape[-1]
-    H.call("q3_attention_fwd", H.code(q.dtype), q.data_ptr(), k.data_ptr(), v.data_ptr(),
-           0 if vt is None else vt.data_ptr(), ldvt, o.data_ptr(), lse.data_ptr(), b, hq, hkv, lq, lk, d,
-           float(scale), H.stream())
+    H.call("q3_attention_fwd", H.code(q.dtype), q.data_ptr(), *_bhsd_strides(q), k.data_ptr(), v.data_ptr(),
+           *_bhsd_strides(k), 0 if vt is None else vt.data_ptr(), ldvt, o.data_ptr(), lse.data_ptr(), b, hq, hkv,
+           lq, lk, d, float(scale), H.stream())
     return o, lse
+
+
+def _like(t, ref):
+    """t re-laid out with ref's strides (a copy only when they differ)."""
+    if t.stride() == ref.stride():
+        return t
+    out = torch.empty_strided(ref.shape, ref.stride(), device=ref.device, dtype=ref.dtype)
+    out.copy_(t)
+    return out
 
 
 def attention_bwd(q, k, v, o, lse, do, scale):
     b, hq, lq, d = q.shape
     hkv, lk = k.shape[1], k.shape[2]
-    dq, dk, dv = torch.empty_like(q), torch.empty_like(k), torch.empty_like(v)
+    o, do = _like(o, q), _like(do, q)
+    v = _like(v, k)
+    dq = torch.empty_strided(q.shape, q.stride(), device=q.device, dtype=q.dtype)
+    dk = torch.empty_strided(k.shape, k.stride(), device=k.device, dtype=k.dtype)
+    dv = torch.empty_strided(k.shape, k.stride(), device=k.device, dtype=k.dtype)
     delta = torch.empty((b, hq, lq), device=q.device, dtype=torch.float32)
     qt = kt = dot = None
     ldq = ldk = 0
     if attention_mfma(q.dtype, d):
-        qt, kt, dot = (transpose_last2(t, pad_to=8) for t in (q, k, do))
+        qt, kt, dot = seq_major(q), seq_major(k), seq_major(do)
         ldq, ldk = qt.shape[-1], kt.shape[-1]
     p = (lambda t: 0 if t is None else t.data_ptr())
-    H.call("q3_attention_bwd", H.code(q.dtype), q.data_ptr(), k.data_ptr(), v.data_ptr(), o.data_ptr(),
-           do.data_ptr(), lse.data_ptr(), p(qt), ldq, p(kt), ldk, p(dot), delta.data_ptr(), dq.data_ptr(),
-           dk.data_ptr(), dv.data_ptr(), b, hq, hkv, lq, lk, d, float(scale), H.stream())
+    H.call("q3_attention_bwd", H.code(q.dtype), q.data_ptr(), *_bhsd_strides(q), k.data_ptr(), v.data_ptr(),
+           *_bhsd_strides(k), o.data_ptr(), do.data_ptr(), lse.data_ptr(), p(qt), ldq, p(kt), ldk, p(dot),
+           delta.data_ptr(), dq.data_ptr(), dk.data_ptr(), dv.data_ptr(), b, hq, hkv, lq, lk, d, float(scale),
+           H.stream())
     return dq, dk, dv
 
 
