@@ -25,6 +25,24 @@ from .kernels.residual import residual_add
 from .kernels.rotary import apply_rotary, rotary_tables
 
 
+def rope_theta(config):
+    """RoPE base of an HF Qwen3 config (``rope_theta``, or ``rope_parameters['rope_theta']`` in
+    newer transformers releases)."""
+    theta = getattr(config, 'rope_theta', None)
+    if theta is None:
+        theta = (getattr(config, 'rope_parameters', None) or {}).get('rope_theta', 10000.0)
+    return float(theta)
+
+
+def scaled_rope(config):
+    """True when the config asks for a RoPE scaling variant (anything but the default rotation)."""
+    for name in ('rope_scaling', 'rope_parameters'):
+        spec = getattr(config, name, None)
+        if spec and spec.get('rope_type', spec.get('type', 'default')) not in (None, 'default'):
+            return True
+    return False
+
+
 @dataclass(frozen=True)
 class ComputeOptions:
     """Switches of ``_model.py:22-27``; ``fused_lm_head_loss`` (new) computes the loss with the
@@ -70,8 +88,8 @@ class TritonRotary(nn.Module):
     def __init__(self, config):
         super().__init__()
         # Frequencies are static configuration: built on the host in fp32 (``_model.py:49-55``).
-        freq = 1. / (config.rope_theta ** (torch.arange(0, config.head_dim, 2, device='cpu',
-                                                        dtype=torch.float32) / config.head_dim))
+        freq = 1. / (rope_theta(config) ** (torch.arange(0, config.head_dim, 2, device='cpu',
+                                                         dtype=torch.float32) / config.head_dim))
         self.register_buffer('inv_freq', freq, persistent=False)
 
     def forward(self, positions, dtype):
@@ -166,7 +184,7 @@ class TritonQwen3ForCausalLM(nn.Module):
             raise ValueError('Official Qwen3 config required')
         if config.hidden_act != 'silu' or config.attention_dropout != 0 or getattr(config, 'attention_bias', False):
             raise ValueError('Only SiLU, zero dropout, bias-free Qwen3 supported')
-        if getattr(config, 'use_sliding_window', False) or getattr(config, 'rope_scaling', None):
+        if getattr(config, 'use_sliding_window', False) or scaled_rope(config):
             raise ValueError('Sliding window and scaled RoPE are not implemented')
         if config.head_dim % 2 or config.num_attention_heads % config.num_key_value_heads:
             raise ValueError('Even rotary dimension and valid GQA required')

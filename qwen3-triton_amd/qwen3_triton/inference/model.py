@@ -8,7 +8,7 @@ from pathlib import Path
 import torch
 from torch import nn
 
-from .._model import TritonQwen3ForCausalLM
+from .._model import TritonQwen3ForCausalLM, rope_theta
 from ..configuration import OptimizationOptions
 from ..kernels import _ops
 from ..kernels.activation import swiglu
@@ -79,7 +79,7 @@ class TritonQwen3Inference(nn.Module):
 
     def _inv_freq(self):
         c = self.config
-        return 1. / (c.rope_theta ** (torch.arange(0, c.head_dim, 2, dtype=torch.float32) / c.head_dim))
+        return 1. / (rope_theta(c) ** (torch.arange(0, c.head_dim, 2, dtype=torch.float32) / c.head_dim))
 
     @classmethod
     def random_init(cls, config, *, seed=0, std=0.02, device='cuda', **kw):

@@ -111,3 +111,29 @@ def test_attention_benchmark_shapes_vs_sdpa_fp32(b, s):
     for a, x in zip((dq, dk, dv), e):
         assert cosine(a, x) >= 0.999
         assert max_rel(a, x) <= 4e-2
+
+
+def test_attention_strided_layouts_bshd_and_cache():
+    """[B,S,H,D] views and a capacity-strided KV cache are read in place (no layout copies)."""
+    from qwen3_triton.kernels.attention import causal_attention_bshd
+    gen = seeded(21)
+    q = randn(2, 40, 8, 128, gen=gen, dtype=torch.bfloat16)
+    k = randn(2, 40, 2, 128, gen=gen, dtype=torch.bfloat16)
+    v = randn(2, 40, 2, 128, gen=gen, dtype=torch.bfloat16)
+    do = randn(2, 40, 8, 128, gen=gen, dtype=torch.bfloat16)
+    qd, kd, vd = (t.cuda().requires_grad_() for t in (q, k, v))
+    o = causal_attention_bshd(qd, kd, vd)
+    grads = torch.autograd.grad(o, (qd, kd, vd), do.cuda())
+    qh, kh, vh, dh = (t.transpose(1, 2) for t in (q, k, v, do))
+    assert max_rel(o.transpose(1, 2), O.scaled_dot_product_attention_reference(qh, kh, vh)) <= 2e-2
+    e = O.scaled_dot_product_attention_backward_reference(qh, kh, vh, dh)
+    for a, x in zip(grads, e):
+        assert cosine(a.transpose(1, 2), x) >= 0.999
+    # cache layout [B,Hkv,C,D] with C > L, queries as the suffix of the key range
+    cache_k = torch.zeros(2, 2, 100, 128, dtype=torch.bfloat16)
+    cache_v = torch.zeros(2, 2, 100, 128, dtype=torch.bfloat16)
+    cache_k[:, :, :40] = kh
+    cache_v[:, :, :40] = vh
+    ck, cv = cache_k.cuda(), cache_v.cuda()
+    oq, _ = _ops.attention_fwd(qh[:, :, 30:].cuda(), ck[:, :, :40], cv[:, :, :40], 128 ** -0.5)
+    assert max_rel(oq, O.scaled_dot_product_attention_reference(qh[:, :, 30:], kh, vh)) <= 2e-2

@@ -1,0 +1,67 @@
+"""Decode kernels: small-M GEMV, KV append, split-KV decode attention, greedy select."""
+import pytest
+import torch
+
+import oracle as O
+from _util import max_rel, randn, seeded
+
+from qwen3_triton.inference import kernels as K
+
+pytestmark = pytest.mark.gpu
+
+
+@pytest.mark.parametrize("m", [1, 2, 5, 8])
+@pytest.mark.parametrize("n,k", [(4096, 4096), (1024, 4096), (4096, 12288), (151936, 4096), (37, 64), (5000, 520)])
+def test_gemv(m, n, k):
+    print(f"gemv m={m} n={n} k={k}", flush=True)
+    gen = seeded(m + n + k)
+    x = randn(m, k, gen=gen, dtype=torch.bfloat16)
+    w = randn(n, k, gen=gen, dtype=torch.bfloat16, scale=0.02)
+    y = K.linear(x.cuda(), w.cuda())
+    e = x.double() @ w.double().t()
+    assert max_rel(y, e) <= 8e-3
+    y2 = K.linear(x.cuda(), w.cuda())
+    assert torch.equal(y, y2)  # deterministic
+
+
+def test_kv_append():
+    gen = seeded(1)
+    k = randn(2, 5, 3, 128, gen=gen, dtype=torch.bfloat16)
+    v = randn(2, 5, 3, 128, gen=gen, dtype=torch.bfloat16)
+    ck = torch.zeros(2, 3, 20, 128, dtype=torch.bfloat16, device="cuda")
+    cv = torch.zeros_like(ck)
+    K.append(k.cuda(), v.cuda(), ck, cv, 7)
+    assert torch.equal(ck[:, :, 7:12].cpu(), k.transpose(1, 2))
+    assert torch.equal(cv[:, :, 7:12].cpu(), v.transpose(1, 2))
+    assert bool((ck[:, :, :7] == 0).all()) and bool((ck[:, :, 12:] == 0).all())
+
+
+@pytest.mark.parametrize("b,hq,hk,t", [(1, 32, 8, 1), (1, 32, 8, 2048), (8, 32, 8, 1100), (2, 4, 2, 129),
+                                       (1, 32, 8, 2304)])
+def test_decode_attention(b, hq, hk, t):
+    gen = seeded(t)
+    cap = t + 5
+    q = randn(b, 1, hq, 128, gen=gen, dtype=torch.bfloat16)
+    kk = randn(b, hk, cap, 128, gen=gen, dtype=torch.bfloat16)
+    vv = randn(b, hk, cap, 128, gen=gen, dtype=torch.bfloat16)
+    out = K.attention(q.cuda(), kk.cuda(), vv.cuda(), t - 1)
+    e = O.scaled_dot_product_attention_reference(q.transpose(1, 2), kk[:, :, :t], vv[:, :, :t])
+    assert max_rel(out.transpose(1, 2), e) <= 2e-2
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
+def test_greedy_select_ties_pad_eos(dtype):
+    v = 151936
+    logits = torch.randn(4, v).to(dtype)
+    logits[0, 5] = logits[0, 77] = logits[0, 150000] = 100.0   # ties -> lowest index
+    logits[1, v - 1] = 50.0
+    logits[2, 3] = 60.0
+    lg = logits.cuda()
+    ids = torch.zeros(4, 10, dtype=torch.int64, device="cuda")
+    nxt = torch.empty(4, 1, dtype=torch.int64, device="cuda")
+    done = torch.tensor([False, False, True, False], device="cuda")
+    K.select(lg, ids, nxt, done, 6, (v - 1,), 9)
+    exp = O.argmax_lowest_reference(logits.float())
+    assert nxt[:, 0].tolist() == [5, v - 1, 9, int(exp[3])]
+    assert ids[:, 6].tolist() == nxt[:, 0].tolist()
+    assert done.tolist() == [False, True, True, False]
