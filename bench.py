@@ -1,0 +1,285 @@
+"""Benchmark: Qwen3-8B decoder layer forward+backward on one MI355X (the headline metric), plus
+greedy decode tokens/s.
+
+One "step" = forward + backward of one Qwen3-8B-shape decoder layer (q/k/v/o 4096->4096/1024/1024/
+4096, gate/up 4096->12288, down 12288->4096, fused per-head QK-norm + RoPE, GQA causal flash
+attention, SwiGLU) over 8192 tokens (batch 4 x seq 2048), bf16 weights/activations, fp32
+accumulation, weight gradients included.  Synthetic data: weights N(0, 0.02) (seed 3), hidden
+states and upstream gradients N(0, 1).
+
+Printed: one JSON line (rank 0).  ``value`` = tokens/s of the step; ``roofline`` = the dominant
+kernel (matrix-core GEMM) timed live with HIP events on its stream inside the timed region;
+``cpu_baseline`` = the fp32 CPU oracle's decoder layer on a bounded sample, on this host's cores;
+``decode`` = greedy decode tokens/s of the 36-layer Qwen3-8B (random bf16 weights, seed 4): eager
+prefill, then one captured decode-step HIP graph replayed per token.
+"""
+import argparse
+import faulthandler
+import json
+import math
+import os
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+for p in (ROOT, os.path.join(ROOT, "qwen3-triton_amd")):
+    if p not in sys.path:
+        sys.path.insert(0, p)
+
+PEAK_BF16_TFLOPS = 2500.0   # MI355X dense bf16 matrix-core peak
+PEAK_HBM_GBS = 8000.0       # MI355X HBM3E
+
+
+def qwen3_8b_config(layers):
+    from transformers import Qwen3Config
+    return Qwen3Config(vocab_size=151936, hidden_size=4096, intermediate_size=12288, num_hidden_layers=layers,
+                       num_attention_heads=32, num_key_value_heads=8, head_dim=128, rope_theta=1e6,
+                       rms_norm_eps=1e-6, tie_word_embeddings=False, max_position_embeddings=40960,
+                       initializer_range=0.02)
+
+
+class GemmTimer:
+    """Wraps the matrix-core GEMM launcher: records a HIP event pair on the launching stream around
+    every GEMM of the timed region, with its algorithmic FLOPs (2*M*N*K)."""
+
+    def __init__(self, linear_module):
+        self.mod = linear_module
+        self.orig = linear_module.gemm_nt_into
+        self.records = []
+        self.active = False
+
+    def __enter__(self):
+        import torch
+        orig = self.orig
+
+        def timed(a, lda, bnk, ldb, out, m, n, k, **kw):
+            if not self.active:
+                return orig(a, lda, bnk, ldb, out, m, n, k, **kw)
+            s, e = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            s.record()
+            orig(a, lda, bnk, ldb, out, m, n, k, **kw)
+            e.record()
+            self.records.append((s, e, 2.0 * m * n * k))
+
+        self.mod.gemm_nt_into = timed
+        return self
+
+    def __exit__(self, *exc):
+        self.mod.gemm_nt_into = self.orig
+
+    def summary(self):
+        ms = sum(s.elapsed_time(e) for s, e, _ in self.records)
+        flops = sum(f for _, _, f in self.records)
+        n = len(self.records)
+        return n, ms, flops
+
+
+def decoder_layer_bench(steps, warmup):
+    import torch
+    from qwen3_triton.components import DecoderLayer
+    from qwen3_triton.configuration import OptimizationOptions
+    from qwen3_triton.kernels import linear as linear_mod
+    from qwen3_triton.kernels.rotary import rotary_tables
+    from qwen3_triton._model import rope_theta
+
+    torch.manual_seed(3)
+    cfg = qwen3_8b_config(1)
+    layer = DecoderLayer(cfg, OptimizationOptions()).to(device="cuda", dtype=torch.bfloat16)
+    gen = torch.Generator(device="cuda").manual_seed(3)
+    with torch.no_grad():
+        for name, p in layer.named_parameters():
+            if name.endswith("norm.weight"):
+                p.fill_(1.0)
+            else:
+                p.normal_(0.0, 0.02, generator=gen)
+    b, s, h = 4, 2048, 4096
+    x = torch.randn(b, s, h, device="cuda", dtype=torch.bfloat16, generator=gen).requires_grad_()
+    dy = torch.randn(b, s, h, device="cuda", dtype=torch.bfloat16, generator=gen)
+    pos = torch.arange(s, device="cuda", dtype=torch.int64).repeat(b, 1)
+    inv = (1.0 / (rope_theta(cfg) ** (torch.arange(0, 128, 2, dtype=torch.float32) / 128))).cuda()
+    cos, sin = rotary_tables(pos, inv, torch.bfloat16)
+    params = list(layer.parameters())
+
+    def step():
+        x.grad = None
+        for p in params:
+            p.grad = None
+        y = layer(x, (cos, sin))
+        y.backward(dy)
+
+    for _ in range(warmup):
+        step()
+    torch.cuda.synchronize()
+    with GemmTimer(linear_mod) as gt:
+        gt.active = True
+        start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        start.record()
+        for _ in range(steps):
+            step()
+        end.record()
+        torch.cuda.synchronize()
+        wall = time.perf_counter() - t0
+        gt.active = False
+    ms_step = start.elapsed_time(end) / steps
+    n, gemm_ms, gemm_flops = gt.summary()
+    tokens = b * s
+    # algorithmic matrix-core work of the step: projections 3x (fwd, dX, dW) + causal attention
+    gemm_step_flops = 3 * 2 * tokens * (h * (4096 + 1024 + 1024 + 4096) + 3 * h * 12288)
+    attn_step_flops = 3.5 * 2 * b * 32 * s * s * 128   # causal fwd (1x) + bwd (2.5x)
+    return {
+        "tokens": tokens, "ms_per_step": ms_step, "wall_s": wall,
+        "tokens_per_s": tokens / (ms_step * 1e-3),
+        "gemm_launches": n, "gemm_ms_per_step": gemm_ms / steps, "gemm_flops_per_step": gemm_flops / steps,
+        "gemm_tflops": gemm_flops / (gemm_ms * 1e-3) / 1e12 if gemm_ms > 0 else 0.0,
+        "algorithmic_tflops_per_step": (gemm_step_flops + attn_step_flops) / 1e12,
+        "step_tflops": (gemm_step_flops + attn_step_flops) / (ms_step * 1e-3) / 1e12,
+    }
+
+
+def cpu_baseline(seconds_budget=20.0):
+    """fp32 CPU oracle decoder layer forward+backward on batch 1 x 512 tokens (same shapes and
+    weight distribution), median of timed repetitions after one warm-up."""
+    import torch
+    import oracle as O
+    threads = os.cpu_count() or 1
+    torch.set_num_threads(threads)
+    oc = O.OracleConfig(vocab_size=16, hidden_size=4096, intermediate_size=12288, num_hidden_layers=1,
+                        num_attention_heads=32, num_key_value_heads=8, head_dim=128)
+    params = {k: v.requires_grad_() for k, v in O.init_params(oc, seed=3).items() if k.startswith("model.layers.0.")}
+    tokens = 512
+    gen = torch.Generator().manual_seed(3)
+    x = torch.randn(1, tokens, 4096, generator=gen).requires_grad_()
+    dy = torch.randn(1, tokens, 4096, generator=gen)
+    cos, sin = O.rotary_tables_reference(torch.arange(tokens)[None], O.rope_inv_freq(1e6, 128))
+
+    def run():
+        for p in params.values():
+            p.grad = None
+        y = O.decoder_layer_reference(x, params, "model.layers.0.", oc, cos, sin)
+        y.backward(dy)
+
+    t0 = time.perf_counter()
+    run()
+    first = time.perf_counter() - t0
+    reps = max(1, min(5, int(seconds_budget / max(first, 1e-3))))
+    times = []
+    for _ in range(reps):
+        t0 = time.perf_counter()
+        run()
+        times.append(time.perf_counter() - t0)
+    times.sort()
+    med = times[len(times) // 2]
+    return {"value": tokens / med, "unit": "tokens/s", "cores": threads, "kind": "port",
+            "sample": f"fp32 oracle decoder layer fwd+bwd, batch 1 x {tokens} tokens, median of {reps}"}
+
+
+def decode_bench(batch, prompt, new_tokens):
+    """Greedy decode of the 36-layer Qwen3-8B: eager prefill, then one captured decode-step graph
+    replayed ``new_tokens`` times (the cache length lives on the device).  Timed with HIP events
+    around the replays only."""
+    import torch
+    from qwen3_triton.inference import DecodeSession, TritonQwen3Inference
+    cfg = qwen3_8b_config(36)
+    model = TritonQwen3Inference.random_init(cfg, seed=4, std=0.02, device="cuda")
+    gen = torch.Generator(device="cuda").manual_seed(4)
+    ids = torch.randint(0, cfg.vocab_size, (batch, prompt), device="cuda", generator=gen)
+    sess = DecodeSession(model, batch, prompt + new_tokens + 1)
+    s0, s1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    s0.record()
+    sess.prefill(ids)
+    s1.record()
+    sess.step()          # one eager step (warms the step's allocations)
+    sess.capture()
+    torch.cuda.synchronize()
+    prefill_ms = s0.elapsed_time(s1)
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    steps = new_tokens - 1
+    e0.record()
+    for _ in range(steps):
+        sess.step()
+    e1.record()
+    torch.cuda.synchronize()
+    per_step_ms = e0.elapsed_time(e1) / steps
+    layer_bytes = 36 * 2 * (4096 * (4096 + 1024 + 1024 + 4096) + 3 * 4096 * 12288)
+    head_bytes = 2 * 4096 * 151936
+    mean_ctx = prompt + 1 + new_tokens / 2
+    kv_bytes = 36 * 2 * 8 * 128 * 2 * mean_ctx * batch
+    step_bytes = layer_bytes + head_bytes + kv_bytes
+    del sess, model
+    torch.cuda.empty_cache()
+    return {"batch": batch, "prompt": prompt, "new_tokens": new_tokens, "prefill_ms": round(prefill_ms, 3),
+            "ms_per_step": round(per_step_ms, 4), "tokens_per_s": round(batch / (per_step_ms * 1e-3), 1),
+            "hbm_gb_per_step": round(step_bytes / 1e9, 3),
+            "hbm_gbs": round(step_bytes / (per_step_ms * 1e-3) / 1e9, 1),
+            "hbm_frac": round(step_bytes / (per_step_ms * 1e-3) / 1e9 / PEAK_HBM_GBS, 4)}
+
+
+def log(msg):
+    print(f"[bench] {msg}", file=sys.stderr, flush=True)
+
+
+def main():
+    faulthandler.enable()
+    ap = argparse.ArgumentParser(description=__doc__)
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=10)
+    ap.add_argument("--warmup", type=int, default=3)
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--no-decode", action="store_true")
+    ap.add_argument("--decode-tokens", type=int, default=256)
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print("bench.py measures one MI355X: this build has no multi-GPU path (collectives are out of scope); "
+              "run with --gpus 1", file=sys.stderr)
+        sys.exit(2)
+    import torch
+    if not torch.cuda.is_available():
+        print("bench.py needs a GPU", file=sys.stderr)
+        sys.exit(2)
+    from qwen3_triton import _hip
+    _hip.load()
+
+    log("decoder layer fwd+bwd")
+    layer = decoder_layer_bench(args.steps, args.warmup)
+    log(f"decoder layer: {layer['ms_per_step']:.3f} ms/step")
+    result = {
+        "metric": "decoder-layer fwd+bwd tokens/s @Qwen3-8B shape, 1 GPU, % roofline; decode tok/s",
+        "value": round(layer["tokens_per_s"], 1),
+        "unit": "tokens/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(layer["ms_per_step"], 3),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic (random N(0,0.02) weights, N(0,1) hidden states and upstream gradients)",
+        "config": {"workload": "qwen3-8b decoder layer fwd+bwd (config #4 layer)", "model": "Qwen3-8B layer",
+                   "global_batch": 4, "seq_len": 2048, "tokens_per_step": layer["tokens"], "parallelism": "none"},
+        "roofline": {"bound": "mfma", "kernel": "gemm_nt_kernel (bf16 MFMA GEMM)",
+                     "achieved": round(layer["gemm_tflops"], 1), "peak": PEAK_BF16_TFLOPS, "unit": "TFLOP/s",
+                     "frac": round(layer["gemm_tflops"] / PEAK_BF16_TFLOPS, 4), "traffic": None,
+                     "launches_per_step": layer["gemm_launches"] // args.steps,
+                     "flops_per_launch": layer["gemm_flops_per_step"] / max(1, layer["gemm_launches"] // args.steps)},
+        "step_roofline": {"algorithmic_tflop_per_step": round(layer["algorithmic_tflops_per_step"], 3),
+                          "achieved_tflops": round(layer["step_tflops"], 1),
+                          "frac": round(layer["step_tflops"] / PEAK_BF16_TFLOPS, 4)},
+    }
+    if not args.no_decode:
+        log("decode")
+        try:
+            result["decode"] = {"b1": decode_bench(1, 2048, args.decode_tokens),
+                                "b8": decode_bench(8, 1024, args.decode_tokens)}
+        except Exception as exc:  # report, do not hide the layer result
+            result["decode"] = {"error": repr(exc)}
+    if not args.no_cpu_baseline:
+        log("cpu baseline")
+        result["cpu_baseline"] = cpu_baseline()
+    print(json.dumps(result), flush=True)
+
+
+if __name__ == "__main__":
+    main()

@@ -87,8 +87,10 @@ int q3_add(int dtype, const void* a, const void* b, void* c, int64_t n, hipStrea
 int q3_cast(int src_dtype, int dst_dtype, const void* x, void* y, int64_t n, hipStream_t stream);
 /* x[:] = value (a kernel, never a memset, so it is safe inside captured graphs). */
 int q3_fill(int dtype, void* x, float value, int64_t n, hipStream_t stream);
-/* out[b, s] = start + s.  Replaces _model.py:29-32 (_positions), inference/kernels.py:12-21. */
-int q3_positions(int64_t* out, int64_t batch, int64_t seq, int64_t start, hipStream_t stream);
+/* out[b, s] = start + s (+ *start_dev when non-NULL).  Replaces _model.py:29-32 (_positions),
+ * inference/kernels.py:12-21. */
+int q3_positions(int64_t* out, int64_t batch, int64_t seq, int64_t start, const int64_t* start_dev,
+                 hipStream_t stream);
 /* y[b][c][r] = x[b][r][c] for 16-bit or 32-bit elements (a layout change, not arithmetic); output rows
  * have stride ldy >= rows and the pad [rows, ldy) is zero-filled. */
 int q3_transpose(int dtype, const void* x, void* y, int64_t batch, int64_t rows, int64_t cols, int64_t ldy,
@@ -177,25 +179,34 @@ int q3_ce_chunk_grad(int dtype, int out_dtype, const void* z, int64_t ld, int64_
  * / linear for M <= 8), inference/accumulation.py:13-84. */
 int q3_gemv(int dtype, const void* x, int64_t ldx, const void* w, void* y, int64_t ldy, int64_t m, int64_t n,
             int64_t k, hipStream_t stream);
-/* cache_{k,v}[b, h, start + s, :] = {k,v}[b, s, h, :]; caches are [B,H,capacity,D].
- * Replaces: inference/kernels.py:24-35 (_inference_cache_append / append). */
+/* cache_{k,v}[b, h, start + s, :] = {k,v}[b, s, h, :]; caches are [B,H,capacity,D].  When start_dev is
+ * non-NULL the start position is read from that device int64 at run time (a graph-replayable decode
+ * step); positions >= capacity are skipped.  Replaces: inference/kernels.py:24-35 (_inference_cache_append). */
 int q3_kv_append(int dtype, const void* k, const void* v, void* cache_k, void* cache_v, int64_t B, int64_t S,
-                 int64_t H, int64_t D, int64_t capacity, int64_t start, hipStream_t stream);
+                 int64_t H, int64_t D, int64_t capacity, int64_t start, const int64_t* start_dev,
+                 hipStream_t stream);
 /* One query per (b, head) against the first T_len cached positions (D = 128): split-KV partials of
  * 128 keys, then a fixed-order merge.  q/out element strides (batch, head); cache strides
- * (ksb, ksh) with position stride D.  Replaces: inference/kernels.py:71-113 (_inference_decode_partial,
- * _inference_decode_merge, attention with s == 1). */
+ * (ksb, ksh) with position stride D.  With len_dev non-NULL, T_len = *len_dev + 1 is read at run
+ * time and the launch covers the whole capacity (workspace sized for T_len = capacity).
+ * Replaces: inference/kernels.py:71-113 (_inference_decode_partial, _inference_decode_merge,
+ * attention with s == 1). */
 size_t q3_decode_attention_workspace_bytes(int64_t B, int64_t Hq, int64_t T_len);
 int q3_decode_attention(int dtype, const void* q, int64_t qsb, int64_t qsh, const void* cache_k, const void* cache_v,
                         int64_t ksb, int64_t ksh, void* out, int64_t osb, int64_t osh, void* workspace, int64_t B,
-                        int64_t Hq, int64_t Hkv, int64_t T_len, int64_t D, float scale, hipStream_t stream);
+                        int64_t Hq, int64_t Hkv, int64_t T_len, const int64_t* len_dev, int64_t capacity, int64_t D,
+                        float scale, hipStream_t stream);
 /* Greedy step: token[b] = argmax logits[b, :vocab] (lowest index on ties), pad if done[b]; writes
- * ids[b, pos] (ids may be NULL), next[b], done[b] |= token in eos[0:n_eos].
+ * ids[b, p] (ids may be NULL; p = pos, plus *pos_dev when pos_dev is non-NULL), next[b],
+ * done[b] |= token in eos[0:n_eos].
  * Replaces: inference/kernels.py:149-173 (_inference_argmax_parts, _inference_select, select). */
 size_t q3_greedy_select_workspace_bytes(int64_t batch);
 int q3_greedy_select(int dtype, const void* logits, int64_t ld, int64_t batch, int64_t vocab, void* workspace,
-                     int64_t* ids, int64_t ld_ids, int64_t pos, int64_t* next, uint8_t* done, const int64_t* eos,
-                     int n_eos, int64_t pad, hipStream_t stream);
+                     int64_t* ids, int64_t ld_ids, int64_t pos, const int64_t* pos_dev, int64_t* next, uint8_t* done,
+                     const int64_t* eos, int n_eos, int64_t pad, hipStream_t stream);
+/* *counter += by on the device (advances a device-resident cache length between graph replays).
+ * No counterpart in the reference: it is what lets one captured decode step serve every position. */
+int q3_advance(int64_t* counter, int64_t by, hipStream_t stream);
 
 #ifdef __cplusplus
 }

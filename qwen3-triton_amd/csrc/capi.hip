@@ -9,6 +9,6 @@ const char* q3_error_string(int code) {
   return hipGetErrorString((hipError_t)code);
 }
 
-int q3_abi_version(void) { return 1; }
+int q3_abi_version(void) { return 2; }
 
 }  // extern "C"

@@ -64,9 +64,13 @@ __global__ __launch_bounds__(kThreads) void gemv_kernel(const u16* __restrict__ 
 
 // ============================================================================ KV append
 // cache[b, h, start + s, :] = kv[b, s, h, :] for K and V ([B,S,H,D] -> [B,H,C,D]), 16-byte moves.
+// With start_dev the position is read from device memory (graph-replayable decode steps);
+// positions at or beyond the capacity are never written.
 __global__ __launch_bounds__(kThreads) void kv_append_kernel(const u16* __restrict__ k, const u16* __restrict__ v,
                                                              u16* __restrict__ ck, u16* __restrict__ cv, int S, int H,
-                                                             int D, int C, int start, int64_t nvec) {
+                                                             int D, int C, int start, const int64_t* start_dev,
+                                                             int64_t nvec) {
+  if (start_dev) start = (int)*start_dev;
   const int dv = D / 8;
   const int64_t stride = (int64_t)gridDim.x * kThreads;
   for (int64_t i = (int64_t)blockIdx.x * kThreads + threadIdx.x; i < nvec; i += stride) {
@@ -74,6 +78,7 @@ __global__ __launch_bounds__(kThreads) void kv_append_kernel(const u16* __restri
     const int64_t rest = i / dv;
     const int h = (int)(rest % H), s = (int)((rest / H) % S);
     const int64_t b = rest / ((int64_t)H * S);
+    if (start + s >= C || start < 0) continue;
     const int64_t dst = (((b * H + h) * C) + start + s) * D + c * 8;
     const int64_t src = rest * D + c * 8;
     *reinterpret_cast<i32x4*>(ck + dst) = *reinterpret_cast<const i32x4*>(k + src);
@@ -93,13 +98,25 @@ __global__ __launch_bounds__(64) void decode_attn_partial(const u16* __restrict_
                                                           const u16* __restrict__ ck, const u16* __restrict__ cv,
                                                           int64_t ksb, int64_t ksh, float* __restrict__ opart,
                                                           float* __restrict__ mpart, float* __restrict__ lpart,
-                                                          int Hq, int Hkv, int T_len, int splits, float scale) {
+                                                          int Hq, int Hkv, int T_len, const int64_t* len_dev,
+                                                          int capacity, int splits, float scale) {
   constexpr int D = 128;
   __shared__ float sc[kChunk];
   const int split = blockIdx.x, bh = blockIdx.y, b = bh / Hq, h = bh % Hq, hk = h / (Hq / Hkv);
   const int lane = threadIdx.x, t = lane & 15, grp = lane >> 4;
+  // len_dev holds the cache length before this token: the token itself is at that position.
+  if (len_dev) T_len = min((int)*len_dev + 1, capacity);
   const int k0 = split * kChunk;
   const int kend = min(T_len, k0 + kChunk);
+  const int64_t pi0 = (int64_t)bh * splits + split;
+  if (k0 >= T_len) {  // split beyond the live length (fixed-size launch): an empty partial
+    for (int e = lane; e < D; e += 64) opart[pi0 * D + e] = 0.f;
+    if (lane == 0) {
+      mpart[pi0] = -INFINITY;
+      lpart[pi0] = 0.f;
+    }
+    return;
+  }
   const u16* kb = ck + b * ksb + hk * ksh;
   const u16* vb = cv + b * ksb + hk * ksh;
   const Vec<T> qv = load_vec<T>(q + b * qsb + h * qsh + t * 8);
@@ -162,6 +179,7 @@ __global__ __launch_bounds__(64) void decode_attn_merge(const float* __restrict_
   float den = 0.f, o0 = 0.f, o1 = 0.f;
   for (int j = 0; j < splits; ++j) {
     const int64_t pi = (int64_t)bh * splits + j;
+    if (mpart[pi] == -INFINITY) continue;  // empty split
     const float w = __expf(mpart[pi] - M);
     den += w * lpart[pi];
     o0 += w * opart[pi * D + lane];
@@ -215,11 +233,12 @@ __global__ __launch_bounds__(kThreads) void argmax_parts_kernel(const typename T
 // Stage 2 (one thread per row): token = argmax (lowest index on ties); rows already done emit pad;
 // ids[row, pos] = next[row] = token; done |= token in eos.
 __global__ void select_kernel(const float* __restrict__ pv, const int* __restrict__ pi, int parts,
-                              int64_t* __restrict__ ids, int64_t ld_ids, int64_t pos, int64_t* __restrict__ next,
-                              uint8_t* __restrict__ done, const int64_t* __restrict__ eos, int n_eos, int64_t pad,
-                              int batch) {
+                              int64_t* __restrict__ ids, int64_t ld_ids, int64_t pos, const int64_t* pos_dev,
+                              int64_t* __restrict__ next, uint8_t* __restrict__ done,
+                              const int64_t* __restrict__ eos, int n_eos, int64_t pad, int batch) {
   const int row = blockIdx.x * blockDim.x + threadIdx.x;
   if (row >= batch) return;
+  if (pos_dev) pos += *pos_dev;
   float best = -INFINITY;
   int bi = 0x7fffffff;
   for (int j = 0; j < parts; ++j) {
@@ -234,10 +253,13 @@ __global__ void select_kernel(const float* __restrict__ pv, const int* __restric
   const int64_t tok = was_done ? pad : (int64_t)bi;
   bool end = false;
   for (int e = 0; e < n_eos; ++e) end = end || (tok == eos[e]);
-  if (ids) ids[row * ld_ids + pos] = tok;
+  if (ids && pos >= 0 && pos < ld_ids) ids[row * ld_ids + pos] = tok;
   next[row] = tok;
   done[row] = (was_done || end) ? 1 : 0;
 }
+
+// *counter += by (single thread): advances a device-resident cache length between replays.
+__global__ void advance_kernel(int64_t* counter, int64_t by) { *counter += by; }
 
 bool al16(const void* p) { return ((uintptr_t)p & 15) == 0; }
 
@@ -285,14 +307,15 @@ int q3_gemv(int dtype, const void* x, int64_t ldx, const void* w, void* y, int64
 }
 
 int q3_kv_append(int dtype, const void* k, const void* v, void* cache_k, void* cache_v, int64_t B, int64_t S,
-                 int64_t H, int64_t D, int64_t capacity, int64_t start, hipStream_t stream) {
+                 int64_t H, int64_t D, int64_t capacity, int64_t start, const int64_t* start_dev,
+                 hipStream_t stream) {
   Q3_REQUIRE((dtype == Q3_BF16 || dtype == Q3_F16) && k && v && cache_k && cache_v && B > 0 && S > 0 && H > 0 &&
-             D > 0 && D % 8 == 0 && start >= 0 && start + S <= capacity && al16(k) && al16(v) && al16(cache_k) &&
-             al16(cache_v));
+             D > 0 && D % 8 == 0 && (start_dev || (start >= 0 && start + S <= capacity)) && al16(k) && al16(v) &&
+             al16(cache_k) && al16(cache_v));
   const int64_t nvec = B * S * H * (D / 8);
   kv_append_kernel<<<q3_grid_for(nvec, kThreads), kThreads, 0, stream>>>(
       (const u16*)k, (const u16*)v, (u16*)cache_k, (u16*)cache_v, (int)S, (int)H, (int)D, (int)capacity, (int)start,
-      nvec);
+      start_dev, nvec);
   return (int)hipGetLastError();
 }
 
@@ -303,10 +326,12 @@ size_t q3_decode_attention_workspace_bytes(int64_t B, int64_t Hq, int64_t T_len)
 
 int q3_decode_attention(int dtype, const void* q, int64_t qsb, int64_t qsh, const void* cache_k, const void* cache_v,
                         int64_t ksb, int64_t ksh, void* out, int64_t osb, int64_t osh, void* workspace, int64_t B,
-                        int64_t Hq, int64_t Hkv, int64_t T_len, int64_t D, float scale, hipStream_t stream) {
+                        int64_t Hq, int64_t Hkv, int64_t T_len, const int64_t* len_dev, int64_t capacity, int64_t D,
+                        float scale, hipStream_t stream) {
   Q3_REQUIRE((dtype == Q3_BF16 || dtype == Q3_F16) && q && cache_k && cache_v && out && workspace && B > 0 &&
-             Hq > 0 && Hkv > 0 && Hq % Hkv == 0 && T_len > 0 && D == 128 && B * Hq < 65536);
-  const int64_t splits = (T_len + kChunk - 1) / kChunk;
+             Hq > 0 && Hkv > 0 && Hq % Hkv == 0 && T_len > 0 && T_len <= capacity && D == 128 && B * Hq < 65536);
+  // A device-resident length launches the fixed split count of the whole capacity (graph replay).
+  const int64_t splits = ((len_dev ? capacity : T_len) + kChunk - 1) / kChunk;
   float* opart = (float*)workspace;
   float* mpart = opart + B * Hq * splits * 128;
   float* lpart = mpart + B * Hq * splits;
@@ -314,13 +339,13 @@ int q3_decode_attention(int dtype, const void* q, int64_t qsb, int64_t qsh, cons
   if (dtype == Q3_BF16) {
     decode_attn_partial<BF16><<<grid, 64, 0, stream>>>((const u16*)q, qsb, qsh, (const u16*)cache_k,
                                                        (const u16*)cache_v, ksb, ksh, opart, mpart, lpart, (int)Hq,
-                                                       (int)Hkv, (int)T_len, (int)splits, scale);
+                                                       (int)Hkv, (int)T_len, len_dev, (int)capacity, (int)splits, scale);
     decode_attn_merge<BF16><<<(unsigned)(B * Hq), 64, 0, stream>>>(opart, mpart, lpart, (u16*)out, osb, osh, (int)Hq,
                                                                    (int)splits);
   } else {
     decode_attn_partial<F16><<<grid, 64, 0, stream>>>((const u16*)q, qsb, qsh, (const u16*)cache_k,
                                                       (const u16*)cache_v, ksb, ksh, opart, mpart, lpart, (int)Hq,
-                                                      (int)Hkv, (int)T_len, (int)splits, scale);
+                                                      (int)Hkv, (int)T_len, len_dev, (int)capacity, (int)splits, scale);
     decode_attn_merge<F16><<<(unsigned)(B * Hq), 64, 0, stream>>>(opart, mpart, lpart, (u16*)out, osb, osh, (int)Hq,
                                                                   (int)splits);
   }
@@ -330,8 +355,8 @@ int q3_decode_attention(int dtype, const void* q, int64_t qsb, int64_t qsh, cons
 size_t q3_greedy_select_workspace_bytes(int64_t batch) { return (size_t)batch * 64 * (sizeof(float) + sizeof(int)); }
 
 int q3_greedy_select(int dtype, const void* logits, int64_t ld, int64_t batch, int64_t vocab, void* workspace,
-                     int64_t* ids, int64_t ld_ids, int64_t pos, int64_t* next, uint8_t* done, const int64_t* eos,
-                     int n_eos, int64_t pad, hipStream_t stream) {
+                     int64_t* ids, int64_t ld_ids, int64_t pos, const int64_t* pos_dev, int64_t* next, uint8_t* done,
+                     const int64_t* eos, int n_eos, int64_t pad, hipStream_t stream) {
   Q3_REQUIRE((dtype == Q3_F32 || dtype == Q3_F16 || dtype == Q3_BF16) && logits && workspace && next && done &&
              batch > 0 && batch < 65536 && vocab > 0 && vocab < (1ll << 31) && n_eos >= 0 && (n_eos == 0 || eos));
   constexpr int parts = 64;
@@ -344,8 +369,14 @@ int q3_greedy_select(int dtype, const void* logits, int64_t ld, int64_t batch, i
     argmax_parts_kernel<F16><<<g, kThreads, 0, stream>>>((const u16*)logits, ld, vocab, pv, pi, parts);
   else
     argmax_parts_kernel<F32><<<g, kThreads, 0, stream>>>((const float*)logits, ld, vocab, pv, pi, parts);
-  select_kernel<<<(unsigned)((batch + 63) / 64), 64, 0, stream>>>(pv, pi, parts, ids, ld_ids, pos, next, done, eos,
-                                                                   n_eos, pad, (int)batch);
+  select_kernel<<<(unsigned)((batch + 63) / 64), 64, 0, stream>>>(pv, pi, parts, ids, ld_ids, pos, pos_dev, next,
+                                                                   done, eos, n_eos, pad, (int)batch);
+  return (int)hipGetLastError();
+}
+
+int q3_advance(int64_t* counter, int64_t by, hipStream_t stream) {
+  Q3_REQUIRE(counter);
+  advance_kernel<<<1, 1, 0, stream>>>(counter, by);
   return (int)hipGetLastError();
 }
 

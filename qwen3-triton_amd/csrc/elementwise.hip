@@ -99,7 +99,8 @@ __global__ __launch_bounds__(kBlock) void fill_kernel(typename T::storage* __res
 }
 
 __global__ __launch_bounds__(kBlock) void positions_kernel(int64_t* __restrict__ out, int64_t n, int64_t seq,
-                                                           int64_t start) {
+                                                           int64_t start, const int64_t* start_dev) {
+  if (start_dev) start += *start_dev;
   const int64_t stride = (int64_t)gridDim.x * kBlock;
   for (int64_t i = (int64_t)blockIdx.x * kBlock + threadIdx.x; i < n; i += stride) out[i] = start + i % seq;
 }
@@ -415,9 +416,10 @@ int q3_fill(int dtype, void* x, float value, int64_t n, hipStream_t stream) {
   return Q3_DISPATCH(dtype, fill_t, x, value, n, stream);
 }
 
-int q3_positions(int64_t* out, int64_t batch, int64_t seq, int64_t start, hipStream_t stream) {
+int q3_positions(int64_t* out, int64_t batch, int64_t seq, int64_t start, const int64_t* start_dev,
+                 hipStream_t stream) {
   Q3_REQUIRE(out && batch > 0 && seq > 0 && start >= 0);
-  positions_kernel<<<q3_grid_for(batch * seq, kBlock), kBlock, 0, stream>>>(out, batch * seq, seq, start);
+  positions_kernel<<<q3_grid_for(batch * seq, kBlock), kBlock, 0, stream>>>(out, batch * seq, seq, start, start_dev);
   return (int)hipGetLastError();
 }
 

@@ -40,7 +40,7 @@ SIGNATURES: dict[str, tuple] = {
     "q3_add": (_i32, [_i32, _p, _p, _p, _i64, _p]),
     "q3_cast": (_i32, [_i32, _i32, _p, _p, _i64, _p]),
     "q3_fill": (_i32, [_i32, _p, _f32, _i64, _p]),
-    "q3_positions": (_i32, [_p, _i64, _i64, _i64, _p]),
+    "q3_positions": (_i32, [_p, _i64, _i64, _i64, _p, _p]),
     "q3_transpose": (_i32, [_i32, _p, _p, _i64, _i64, _i64, _i64, _p]),
     "q3_embedding_fwd": (_i32, [_i32, _p, _i32, _p, _p, _p, _i64, _i64, _i64, _p]),
     "q3_embedding_bwd_workspace_bytes": (_sz, [_i64]),
@@ -57,12 +57,13 @@ SIGNATURES: dict[str, tuple] = {
     "q3_ce_finish": (_i32, [_p, _p, _i32, _p, _p, _p, _p, _p, _p, _p, _i64, _i64, _i64, _p]),
     "q3_ce_chunk_grad": (_i32, [_i32, _i32, _p, _i64, _i64, _i64, _p, _p, _p, _p, _p, _i64, _i64, _i64, _i64, _p]),
     "q3_gemv": (_i32, [_i32, _p, _i64, _p, _p, _i64, _i64, _i64, _i64, _p]),
-    "q3_kv_append": (_i32, [_i32, _p, _p, _p, _p, _i64, _i64, _i64, _i64, _i64, _i64, _p]),
+    "q3_kv_append": (_i32, [_i32, _p, _p, _p, _p, _i64, _i64, _i64, _i64, _i64, _i64, _p, _p]),
     "q3_decode_attention_workspace_bytes": (_sz, [_i64, _i64, _i64]),
     "q3_decode_attention": (_i32, [_i32, _p, _i64, _i64, _p, _p, _i64, _i64, _p, _i64, _i64, _p, _i64, _i64, _i64,
-                                    _i64, _i64, _f32, _p]),
+                                    _i64, _p, _i64, _i64, _f32, _p]),
     "q3_greedy_select_workspace_bytes": (_sz, [_i64]),
-    "q3_greedy_select": (_i32, [_i32, _p, _i64, _i64, _i64, _p, _p, _i64, _i64, _p, _p, _p, _i32, _i64, _p]),
+    "q3_greedy_select": (_i32, [_i32, _p, _i64, _i64, _i64, _p, _p, _i64, _i64, _p, _p, _p, _p, _i32, _i64, _p]),
+    "q3_advance": (_i32, [_p, _i64, _p]),
     "q3_gemm_strided": (_i32, [_i32, _i32, _p, _i64, _i64, _p, _i64, _i64, _p, _i64, _i64, _i64, _i64, _f32, _i32,
                                 _p]),
 }

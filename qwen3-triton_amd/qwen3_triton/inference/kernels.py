@@ -9,33 +9,41 @@ from ..kernels import _ops
 from ..kernels.linear import matmul
 
 
-def positions(batch, sequence, start, device):
-    """``inference/kernels.py:18``: [B,S] int64 positions start..start+S-1."""
-    return _ops.positions(batch, sequence, start, device)
+def positions(batch, sequence, start, device, start_dev=None):
+    """``inference/kernels.py:18``: [B,S] int64 positions start..start+S-1 (offset by the device
+    int64 ``start_dev`` when given)."""
+    return _ops.positions(batch, sequence, start if start_dev is None else 0, device, start_dev)
 
 
-def append(k, v, cache_k, cache_v, start):
-    """``inference/kernels.py:33``: write k/v [B,S,Hkv,D] into the caches [B,Hkv,C,D] at ``start``."""
+def append(k, v, cache_k, cache_v, start, start_dev=None):
+    """``inference/kernels.py:33``: write k/v [B,S,Hkv,D] into the caches [B,Hkv,C,D] at ``start``
+    (or at the device int64 ``start_dev``, read when the kernel runs)."""
     b, s, h, d = k.shape
     H.call("q3_kv_append", H.code(k.dtype), k.data_ptr(), v.data_ptr(), cache_k.data_ptr(), cache_v.data_ptr(), b, s,
-           h, d, cache_k.shape[2], start, H.stream())
+           h, d, cache_k.shape[2], start, 0 if start_dev is None else start_dev.data_ptr(), H.stream())
 
 
-def attention(q, cache_k, cache_v, start, *, split_decode=False):
+def attention(q, cache_k, cache_v, start, *, split_decode=False, start_dev=None):
     """``inference/kernels.py:95``: q [B,S,Hq,D] against cache positions [0, start+S).
 
-    S == 1 runs the split-KV decode kernel; S > 1 (prefill, chunked prefill) runs the flash kernel
-    on the cache in place (the query block is the suffix of the key range)."""
+    S == 1 runs the split-KV decode kernel (with ``start_dev`` the length is read on the device and
+    the launch spans the whole capacity, so a captured step replays at any position); S > 1
+    (prefill, chunked prefill) runs the flash kernel on the cache in place (the query block is the
+    suffix of the key range)."""
     b, s, hq, d = q.shape
-    hkv = cache_k.shape[1]
+    hkv, cap = cache_k.shape[1], cache_k.shape[2]
     total = start + s
     if s == 1 and d == 128 and q.dtype in (torch.bfloat16, torch.float16):
         out = torch.empty_like(q)
-        ws = H.workspace(H.query("q3_decode_attention_workspace_bytes", b, hq, total), q.device)
+        span = cap if start_dev is not None else total
+        ws = H.workspace(H.query("q3_decode_attention_workspace_bytes", b, hq, span), q.device)
         H.call("q3_decode_attention", H.code(q.dtype), q.data_ptr(), q.stride(0), q.stride(2), cache_k.data_ptr(),
                cache_v.data_ptr(), cache_k.stride(0), cache_k.stride(1), out.data_ptr(), out.stride(0),
-               out.stride(2), ws.data_ptr(), b, hq, hkv, total, d, d ** -0.5, H.stream())
+               out.stride(2), ws.data_ptr(), b, hq, hkv, total, 0 if start_dev is None else start_dev.data_ptr(),
+               cap, d, d ** -0.5, H.stream())
         return out
+    if start_dev is not None:
+        raise ValueError('device-resident positions are for single-token decode steps')
     o, _ = _ops.attention_fwd(q.transpose(1, 2), cache_k[:, :, :total], cache_v[:, :, :total], d ** -0.5)
     return o.transpose(1, 2)
 
@@ -59,9 +67,9 @@ def linear(x, weight, *, gemv=True, accurate=False, sliced=False, prefill_tiling
 _EOS_CACHE = {}
 
 
-def select(logits, ids, next_token, done, position, eos, pad):
+def select(logits, ids, next_token, done, position, eos, pad, position_dev=None):
     """``inference/kernels.py:168``: greedy token (lowest index on ties), pad for finished rows,
-    EOS bookkeeping; writes ids[:, position], next_token and done."""
+    EOS bookkeeping; writes ids[:, position (+ *position_dev)], next_token and done."""
     b, n = logits.shape
     key = (tuple(eos), logits.device)
     if key not in _EOS_CACHE:
@@ -70,7 +78,13 @@ def select(logits, ids, next_token, done, position, eos, pad):
     ws = H.workspace(H.query("q3_greedy_select_workspace_bytes", b), logits.device)
     H.call("q3_greedy_select", H.code(logits.dtype), logits.data_ptr(), logits.stride(0), b, n, ws.data_ptr(),
            0 if ids is None else ids.data_ptr(), 0 if ids is None else ids.stride(0), position,
-           next_token.data_ptr(), done.data_ptr(), eos_t.data_ptr(), len(eos), pad, H.stream())
+           0 if position_dev is None else position_dev.data_ptr(), next_token.data_ptr(), done.data_ptr(),
+           eos_t.data_ptr(), len(eos), pad, H.stream())
+
+
+def advance(counter, by):
+    """counter (device int64) += by, as a kernel on the current stream."""
+    H.call("q3_advance", counter.data_ptr(), by, H.stream())
 
 
 def rms_norm(x, weight, eps, *, reference_accumulation=False):

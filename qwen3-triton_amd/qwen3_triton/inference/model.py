@@ -140,7 +140,7 @@ class TritonQwen3Inference(nn.Module):
         return KVCache(keys, values, max_length, batch_size, self._cache_owner)
 
     # ------------------------------------------------------------------ forward
-    def _forward(self, input_ids, cache, logits_to_keep, *, validate_ids=True):
+    def _forward(self, input_ids, cache, logits_to_keep, *, validate_ids=True, start_dev=None):
         from transformers.modeling_outputs import CausalLMOutputWithPast
         if input_ids.ndim != 2 or input_ids.dtype not in (torch.int32, torch.int64) or \
                 input_ids.device != self.device or not input_ids.is_contiguous():
@@ -156,7 +156,9 @@ class TritonQwen3Inference(nn.Module):
         if validate_ids and not bool(((input_ids >= 0) & (input_ids < self.config.vocab_size)).all()):
             raise ValueError('Token ID outside vocabulary')
         start = cache.length
-        pos = kernels.positions(b, s, start, self.device)
+        if start_dev is not None and s != 1:
+            raise ValueError('device-resident positions are for single-token decode steps')
+        pos = kernels.positions(b, s, start, self.device, start_dev)
         try:
             x = embedding(input_ids, self.model.embed_tokens.weight)
             cos, sin = self.model.rotary_emb(pos, torch.bfloat16)
@@ -169,9 +171,9 @@ class TritonQwen3Inference(nn.Module):
                 v = kernels.linear(h, a.v_proj.weight, gemv=self.gemv).view(b, s, a.num_kv_heads, d)
                 q = kernels.norm_rope(q, a.q_norm.weight, cos, sin, a.q_norm.eps)
                 k = kernels.norm_rope(k, a.k_norm.weight, cos, sin, a.k_norm.eps)
-                kernels.append(k, v, cache.keys[i], cache.values[i], start)
-                y = kernels.attention(q, cache.keys[i], cache.values[i], start,
-                                      split_decode=self.split_decode).reshape(b, s, -1)
+                kernels.append(k, v, cache.keys[i], cache.values[i], start, start_dev)
+                y = kernels.attention(q, cache.keys[i], cache.values[i], start, split_decode=self.split_decode,
+                                      start_dev=start_dev).reshape(b, s, -1)
                 x = residual_add(x, kernels.linear(y, a.o_proj.weight, gemv=self.gemv))
                 h = kernels.rms_norm(x, layer.post_attention_layernorm.weight, layer.post_attention_layernorm.eps)
                 m = layer.mlp
@@ -243,6 +245,73 @@ class TritonQwen3Inference(nn.Module):
             if eos and bool(done.all()):
                 break
         return output[:, :s + step + 1].contiguous()
+
+
+class DecodeSession:
+    """Greedy decoding with ONE captured HIP graph for the decode step, replayed at every position.
+
+    The cache length lives in device memory; the position-dependent kernels (positions, KV
+    append, split-KV attention, token write) read it when they run and the step ends with a
+    device-side increment, so the same graph serves the whole request.  Prefill runs eagerly.
+    No counterpart in the reference (its captured request bakes every position into one graph,
+    ``inference/model.py:191-225``); the tokens match ``generate``.
+    """
+
+    @torch.inference_mode()
+    def __init__(self, model, batch, capacity, *, eos=(), pad=0):
+        self.model, self.batch, self.capacity = model, batch, capacity
+        self.eos, self.pad = tuple(eos), pad
+        dev = model.device
+        self.cache = model.new_cache(batch, capacity)
+        self.ids = torch.zeros((batch, capacity), device=dev, dtype=torch.int64)
+        self.current = torch.zeros((batch, 1), device=dev, dtype=torch.int64)
+        self.length = torch.zeros((1,), device=dev, dtype=torch.int64)
+        self.done = torch.zeros((batch,), device=dev, dtype=torch.bool)
+        self.graph = None
+        self.prompt_len = 0
+
+    @torch.inference_mode()
+    def prefill(self, input_ids):
+        b, s = input_ids.shape
+        if b != self.batch or s + 1 > self.capacity or self.cache.length:
+            raise ValueError('Prompt does not fit this session')
+        self.ids[:, :s].copy_(input_ids)
+        logits = self.model._forward(input_ids, self.cache, 1).logits[:, 0, :]
+        kernels.select(logits, self.ids, self.current, self.done, s, self.eos, self.pad)
+        kernels.advance(self.length, s)
+        self.prompt_len = s
+
+    def _step(self):
+        logits = self.model._forward(self.current, self.cache, 1, validate_ids=False,
+                                     start_dev=self.length).logits[:, 0, :]
+        kernels.select(logits, self.ids, self.current, self.done, 1, self.eos, self.pad, position_dev=self.length)
+        kernels.advance(self.length, 1)
+
+    @torch.inference_mode()
+    def capture(self):
+        """Record one decode step (nothing runs; the host-side length is restored)."""
+        host_len = self.cache.length
+        stream = torch.cuda.Stream(device=self.model.device)
+        stream.wait_stream(torch.cuda.current_stream())
+        self.graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(self.graph, stream=stream):
+            self._step()
+        torch.cuda.current_stream().wait_stream(stream)
+        self.cache.length = host_len
+
+    @torch.inference_mode()
+    def step(self):
+        if self.cache.length + 1 > self.capacity:
+            raise ValueError('KV cache exhausted')
+        if self.graph is None:
+            self._step()
+            return
+        self.graph.replay()
+        self.cache.length += 1
+
+    def tokens(self):
+        """Prompt plus generated tokens so far ([B, cache.length + 1])."""
+        return self.ids[:, :self.cache.length + 1]
 
 
 class CapturedGreedyRequest:

@@ -112,9 +112,11 @@ def fill_(x, value):
     return x
 
 
-def positions(batch, seq, start, device):
+def positions(batch, seq, start, device, start_dev=None):
+    """[B,S] int64 positions start + s (+ the device int64 ``start_dev`` when given)."""
     out = torch.empty((batch, seq), device=device, dtype=torch.int64)
-    H.call("q3_positions", out.data_ptr(), batch, seq, start, H.stream())
+    H.call("q3_positions", out.data_ptr(), batch, seq, start, 0 if start_dev is None else start_dev.data_ptr(),
+           H.stream())
     return out
 
 

@@ -175,3 +175,23 @@ def test_generate_eos_and_padding():
     out = model.generate(ids, max_new_tokens=4, eos_token_id=[eos], pad_token_id=7)
     assert out[0, 11] == eos
     assert bool((out[0, 12:] == 7).all())
+
+
+@pytest.mark.parametrize("b,s", [(1, 12), (2, 7)])
+def test_decode_session_replays_one_step_graph(b, s):
+    """One captured decode step replayed at every position (device-resident cache length) gives the
+    same tokens as the eager generate loop."""
+    from qwen3_triton.inference import DecodeSession
+    model, _ = small_model(seed=6)
+    ids = torch.randint(0, SMALL.vocab_size, (b, s), generator=seeded(10)).cuda()
+    n = 6
+    eager = model.generate(ids, max_new_tokens=n, eos_token_id=[], pad_token_id=0)
+    sess = DecodeSession(model, b, s + n + 2)
+    sess.prefill(ids)
+    sess.step()          # eager step
+    sess.capture()
+    for _ in range(n - 2):
+        sess.step()      # replays
+    torch.cuda.synchronize()
+    assert sess.cache.length == s + n - 1
+    assert torch.equal(sess.tokens(), eager)
