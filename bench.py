@@ -228,6 +228,7 @@ def main():
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-decode", action="store_true")
+    ap.add_argument("--no-layer", action="store_true", help="skip the decoder-layer step (profiling decode)")
     ap.add_argument("--decode-tokens", type=int, default=256)
     args = ap.parse_args()
     if args.gpus != 1:
@@ -241,9 +242,14 @@ def main():
     from qwen3_triton import _hip
     _hip.load()
 
-    log("decoder layer fwd+bwd")
-    layer = decoder_layer_bench(args.steps, args.warmup)
-    log(f"decoder layer: {layer['ms_per_step']:.3f} ms/step")
+    if args.no_layer:
+        layer = {"tokens_per_s": float("nan"), "ms_per_step": float("nan"), "tokens": 8192, "gemm_tflops": 0.0,
+                 "gemm_launches": 0, "gemm_flops_per_step": 0.0, "algorithmic_tflops_per_step": 0.0,
+                 "step_tflops": 0.0}
+    else:
+        log("decoder layer fwd+bwd")
+        layer = decoder_layer_bench(args.steps, args.warmup)
+        log(f"decoder layer: {layer['ms_per_step']:.3f} ms/step")
     result = {
         "metric": "decoder-layer fwd+bwd tokens/s @Qwen3-8B shape, 1 GPU, % roofline; decode tok/s",
         "value": round(layer["tokens_per_s"], 1),
