@@ -137,6 +137,119 @@ __global__ __launch_bounds__(kThreads) void gemm_nt_kernel(const u16* __restrict
     }
 }
 
+// ---------------------------------------------------------------- v2: direct-to-LDS, swizzled
+// Same contract as gemm_nt_kernel for K % 64 == 0.  Each wave-wide global_load_lds_dwordx4 moves
+// 64 x 16 bytes straight into LDS (no register staging), so a k-tile of A and B rows is in flight
+// while the previous one feeds the matrix cores.  LDS rows are 128 bytes (64 bf16) unpadded; the
+// 16-byte chunk c of row R is stored at physical chunk c ^ swz(R), swz(R) = (R ^ (R >> 3)) & 7,
+// which keeps both the 8- and 16-lane groups of every MFMA operand read (32 rows, one logical
+// chunk) on distinct banks.  The lane -> global address map applies the inverse swizzle, because
+// the LDS destination of a wave load is fixed (base + lane * 16).  Rows beyond M/N load a clamped
+// valid row: they only feed output rows/columns that are never stored.
+Q3_DEV int lds_swz(int r) { return (r ^ (r >> 3)) & 7; }
+
+template <typename T, typename O, int BM, int BN, int WM, int WN>
+__global__ __launch_bounds__(WM * WN * 64) void gemm_nt_v2_kernel(const u16* __restrict__ A,
+                                                                  const u16* __restrict__ B,
+                                                                  typename O::storage* __restrict__ C, int M, int N,
+                                                                  int K, int64_t lda, int64_t ldb, int64_t ldc,
+                                                                  float alpha, int accumulate) {
+  constexpr int BK = 64, NW = WM * WN, ROWB = BK * 2;  // bytes per LDS row
+  constexpr int TMW = BM / WM, TNW = BN / WN, TM = TMW / 32, TN = TNW / 32;
+  constexpr int RG = (BM + BN) / 8;                    // 8-row groups per stage (one wave load each)
+  static_assert(RG % NW == 0, "row groups must split evenly over the waves");
+  constexpr int LPW = RG / NW;                         // wave loads per k-tile
+  constexpr int STAGE = (BM + BN) * BK;                // elements per stage
+  __shared__ __attribute__((aligned(1024))) u16 lds[2 * STAGE];
+
+  int tm, tn;
+  tile_coords(blockIdx.x, (M + BM - 1) / BM, (N + BN - 1) / BN, tm, tn);
+  const int m0 = tm * BM, n0 = tn * BN;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int wm = wave / WN, wn = wave % WN;
+
+  // Per-lane source pointers of the LPW wave loads (k offset added per tile).
+  const u16* src[LPW];
+#pragma unroll
+  for (int i = 0; i < LPW; ++i) {
+    const int rg = wave + NW * i;
+    const int R = rg * 8 + (lane >> 3);                // row in the combined [A; B] stage
+    const int c = (lane & 7) ^ lds_swz(R);             // logical 16-byte chunk this lane fetches
+    if (R < BM) {
+      const int row = min(m0 + R, M - 1);
+      src[i] = A + (int64_t)row * lda + c * 8;
+    } else {
+      const int row = min(n0 + R - BM, N - 1);
+      src[i] = B + (int64_t)row * ldb + c * 8;
+    }
+  }
+  auto issue = [&](int stage, int k0) {
+#pragma unroll
+    for (int i = 0; i < LPW; ++i) {
+      const int rg = wave + NW * i;
+      __builtin_amdgcn_global_load_lds((const void*)(src[i] + k0),
+                                       (__attribute__((address_space(3))) void*)(lds + stage * STAGE + rg * 8 * BK),
+                                       16, 0, 0);
+    }
+  };
+
+  f32x16 acc[TM][TN];
+#pragma unroll
+  for (int i = 0; i < TM; ++i)
+#pragma unroll
+    for (int j = 0; j < TN; ++j)
+#pragma unroll
+      for (int v = 0; v < 16; ++v) acc[i][j][v] = 0.f;
+
+  const int nk = K / BK;
+  issue(0, 0);
+  // Operand rows of this lane (combined-stage row index) and their swizzles.
+  int ra[TM], rb[TN];
+#pragma unroll
+  for (int i = 0; i < TM; ++i) ra[i] = wm * TMW + i * 32 + (lane & 31);
+#pragma unroll
+  for (int j = 0; j < TN; ++j) rb[j] = BM + wn * TNW + j * 32 + (lane & 31);
+  const int half = lane >> 5;
+  for (int kt = 0; kt < nk; ++kt) {
+    __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0): this wave's loads of tile kt have landed
+    __syncthreads();                     // ... and everyone's; buffer (kt+1)&1 is free again
+    if (kt + 1 < nk) issue((kt + 1) & 1, (kt + 1) * BK);
+    const char* base = reinterpret_cast<const char*>(lds + (kt & 1) * STAGE);
+#pragma unroll
+    for (int ks = 0; ks < BK / 16; ++ks) {
+      const int c = ks * 2 + half;
+      bf16x8_t af[TM], bfr[TN];
+#pragma unroll
+      for (int i = 0; i < TM; ++i)
+        af[i] = *reinterpret_cast<const bf16x8_t*>(base + ra[i] * ROWB + ((c ^ lds_swz(ra[i])) << 4));
+#pragma unroll
+      for (int j = 0; j < TN; ++j)
+        bfr[j] = *reinterpret_cast<const bf16x8_t*>(base + rb[j] * ROWB + ((c ^ lds_swz(rb[j])) << 4));
+#pragma unroll
+      for (int i = 0; i < TM; ++i)
+#pragma unroll
+        for (int j = 0; j < TN; ++j) acc[i][j] = mfma_32x32x16<T>(af[i], bfr[j], acc[i][j]);
+    }
+  }
+
+#pragma unroll
+  for (int i = 0; i < TM; ++i)
+#pragma unroll
+    for (int j = 0; j < TN; ++j) {
+      const int col = n0 + wn * TNW + j * 32 + (lane & 31);
+#pragma unroll
+      for (int v = 0; v < 16; ++v) {
+        const int row = m0 + wm * TMW + i * 32 + 8 * (v >> 2) + 4 * (lane >> 5) + (v & 3);
+        if (row < M && col < N) {
+          typename O::storage* c = C + (int64_t)row * ldc + col;
+          float r = alpha * acc[i][j][v];
+          if (accumulate) r += to_f32<O>(*c);
+          *c = from_f32<O>(r);
+        }
+      }
+    }
+}
+
 // ---------------------------------------------------------------- strided SIMT fallback
 // C[m,n] = alpha * sum_k A[m*sam + k*sak] * B[k*sbk + n*sbn] (+ C).  64x64 tile, 4x4 per thread.
 template <typename T, typename O>
@@ -181,9 +294,26 @@ __global__ __launch_bounds__(kThreads) void gemm_generic_kernel(const typename T
 
 constexpr int kBM = 256, kBN = 128, kBK = 64;
 
+template <typename T, typename O, int BM, int BN, int WM, int WN>
+int launch_v2(const void* A, int64_t lda, const void* B, int64_t ldb, void* C, int64_t ldc, int64_t M, int64_t N,
+              int64_t K, float alpha, int acc, hipStream_t s) {
+  const int64_t tiles = ((M + BM - 1) / BM) * ((N + BN - 1) / BN);
+  gemm_nt_v2_kernel<T, O, BM, BN, WM, WN><<<(unsigned)tiles, WM * WN * 64, 0, s>>>(
+      (const u16*)A, (const u16*)B, (typename O::storage*)C, (int)M, (int)N, (int)K, lda, ldb, ldc, alpha, acc);
+  return (int)hipGetLastError();
+}
+
+int64_t tiles_of(int64_t M, int64_t N, int64_t bm, int64_t bn) { return ((M + bm - 1) / bm) * ((N + bn - 1) / bn); }
+
 template <typename T, typename O>
 int launch_nt(const void* A, int64_t lda, const void* B, int64_t ldb, void* C, int64_t ldc, int64_t M, int64_t N,
               int64_t K, float alpha, int acc, hipStream_t s) {
+  if (K % 64 == 0) {
+    // Largest tile that still gives every CU (256) a workgroup.
+    if (tiles_of(M, N, 256, 256) >= 256) return launch_v2<T, O, 256, 256, 2, 4>(A, lda, B, ldb, C, ldc, M, N, K, alpha, acc, s);
+    if (tiles_of(M, N, 256, 128) >= 256) return launch_v2<T, O, 256, 128, 2, 2>(A, lda, B, ldb, C, ldc, M, N, K, alpha, acc, s);
+    return launch_v2<T, O, 128, 128, 2, 2>(A, lda, B, ldb, C, ldc, M, N, K, alpha, acc, s);
+  }
   const int64_t tiles = ((M + kBM - 1) / kBM) * ((N + kBN - 1) / kBN);
   gemm_nt_kernel<T, O, kBM, kBN, kBK, 128, 64><<<(unsigned)tiles, kThreads, 0, s>>>(
       (const u16*)A, (const u16*)B, (typename O::storage*)C, (int)M, (int)N, (int)K, lda, ldb, ldc, alpha, acc);
