@@ -137,30 +137,39 @@ __global__ __launch_bounds__(kThreads) void gemm_nt_kernel(const u16* __restrict
     }
 }
 
-// ---------------------------------------------------------------- v2: direct-to-LDS, swizzled
-// Same contract as gemm_nt_kernel for K % 64 == 0.  Each wave-wide global_load_lds_dwordx4 moves
-// 64 x 16 bytes straight into LDS (no register staging), so a k-tile of A and B rows is in flight
-// while the previous one feeds the matrix cores.  LDS rows are 128 bytes (64 bf16) unpadded; the
-// 16-byte chunk c of row R is stored at physical chunk c ^ swz(R), swz(R) = (R ^ (R >> 3)) & 7,
-// which keeps both the 8- and 16-lane groups of every MFMA operand read (32 rows, one logical
-// chunk) on distinct banks.  The lane -> global address map applies the inverse swizzle, because
-// the LDS destination of a wave load is fixed (base + lane * 16).  Rows beyond M/N load a clamped
-// valid row: they only feed output rows/columns that are never stored.
-Q3_DEV int lds_swz(int r) { return (r ^ (r >> 3)) & 7; }
+// ---------------------------------------------------------------- v2: direct-to-LDS, swizzled ring
+// Same contract as gemm_nt_kernel for K % BK == 0.  Each wave-wide global_load_lds_dwordx4 moves
+// 64 x 16 bytes straight into LDS (no register staging) into a ring of STAGES k-tiles, so
+// STAGES-1 tiles of A and B rows are in flight while one feeds the matrix cores.  LDS rows are
+// BK*2 bytes unpadded; the 16-byte chunk c of stage row R is stored at physical chunk c ^ swz(R),
+// chosen so that the 8- and 16-lane groups of every MFMA operand read (32 rows, one logical chunk)
+// hit distinct banks.  The lane -> global address map applies the same swizzle, because the LDS
+// destination of a wave load is fixed (base + lane * 16).  Rows beyond M/N load a clamped valid row:
+// they only feed output rows/columns that are never stored.
+template <int CPR> Q3_DEV int lds_swz(int r) {
+  if constexpr (CPR == 8) return (r ^ (r >> 3)) & 7;
+  else return ((r >> 1) ^ (r >> 3)) & 3;  // 4 chunks (64-byte rows)
+}
 
-template <typename T, typename O, int BM, int BN, int WM, int WN>
+// s_waitcnt with vmcnt = N (N < 64) and lgkm/exp counters left unconstrained.
+template <int N> Q3_DEV void wait_vmcnt() {
+  static_assert(N >= 0 && N < 64, "vmcnt range");
+  __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (7 << 4) | (15 << 8));
+}
+
+template <typename T, typename O, int BM, int BN, int WM, int WN, int BK, int STAGES, bool PIPE = false>
 __global__ __launch_bounds__(WM * WN * 64) void gemm_nt_v2_kernel(const u16* __restrict__ A,
                                                                   const u16* __restrict__ B,
                                                                   typename O::storage* __restrict__ C, int M, int N,
                                                                   int K, int64_t lda, int64_t ldb, int64_t ldc,
                                                                   float alpha, int accumulate) {
-  constexpr int BK = 64, NW = WM * WN, ROWB = BK * 2;  // bytes per LDS row
+  constexpr int NW = WM * WN, ROWB = BK * 2, CPR = BK / 8, RPL = 64 / CPR;
   constexpr int TMW = BM / WM, TNW = BN / WN, TM = TMW / 32, TN = TNW / 32;
-  constexpr int RG = (BM + BN) / 8;                    // 8-row groups per stage (one wave load each)
+  constexpr int RG = (BM + BN) / RPL;                  // row groups per stage (one wave load each)
   static_assert(RG % NW == 0, "row groups must split evenly over the waves");
   constexpr int LPW = RG / NW;                         // wave loads per k-tile
   constexpr int STAGE = (BM + BN) * BK;                // elements per stage
-  __shared__ __attribute__((aligned(1024))) u16 lds[2 * STAGE];
+  __shared__ __attribute__((aligned(1024))) u16 lds[STAGES * STAGE];
 
   int tm, tn;
   tile_coords(blockIdx.x, (M + BM - 1) / BM, (N + BN - 1) / BN, tm, tn);
@@ -168,19 +177,16 @@ __global__ __launch_bounds__(WM * WN * 64) void gemm_nt_v2_kernel(const u16* __r
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int wm = wave / WN, wn = wave % WN;
 
-  // Per-lane source pointers of the LPW wave loads (k offset added per tile).
   const u16* src[LPW];
 #pragma unroll
   for (int i = 0; i < LPW; ++i) {
     const int rg = wave + NW * i;
-    const int R = rg * 8 + (lane >> 3);                // row in the combined [A; B] stage
-    const int c = (lane & 7) ^ lds_swz(R);             // logical 16-byte chunk this lane fetches
+    const int R = rg * RPL + lane / CPR;                 // row in the combined [A; B] stage
+    const int c = (lane % CPR) ^ lds_swz<CPR>(R);        // logical 16-byte chunk this lane fetches
     if (R < BM) {
-      const int row = min(m0 + R, M - 1);
-      src[i] = A + (int64_t)row * lda + c * 8;
+      src[i] = A + (int64_t)min(m0 + R, M - 1) * lda + c * 8;
     } else {
-      const int row = min(n0 + R - BM, N - 1);
-      src[i] = B + (int64_t)row * ldb + c * 8;
+      src[i] = B + (int64_t)min(n0 + R - BM, N - 1) * ldb + c * 8;
     }
   }
   auto issue = [&](int stage, int k0) {
@@ -188,7 +194,7 @@ __global__ __launch_bounds__(WM * WN * 64) void gemm_nt_v2_kernel(const u16* __r
     for (int i = 0; i < LPW; ++i) {
       const int rg = wave + NW * i;
       __builtin_amdgcn_global_load_lds((const void*)(src[i] + k0),
-                                       (__attribute__((address_space(3))) void*)(lds + stage * STAGE + rg * 8 * BK),
+                                       (__attribute__((address_space(3))) void*)(lds + stage * STAGE + rg * RPL * BK),
                                        16, 0, 0);
     }
   };
@@ -202,33 +208,77 @@ __global__ __launch_bounds__(WM * WN * 64) void gemm_nt_v2_kernel(const u16* __r
       for (int v = 0; v < 16; ++v) acc[i][j][v] = 0.f;
 
   const int nk = K / BK;
-  issue(0, 0);
-  // Operand rows of this lane (combined-stage row index) and their swizzles.
-  int ra[TM], rb[TN];
 #pragma unroll
-  for (int i = 0; i < TM; ++i) ra[i] = wm * TMW + i * 32 + (lane & 31);
+  for (int st = 0; st < STAGES - 1; ++st)
+    if (st < nk) issue(st, st * BK);
+  int ra[TM], rb[TN], sa[TM], sb[TN];
 #pragma unroll
-  for (int j = 0; j < TN; ++j) rb[j] = BM + wn * TNW + j * 32 + (lane & 31);
+  for (int i = 0; i < TM; ++i) {
+    ra[i] = wm * TMW + i * 32 + (lane & 31);
+    sa[i] = lds_swz<CPR>(ra[i]);
+  }
+#pragma unroll
+  for (int j = 0; j < TN; ++j) {
+    rb[j] = BM + wn * TNW + j * 32 + (lane & 31);
+    sb[j] = lds_swz<CPR>(rb[j]);
+  }
   const int half = lane >> 5;
   for (int kt = 0; kt < nk; ++kt) {
-    __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0): this wave's loads of tile kt have landed
-    __syncthreads();                     // ... and everyone's; buffer (kt+1)&1 is free again
-    if (kt + 1 < nk) issue((kt + 1) & 1, (kt + 1) * BK);
-    const char* base = reinterpret_cast<const char*>(lds + (kt & 1) * STAGE);
+    // Tile kt must have landed; the later tiles of the ring may stay in flight.
+    if (nk - 1 - kt >= STAGES - 2) wait_vmcnt<(STAGES - 2) * LPW>();
+    else wait_vmcnt<0>();
+    __syncthreads();  // every wave's share of tile kt is in LDS; stage (kt-1) % STAGES is free
+    if (kt + STAGES - 1 < nk) issue((kt + STAGES - 1) % STAGES, (kt + STAGES - 1) * BK);
+    const char* base = reinterpret_cast<const char*>(lds + (kt % STAGES) * STAGE);
+    if constexpr (!PIPE) {
 #pragma unroll
-    for (int ks = 0; ks < BK / 16; ++ks) {
-      const int c = ks * 2 + half;
-      bf16x8_t af[TM], bfr[TN];
+      for (int ks = 0; ks < BK / 16; ++ks) {
+        const int c = ks * 2 + half;
+        bf16x8_t af[TM], bfr[TN];
 #pragma unroll
-      for (int i = 0; i < TM; ++i)
-        af[i] = *reinterpret_cast<const bf16x8_t*>(base + ra[i] * ROWB + ((c ^ lds_swz(ra[i])) << 4));
+        for (int i = 0; i < TM; ++i)
+          af[i] = *reinterpret_cast<const bf16x8_t*>(base + ra[i] * ROWB + ((c ^ sa[i]) << 4));
 #pragma unroll
-      for (int j = 0; j < TN; ++j)
-        bfr[j] = *reinterpret_cast<const bf16x8_t*>(base + rb[j] * ROWB + ((c ^ lds_swz(rb[j])) << 4));
+        for (int j = 0; j < TN; ++j)
+          bfr[j] = *reinterpret_cast<const bf16x8_t*>(base + rb[j] * ROWB + ((c ^ sb[j]) << 4));
 #pragma unroll
-      for (int i = 0; i < TM; ++i)
+        for (int i = 0; i < TM; ++i)
 #pragma unroll
-        for (int j = 0; j < TN; ++j) acc[i][j] = mfma_32x32x16<T>(af[i], bfr[j], acc[i][j]);
+          for (int j = 0; j < TN; ++j) acc[i][j] = mfma_32x32x16<T>(af[i], bfr[j], acc[i][j]);
+      }
+    } else {
+      // Fragments double-buffered across k-steps: the reads of step ks+1 are issued before the
+      // MFMAs of step ks and the scheduler is asked to interleave them one for one.
+      constexpr int KS = BK / 16;
+      bf16x8_t af[2][TM], bfr[2][TN];
+      auto load = [&](int buf, int ks) {
+        const int c = ks * 2 + half;
+#pragma unroll
+        for (int i = 0; i < TM; ++i)
+          af[buf][i] = *reinterpret_cast<const bf16x8_t*>(base + ra[i] * ROWB + ((c ^ sa[i]) << 4));
+#pragma unroll
+        for (int j = 0; j < TN; ++j)
+          bfr[buf][j] = *reinterpret_cast<const bf16x8_t*>(base + rb[j] * ROWB + ((c ^ sb[j]) << 4));
+      };
+      load(0, 0);
+#pragma unroll
+      for (int ks = 0; ks < KS; ++ks) {
+        if (ks + 1 < KS) load((ks + 1) & 1, ks + 1);
+#pragma unroll
+        for (int i = 0; i < TM; ++i)
+#pragma unroll
+          for (int j = 0; j < TN; ++j) acc[i][j] = mfma_32x32x16<T>(af[ks & 1][i], bfr[ks & 1][j], acc[i][j]);
+        if (ks + 1 < KS) {
+#pragma unroll
+          for (int x = 0; x < TM + TN; ++x) {
+            __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);  // one LDS read
+            __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // one MFMA
+          }
+          if (TM * TN > TM + TN) __builtin_amdgcn_sched_group_barrier(0x008, TM * TN - (TM + TN), 0);
+        } else {
+          __builtin_amdgcn_sched_group_barrier(0x008, TM * TN, 0);
+        }
+      }
     }
   }
 
@@ -294,11 +344,11 @@ __global__ __launch_bounds__(kThreads) void gemm_generic_kernel(const typename T
 
 constexpr int kBM = 256, kBN = 128, kBK = 64;
 
-template <typename T, typename O, int BM, int BN, int WM, int WN>
+template <typename T, typename O, int BM, int BN, int WM, int WN, int BK = 64, int ST = 2, bool PIPE = false>
 int launch_v2(const void* A, int64_t lda, const void* B, int64_t ldb, void* C, int64_t ldc, int64_t M, int64_t N,
               int64_t K, float alpha, int acc, hipStream_t s) {
   const int64_t tiles = ((M + BM - 1) / BM) * ((N + BN - 1) / BN);
-  gemm_nt_v2_kernel<T, O, BM, BN, WM, WN><<<(unsigned)tiles, WM * WN * 64, 0, s>>>(
+  gemm_nt_v2_kernel<T, O, BM, BN, WM, WN, BK, ST, PIPE><<<(unsigned)tiles, WM * WN * 64, 0, s>>>(
       (const u16*)A, (const u16*)B, (typename O::storage*)C, (int)M, (int)N, (int)K, lda, ldb, ldc, alpha, acc);
   return (int)hipGetLastError();
 }
@@ -309,10 +359,13 @@ template <typename T, typename O>
 int launch_nt(const void* A, int64_t lda, const void* B, int64_t ldb, void* C, int64_t ldc, int64_t M, int64_t N,
               int64_t K, float alpha, int acc, hipStream_t s) {
   if (K % 64 == 0) {
-    // Largest tile that still gives every CU (256) a workgroup.
-    if (tiles_of(M, N, 256, 256) >= 256) return launch_v2<T, O, 256, 256, 2, 4>(A, lda, B, ldb, C, ldc, M, N, K, alpha, acc, s);
-    if (tiles_of(M, N, 256, 128) >= 256) return launch_v2<T, O, 256, 128, 2, 2>(A, lda, B, ldb, C, ldc, M, N, K, alpha, acc, s);
-    return launch_v2<T, O, 128, 128, 2, 2>(A, lda, B, ldb, C, ldc, M, N, K, alpha, acc, s);
+    // Largest tile that still gives every CU (256) a workgroup (tile choice measured on MI355X
+    // for the Qwen3-8B projection shapes).
+    if (tiles_of(M, N, 256, 256) >= 256)
+      return launch_v2<T, O, 256, 256, 2, 4, 64, 2, true>(A, lda, B, ldb, C, ldc, M, N, K, alpha, acc, s);
+    if (tiles_of(M, N, 256, 128) >= 256)
+      return launch_v2<T, O, 256, 128, 2, 2, 64, 3>(A, lda, B, ldb, C, ldc, M, N, K, alpha, acc, s);
+    return launch_v2<T, O, 128, 128, 2, 2, 64, 4>(A, lda, B, ldb, C, ldc, M, N, K, alpha, acc, s);
   }
   const int64_t tiles = ((M + kBM - 1) / kBM) * ((N + kBN - 1) / kBN);
   gemm_nt_kernel<T, O, kBM, kBN, kBK, 128, 64><<<(unsigned)tiles, kThreads, 0, s>>>(
@@ -351,6 +404,28 @@ bool dtype_ok(int dt) { return dt == Q3_F32 || dt == Q3_F16 || dt == Q3_BF16; }
 bool al16(const void* p) { return ((uintptr_t)p & 15) == 0; }
 
 }  // namespace
+
+// Tuning hook (not part of the public ABI header): runs one fixed tile variant of the bf16 NT GEMM
+// with bf16 output, so configurations can be timed side by side.
+extern "C" int q3_gemm_nt_variant(int variant, const void* A, int64_t lda, const void* B, int64_t ldb, void* C,
+                                  int64_t ldc, int64_t M, int64_t N, int64_t K, hipStream_t s) {
+  switch (variant) {
+    case 0: return launch_v2<BF16, BF16, 256, 256, 2, 4, 64, 2>(A, lda, B, ldb, C, ldc, M, N, K, 1.f, 0, s);
+    case 1: return launch_v2<BF16, BF16, 256, 256, 2, 4, 32, 4>(A, lda, B, ldb, C, ldc, M, N, K, 1.f, 0, s);
+    case 2: return launch_v2<BF16, BF16, 256, 128, 2, 2, 64, 3>(A, lda, B, ldb, C, ldc, M, N, K, 1.f, 0, s);
+    case 3: return launch_v2<BF16, BF16, 256, 128, 2, 2, 32, 4>(A, lda, B, ldb, C, ldc, M, N, K, 1.f, 0, s);
+    case 4: return launch_v2<BF16, BF16, 128, 128, 2, 2, 64, 4>(A, lda, B, ldb, C, ldc, M, N, K, 1.f, 0, s);
+    case 5: return launch_v2<BF16, BF16, 256, 256, 2, 4, 32, 3>(A, lda, B, ldb, C, ldc, M, N, K, 1.f, 0, s);
+    case 6: return launch_v2<BF16, BF16, 256, 256, 4, 2, 64, 2>(A, lda, B, ldb, C, ldc, M, N, K, 1.f, 0, s);
+    case 7: return launch_v2<BF16, BF16, 128, 256, 2, 2, 64, 3>(A, lda, B, ldb, C, ldc, M, N, K, 1.f, 0, s);
+    case 8: return launch_v2<BF16, BF16, 256, 256, 2, 4, 64, 2, true>(A, lda, B, ldb, C, ldc, M, N, K, 1.f, 0, s);
+    case 9: return launch_v2<BF16, BF16, 256, 256, 4, 2, 64, 2, true>(A, lda, B, ldb, C, ldc, M, N, K, 1.f, 0, s);
+    case 10: return launch_v2<BF16, BF16, 256, 128, 2, 2, 64, 3, true>(A, lda, B, ldb, C, ldc, M, N, K, 1.f, 0, s);
+    case 11: return launch_v2<BF16, BF16, 128, 128, 2, 2, 64, 4, true>(A, lda, B, ldb, C, ldc, M, N, K, 1.f, 0, s);
+    case 12: return launch_v2<BF16, BF16, 256, 256, 2, 2, 64, 2, true>(A, lda, B, ldb, C, ldc, M, N, K, 1.f, 0, s);
+    default: return Q3_ERR_INVALID;
+  }
+}
 
 extern "C" {
 
