@@ -58,10 +58,7 @@ Q3_DEV bf16x8_t perm_frag(const u16* row, int c16, int g) {
 template <typename T> Q3_DEV bf16x8_t pack8(const f32x16& a, int v0) {
   i32x4 r;
 #pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    const uint32_t lo = from_f32<T>(a[v0 + 2 * i]), hi = from_f32<T>(a[v0 + 2 * i + 1]);
-    r[i] = (int)(lo | (hi << 16));
-  }
+  for (int i = 0; i < 4; ++i) r[i] = (int)pack2<T>(a[v0 + 2 * i], a[v0 + 2 * i + 1]);
   return as_frag(r);
 }
 
@@ -74,20 +71,34 @@ struct Lay {
 };
 
 // ============================================================================ forward (MFMA)
-// Workgroup: 4 waves x 32 queries of one (b, h); key tiles of 64 double-buffered in LDS.
+// Workgroup: 4 waves x 32 queries of one (b, h); each lane owns one query (scores are computed
+// transposed, S^T = K Q^T) and walks key tiles of 64 with an online softmax.  K and V^T tiles go
+// global -> LDS with wave-wide global_load_lds_dwordx4 into a 2-stage ring (no register staging, so two 4-wave
+// workgroups fit per CU); LDS rows are unpadded and XOR-swizzled by 16-byte chunk so every MFMA
+// operand read is bank-conflict free.  Tiles entirely below the causal diagonal skip the mask, and
+// the output rescale is skipped when no lane's running max moved.
+template <int CPR> Q3_DEV int chunk_swz(int r) {
+  if constexpr (CPR == 16) return r & 15;
+  else if constexpr (CPR == 8) return (r ^ (r >> 3)) & 7;
+  else return ((r >> 1) ^ (r >> 3)) & 3;
+}
+
 template <typename T, int D>
-__global__ __launch_bounds__(kThreads) void attn_fwd_mfma(const u16* __restrict__ Q, Lay ql, const u16* __restrict__ K,
-                                                          Lay kl, const u16* __restrict__ Vt, u16* __restrict__ O,
-                                                          float* __restrict__ LSE, int Hq, int Hkv, int Lq, int Lk,
-                                                          int ldvt, float scale2) {
-  constexpr int BN = 64, KP = D + 8, VP = BN + 8, KS = D / 16, DT = D / 32;
-  constexpr int KCH = BN * D / 8 / kThreads, VCH = D * BN / 8 / kThreads;
-  static_assert(KCH >= 1 && VCH >= 1, "tile too small");
-  __shared__ __attribute__((aligned(16))) u16 lk[2][BN * KP];
-  __shared__ __attribute__((aligned(16))) u16 lv[2][D * VP];
+__global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2, 2))) void attn_fwd_v2(const u16* __restrict__ Q, Lay ql, const u16* __restrict__ K,
+                                                        Lay kl, const u16* __restrict__ Vt, u16* __restrict__ O,
+                                                        float* __restrict__ LSE, int Hq, int Hkv, int Lq, int Lk,
+                                                        int ldvt, float scale2) {
+  constexpr int BN = 64, KS = D / 16, DT = D / 32;
+  constexpr int CPK = D / 8, RPK = 64 / CPK;      // K: 16-byte chunks per row, rows per wave load
+  constexpr int CPV = BN / 8, RPV = 64 / CPV;     // V^T rows (one d each) of BN keys
+  constexpr int KLOADS = BN / RPK, VLOADS = D / RPV;
+  constexpr int LPW = (KLOADS + VLOADS) / 4;      // wave loads per tile (4 waves)
+  static_assert((KLOADS + VLOADS) % 4 == 0, "loads split over 4 waves");
+  constexpr int KBYTES = BN * D * 2, STAGE = KBYTES + D * BN * 2;
+  __shared__ __attribute__((aligned(1024))) char lds[2 * STAGE];
 
   const int nqt = (Lq + 127) / 128;
-  const int qt = nqt - 1 - (int)blockIdx.x;  // the longest (latest) query tiles start first
+  const int qt = nqt - 1 - (int)blockIdx.x;
   const int bh = blockIdx.y, b = bh / Hq, h = bh % Hq, hk = h / (Hq / Hkv);
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, g = lane >> 5;
   const int off = Lk - Lq;
@@ -103,35 +114,31 @@ __global__ __launch_bounds__(kThreads) void attn_fwd_mfma(const u16* __restrict_
     qf[ks] = qi < Lq ? as_frag(ld16(Qb + qi * ql.s + ks * 16 + g * 8)) : as_frag(i32x4{0, 0, 0, 0});
 
   const int qlast_blk = min(qt * 128 + 127, Lq - 1) + off;
-  const int kend = min(Lk, qlast_blk + 1);
-  const int ntiles = (kend + BN - 1) / BN;
+  const int ntiles = (min(Lk, qlast_blk + 1) + BN - 1) / BN;
+  const int qfirst_wave = q0 + off;
   const int qlast_wave = min(q0 + 31, Lq - 1) + off;
   const int qpos = qi + off;
 
-  i32x4 rk[KCH], rv[VCH];
-  auto gload = [&](int t) {
+  // wave load i of a tile: global row/chunk of this lane and its LDS destination offset
+  auto issue = [&](int stage, int t) {
     const int k0 = t * BN;
 #pragma unroll
-    for (int i = 0; i < KCH; ++i) {
-      const int c = tid + i * kThreads, row = c / (D / 8), col = (c % (D / 8)) * 8, key = k0 + row;
-      rk[i] = key < Lk ? ld16(Kb + key * kl.s + col) : i32x4{0, 0, 0, 0};
-    }
-#pragma unroll
-    for (int i = 0; i < VCH; ++i) {
-      const int c = tid + i * kThreads, d = c / (BN / 8), kc = k0 + (c % (BN / 8)) * 8;
-      rv[i] = kc < ldvt ? ld16(Vb + (int64_t)d * ldvt + kc) : i32x4{0, 0, 0, 0};
-    }
-  };
-  auto swrite = [&](int buf) {
-#pragma unroll
-    for (int i = 0; i < KCH; ++i) {
-      const int c = tid + i * kThreads;
-      st16(&lk[buf][(c / (D / 8)) * KP + (c % (D / 8)) * 8], rk[i]);
-    }
-#pragma unroll
-    for (int i = 0; i < VCH; ++i) {
-      const int c = tid + i * kThreads;
-      st16(&lv[buf][(c / (BN / 8)) * VP + (c % (BN / 8)) * 8], rv[i]);
+    for (int i = 0; i < LPW; ++i) {
+      const int w = wave + 4 * i;
+      const void* src;
+      int dst;
+      if (w < KLOADS) {
+        const int r = w * RPK + lane / CPK;
+        const int c = (lane % CPK) ^ chunk_swz<CPK>(r);
+        src = Kb + (int64_t)min(k0 + r, Lk - 1) * kl.s + c * 8;
+        dst = stage * STAGE + w * RPK * D * 2;
+      } else {
+        const int r = (w - KLOADS) * RPV + lane / CPV;   // d
+        const int c = (lane % CPV) ^ chunk_swz<CPV>(r);
+        src = Vb + (int64_t)r * ldvt + min(k0 + c * 8, ldvt - 8);
+        dst = stage * STAGE + KBYTES + (w - KLOADS) * RPV * BN * 2;
+      }
+      __builtin_amdgcn_global_load_lds(src, (__attribute__((address_space(3))) void*)(lds + dst), 16, 0, 0);
     }
   };
 
@@ -139,64 +146,84 @@ __global__ __launch_bounds__(kThreads) void attn_fwd_mfma(const u16* __restrict_
   f32x16 oacc[DT];
 #pragma unroll
   for (int i = 0; i < DT; ++i) oacc[i] = zero16();
+  const int kr = lane & 31;
+  const int kswz = chunk_swz<CPK>(kr), kswz2 = chunk_swz<CPK>(kr + 32);
 
-  if (ntiles > 0) {
-    gload(0);
-    swrite(0);
-  }
-  __syncthreads();
+  if (ntiles > 0) issue(0, 0);
   for (int t = 0; t < ntiles; ++t) {
-    const int cur = t & 1;
-    if (t + 1 < ntiles) gload(t + 1);
+    __builtin_amdgcn_s_waitcnt((0 & 15) | (7 << 4) | (15 << 8));  // vmcnt(0)
+    __syncthreads();
+    if (t + 1 < ntiles) issue((t + 1) & 1, t + 1);
     const int k0 = t * BN;
-    if (k0 <= qlast_wave) {
-      f32x16 sacc[2] = {zero16(), zero16()};
-      const u16* kl = &lk[cur][(lane & 31) * KP + g * 8];
+    if (k0 > qlast_wave) continue;
+    const char* kbase = lds + (t & 1) * STAGE;
+    const char* vbase = kbase + KBYTES;
+    f32x16 sacc[2] = {zero16(), zero16()};
 #pragma unroll
-      for (int ks = 0; ks < KS; ++ks)
+    for (int ks = 0; ks < KS; ++ks) {
+      const int c = ks * 2 + g;
+      sacc[0] = mma<T>(as_frag(*reinterpret_cast<const i32x4*>(kbase + kr * D * 2 + ((c ^ kswz) << 4))), qf[ks], sacc[0]);
+      sacc[1] = mma<T>(as_frag(*reinterpret_cast<const i32x4*>(kbase + (kr + 32) * D * 2 + ((c ^ kswz2) << 4))), qf[ks],
+                       sacc[1]);
+    }
+    float mx = -INFINITY;
+    if (k0 + BN - 1 <= qfirst_wave) {  // whole tile visible to every query of the wave
 #pragma unroll
-        for (int tt = 0; tt < 2; ++tt)
-          sacc[tt] = mma<T>(as_frag(ld16(kl + tt * 32 * KP + ks * 16)), qf[ks], sacc[tt]);
-      float mx = -INFINITY;
+      for (int tt = 0; tt < 2; ++tt)
+#pragma unroll
+        for (int v = 0; v < 16; ++v) {
+          sacc[tt][v] *= scale2;
+          mx = fmaxf(mx, sacc[tt][v]);
+        }
+    } else {
 #pragma unroll
       for (int tt = 0; tt < 2; ++tt)
 #pragma unroll
         for (int v = 0; v < 16; ++v) {
           const int key = k0 + tt * 32 + acc_row(v, lane);
-          const float s = key <= qpos ? sacc[tt][v] * scale2 : -INFINITY;
-          sacc[tt][v] = s;
-          mx = fmaxf(mx, s);
+          const float sv = key <= qpos ? sacc[tt][v] * scale2 : -INFINITY;
+          sacc[tt][v] = sv;
+          mx = fmaxf(mx, sv);
         }
-      mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
-      const float mnew = fmaxf(m, mx);
-      const float muse = mnew == -INFINITY ? 0.f : mnew;
+    }
+    mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
+    const float mnew = fmaxf(m, mx);
+    const float muse = mnew == -INFINITY ? 0.f : mnew;
+    float ps = 0.f;
+#pragma unroll
+    for (int tt = 0; tt < 2; ++tt)
+#pragma unroll
+      for (int v = 0; v < 16; ++v) {
+        const float p = __builtin_amdgcn_exp2f(sacc[tt][v] - muse);
+        sacc[tt][v] = p;
+        ps += p;
+      }
+    ps += __shfl_xor(ps, 32, 64);
+    if (__any(mnew != m)) {
       const float alpha = __builtin_amdgcn_exp2f(m - muse);
-      float ps = 0.f;
-#pragma unroll
-      for (int tt = 0; tt < 2; ++tt)
-#pragma unroll
-        for (int v = 0; v < 16; ++v) {
-          const float p = __builtin_amdgcn_exp2f(sacc[tt][v] - muse);
-          sacc[tt][v] = p;
-          ps += p;
-        }
-      ps += __shfl_xor(ps, 32, 64);
-      l = l * alpha + ps;
-      m = mnew;
+      l *= alpha;
 #pragma unroll
       for (int dt = 0; dt < DT; ++dt)
 #pragma unroll
         for (int v = 0; v < 16; ++v) oacc[dt][v] *= alpha;
+    }
+    l += ps;
+    m = mnew;
 #pragma unroll
-      for (int c = 0; c < BN / 16; ++c) {
-        const bf16x8_t pb = pack8<T>(sacc[c >> 1], (c & 1) * 8);
+    for (int c = 0; c < BN / 16; ++c) {
+      const bf16x8_t pb = pack8<T>(sacc[c >> 1], (c & 1) * 8);
 #pragma unroll
-        for (int dt = 0; dt < DT; ++dt)
-          oacc[dt] = mma<T>(perm_frag(&lv[cur][(dt * 32 + (lane & 31)) * VP], c * 16, g), pb, oacc[dt]);
+      for (int dt = 0; dt < DT; ++dt) {
+        const int r = dt * 32 + (lane & 31);
+        const int sw = chunk_swz<CPV>(r);
+        const char* row = vbase + r * BN * 2;
+        typedef __attribute__((__vector_size__(2 * sizeof(int)))) int i32x2;
+        const i32x2 lo = *reinterpret_cast<const i32x2*>(row + (((2 * c) ^ sw) << 4) + 8 * g);
+        const i32x2 hi = *reinterpret_cast<const i32x2*>(row + (((2 * c + 1) ^ sw) << 4) + 8 * g);
+        const i32x4 v4 = {lo[0], lo[1], hi[0], hi[1]};
+        oacc[dt] = mma<T>(as_frag(v4), pb, oacc[dt]);
       }
     }
-    if (t + 1 < ntiles) swrite(cur ^ 1);
-    __syncthreads();
   }
 
   if (qi < Lq) {
@@ -209,8 +236,8 @@ __global__ __launch_bounds__(kThreads) void attn_fwd_mfma(const u16* __restrict_
         const int d = dt * 32 + 8 * vg + 4 * g;
         typedef __attribute__((__vector_size__(2 * sizeof(int)))) int i32x2;
         i32x2 w;
-        w[0] = (int)(from_f32<T>(oacc[dt][4 * vg] * inv) | ((uint32_t)from_f32<T>(oacc[dt][4 * vg + 1] * inv) << 16));
-        w[1] = (int)(from_f32<T>(oacc[dt][4 * vg + 2] * inv) | ((uint32_t)from_f32<T>(oacc[dt][4 * vg + 3] * inv) << 16));
+        w[0] = (int)pack2<T>(oacc[dt][4 * vg] * inv, oacc[dt][4 * vg + 1] * inv);
+        w[1] = (int)pack2<T>(oacc[dt][4 * vg + 2] * inv, oacc[dt][4 * vg + 3] * inv);
         *reinterpret_cast<i32x2*>(orow + d) = w;
       }
     if (g == 0) LSE[(int64_t)bh * Lq + qi] = (m + __log2f(l)) * kLn2;
@@ -234,92 +261,140 @@ __global__ __launch_bounds__(kThreads) void attn_delta_kernel(const typename T::
   if (lane_id() == 0) delta[row] = s;
 }
 
-// ============================================================================ backward: dQ (MFMA)
-// Workgroup: 4 waves x 32 queries of one (b, h).  Per key tile: S^T = K Q^T, dP^T = V dO^T,
-// dS = P (dP - delta), dQ^T += Kt dS^T.
-template <typename T, int D>
-__global__ __launch_bounds__(kThreads) void attn_bwd_dq_mfma(const u16* __restrict__ Q, Lay ql,
-                                                             const u16* __restrict__ K, const u16* __restrict__ V,
-                                                             Lay kl, const u16* __restrict__ Kt,
-                                                             const u16* __restrict__ dO,
-                                                             const float* __restrict__ LSE,
-                                                             const float* __restrict__ Delta, u16* __restrict__ dQ,
-                                                             int Hq, int Hkv, int Lq, int Lk, int ldkt, float scale,
-                                                             float scale2) {
-  constexpr int BN = 64, KP = D + 8, VP = BN + 8, KS = D / 16, DT = D / 32;
-  constexpr int KCH = BN * D / 8 / kThreads;
-  __shared__ __attribute__((aligned(16))) u16 lk[BN * KP];
-  __shared__ __attribute__((aligned(16))) u16 lvv[BN * KP];
-  __shared__ __attribute__((aligned(16))) u16 lkt[D * VP];
+// ============================================================================ backward (MFMA)
+// dQ kernel -- workgroup: 4 waves x 32 queries of one (b, h).  Per 64-key tile: S^T = K Q^T,
+// dP^T = V dO^T, dS = P (dP - delta), dQ^T += Kt dS^T.
+// dK/dV kernel -- workgroup: 4 waves x 32 keys of one (b, kv head); loops over the Hq/Hkv query
+// heads of the group and the 32-query tiles at or after the diagonal.  Per tile: S = Q K^T,
+// dP = dO V^T (lane = key), P, dS; dV^T += dOt P, dK^T += Qt dS.  The group's query heads
+// accumulate into the same registers: no partial buffers, no atomics, deterministic.
+// Operand tiles move global -> LDS with wave-wide global_load_lds_dwordx4 into swizzled, unpadded
+// LDS rows (no register staging); two waves per SIMD except dK/dV at D = 128 (its K/V fragments and
+// two accumulators need the full register file); causal masks only on tiles that cross the diagonal, and
+// the grid is ordered longest-work-first.
+template <typename T, int D, int STAGES>
+__global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2, 2))) void attn_bwd_dq_v2(
+    const u16* __restrict__ Q, Lay ql, const u16* __restrict__ K, const u16* __restrict__ V, Lay kl,
+    const u16* __restrict__ Kt, const u16* __restrict__ dO, const float* __restrict__ LSE,
+    const float* __restrict__ Delta, u16* __restrict__ dQ, int Hq, int Hkv, int Lq, int Lk, int ldkt, float scale,
+    float scale2) {
+  constexpr int BN = 64, KS = D / 16, DT = D / 32;
+  constexpr int CPK = D / 8, RPK = 64 / CPK, CPV = BN / 8, RPV = 64 / CPV;
+  constexpr int KLOADS = BN / RPK, TLOADS = D / RPV;
+  constexpr int NLOADS = 2 * KLOADS + TLOADS;
+  static_assert(NLOADS % 4 == 0, "loads split over 4 waves");
+  constexpr int LPW = NLOADS / 4;
+  constexpr int KB = BN * D * 2, STAGE = 2 * KB + D * BN * 2;
+  __shared__ __attribute__((aligned(1024))) char lds[STAGES * STAGE];
 
   const int nqt = (Lq + 127) / 128;
-  const int qt = nqt - 1 - (int)blockIdx.x;
-  const int bh = blockIdx.y, b = bh / Hq, h = bh % Hq, hk = h / (Hq / Hkv);
+  const int qt = nqt - 1 - (int)blockIdx.y;  // longest query tiles first
+  const int bh = blockIdx.x, b = bh / Hq, h = bh % Hq, hk = h / (Hq / Hkv);
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, g = lane >> 5;
   const int off = Lk - Lq;
   const int q0 = qt * 128 + wave * 32;
   const int qi = q0 + (lane & 31);
-  const int64_t kvbase = (int64_t)(b * Hkv + hk);
   const u16* Kb = K + b * kl.b + hk * kl.h;
   const u16* Vb = V + b * kl.b + hk * kl.h;
-  const u16* Ktb = Kt + kvbase * D * ldkt;
-  const int64_t qrow = b * ql.b + h * ql.h + (int64_t)qi * ql.s;
+  const u16* Ktb = Kt + (int64_t)(b * Hkv + hk) * D * ldkt;
+  const int64_t qrow = b * ql.b + h * ql.h + (int64_t)min(qi, Lq - 1) * ql.s;
 
   bf16x8_t qf[KS], dof[KS];
 #pragma unroll
   for (int ks = 0; ks < KS; ++ks) {
-    const bool ok = qi < Lq;
-    qf[ks] = ok ? as_frag(ld16(Q + qrow + ks * 16 + g * 8)) : as_frag(i32x4{0, 0, 0, 0});
-    dof[ks] = ok ? as_frag(ld16(dO + qrow + ks * 16 + g * 8)) : as_frag(i32x4{0, 0, 0, 0});
+    qf[ks] = as_frag(ld16(Q + qrow + ks * 16 + g * 8));
+    dof[ks] = as_frag(ld16(dO + qrow + ks * 16 + g * 8));
   }
   const float lse2 = qi < Lq ? LSE[(int64_t)bh * Lq + qi] * kLog2e : 0.f;
   const float dlt = qi < Lq ? Delta[(int64_t)bh * Lq + qi] : 0.f;
   const int qpos = qi + off;
   const int qlast_blk = min(qt * 128 + 127, Lq - 1) + off;
   const int ntiles = (min(Lk, qlast_blk + 1) + BN - 1) / BN;
+  const int qfirst_wave = q0 + off;
   const int qlast_wave = min(q0 + 31, Lq - 1) + off;
+
+  auto issue = [&](int stage, int t) {
+    const int k0 = t * BN;
+#pragma unroll
+    for (int i = 0; i < LPW; ++i) {
+      const int w = wave + 4 * i;
+      const void* src;
+      int dst;
+      if (w < 2 * KLOADS) {
+        const int which = w / KLOADS, wl = w % KLOADS;
+        const int r = wl * RPK + lane / CPK;
+        const int c = (lane % CPK) ^ chunk_swz<CPK>(r);
+        src = (which ? Vb : Kb) + (int64_t)min(k0 + r, Lk - 1) * kl.s + c * 8;
+        dst = stage * STAGE + which * KB + wl * RPK * D * 2;
+      } else {
+        const int wl = w - 2 * KLOADS;
+        const int r = wl * RPV + lane / CPV;
+        const int c = (lane % CPV) ^ chunk_swz<CPV>(r);
+        src = Ktb + (int64_t)r * ldkt + min(k0 + c * 8, ldkt - 8);
+        dst = stage * STAGE + 2 * KB + wl * RPV * BN * 2;
+      }
+      __builtin_amdgcn_global_load_lds(src, (__attribute__((address_space(3))) void*)(lds + dst), 16, 0, 0);
+    }
+  };
 
   f32x16 dq[DT];
 #pragma unroll
   for (int i = 0; i < DT; ++i) dq[i] = zero16();
+  const int kr = lane & 31;
+  const int ksw = chunk_swz<CPK>(kr), ksw2 = chunk_swz<CPK>(kr + 32);
 
+#pragma unroll
+  for (int st = 0; st < STAGES - 1; ++st)
+    if (st < ntiles) issue(st, st);
   for (int t = 0; t < ntiles; ++t) {
-    const int k0 = t * BN;
-    __syncthreads();
-#pragma unroll
-    for (int i = 0; i < KCH; ++i) {
-      const int c = tid + i * kThreads, row = c / (D / 8), col = (c % (D / 8)) * 8, key = k0 + row;
-      const bool ok = key < Lk;
-      st16(&lk[row * KP + col], ok ? ld16(Kb + key * kl.s + col) : i32x4{0, 0, 0, 0});
-      st16(&lvv[row * KP + col], ok ? ld16(Vb + key * kl.s + col) : i32x4{0, 0, 0, 0});
-      const int d = c / (BN / 8), kc = k0 + (c % (BN / 8)) * 8;
-      st16(&lkt[d * VP + (c % (BN / 8)) * 8], kc < ldkt ? ld16(Ktb + (int64_t)d * ldkt + kc) : i32x4{0, 0, 0, 0});
+    if constexpr (STAGES == 1) {
+      __syncthreads();  // everyone is done reading the single stage
+      issue(0, t);
     }
+    __builtin_amdgcn_s_waitcnt((0 & 15) | (7 << 4) | (15 << 8));  // vmcnt(0)
     __syncthreads();
+    if constexpr (STAGES > 1) {
+      if (t + STAGES - 1 < ntiles) issue((t + STAGES - 1) % STAGES, t + STAGES - 1);
+    }
+    const int k0 = t * BN;
     if (k0 > qlast_wave) continue;
-    f32x16 s[2] = {zero16(), zero16()}, dp[2] = {zero16(), zero16()};
-    const u16* kl = &lk[(lane & 31) * KP + g * 8];
-    const u16* vl = &lvv[(lane & 31) * KP + g * 8];
+    const char* kb = lds + (t % STAGES) * STAGE;
+    const char* vb = kb + KB;
+    const char* tb = kb + 2 * KB;
+    const bool full = k0 + BN - 1 <= qfirst_wave && q0 + 31 < Lq;
+#pragma nounroll
+    for (int tt = 0; tt < 2; ++tt) {  // two 32-key halves keep only one score tile live
+      f32x16 sc = zero16(), dp = zero16();
+      const int kro = kr + tt * 32, kswt = tt ? ksw2 : ksw;
 #pragma unroll
-    for (int ks = 0; ks < KS; ++ks)
-#pragma unroll
-      for (int tt = 0; tt < 2; ++tt) {
-        s[tt] = mma<T>(as_frag(ld16(kl + tt * 32 * KP + ks * 16)), qf[ks], s[tt]);
-        dp[tt] = mma<T>(as_frag(ld16(vl + tt * 32 * KP + ks * 16)), dof[ks], dp[tt]);
+      for (int ks = 0; ks < KS; ++ks) {
+        const int o = kro * D * 2 + (((ks * 2 + g) ^ kswt) << 4);
+        sc = mma<T>(as_frag(*reinterpret_cast<const i32x4*>(kb + o)), qf[ks], sc);
+        dp = mma<T>(as_frag(*reinterpret_cast<const i32x4*>(vb + o)), dof[ks], dp);
       }
-#pragma unroll
-    for (int tt = 0; tt < 2; ++tt)
 #pragma unroll
       for (int v = 0; v < 16; ++v) {
         const int key = k0 + tt * 32 + acc_row(v, lane);
-        const float p = key <= qpos ? __builtin_amdgcn_exp2f(s[tt][v] * scale2 - lse2) : 0.f;
-        s[tt][v] = p * (dp[tt][v] - dlt);
+        float p = __builtin_amdgcn_exp2f(sc[v] * scale2 - lse2);
+        if (!full) p = key <= qpos ? p : 0.f;
+        sc[v] = p * (dp[v] - dlt);
       }
 #pragma unroll
-    for (int c = 0; c < BN / 16; ++c) {
-      const bf16x8_t db = pack8<T>(s[c >> 1], (c & 1) * 8);
+      for (int c2 = 0; c2 < 2; ++c2) {
+        const int c = tt * 2 + c2;
+        const bf16x8_t db = pack8<T>(sc, c2 * 8);
 #pragma unroll
-      for (int dt = 0; dt < DT; ++dt) dq[dt] = mma<T>(perm_frag(&lkt[(dt * 32 + (lane & 31)) * VP], c * 16, g), db, dq[dt]);
+        for (int dt = 0; dt < DT; ++dt) {
+          const int r = dt * 32 + (lane & 31);
+          const int sw = chunk_swz<CPV>(r);
+          const char* row = tb + r * BN * 2;
+          typedef __attribute__((__vector_size__(2 * sizeof(int)))) int i32x2;
+          const i32x2 lo = *reinterpret_cast<const i32x2*>(row + (((2 * c) ^ sw) << 4) + 8 * g);
+          const i32x2 hi = *reinterpret_cast<const i32x2*>(row + (((2 * c + 1) ^ sw) << 4) + 8 * g);
+          const i32x4 v4 = {lo[0], lo[1], hi[0], hi[1]};
+          dq[dt] = mma<T>(as_frag(v4), db, dq[dt]);
+        }
+      }
     }
   }
   if (qi < Lq) {
@@ -327,124 +402,155 @@ __global__ __launch_bounds__(kThreads) void attn_bwd_dq_mfma(const u16* __restri
 #pragma unroll
     for (int dt = 0; dt < DT; ++dt)
 #pragma unroll
-      for (int v = 0; v < 16; ++v) row[dt * 32 + acc_row(v, lane)] = from_f32<T>(dq[dt][v] * scale);
+      for (int vg = 0; vg < 4; ++vg) {
+        const int d = dt * 32 + 8 * vg + 4 * g;
+        typedef __attribute__((__vector_size__(2 * sizeof(int)))) int i32x2;
+        i32x2 w;
+        w[0] = (int)pack2<T>(dq[dt][4 * vg] * scale, dq[dt][4 * vg + 1] * scale);
+        w[1] = (int)pack2<T>(dq[dt][4 * vg + 2] * scale, dq[dt][4 * vg + 3] * scale);
+        *reinterpret_cast<i32x2*>(row + d) = w;
+      }
   }
 }
 
-// ============================================================================ backward: dK, dV (MFMA)
-// Workgroup: 4 waves x 32 keys of one (b, kv head); loops over the Hq/Hkv query heads of the group
-// and over 32-query tiles at or after the diagonal.  Per tile: S = Q K^T, dP = dO V^T (lane = key),
-// P, dS; dV^T += dOt P, dK^T += Qt dS.  The group's query heads accumulate into the same
-// registers: no partial buffers, no atomics.
-template <typename T, int D>
-__global__ __launch_bounds__(kThreads) void attn_bwd_dkdv_mfma(const u16* __restrict__ Q, Lay ql,
-                                                               const u16* __restrict__ K, const u16* __restrict__ V,
-                                                               Lay kl, const u16* __restrict__ Qt,
-                                                               const u16* __restrict__ dO,
-                                                               const u16* __restrict__ dOt,
-                                                               const float* __restrict__ LSE,
-                                                               const float* __restrict__ Delta, u16* __restrict__ dK,
-                                                               u16* __restrict__ dV, int Hq, int Hkv, int Lq, int Lk,
-                                                               int ldqt, float scale, float scale2) {
-  constexpr int BM = 32, KP = D + 8, QP = BM + 8, KS = D / 16, DT = D / 32;
-  constexpr int RCH = BM * D / 8;  // 16-byte chunks of one [BM][D] tile
-  __shared__ __attribute__((aligned(16))) u16 lq[BM * KP];
-  __shared__ __attribute__((aligned(16))) u16 ldo[BM * KP];
-  __shared__ __attribute__((aligned(16))) u16 lqt[D * QP];
-  __shared__ __attribute__((aligned(16))) u16 ldot[D * QP];
-  __shared__ float llse[BM], ldel[BM];
+template <typename T, int D, int OCC>
+__global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(OCC, OCC))) void attn_bwd_dkdv_v2(
+    const u16* __restrict__ Q, Lay ql, const u16* __restrict__ K, const u16* __restrict__ V, Lay kl,
+    const u16* __restrict__ Qt, const u16* __restrict__ dO, const u16* __restrict__ dOt,
+    const float* __restrict__ LSE, const float* __restrict__ Delta, u16* __restrict__ dK, u16* __restrict__ dV,
+    int Hq, int Hkv, int Lq, int Lk, int ldqt, float scale, float scale2) {
+  constexpr int BM = 32, KS = D / 16, DT = D / 32;
+  constexpr int CPK = D / 8, RPK = 64 / CPK, CPQ = BM / 8, RPQ = 64 / CPQ;
+  constexpr int QLOADS = BM / RPK, TLOADS = D / RPQ;
+  constexpr int NLOADS = 2 * QLOADS + 2 * TLOADS;
+  static_assert(NLOADS % 4 == 0, "loads split over 4 waves");
+  constexpr int LPW = NLOADS / 4;
+  constexpr int QB = BM * D * 2, STAGE = 4 * QB + 2 * BM * 4;
+  __shared__ __attribute__((aligned(1024))) char lds[2 * STAGE];
 
-  const int nkt = (Lk + 127) / 128;
-  const int kt = (int)blockIdx.x;
-  const int bk = blockIdx.y, b = bk / Hkv, hk = bk % Hkv, ratio = Hq / Hkv;
+  const int kt = (int)blockIdx.y;  // smallest key tiles (the most query tiles) first
+  const int bk = blockIdx.x, b = bk / Hkv, hk = bk % Hkv, ratio = Hq / Hkv;
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, g = lane >> 5;
   const int off = Lk - Lq;
   const int k0w = kt * 128 + wave * 32;
   const int kj = k0w + (lane & 31);
-  const u16* Kb = K + b * kl.b + hk * kl.h;
-  const u16* Vb = V + b * kl.b + hk * kl.h;
-  (void)nkt;
+  const int64_t krow = b * kl.b + hk * kl.h + (int64_t)min(kj, Lk - 1) * kl.s;
 
   bf16x8_t kf[KS], vf[KS];
 #pragma unroll
   for (int ks = 0; ks < KS; ++ks) {
-    const bool ok = kj < Lk;
-    kf[ks] = ok ? as_frag(ld16(Kb + kj * kl.s + ks * 16 + g * 8)) : as_frag(i32x4{0, 0, 0, 0});
-    vf[ks] = ok ? as_frag(ld16(Vb + kj * kl.s + ks * 16 + g * 8)) : as_frag(i32x4{0, 0, 0, 0});
+    kf[ks] = as_frag(ld16(K + krow + ks * 16 + g * 8));
+    vf[ks] = as_frag(ld16(V + krow + ks * 16 + g * 8));
   }
   f32x16 dk[DT], dv[DT];
 #pragma unroll
   for (int i = 0; i < DT; ++i) dk[i] = dv[i] = zero16();
 
-  // First query index that can see this workgroup's first key: q + off >= kt*128.
-  const int qstart_blk = max(0, kt * 128 - off) / BM * BM;
-  const int kfirst_wave = k0w;  // wave skips query tiles that end before its first key
-  for (int hh = 0; hh < ratio; ++hh) {
+  const int qstart = max(0, kt * 128 - off) / BM * BM;
+  const int nq = (Lq - qstart + BM - 1) / BM;  // query tiles per head
+  const int total = ratio * nq;
+
+  // tile u = (head hh, query tile): operands Q, dO rows and Q^T, dO^T columns, plus lse/delta
+  auto issue = [&](int stage, int u) {
+    const int hh = u / nq, q0 = qstart + (u % nq) * BM;
     const int h = hk * ratio + hh;
     const int64_t bh = (int64_t)b * Hq + h;
     const u16* Qb = Q + b * ql.b + h * ql.h;
     const u16* dOb = dO + b * ql.b + h * ql.h;
     const u16* Qtb = Qt + bh * D * ldqt;
     const u16* dOtb = dOt + bh * D * ldqt;
-    for (int q0 = qstart_blk; q0 < Lq; q0 += BM) {
-      __syncthreads();
-      for (int c = tid; c < RCH; c += kThreads) {
-        const int row = c / (D / 8), col = (c % (D / 8)) * 8, qq = q0 + row;
-        const bool ok = qq < Lq;
-        st16(&lq[row * KP + col], ok ? ld16(Qb + qq * ql.s + col) : i32x4{0, 0, 0, 0});
-        st16(&ldo[row * KP + col], ok ? ld16(dOb + qq * ql.s + col) : i32x4{0, 0, 0, 0});
-        const int d = c / (BM / 8), qc = q0 + (c % (BM / 8)) * 8;
-        const bool okt = qc < ldqt;
-        st16(&lqt[d * QP + (c % (BM / 8)) * 8], okt ? ld16(Qtb + (int64_t)d * ldqt + qc) : i32x4{0, 0, 0, 0});
-        st16(&ldot[d * QP + (c % (BM / 8)) * 8], okt ? ld16(dOtb + (int64_t)d * ldqt + qc) : i32x4{0, 0, 0, 0});
-      }
-      if (tid < BM) {
-        const int qq = q0 + tid;
-        llse[tid] = qq < Lq ? LSE[bh * Lq + qq] * kLog2e : 0.f;
-        ldel[tid] = qq < Lq ? Delta[bh * Lq + qq] : 0.f;
-      }
-      __syncthreads();
-      // the last query of this tile must reach the wave's first key
-      if (min(q0 + BM - 1, Lq - 1) + off < kfirst_wave) continue;
-      f32x16 s = zero16(), dp = zero16();
-      const u16* ql = &lq[(lane & 31) * KP + g * 8];
-      const u16* dl = &ldo[(lane & 31) * KP + g * 8];
 #pragma unroll
-      for (int ks = 0; ks < KS; ++ks) {
-        s = mma<T>(as_frag(ld16(ql + ks * 16)), kf[ks], s);
-        dp = mma<T>(as_frag(ld16(dl + ks * 16)), vf[ks], dp);
+    for (int i = 0; i < LPW; ++i) {
+      const int w = wave + 4 * i;
+      const void* src;
+      int dst;
+      if (w < 2 * QLOADS) {
+        const int which = w / QLOADS, wl = w % QLOADS;
+        const int r = wl * RPK + lane / CPK;
+        const int c = (lane % CPK) ^ chunk_swz<CPK>(r);
+        src = (which ? dOb : Qb) + (int64_t)min(q0 + r, Lq - 1) * ql.s + c * 8;
+        dst = stage * STAGE + which * QB + wl * RPK * D * 2;
+      } else {
+        const int which = (w - 2 * QLOADS) / TLOADS, wl = (w - 2 * QLOADS) % TLOADS;
+        const int r = wl * RPQ + lane / CPQ;
+        const int c = (lane % CPQ) ^ chunk_swz<CPQ>(r);
+        src = (which ? dOtb : Qtb) + (int64_t)r * ldqt + min(q0 + c * 8, ldqt - 8);
+        dst = stage * STAGE + (2 + which) * QB + wl * RPQ * BM * 2;
       }
-      // element v: query q0 + acc_row(v), key kj (= lane's column)
-      f32x16 ds;
+      __builtin_amdgcn_global_load_lds(src, (__attribute__((address_space(3))) void*)(lds + dst), 16, 0, 0);
+    }
+    if (tid < BM) {
+      const int qq = q0 + tid;
+      float* side = reinterpret_cast<float*>(lds + stage * STAGE + 4 * QB);
+      side[tid] = qq < Lq ? LSE[bh * Lq + qq] * kLog2e : 0.f;
+      side[BM + tid] = qq < Lq ? Delta[bh * Lq + qq] : 0.f;
+    }
+  };
+
+  if (total > 0) issue(0, 0);
+  for (int u = 0; u < total; ++u) {
+    __builtin_amdgcn_s_waitcnt((0 & 15) | (7 << 4) | (15 << 8));  // vmcnt(0)
+    __syncthreads();
+    if (u + 1 < total) issue((u + 1) & 1, u + 1);
+    const int q0 = qstart + (u % nq) * BM;
+    if (min(q0 + BM - 1, Lq - 1) + off < k0w) continue;  // no query of the tile sees the wave's keys
+    const char* qb = lds + (u & 1) * STAGE;
+    const char* db = qb + QB;
+    const char* qtb = qb + 2 * QB;
+    const char* dtb = qb + 3 * QB;
+    const float* side = reinterpret_cast<const float*>(qb + 4 * QB);
+    f32x16 s = zero16(), dp = zero16();
+    const int qr = lane & 31, qsw = chunk_swz<CPK>(qr);
 #pragma unroll
-      for (int v = 0; v < 16; ++v) {
-        const int r = acc_row(v, lane), qq = q0 + r;
-        const float p = (qq < Lq && kj <= qq + off) ? __builtin_amdgcn_exp2f(s[v] * scale2 - llse[r]) : 0.f;
-        s[v] = p;
-        ds[v] = p * (dp[v] - ldel[r]);
-      }
+    for (int ks = 0; ks < KS; ++ks) {
+      const int o = qr * D * 2 + (((ks * 2 + g) ^ qsw) << 4);
+      s = mma<T>(as_frag(*reinterpret_cast<const i32x4*>(qb + o)), kf[ks], s);
+      dp = mma<T>(as_frag(*reinterpret_cast<const i32x4*>(db + o)), vf[ks], dp);
+    }
+    const bool full = k0w + 31 <= q0 + off && q0 + BM - 1 < Lq;
+    f32x16 ds;
 #pragma unroll
-      for (int c = 0; c < BM / 16; ++c) {
-        const bf16x8_t pb = pack8<T>(s, c * 8);
-        const bf16x8_t db = pack8<T>(ds, c * 8);
+    for (int v = 0; v < 16; ++v) {
+      const int r = acc_row(v, lane), qq = q0 + r;
+      float p = __builtin_amdgcn_exp2f(s[v] * scale2 - side[r]);
+      if (!full) p = (qq < Lq && kj <= qq + off) ? p : 0.f;
+      s[v] = p;
+      ds[v] = p * (dp[v] - side[BM + r]);
+    }
 #pragma unroll
-        for (int dt = 0; dt < DT; ++dt) {
-          dv[dt] = mma<T>(perm_frag(&ldot[(dt * 32 + (lane & 31)) * QP], c * 16, g), pb, dv[dt]);
-          dk[dt] = mma<T>(perm_frag(&lqt[(dt * 32 + (lane & 31)) * QP], c * 16, g), db, dk[dt]);
-        }
+    for (int c = 0; c < BM / 16; ++c) {
+      const bf16x8_t pb = pack8<T>(s, c * 8);
+      const bf16x8_t dsb = pack8<T>(ds, c * 8);
+#pragma unroll
+      for (int dt = 0; dt < DT; ++dt) {
+        const int r = dt * 32 + (lane & 31);
+        const int sw = chunk_swz<CPQ>(r);
+        typedef __attribute__((__vector_size__(2 * sizeof(int)))) int i32x2;
+        const int olo = r * BM * 2 + (((2 * c) ^ sw) << 4) + 8 * g, ohi = r * BM * 2 + (((2 * c + 1) ^ sw) << 4) + 8 * g;
+        const i32x2 a0 = *reinterpret_cast<const i32x2*>(dtb + olo), a1 = *reinterpret_cast<const i32x2*>(dtb + ohi);
+        const i32x2 b0 = *reinterpret_cast<const i32x2*>(qtb + olo), b1 = *reinterpret_cast<const i32x2*>(qtb + ohi);
+        const i32x4 va = {a0[0], a0[1], a1[0], a1[1]}, vb4 = {b0[0], b0[1], b1[0], b1[1]};
+        dv[dt] = mma<T>(as_frag(va), pb, dv[dt]);
+        dk[dt] = mma<T>(as_frag(vb4), dsb, dk[dt]);
       }
     }
   }
   if (kj < Lk) {
-    u16* krow = dK + b * kl.b + hk * kl.h + kj * kl.s;
-    u16* vrow = dV + b * kl.b + hk * kl.h + kj * kl.s;
+    u16* kout = dK + krow;
+    u16* vout = dV + krow;
 #pragma unroll
     for (int dt = 0; dt < DT; ++dt)
 #pragma unroll
-      for (int v = 0; v < 16; ++v) {
-        const int d = dt * 32 + acc_row(v, lane);
-        krow[d] = from_f32<T>(dk[dt][v] * scale);
-        vrow[d] = from_f32<T>(dv[dt][v]);
+      for (int vg = 0; vg < 4; ++vg) {
+        const int d = dt * 32 + 8 * vg + 4 * g;
+        typedef __attribute__((__vector_size__(2 * sizeof(int)))) int i32x2;
+        i32x2 wk, wv;
+        wk[0] = (int)pack2<T>(dk[dt][4 * vg] * scale, dk[dt][4 * vg + 1] * scale);
+        wk[1] = (int)pack2<T>(dk[dt][4 * vg + 2] * scale, dk[dt][4 * vg + 3] * scale);
+        wv[0] = (int)pack2<T>(dv[dt][4 * vg], dv[dt][4 * vg + 1]);
+        wv[1] = (int)pack2<T>(dv[dt][4 * vg + 2], dv[dt][4 * vg + 3]);
+        *reinterpret_cast<i32x2*>(kout + d) = wk;
+        *reinterpret_cast<i32x2*>(vout + d) = wv;
       }
   }
 }
@@ -619,9 +725,10 @@ bool dtype_ok(int dt) { return dt == Q3_F32 || dt == Q3_F16 || dt == Q3_BF16; }
 template <typename T, int D>
 int fwd_mfma(const void* q, Lay ql, const void* k, Lay kl, const void* vt, void* o, float* lse, int B, int Hq,
              int Hkv, int Lq, int Lk, int ldvt, float scale, hipStream_t s) {
+  // Direct-to-LDS kernel: K rows and V^T rows are 16-byte aligned (checked by the caller).
   dim3 grid((unsigned)((Lq + 127) / 128), (unsigned)(B * Hq));
-  attn_fwd_mfma<T, D><<<grid, kThreads, 0, s>>>((const u16*)q, ql, (const u16*)k, kl, (const u16*)vt, (u16*)o, lse,
-                                                 Hq, Hkv, Lq, Lk, ldvt, scale * kLog2e);
+  attn_fwd_v2<T, D><<<grid, kThreads, 0, s>>>((const u16*)q, ql, (const u16*)k, kl, (const u16*)vt, (u16*)o, lse, Hq,
+                                               Hkv, Lq, Lk, ldvt, scale * kLog2e);
   return (int)hipGetLastError();
 }
 
@@ -629,14 +736,15 @@ template <typename T, int D>
 int bwd_mfma(const void* q, Lay ql, const void* k, const void* v, Lay kl, const void* qt, const void* kt,
              const void* dout, const void* dot, const float* lse, const float* delta, void* dq, void* dk, void* dv,
              int B, int Hq, int Hkv, int Lq, int Lk, int ldqt, int ldkt, float scale, hipStream_t s) {
-  dim3 g1((unsigned)((Lq + 127) / 128), (unsigned)(B * Hq));
-  attn_bwd_dq_mfma<T, D><<<g1, kThreads, 0, s>>>((const u16*)q, ql, (const u16*)k, (const u16*)v, kl,
-                                                  (const u16*)kt, (const u16*)dout, lse, delta, (u16*)dq, Hq, Hkv, Lq,
-                                                  Lk, ldkt, scale, scale * kLog2e);
-  dim3 g2((unsigned)((Lk + 127) / 128), (unsigned)(B * Hkv));
-  attn_bwd_dkdv_mfma<T, D><<<g2, kThreads, 0, s>>>((const u16*)q, ql, (const u16*)k, (const u16*)v, kl,
-                                                    (const u16*)qt, (const u16*)dout, (const u16*)dot, lse, delta,
-                                                    (u16*)dk, (u16*)dv, Hq, Hkv, Lq, Lk, ldqt, scale, scale * kLog2e);
+  // Direct-to-LDS kernels need 16-byte aligned rows of every operand (checked by the caller).
+  dim3 g1((unsigned)(B * Hq), (unsigned)((Lq + 127) / 128));
+  attn_bwd_dq_v2<T, D, 1><<<g1, kThreads, 0, s>>>((const u16*)q, ql, (const u16*)k, (const u16*)v, kl,
+                                                   (const u16*)kt, (const u16*)dout, lse, delta, (u16*)dq, Hq, Hkv,
+                                                   Lq, Lk, ldkt, scale, scale * kLog2e);
+  dim3 g2((unsigned)(B * Hkv), (unsigned)((Lk + 127) / 128));
+  attn_bwd_dkdv_v2<T, D, (D > 64 ? 1 : 2)><<<g2, kThreads, 0, s>>>((const u16*)q, ql, (const u16*)k, (const u16*)v, kl,
+                                                  (const u16*)qt, (const u16*)dout, (const u16*)dot, lse, delta,
+                                                  (u16*)dk, (u16*)dv, Hq, Hkv, Lq, Lk, ldqt, scale, scale * kLog2e);
   return (int)hipGetLastError();
 }
 

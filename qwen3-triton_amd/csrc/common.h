@@ -20,13 +20,15 @@ typedef __attribute__((__vector_size__(4 * sizeof(float)))) float f32x4;
 typedef __attribute__((__vector_size__(16 * sizeof(float)))) float f32x16;
 
 // ------------------------------------------------------------------ scalar conversions
+typedef float f32x2_t __attribute__((ext_vector_type(2)));
+typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
 Q3_DEV float bf16_to_f32(u16 h) { return __uint_as_float(((uint32_t)h) << 16); }
-Q3_DEV u16 f32_to_bf16(float f) {
-  // IEEE round-to-nearest-even; NaN stays NaN (quiet bit forced).
-  uint32_t u = __float_as_uint(f);
-  if ((u & 0x7fffffffu) > 0x7f800000u) return (u16)((u >> 16) | 0x40);
-  u += 0x7fffu + ((u >> 16) & 1u);
-  return (u16)(u >> 16);
+// fp32 -> bf16 with IEEE round-to-nearest-even: one v_cvt_pk_bf16_f32 (gfx950 hardware convert).
+Q3_DEV u16 f32_to_bf16(float f) { return __builtin_bit_cast(u16, (__bf16)f); }
+// Two fp32 -> packed bf16 pair (lo in bits 0..15) in a single v_cvt_pk_bf16_f32.
+Q3_DEV uint32_t pack_bf16x2(float lo, float hi) {
+  const f32x2_t v = {lo, hi};
+  return __builtin_bit_cast(uint32_t, __builtin_convertvector(v, bf16x2_t));
 }
 Q3_DEV float f16_to_f32(u16 h) { return (float)__builtin_bit_cast(_Float16, h); }
 Q3_DEV u16 f32_to_f16(float f) { return __builtin_bit_cast(u16, (_Float16)f); }
@@ -44,6 +46,12 @@ template <typename T> Q3_DEV typename T::storage from_f32(float v);
 template <> Q3_DEV float from_f32<F32>(float v) { return v; }
 template <> Q3_DEV u16 from_f32<F16>(float v) { return f32_to_f16(v); }
 template <> Q3_DEV u16 from_f32<BF16>(float v) { return f32_to_bf16(v); }
+
+// Two values of a 16-bit type packed into one 32-bit word (lo in bits 0..15).
+template <typename T> Q3_DEV uint32_t pack2(float lo, float hi) {
+  return (uint32_t)from_f32<T>(lo) | ((uint32_t)from_f32<T>(hi) << 16);
+}
+template <> Q3_DEV uint32_t pack2<BF16>(float lo, float hi) { return pack_bf16x2(lo, hi); }
 
 // One 16-byte vector unpacked to fp32: VEC = 8 for 16-bit types, 4 for fp32.
 template <typename T> struct Vec { float v[T::vec]; };
@@ -71,10 +79,7 @@ template <typename T> Q3_DEV void store_vec(typename T::storage* p, const Vec<T>
     for (int i = 0; i < 4; ++i) raw[i] = __float_as_int(r.v[i]);
   } else {
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      uint32_t lo = from_f32<T>(r.v[2 * i]), hi = from_f32<T>(r.v[2 * i + 1]);
-      raw[i] = (int)(lo | (hi << 16));
-    }
+    for (int i = 0; i < 4; ++i) raw[i] = (int)pack2<T>(r.v[2 * i], r.v[2 * i + 1]);
   }
   *reinterpret_cast<i32x4*>(p) = raw;
 }
