@@ -227,6 +227,40 @@ __global__ __launch_bounds__(kBlock) void transpose_kernel(const W* __restrict__
   }
 }
 
+// 16-bit transpose without LDS: each lane loads an 8x8 block as eight 16-byte row vectors,
+// transposes it in registers and stores eight 16-byte vectors.  Within a wave, lane = 8 * g + c
+// covers input rows r0 + 8g..+7 and columns c0 + 8c..+7, so both the loads (8 lanes per input row)
+// and the stores (8 lanes per output row) move 128 contiguous bytes.  A workgroup (4 waves) covers
+// 64 rows x 256 columns.  Needs cols % 8 == 0, ldy % 8 == 0 and 16-byte aligned pointers; rows past
+// `rows` (up to ldy) are written as zeros.
+__global__ __launch_bounds__(kBlock) void transpose16_kernel(const u16* __restrict__ x, u16* __restrict__ y,
+                                                             int64_t rows, int64_t cols, int64_t ldy) {
+  const int64_t b = blockIdx.z;
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int64_t r = (int64_t)blockIdx.y * 64 + 8 * (lane >> 3);
+  const int64_t c = (int64_t)blockIdx.x * 256 + wave * 64 + 8 * (lane & 7);
+  if (c >= cols || r >= ldy) return;
+  const u16* xb = x + b * rows * cols + c;
+  uint32_t in[8][4];
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    i32x4 v = {0, 0, 0, 0};
+    if (r + i < rows) v = *reinterpret_cast<const i32x4*>(xb + (r + i) * cols);
+#pragma unroll
+    for (int w = 0; w < 4; ++w) in[i][w] = (uint32_t)v[w];
+  }
+  u16* yb = y + b * cols * ldy + c * ldy + r;
+#pragma unroll
+  for (int j = 0; j < 8; ++j) {  // output row c + j holds element j of every input row
+    const int w = j >> 1, sh = (j & 1) * 16;
+    i32x4 o;
+#pragma unroll
+    for (int k = 0; k < 4; ++k)
+      o[k] = (int)(((in[2 * k][w] >> sh) & 0xffffu) | (((in[2 * k + 1][w] >> sh) & 0xffffu) << 16));
+    *reinterpret_cast<i32x4*>(yb + (int64_t)j * ldy) = o;
+  }
+}
+
 // ---------------------------------------------------------------- embedding
 template <typename T>
 __global__ __launch_bounds__(kBlock) void embedding_fwd_kernel(const void* __restrict__ ids, int ids64,
@@ -427,6 +461,11 @@ int q3_transpose(int dtype, const void* x, void* y, int64_t batch, int64_t rows,
                  hipStream_t stream) {
   Q3_REQUIRE(dtype_ok(dtype) && x && y && batch > 0 && rows > 0 && cols > 0 && batch < 65536 && ldy >= rows);
   Q3_REQUIRE((ldy + 63) / 64 < 65536);
+  if (dtype != Q3_F32 && cols % 8 == 0 && ldy % 8 == 0 && aligned16<u16>(x) && aligned16<u16>(y)) {
+    dim3 g16((unsigned)((cols + 255) / 256), (unsigned)((ldy + 63) / 64), (unsigned)batch);
+    transpose16_kernel<<<g16, kBlock, 0, stream>>>((const u16*)x, (u16*)y, rows, cols, ldy);
+    return (int)hipGetLastError();
+  }
   dim3 grid((unsigned)((cols + 63) / 64), (unsigned)((ldy + 63) / 64), (unsigned)batch);
   if (dtype == Q3_F32)
     transpose_kernel<uint32_t><<<grid, kBlock, 0, stream>>>((const uint32_t*)x, (uint32_t*)y, rows, cols, ldy);

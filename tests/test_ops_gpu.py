@@ -160,6 +160,21 @@ def test_residual_cast_fill_transpose(dtype):
     assert p.cpu().tolist() == [[7, 8, 9, 10, 11]] * 2
 
 
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
+@pytest.mark.parametrize("batch,r,c,pad", [(1, 8192, 4096, 1), (2, 67, 136, 8), (1, 70, 264, 64), (3, 5, 8, 16),
+                                           (1, 2048, 1024, 8), (2, 67, 130, 1)])
+def test_transpose_shapes(batch, r, c, pad, dtype):
+    """Bit-exact layout change, vector (cols % 8 == 0, padded ld % 8 == 0) and scalar paths; the pad
+    columns are zero."""
+    print(f"transpose {batch}x{r}x{c} pad {pad} {dtype}", flush=True)
+    x = torch.randn(batch, r, c, generator=seeded(r + c), dtype=torch.float32).to(dtype)
+    y = _ops.transpose_last2(x.cuda(), pad_to=pad).cpu()
+    rp = -(-r // pad) * pad
+    assert y.shape == (batch, c, rp)
+    assert torch.equal(y[..., :r], x.transpose(1, 2))
+    assert not bool(y[..., r:].any())
+
+
 @pytest.mark.parametrize("dtype", DTYPES)
 @pytest.mark.parametrize("h", [64, 4096, 12])
 def test_embedding_fwd_bwd_deterministic(h, dtype):
