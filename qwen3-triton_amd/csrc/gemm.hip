@@ -1,17 +1,21 @@
 // bf16/fp16 GEMM on CDNA4 matrix cores, plus a strided SIMT fallback.
 //
 // gemm_nt:  C[M,N] = alpha * A[M,K] . B[N,K]^T (+ C if accumulate), both operands K-contiguous
-// (the layout of X and of a row-major weight W[N,K] in Y = X W^T).  fp32 accumulation in
-// v_mfma_f32_32x32x16_{bf16,f16}; output in bf16/fp16/fp32.
+// (the layout of X and of a row-major weight W[N,K] in Y = X W^T); fp32 accumulation, output in
+// bf16/fp16/fp32.
 //
-// Tiling: workgroup tile BM x BN x BK = 256 x 128 x 64, 4 waves in a 2 x 2 grid, each wave a
-// 128 x 64 sub-tile = 4 x 2 MFMA 32x32 tiles (128 fp32 accumulators per lane).  Global -> LDS
-// moves 16-byte vectors (8 consecutive k) staged through registers one k-tile ahead; LDS is
-// double-buffered so one barrier per k-tile suffices.  LDS rows are padded to BK+8 elements
-// (144 B): the 32 rows read by one MFMA operand fetch land on distinct 4-bank groups, so every
-// ds_read_b128 is conflict free.  Workgroup ids are remapped so that each XCD (ids congruent
-// mod 8) owns a contiguous range of output tiles, then rastered in groups of 8 tile-rows so
-// consecutive tiles share A rows in that XCD's L2.
+// Main path (K % 64 == 0), gemm_nt_v4_kernel: v_mfma_f32_16x16x32 (on MI355X it sustains a higher
+// rate than the 32x32x16 form under the board power limit with random data), 8 waves per
+// 256 x 256 x 64 tile (each 64 x 128) or 4 waves for 256 x 128 / 128 x 128 tiles, picked so the grid
+// still covers the 256 CUs.  Operand tiles go global -> LDS with wave-wide global_load_lds_dwordx4
+// into a ring of k-tiles (no register staging); LDS rows are unpadded and XOR-swizzled so the
+// fragment reads are bank-conflict free; fragment reads are software-pipelined one k-step ahead.
+// Workgroup ids are remapped so that each XCD (ids congruent mod 8) owns a contiguous range of
+// output tiles, rastered in groups of 8 tile-rows so concurrently running tiles share operand rows
+// in that XCD's L2.
+//
+// K % 64 != 0: gemm_nt_kernel, a register-staged 256 x 128 x 64 tile with padded LDS rows and
+// v_mfma_f32_32x32x16 (the k tail is zero-filled).
 #include "common.h"
 
 namespace {
@@ -24,6 +28,15 @@ template <> Q3_DEV f32x16 mfma_32x32x16<BF16>(bf16x8_t a, bf16x8_t b, f32x16 c) 
 }
 template <> Q3_DEV f32x16 mfma_32x32x16<F16>(bf16x8_t a, bf16x8_t b, f32x16 c) {
   return __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(f16x8_t, a), __builtin_bit_cast(f16x8_t, b), c,
+                                                 0, 0, 0);
+}
+
+template <typename T> Q3_DEV f32x4 mfma_16x16x32(bf16x8_t a, bf16x8_t b, f32x4 c);
+template <> Q3_DEV f32x4 mfma_16x16x32<BF16>(bf16x8_t a, bf16x8_t b, f32x4 c) {
+  return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
+}
+template <> Q3_DEV f32x4 mfma_16x16x32<F16>(bf16x8_t a, bf16x8_t b, f32x4 c) {
+  return __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(f16x8_t, a), __builtin_bit_cast(f16x8_t, b), c,
                                                  0, 0, 0);
 }
 
@@ -137,38 +150,42 @@ __global__ __launch_bounds__(kThreads) void gemm_nt_kernel(const u16* __restrict
     }
 }
 
-// ---------------------------------------------------------------- v2: direct-to-LDS, swizzled ring
-// Same contract as gemm_nt_kernel for K % BK == 0.  Each wave-wide global_load_lds_dwordx4 moves
-// 64 x 16 bytes straight into LDS (no register staging) into a ring of STAGES k-tiles, so
-// STAGES-1 tiles of A and B rows are in flight while one feeds the matrix cores.  LDS rows are
-// BK*2 bytes unpadded; the 16-byte chunk c of stage row R is stored at physical chunk c ^ swz(R),
-// chosen so that the 8- and 16-lane groups of every MFMA operand read (32 rows, one logical chunk)
-// hit distinct banks.  The lane -> global address map applies the same swizzle, because the LDS
-// destination of a wave load is fixed (base + lane * 16).  Rows beyond M/N load a clamped valid row:
-// they only feed output rows/columns that are never stored.
-template <int CPR> Q3_DEV int lds_swz(int r) {
-  if constexpr (CPR == 8) return (r ^ (r >> 3)) & 7;
-  else return ((r >> 1) ^ (r >> 3)) & 3;  // 4 chunks (64-byte rows)
-}
-
-// s_waitcnt with vmcnt = N (N < 64) and lgkm/exp counters left unconstrained.
-template <int N> Q3_DEV void wait_vmcnt() {
+// ---------------------------------------------------------------- direct-to-LDS ring helpers
+// Workgroup barrier for a direct-to-LDS ring: this wave's loads older than its newest N have
+// landed in LDS and its own LDS reads are done (vmcnt(N) lgkmcnt(0)), then s_barrier.
+// __syncthreads() would add a release fence, which waits for vmcnt(0) and so drains every
+// prefetched stage of the ring at each k-tile.
+template <int N> Q3_DEV void ring_sync() {
   static_assert(N >= 0 && N < 64, "vmcnt range");
-  __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (7 << 4) | (15 << 8));
+  __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (7 << 4) | (0 << 8));
+  asm volatile("" ::: "memory");
+  __builtin_amdgcn_s_barrier();
+  asm volatile("" ::: "memory");
 }
 
-template <typename T, typename O, int BM, int BN, int WM, int WN, int BK, int STAGES, bool PIPE = false>
-__global__ __launch_bounds__(WM * WN * 64) void gemm_nt_v2_kernel(const u16* __restrict__ A,
+// ---------------------------------------------------------------- v4: register-lean 16x16x32 pipeline
+// 128-byte LDS rows (BK = 64) with swizzle swz(r) = (r & 7) ^ ((r >> 3) & 1): it depends on r mod 16
+// only, and any 16 consecutive rows reading one logical 16-byte chunk hit 16 distinct (bank half,
+// chunk) slots of the 64-bank LDS -- conflict free.  Because every 16x16x32 fragment starts on a
+// multiple of 16 rows, all fragments of a wave share one swizzle: a fragment address is one
+// per-k-step base register plus an immediate offset, which leaves room for a fenced double buffer
+// of fragments (reads of k-step ks+1 in flight during the MFMAs of ks, the first reads of tile
+// kt+1 during the last MFMAs of tile kt) at two waves per SIMD.
+Q3_DEV int swz16(int r) { return (r & 7) ^ ((r >> 3) & 1); }
+
+template <typename T, typename O, int BM, int BN, int WM, int WN, int STAGES, bool EVEN>
+__global__ __launch_bounds__(WM * WN * 64) void gemm_nt_v4_kernel(const u16* __restrict__ A,
                                                                   const u16* __restrict__ B,
                                                                   typename O::storage* __restrict__ C, int M, int N,
                                                                   int K, int64_t lda, int64_t ldb, int64_t ldc,
-                                                                  float alpha, int accumulate) {
-  constexpr int NW = WM * WN, ROWB = BK * 2, CPR = BK / 8, RPL = 64 / CPR;
-  constexpr int TMW = BM / WM, TNW = BN / WN, TM = TMW / 32, TN = TNW / 32;
-  constexpr int RG = (BM + BN) / RPL;                  // row groups per stage (one wave load each)
-  static_assert(RG % NW == 0, "row groups must split evenly over the waves");
-  constexpr int LPW = RG / NW;                         // wave loads per k-tile
-  constexpr int STAGE = (BM + BN) * BK;                // elements per stage
+                                                                  float alpha, int accumulate, int vec_store) {
+  constexpr int BK = 64, NW = WM * WN, ROWB = BK * 2, CPR = 8, RPL = 8;
+  constexpr int TMW = BM / WM, TNW = BN / WN, FM = TMW / 16, FN = TNW / 16;
+  constexpr int RG = (BM + BN) / RPL;
+  static_assert(RG % NW == 0 && (BM / RPL) % NW == 0, "row groups must split evenly over the waves");
+  constexpr int LPW = RG / NW, A_LOADS = (BM / RPL) / NW;
+  constexpr int STAGE = (BM + BN) * BK;  // elements
+  constexpr int KS = BK / 32;            // 2 k-steps per tile
   __shared__ __attribute__((aligned(1024))) u16 lds[STAGES * STAGE];
 
   int tm, tn;
@@ -176,128 +193,162 @@ __global__ __launch_bounds__(WM * WN * 64) void gemm_nt_v2_kernel(const u16* __r
   const int m0 = tm * BM, n0 = tn * BN;
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int wm = wave / WN, wn = wave % WN;
+  const int wave_u = __builtin_amdgcn_readfirstlane(wave);
 
-  const u16* src[LPW];
+  // ---- global -> LDS: row R of the [A; B] stage, logical chunk c lands at physical c ^ swz16(R).
+  // Row groups of 8 rows; the swizzle repeats every 2 groups, so one lane offset per group parity.
+  uint32_t offa[2], offb[2];
+  const u16* src[EVEN ? 1 : LPW];
 #pragma unroll
-  for (int i = 0; i < LPW; ++i) {
-    const int rg = wave + NW * i;
-    const int R = rg * RPL + lane / CPR;                 // row in the combined [A; B] stage
-    const int c = (lane % CPR) ^ lds_swz<CPR>(R);        // logical 16-byte chunk this lane fetches
-    if (R < BM) {
-      src[i] = A + (int64_t)min(m0 + R, M - 1) * lda + c * 8;
-    } else {
-      src[i] = B + (int64_t)min(n0 + R - BM, N - 1) * ldb + c * 8;
+  for (int par = 0; par < 2; ++par) {
+    const int R = par * RPL + lane / CPR;
+    const int c = (lane % CPR) ^ swz16(R);
+    offa[par] = (uint32_t)(((lane / CPR) * lda + c * 8) * 2);
+    offb[par] = (uint32_t)(((lane / CPR) * ldb + c * 8) * 2);
+  }
+  if constexpr (!EVEN) {
+#pragma unroll
+    for (int i = 0; i < LPW; ++i) {
+      const int R = (wave + NW * i) * RPL + lane / CPR;
+      const int c = (lane % CPR) ^ swz16(R);
+      if (R < BM) src[i] = A + (int64_t)min(m0 + R, M - 1) * lda + c * 8;
+      else src[i] = B + (int64_t)min(n0 + R - BM, N - 1) * ldb + c * 8;
     }
   }
   auto issue = [&](int stage, int k0) {
 #pragma unroll
     for (int i = 0; i < LPW; ++i) {
-      const int rg = wave + NW * i;
-      __builtin_amdgcn_global_load_lds((const void*)(src[i] + k0),
-                                       (__attribute__((address_space(3))) void*)(lds + stage * STAGE + rg * RPL * BK),
+      const int rg = wave_u + NW * i;
+      const void* g;
+      if constexpr (EVEN) {
+        if (i < A_LOADS)
+          g = reinterpret_cast<const char*>(A + (int64_t)(m0 + rg * RPL) * lda + k0) + offa[rg & 1];
+        else
+          g = reinterpret_cast<const char*>(B + (int64_t)(n0 + rg * RPL - BM) * ldb + k0) + offb[rg & 1];
+      } else {
+        g = src[i] + k0;
+      }
+      __builtin_amdgcn_global_load_lds(g, (__attribute__((address_space(3))) void*)(lds + stage * STAGE + rg * RPL * BK),
                                        16, 0, 0);
     }
   };
 
-  f32x16 acc[TM][TN];
+  // ---- LDS -> fragments.  Lane l reads row (fragment base + l % 16), logical chunk ks*4 + l/16.
+  const int quarter = lane >> 4, sw = swz16(lane & 15);
+  uint32_t va[KS], vb[KS];
 #pragma unroll
-  for (int i = 0; i < TM; ++i)
+  for (int ks = 0; ks < KS; ++ks) {
+    const uint32_t coff = (uint32_t)(((ks * 4 + quarter) ^ sw) << 4);
+    va[ks] = (uint32_t)((wm * TMW + (lane & 15)) * ROWB) + coff;
+    vb[ks] = (uint32_t)((BM + wn * TNW + (lane & 15)) * ROWB) + coff;
+  }
+  const char* lds_c = reinterpret_cast<const char*>(lds);
+  bf16x8_t af[2][FM], bfr[2][FN];
+  auto load = [&](int stage, int buf, int ks) {
+    const char* sb = lds_c + stage * (STAGE * 2);
 #pragma unroll
-    for (int j = 0; j < TN; ++j)
+    for (int i = 0; i < FM; ++i) af[buf][i] = *reinterpret_cast<const bf16x8_t*>(sb + va[ks] + i * 16 * ROWB);
 #pragma unroll
-      for (int v = 0; v < 16; ++v) acc[i][j][v] = 0.f;
+    for (int j = 0; j < FN; ++j) bfr[buf][j] = *reinterpret_cast<const bf16x8_t*>(sb + vb[ks] + j * 16 * ROWB);
+  };
+
+  f32x4 acc[FM][FN];
+#pragma unroll
+  for (int i = 0; i < FM; ++i)
+#pragma unroll
+    for (int j = 0; j < FN; ++j) acc[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
 
   const int nk = K / BK;
 #pragma unroll
   for (int st = 0; st < STAGES - 1; ++st)
     if (st < nk) issue(st, st * BK);
-  int ra[TM], rb[TN], sa[TM], sb[TN];
-#pragma unroll
-  for (int i = 0; i < TM; ++i) {
-    ra[i] = wm * TMW + i * 32 + (lane & 31);
-    sa[i] = lds_swz<CPR>(ra[i]);
-  }
-#pragma unroll
-  for (int j = 0; j < TN; ++j) {
-    rb[j] = BM + wn * TNW + j * 32 + (lane & 31);
-    sb[j] = lds_swz<CPR>(rb[j]);
-  }
-  const int half = lane >> 5;
+  if (nk - 1 >= STAGES - 2) ring_sync<(STAGES - 2) * LPW>();
+  else ring_sync<0>();
+  if (STAGES - 1 < nk) issue(STAGES - 1, (STAGES - 1) * BK);
+  load(0, 0, 0);
   for (int kt = 0; kt < nk; ++kt) {
-    // Tile kt must have landed; the later tiles of the ring may stay in flight.
-    if (nk - 1 - kt >= STAGES - 2) wait_vmcnt<(STAGES - 2) * LPW>();
-    else wait_vmcnt<0>();
-    __syncthreads();  // every wave's share of tile kt is in LDS; stage (kt-1) % STAGES is free
-    if (kt + STAGES - 1 < nk) issue((kt + STAGES - 1) % STAGES, (kt + STAGES - 1) * BK);
-    const char* base = reinterpret_cast<const char*>(lds + (kt % STAGES) * STAGE);
-    if constexpr (!PIPE) {
+    const int stage = kt % STAGES;
+    // k-step 0: fragments of step 1 in flight during its MFMAs.  Step 0's fragments were read
+    // during the previous tile's last MFMAs; waiting for them here (already landed) keeps the
+    // outstanding-read count within what the LDS counter tracks, so the MFMAs below need no wait.
+    __builtin_amdgcn_sched_barrier(0);
+    __builtin_amdgcn_s_waitcnt((15) | (7 << 4) | (0 << 8) | (3 << 14));  // lgkmcnt(0)
+    load(stage, 1, 1);
+    __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-      for (int ks = 0; ks < BK / 16; ++ks) {
-        const int c = ks * 2 + half;
-        bf16x8_t af[TM], bfr[TN];
+    for (int i = 0; i < FM; ++i)
 #pragma unroll
-        for (int i = 0; i < TM; ++i)
-          af[i] = *reinterpret_cast<const bf16x8_t*>(base + ra[i] * ROWB + ((c ^ sa[i]) << 4));
+      for (int j = 0; j < FN; ++j) acc[i][j] = mfma_16x16x32<T>(bfr[0][j], af[0][i], acc[i][j]);
+    __builtin_amdgcn_sched_barrier(0);
+    // k-step 1: make tile kt+1 resident, refill the ring, read its first fragments.  The barrier
+    // and the fragment reads run on the last tile too (re-reading a resident stage), so the LDS
+    // counter state is the same on every path into the MFMAs below.
+    if (kt + STAGES - 1 < nk) ring_sync<(STAGES - 2) * LPW>();
+    else ring_sync<0>();
+    if (kt + STAGES < nk) issue(stage, (kt + STAGES) * BK);
+    load((kt + 1) % STAGES, 0, 0);
+    __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-        for (int j = 0; j < TN; ++j)
-          bfr[j] = *reinterpret_cast<const bf16x8_t*>(base + rb[j] * ROWB + ((c ^ sb[j]) << 4));
+    for (int i = 0; i < FM; ++i)
 #pragma unroll
-        for (int i = 0; i < TM; ++i)
-#pragma unroll
-          for (int j = 0; j < TN; ++j) acc[i][j] = mfma_32x32x16<T>(af[i], bfr[j], acc[i][j]);
-      }
-    } else {
-      // Fragments double-buffered across k-steps: the reads of step ks+1 are issued before the
-      // MFMAs of step ks and the scheduler is asked to interleave them one for one.
-      constexpr int KS = BK / 16;
-      bf16x8_t af[2][TM], bfr[2][TN];
-      auto load = [&](int buf, int ks) {
-        const int c = ks * 2 + half;
-#pragma unroll
-        for (int i = 0; i < TM; ++i)
-          af[buf][i] = *reinterpret_cast<const bf16x8_t*>(base + ra[i] * ROWB + ((c ^ sa[i]) << 4));
-#pragma unroll
-        for (int j = 0; j < TN; ++j)
-          bfr[buf][j] = *reinterpret_cast<const bf16x8_t*>(base + rb[j] * ROWB + ((c ^ sb[j]) << 4));
-      };
-      load(0, 0);
-#pragma unroll
-      for (int ks = 0; ks < KS; ++ks) {
-        if (ks + 1 < KS) load((ks + 1) & 1, ks + 1);
-#pragma unroll
-        for (int i = 0; i < TM; ++i)
-#pragma unroll
-          for (int j = 0; j < TN; ++j) acc[i][j] = mfma_32x32x16<T>(af[ks & 1][i], bfr[ks & 1][j], acc[i][j]);
-        if (ks + 1 < KS) {
-#pragma unroll
-          for (int x = 0; x < TM + TN; ++x) {
-            __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);  // one LDS read
-            __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // one MFMA
-          }
-          if (TM * TN > TM + TN) __builtin_amdgcn_sched_group_barrier(0x008, TM * TN - (TM + TN), 0);
-        } else {
-          __builtin_amdgcn_sched_group_barrier(0x008, TM * TN, 0);
-        }
-      }
-    }
+      for (int j = 0; j < FN; ++j) acc[i][j] = mfma_16x16x32<T>(bfr[1][j], af[1][i], acc[i][j]);
+    __builtin_amdgcn_sched_barrier(0);
   }
 
+  // ---- epilogue: lane owns row m and 4 consecutive columns of each 16x16 block (C^T layout)
 #pragma unroll
-  for (int i = 0; i < TM; ++i)
+  for (int i = 0; i < FM; ++i) {
+    const int row = m0 + wm * TMW + i * 16 + (lane & 15);
+    if (row >= M) continue;
+    typename O::storage* crow = C + (int64_t)row * ldc;
 #pragma unroll
-    for (int j = 0; j < TN; ++j) {
-      const int col = n0 + wn * TNW + j * 32 + (lane & 31);
+    for (int j = 0; j < FN; ++j) {
+      const int col = n0 + wn * TNW + j * 16 + 4 * quarter;
+      float r[4];
 #pragma unroll
-      for (int v = 0; v < 16; ++v) {
-        const int row = m0 + wm * TMW + i * 32 + 8 * (v >> 2) + 4 * (lane >> 5) + (v & 3);
-        if (row < M && col < N) {
-          typename O::storage* c = C + (int64_t)row * ldc + col;
-          float r = alpha * acc[i][j][v];
-          if (accumulate) r += to_f32<O>(*c);
-          *c = from_f32<O>(r);
+      for (int v = 0; v < 4; ++v) r[v] = alpha * acc[i][j][v];
+      if (vec_store && col + 3 < N) {
+        if constexpr (O::vec == 4) {
+          f32x4* p = reinterpret_cast<f32x4*>(crow + col);
+          if (accumulate) {
+            const f32x4 o = *p;
+#pragma unroll
+            for (int v = 0; v < 4; ++v) r[v] += o[v];
+          }
+          *p = f32x4{r[0], r[1], r[2], r[3]};
+        } else {
+          typedef __attribute__((__vector_size__(2 * sizeof(int)))) int i32x2;
+          i32x2* p = reinterpret_cast<i32x2*>(crow + col);
+          if (accumulate) {
+            const i32x2 o = *p;
+            r[0] += to_f32<O>((u16)(o[0] & 0xffff));
+            r[1] += to_f32<O>((u16)((uint32_t)o[0] >> 16));
+            r[2] += to_f32<O>((u16)(o[1] & 0xffff));
+            r[3] += to_f32<O>((u16)((uint32_t)o[1] >> 16));
+          }
+          *p = i32x2{(int)pack2<O>(r[0], r[1]), (int)pack2<O>(r[2], r[3])};
         }
+      } else {
+#pragma unroll
+        for (int v = 0; v < 4; ++v)
+          if (col + v < N) {
+            float x = r[v];
+            if (accumulate) x += to_f32<O>(crow[col + v]);
+            crow[col + v] = from_f32<O>(x);
+          }
       }
     }
+  }
+}
+
+template <typename T, typename O, int BM, int BN, int WM, int WN, int ST, bool EVEN>
+int launch_v4(const void* A, int64_t lda, const void* B, int64_t ldb, void* C, int64_t ldc, int64_t M, int64_t N,
+              int64_t K, float alpha, int acc, hipStream_t s) {
+  const int64_t tiles = ((M + BM - 1) / BM) * ((N + BN - 1) / BN);
+  const int vec = (ldc % 4 == 0) && (((uintptr_t)C & (O::vec == 4 ? 15 : 7)) == 0);
+  gemm_nt_v4_kernel<T, O, BM, BN, WM, WN, ST, EVEN><<<(unsigned)tiles, WM * WN * 64, 0, s>>>(
+      (const u16*)A, (const u16*)B, (typename O::storage*)C, (int)M, (int)N, (int)K, lda, ldb, ldc, alpha, acc, vec);
+  return (int)hipGetLastError();
 }
 
 // ---------------------------------------------------------------- strided SIMT fallback
@@ -344,15 +395,6 @@ __global__ __launch_bounds__(kThreads) void gemm_generic_kernel(const typename T
 
 constexpr int kBM = 256, kBN = 128, kBK = 64;
 
-template <typename T, typename O, int BM, int BN, int WM, int WN, int BK = 64, int ST = 2, bool PIPE = false>
-int launch_v2(const void* A, int64_t lda, const void* B, int64_t ldb, void* C, int64_t ldc, int64_t M, int64_t N,
-              int64_t K, float alpha, int acc, hipStream_t s) {
-  const int64_t tiles = ((M + BM - 1) / BM) * ((N + BN - 1) / BN);
-  gemm_nt_v2_kernel<T, O, BM, BN, WM, WN, BK, ST, PIPE><<<(unsigned)tiles, WM * WN * 64, 0, s>>>(
-      (const u16*)A, (const u16*)B, (typename O::storage*)C, (int)M, (int)N, (int)K, lda, ldb, ldc, alpha, acc);
-  return (int)hipGetLastError();
-}
-
 int64_t tiles_of(int64_t M, int64_t N, int64_t bm, int64_t bn) { return ((M + bm - 1) / bm) * ((N + bn - 1) / bn); }
 
 template <typename T, typename O>
@@ -361,11 +403,19 @@ int launch_nt(const void* A, int64_t lda, const void* B, int64_t ldb, void* C, i
   if (K % 64 == 0) {
     // Largest tile that still gives every CU (256) a workgroup (tile choice measured on MI355X
     // for the Qwen3-8B projection shapes).
-    if (tiles_of(M, N, 256, 256) >= 256)
-      return launch_v2<T, O, 256, 256, 2, 4, 64, 2, true>(A, lda, B, ldb, C, ldc, M, N, K, alpha, acc, s);
-    if (tiles_of(M, N, 256, 128) >= 256)
-      return launch_v2<T, O, 256, 128, 2, 2, 64, 3>(A, lda, B, ldb, C, ldc, M, N, K, alpha, acc, s);
-    return launch_v2<T, O, 128, 128, 2, 2, 64, 4>(A, lda, B, ldb, C, ldc, M, N, K, alpha, acc, s);
+    if (tiles_of(M, N, 256, 256) >= 256) {
+      if (M % 256 == 0 && N % 256 == 0)
+        return launch_v4<T, O, 256, 256, 4, 2, 2, true>(A, lda, B, ldb, C, ldc, M, N, K, alpha, acc, s);
+      return launch_v4<T, O, 256, 256, 4, 2, 2, false>(A, lda, B, ldb, C, ldc, M, N, K, alpha, acc, s);
+    }
+    if (tiles_of(M, N, 256, 128) >= 256) {
+      if (M % 256 == 0 && N % 128 == 0)
+        return launch_v4<T, O, 256, 128, 2, 2, 3, true>(A, lda, B, ldb, C, ldc, M, N, K, alpha, acc, s);
+      return launch_v4<T, O, 256, 128, 2, 2, 3, false>(A, lda, B, ldb, C, ldc, M, N, K, alpha, acc, s);
+    }
+    if (M % 128 == 0 && N % 128 == 0)
+      return launch_v4<T, O, 128, 128, 2, 2, 4, true>(A, lda, B, ldb, C, ldc, M, N, K, alpha, acc, s);
+    return launch_v4<T, O, 128, 128, 2, 2, 4, false>(A, lda, B, ldb, C, ldc, M, N, K, alpha, acc, s);
   }
   const int64_t tiles = ((M + kBM - 1) / kBM) * ((N + kBN - 1) / kBN);
   gemm_nt_kernel<T, O, kBM, kBN, kBK, 128, 64><<<(unsigned)tiles, kThreads, 0, s>>>(
@@ -410,19 +460,11 @@ bool al16(const void* p) { return ((uintptr_t)p & 15) == 0; }
 extern "C" int q3_gemm_nt_variant(int variant, const void* A, int64_t lda, const void* B, int64_t ldb, void* C,
                                   int64_t ldc, int64_t M, int64_t N, int64_t K, hipStream_t s) {
   switch (variant) {
-    case 0: return launch_v2<BF16, BF16, 256, 256, 2, 4, 64, 2>(A, lda, B, ldb, C, ldc, M, N, K, 1.f, 0, s);
-    case 1: return launch_v2<BF16, BF16, 256, 256, 2, 4, 32, 4>(A, lda, B, ldb, C, ldc, M, N, K, 1.f, 0, s);
-    case 2: return launch_v2<BF16, BF16, 256, 128, 2, 2, 64, 3>(A, lda, B, ldb, C, ldc, M, N, K, 1.f, 0, s);
-    case 3: return launch_v2<BF16, BF16, 256, 128, 2, 2, 32, 4>(A, lda, B, ldb, C, ldc, M, N, K, 1.f, 0, s);
-    case 4: return launch_v2<BF16, BF16, 128, 128, 2, 2, 64, 4>(A, lda, B, ldb, C, ldc, M, N, K, 1.f, 0, s);
-    case 5: return launch_v2<BF16, BF16, 256, 256, 2, 4, 32, 3>(A, lda, B, ldb, C, ldc, M, N, K, 1.f, 0, s);
-    case 6: return launch_v2<BF16, BF16, 256, 256, 4, 2, 64, 2>(A, lda, B, ldb, C, ldc, M, N, K, 1.f, 0, s);
-    case 7: return launch_v2<BF16, BF16, 128, 256, 2, 2, 64, 3>(A, lda, B, ldb, C, ldc, M, N, K, 1.f, 0, s);
-    case 8: return launch_v2<BF16, BF16, 256, 256, 2, 4, 64, 2, true>(A, lda, B, ldb, C, ldc, M, N, K, 1.f, 0, s);
-    case 9: return launch_v2<BF16, BF16, 256, 256, 4, 2, 64, 2, true>(A, lda, B, ldb, C, ldc, M, N, K, 1.f, 0, s);
-    case 10: return launch_v2<BF16, BF16, 256, 128, 2, 2, 64, 3, true>(A, lda, B, ldb, C, ldc, M, N, K, 1.f, 0, s);
-    case 11: return launch_v2<BF16, BF16, 128, 128, 2, 2, 64, 4, true>(A, lda, B, ldb, C, ldc, M, N, K, 1.f, 0, s);
-    case 12: return launch_v2<BF16, BF16, 256, 256, 2, 2, 64, 2, true>(A, lda, B, ldb, C, ldc, M, N, K, 1.f, 0, s);
+    case 0: return launch_v4<BF16, BF16, 256, 256, 4, 2, 2, true>(A, lda, B, ldb, C, ldc, M, N, K, 1.f, 0, s);
+    case 1: return launch_v4<BF16, BF16, 256, 256, 2, 4, 2, true>(A, lda, B, ldb, C, ldc, M, N, K, 1.f, 0, s);
+    case 2: return launch_v4<BF16, BF16, 256, 256, 4, 2, 2, false>(A, lda, B, ldb, C, ldc, M, N, K, 1.f, 0, s);
+    case 3: return launch_v4<BF16, BF16, 256, 128, 2, 2, 3, true>(A, lda, B, ldb, C, ldc, M, N, K, 1.f, 0, s);
+    case 4: return launch_v4<BF16, BF16, 128, 128, 2, 2, 4, true>(A, lda, B, ldb, C, ldc, M, N, K, 1.f, 0, s);
     default: return Q3_ERR_INVALID;
   }
 }
