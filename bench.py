@@ -230,6 +230,7 @@ def main():
     ap.add_argument("--no-decode", action="store_true")
     ap.add_argument("--no-layer", action="store_true", help="skip the decoder-layer step (profiling decode)")
     ap.add_argument("--decode-tokens", type=int, default=256)
+    ap.add_argument("--decode-batches", default="1,8", help="comma list of decode batches among 1 and 8")
     args = ap.parse_args()
     if args.gpus != 1:
         print("bench.py measures one MI355X: this build has no multi-GPU path (collectives are out of scope); "
@@ -277,8 +278,9 @@ def main():
     if not args.no_decode:
         log("decode")
         try:
-            result["decode"] = {"b1": decode_bench(1, 2048, args.decode_tokens),
-                                "b8": decode_bench(8, 1024, args.decode_tokens)}
+            prompts = {1: 2048, 8: 1024}
+            result["decode"] = {f"b{b}": decode_bench(b, prompts[b], args.decode_tokens)
+                                for b in (int(x) for x in args.decode_batches.split(","))}
         except Exception as exc:  # report, do not hide the layer result
             result["decode"] = {"error": repr(exc)}
     if not args.no_cpu_baseline:

@@ -174,24 +174,39 @@ int q3_ce_chunk_grad(int dtype, int out_dtype, const void* z, int64_t ld, int64_
                      int64_t vocab, int64_t ignore_index, hipStream_t stream);
 
 /* ------------------------------------------------------------------ greedy decode
- * y[m, n] = sum_k x[m, k] * W[n, k] for m < M <= 8 (x rows at stride ldx, y rows at stride ldy),
- * fp32 accumulation, weights streamed once.  Replaces: inference/kernels.py:116-146 (_inference_gemv
- * / linear for M <= 8), inference/accumulation.py:13-84. */
+ * y[m, n] = sum_k x[m, k] * W[n, k] for m < M <= 16 (x rows at stride ldx, y rows at stride ldy),
+ * fp32 accumulation on the matrix cores, weights streamed once (q3_decode_linear, mode 0, no norm).
+ * Replaces: inference/kernels.py:116-146 (_inference_gemv / linear for small M),
+ * inference/accumulation.py:13-84. */
 int q3_gemv(int dtype, const void* x, int64_t ldx, const void* w, void* y, int64_t ldy, int64_t m, int64_t n,
             int64_t k, hipStream_t stream);
+/* Fused decode-step projection for M <= 16 token rows (K % 8 == 0, 16-byte aligned rows):
+ *   xn = norm_w ? RMSNorm(x) * norm_w (eps, rounded to dtype) : x
+ *   mode 0: y_i[m, :n_i] = xn W_i^T for each of the nseg <= 3 segments (W_i [n_i, K], row-major);
+ *   mode 1: y_0 = res + dtype(xn W_0^T)  (residual add; res rows at stride ldres, may alias y_0);
+ *   mode 2: y_0 = silu(dtype(xn W_0^T)) * dtype(xn W_1^T)  (SwiGLU; nseg == 2, n_0 == n_1).
+ * w, y, ldy and n are host arrays of nseg entries.  Deterministic (fixed-order reductions).
+ * Replaces, in one launch each: inference/model.py:117-121 (rms_norm + q/k/v linear),
+ * inference/model.py:126 (o_proj linear + residual_add), inference/model.py:127-130 (rms_norm +
+ * gate/up linear + swiglu), inference/model.py:134 (down linear + residual_add). */
+int q3_decode_linear(int dtype, const void* x, int64_t ldx, int64_t m, int64_t k, const void* norm_w, float eps,
+                     int mode, int nseg, const void* const* w, void* const* y, const int64_t* ldy, const int64_t* n,
+                     const void* res, int64_t ldres, hipStream_t stream);
 /* cache_{k,v}[b, h, start + s, :] = {k,v}[b, s, h, :]; caches are [B,H,capacity,D].  When start_dev is
  * non-NULL the start position is read from that device int64 at run time (a graph-replayable decode
  * step); positions >= capacity are skipped.  Replaces: inference/kernels.py:24-35 (_inference_cache_append). */
 int q3_kv_append(int dtype, const void* k, const void* v, void* cache_k, void* cache_v, int64_t B, int64_t S,
                  int64_t H, int64_t D, int64_t capacity, int64_t start, const int64_t* start_dev,
                  hipStream_t stream);
-/* One query per (b, head) against the first T_len cached positions (D = 128): split-KV partials of
- * 128 keys, then a fixed-order merge.  q/out element strides (batch, head); cache strides
- * (ksb, ksh) with position stride D.  With len_dev non-NULL, T_len = *len_dev + 1 is read at run
- * time and the launch covers the whole capacity (workspace sized for T_len = capacity).
+/* One query per (b, head) against the first T_len cached positions (D = 128, Hq/Hkv <= 8): one
+ * workgroup per (b, kv head, 64-key split) serves the whole GQA group,
+ * then a fixed-order merge of the split partials.  q/out element strides (batch, head);
+ * cache strides (ksb, ksh) with position stride D.  With len_dev non-NULL, T_len = *len_dev + 1 is
+ * read at run time and the launch covers the whole capacity (workspace sized for T_len = capacity).
+ * The launched span (T_len, or capacity with len_dev) is at most 65536 positions.
  * Replaces: inference/kernels.py:71-113 (_inference_decode_partial, _inference_decode_merge,
  * attention with s == 1). */
-size_t q3_decode_attention_workspace_bytes(int64_t B, int64_t Hq, int64_t T_len);
+size_t q3_decode_attention_workspace_bytes(int64_t B, int64_t Hq, int64_t Hkv, int64_t T_len);
 int q3_decode_attention(int dtype, const void* q, int64_t qsb, int64_t qsh, const void* cache_k, const void* cache_v,
                         int64_t ksb, int64_t ksh, void* out, int64_t osb, int64_t osh, void* workspace, int64_t B,
                         int64_t Hq, int64_t Hkv, int64_t T_len, const int64_t* len_dev, int64_t capacity, int64_t D,

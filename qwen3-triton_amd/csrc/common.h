@@ -84,6 +84,18 @@ template <typename T> Q3_DEV void store_vec(typename T::storage* p, const Vec<T>
   *reinterpret_cast<i32x4*>(p) = raw;
 }
 
+// ------------------------------------------------------------------ matrix cores
+// D(16x16, fp32) += A(16x32) B(32x16), 16-bit inputs: lane l holds A[l % 16][8 (l / 16) + 0..7],
+// B[8 (l / 16) + 0..7][l % 16] and D[4 (l / 16) + 0..3][l % 16].
+template <typename T> Q3_DEV f32x4 mfma_16x16x32(bf16x8_t a, bf16x8_t b, f32x4 c);
+template <> Q3_DEV f32x4 mfma_16x16x32<BF16>(bf16x8_t a, bf16x8_t b, f32x4 c) {
+  return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
+}
+template <> Q3_DEV f32x4 mfma_16x16x32<F16>(bf16x8_t a, bf16x8_t b, f32x4 c) {
+  return __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(f16x8_t, a), __builtin_bit_cast(f16x8_t, b), c,
+                                                 0, 0, 0);
+}
+
 // ------------------------------------------------------------------ wave64 reductions
 // Butterfly over aligned groups of WIDTH lanes (WIDTH a power of two <= 64); every lane in
 // the group ends with the full result.  Offsets 1/2 use DPP quad permutes, 4/8 DPP row
@@ -108,6 +120,11 @@ template <int WIDTH> Q3_DEV float group_max(float x) {
 }
 
 Q3_DEV int lane_id() { return (int)(threadIdx.x & 63); }
+
+// sigmoid(g) = 1 / (1 + e^-g) with the hardware exp2 and reciprocal (SiLU(g) = g * q3_sigmoid(g)).
+Q3_DEV float q3_sigmoid(float g) {
+  return __builtin_amdgcn_rcpf(1.f + __builtin_amdgcn_exp2f(-g * 1.4426950408889634f));
+}
 
 // Launch helpers: every entry point returns the launch status as an int.
 #define Q3_CHECK_LAUNCH() return (int)hipGetLastError()

@@ -6,60 +6,155 @@ namespace {
 
 constexpr int kThreads = 256;
 
-// ============================================================================ GEMV
-// y[m, n] = sum_k x[m, k] * W[n, k] for M <= 8 rows of x.  A workgroup owns R consecutive rows of
-// W and its 4 waves split K into interleaved 16-byte chunks (lane chunk c = wave*64 + lane +
-// 256*i), so every weight byte is read once with fully coalesced 16-byte loads and each x chunk
-// load is shared by R weight rows.  The R*M fp32 partials are reduced inside each wave (DPP /
-// swizzle butterflies) and then across the 4 waves through LDS in a fixed order: deterministic.
-template <typename T, int M, int R>
-__global__ __launch_bounds__(kThreads) void gemv_kernel(const u16* __restrict__ x, int64_t ldx,
-                                                        const u16* __restrict__ W, u16* __restrict__ y, int64_t ldy,
-                                                        int N, int K) {
-  __shared__ float red[4][R * M];
-  const int n0 = blockIdx.x * R;
+// ============================================================================ decode linear
+// y_s[m, n] = epilogue(sum_k xn[m, k] W_s[n, k]) for M <= 16 token rows (a decode step), on matrix
+// cores: v_mfma_f32_16x16x32 with the token rows as the A operand (rows >= M are zero) and 16 weight
+// rows as the B operand.  The weights stream straight into registers: per 128-wide k block, lane l
+// (row n = l % 16, quarter kq = l / 16) loads the 64 contiguous bytes W[n][kb + 32 kq, +32) and feeds
+// them to the 4 MFMA k-steps of the block (k-step s takes its 8 k at kb + 32 kq + 8 s); the token
+// fragments use the same k order, which the sum does not see.  A workgroup owns 16 output rows and
+// its 4 waves take interleaved k blocks; the partial 16 x 16 tiles fold in LDS in fixed order.
+//   * NORM: xn = x * rsqrt(mean(x^2) + eps) * norm_w (RMSNorm of the input rows, recomputed per
+//     workgroup from the M rows of x, rounded to the storage type like the standalone kernel);
+//   * MODE 0: y = acc;  MODE 1: y = res + T(acc) (residual add);  MODE 2: segments 0 and 1 are the
+//     gate and up weights, y_0 = silu(T(acc_gate)) * T(acc_up) (SwiGLU);
+//   * up to 3 weight segments share the input (the Q, K and V projections in one launch).
+// Rounding points match the unfused path (GEMV output, then residual / SwiGLU), and every output is
+// a fixed-order reduction: deterministic.
+struct DecSeg {
+  const u16* w;
+  u16* y;
+  int64_t ldy;
+  int n, tiles;
+};
+struct DecArgs {
+  DecSeg seg[3];
+  int nseg;
+  const u16* x;
+  int64_t ldx;
+  int M, K;
+  const u16* nw;
+  float eps;
+  const u16* res;
+  int64_t ldres;
+};
+
+template <typename T, int MODE, bool NORM>
+__global__ __launch_bounds__(256) void dlinear_kernel(DecArgs a) {
+  constexpr int NB = MODE == 2 ? 2 : 1;  // weight tiles per workgroup (gate + up)
+  __shared__ float inv_s[16];
+  __shared__ f32x4 red[4][NB][64];
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  const int nch = K / 8;
-  float acc[R][M];
+  int tile = blockIdx.x, s = 0;
+  if constexpr (MODE != 2) {
+    while (s + 1 < a.nseg && tile >= a.seg[s].tiles) tile -= a.seg[s++].tiles;
+  }
+  const DecSeg sg = a.seg[s];
+  const int n0 = tile * 16, K = a.K, M = a.M;
+  const int r = lane & 15, kq = lane >> 4;  // r: token row (A) and weight row (B) of this lane
+
+  if constexpr (NORM) {
+    for (int m = wave; m < M; m += 4) {
+      const u16* xr = a.x + m * a.ldx;
+      float ss = 0.f;
+      for (int c = lane; c < K / 8; c += 64) {
+        const Vec<T> v = load_vec<T>(xr + c * 8);
 #pragma unroll
-  for (int r = 0; r < R; ++r)
-#pragma unroll
-    for (int m = 0; m < M; ++m) acc[r][m] = 0.f;
-  for (int c = tid; c < nch; c += kThreads) {
-    Vec<T> wv[R];
-#pragma unroll
-    for (int r = 0; r < R; ++r) {
-      if (n0 + r < N) {
-        wv[r] = load_vec<T>(W + (int64_t)(n0 + r) * K + (int64_t)c * 8);
-      } else {
-#pragma unroll
-        for (int e = 0; e < 8; ++e) wv[r].v[e] = 0.f;
+        for (int e = 0; e < 8; ++e) ss += v.v[e] * v.v[e];
       }
+      ss = group_sum<64>(ss);
+      if (lane == 0) inv_s[m] = rsqrtf(ss * (1.f / (float)K) + a.eps);
     }
-#pragma unroll
-    for (int m = 0; m < M; ++m) {
-      const Vec<T> xv = load_vec<T>(x + m * ldx + (int64_t)c * 8);
-#pragma unroll
-      for (int r = 0; r < R; ++r)
-#pragma unroll
-        for (int e = 0; e < 8; ++e) acc[r][m] += wv[r].v[e] * xv.v[e];
-    }
+    __syncthreads();
   }
+  const bool xrow = r < M;
+  const float inv = NORM && xrow ? inv_s[r] : 1.f;
+  const u16* xr = a.x + (xrow ? r : 0) * a.ldx + 32 * kq;
+  const u16* wr[NB];
 #pragma unroll
-  for (int r = 0; r < R; ++r)
+  for (int j = 0; j < NB; ++j)
+    wr[j] = a.seg[MODE == 2 ? j : s].w + (int64_t)min(n0 + r, sg.n - 1) * K + 32 * kq;
+
+  f32x4 acc[NB];
 #pragma unroll
-    for (int m = 0; m < M; ++m) {
-      const float s = group_sum<64>(acc[r][m]);
-      if (lane == 0) red[wave][r * M + m] = s;
+  for (int j = 0; j < NB; ++j) acc[j] = f32x4{0.f, 0.f, 0.f, 0.f};
+
+  // One 128-wide k block; `guard` bounds each 16-byte chunk by K (the ragged last block).
+  auto block = [&](int kb, bool guard) {
+    i32x4 wv[NB][4], xv[4], nv[4];
+#pragma unroll
+    for (int c = 0; c < 4; ++c) {
+      const int k = kb + 32 * kq + 8 * c;
+      const bool ok = !guard || k < K;
+#pragma unroll
+      for (int j = 0; j < NB; ++j) wv[j][c] = ok ? *reinterpret_cast<const i32x4*>(wr[j] + kb + 8 * c) : i32x4{0, 0, 0, 0};
+      xv[c] = ok && xrow ? *reinterpret_cast<const i32x4*>(xr + kb + 8 * c) : i32x4{0, 0, 0, 0};
+      if constexpr (NORM) nv[c] = ok ? *reinterpret_cast<const i32x4*>(a.nw + k) : i32x4{0, 0, 0, 0};
     }
+#pragma unroll
+    for (int c = 0; c < 4; ++c) {
+      i32x4 xf = xv[c];
+      if constexpr (NORM) {
+#pragma unroll
+        for (int w = 0; w < 4; ++w) {
+          const uint32_t xx = (uint32_t)xv[c][w], ww = (uint32_t)nv[c][w];
+          const float lo = to_f32<T>((u16)(xx & 0xffffu)) * inv * to_f32<T>((u16)(ww & 0xffffu));
+          const float hi = to_f32<T>((u16)(xx >> 16)) * inv * to_f32<T>((u16)(ww >> 16));
+          xf[w] = (int)pack2<T>(lo, hi);
+        }
+      }
+#pragma unroll
+      for (int j = 0; j < NB; ++j)
+        acc[j] = mfma_16x16x32<T>(__builtin_bit_cast(bf16x8_t, xf), __builtin_bit_cast(bf16x8_t, wv[j][c]), acc[j]);
+    }
+  };
+  const int nfull = K / 128, nblk = (K + 127) / 128;
+  int b = wave;
+  for (; b + 4 < nfull; b += 8) {  // two blocks per step: more loads in flight
+    block(b * 128, false);
+    block((b + 4) * 128, false);
+  }
+  for (; b < nblk; b += 4) block(b * 128, b >= nfull);
+
+#pragma unroll
+  for (int j = 0; j < NB; ++j) red[wave][j][lane] = acc[j];
   __syncthreads();
-  if (tid < R * M) {
-    const int r = tid / M, m = tid % M;
-    if (n0 + r < N) {
-      const float s = ((red[0][tid] + red[1][tid]) + red[2][tid]) + red[3][tid];
-      y[m * ldy + n0 + r] = from_f32<T>(s);
-    }
+  if (wave != 0) return;
+  float v[NB][4];
+#pragma unroll
+  for (int j = 0; j < NB; ++j) {
+    const f32x4 t = ((red[0][j][lane] + red[1][j][lane]) + red[2][j][lane]) + red[3][j][lane];
+#pragma unroll
+    for (int e = 0; e < 4; ++e) v[j][e] = t[e];
   }
+  // lane holds D[m = 4 kq + e][n = r]
+  const int n = n0 + r;
+  if (n >= sg.n) return;
+#pragma unroll
+  for (int e = 0; e < 4; ++e) {
+    const int m = 4 * kq + e;
+    if (m >= M) continue;
+    float o = to_f32<T>(from_f32<T>(v[0][e]));
+    if constexpr (MODE == 1) o = to_f32<T>(a.res[m * a.ldres + n]) + o;
+    if constexpr (MODE == 2) {
+      const float u = to_f32<T>(from_f32<T>(v[1][e]));
+      o = o * q3_sigmoid(o) * u;
+    }
+    sg.y[m * sg.ldy + n] = from_f32<T>(o);
+  }
+}
+
+template <typename T, int MODE, bool NORM>
+int dlinear_launch(const DecArgs& a, int tiles, hipStream_t s) {
+  dlinear_kernel<T, MODE, NORM><<<(unsigned)tiles, 256, 0, s>>>(a);
+  return (int)hipGetLastError();
+}
+
+template <typename T>
+int dlinear_t(const DecArgs& a, int tiles, int mode, bool norm, hipStream_t s) {
+  if (mode == 0) return norm ? dlinear_launch<T, 0, true>(a, tiles, s) : dlinear_launch<T, 0, false>(a, tiles, s);
+  if (mode == 1) return norm ? dlinear_launch<T, 1, true>(a, tiles, s) : dlinear_launch<T, 1, false>(a, tiles, s);
+  return norm ? dlinear_launch<T, 2, true>(a, tiles, s) : dlinear_launch<T, 2, false>(a, tiles, s);
 }
 
 // ============================================================================ KV append
@@ -87,107 +182,176 @@ __global__ __launch_bounds__(kThreads) void kv_append_kernel(const u16* __restri
 }
 
 // ============================================================================ decode attention
-// One wave per (b, query head, chunk of kChunk cached keys).  16 lanes own one key (8 of its 128
-// dims each), so a wave scores 4 keys per step with 16-byte loads and a 16-lane DPP reduction; the
-// chunk's scores sit in LDS for the max/exp pass; the V pass mirrors the K pass and the 4 key
-// groups are folded at the end.  Writes the unnormalised partial output, its max and its sum.
-constexpr int kChunk = 128;
+// One workgroup (4 waves) per (b, kv head, split of kSplit = 64 cached keys) computes all G query
+// heads of the GQA group, so every K/V byte is read once; each wave owns 16 keys and issues all of
+// its K and V loads before using any.  Scores: 16 lanes per key (8 of its 128 dims each), 4 keys per
+// step, a 16-lane DPP reduction per query head; they go to LDS.  Softmax: every wave takes the
+// workgroup's 64 scores one per lane (wave max / sum by DPP, identical in all waves).  P V: each lane
+// owns 2 of the 128 output dims for the wave's 16 keys (V read as 256 contiguous bytes per key) and
+// takes each key's probability with a lane read, so no cross-lane output reduction is needed; the
+// 4 waves fold through LDS.  A second kernel merges the splits in fixed order (deterministic).
+constexpr int kSplit = 64;
 
-template <typename T>
-__global__ __launch_bounds__(64) void decode_attn_partial(const u16* __restrict__ q, int64_t qsb, int64_t qsh,
+template <typename T, int G>
+__global__ __launch_bounds__(256) void decode_attn_kernel(const u16* __restrict__ q, int64_t qsb, int64_t qsh,
                                                           const u16* __restrict__ ck, const u16* __restrict__ cv,
                                                           int64_t ksb, int64_t ksh, float* __restrict__ opart,
                                                           float* __restrict__ mpart, float* __restrict__ lpart,
-                                                          int Hq, int Hkv, int T_len, const int64_t* len_dev,
-                                                          int capacity, int splits, float scale) {
-  constexpr int D = 128;
-  __shared__ float sc[kChunk];
-  const int split = blockIdx.x, bh = blockIdx.y, b = bh / Hq, h = bh % Hq, hk = h / (Hq / Hkv);
-  const int lane = threadIdx.x, t = lane & 15, grp = lane >> 4;
+                                                          int Hkv, int T_len, const int64_t* len_dev, int capacity,
+                                                          int splits, float scale2) {
+  constexpr int D = 128, KPW = kSplit / 4;  // keys per wave
+  __shared__ float sc[G][kSplit];
+  __shared__ float red_o[4][G][D];
+  const int split = blockIdx.x, bk = blockIdx.y, b = bk / Hkv, hk = bk % Hkv;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, t = lane & 15, kg = lane >> 4;
   // len_dev holds the cache length before this token: the token itself is at that position.
   if (len_dev) T_len = min((int)*len_dev + 1, capacity);
-  const int k0 = split * kChunk;
-  const int kend = min(T_len, k0 + kChunk);
-  const int64_t pi0 = (int64_t)bh * splits + split;
-  if (k0 >= T_len) {  // split beyond the live length (fixed-size launch): an empty partial
-    for (int e = lane; e < D; e += 64) opart[pi0 * D + e] = 0.f;
-    if (lane == 0) {
-      mpart[pi0] = -INFINITY;
-      lpart[pi0] = 0.f;
-    }
-    return;
-  }
+  const int k0 = split * kSplit, kw = k0 + wave * KPW;
+
   const u16* kb = ck + b * ksb + hk * ksh;
   const u16* vb = cv + b * ksb + hk * ksh;
-  const Vec<T> qv = load_vec<T>(q + b * qsb + h * qsh + t * 8);
-  for (int it = 0; it < kChunk / 4; ++it) {
-    const int j = it * 4 + grp, key = k0 + j;
-    float s = 0.f;
-    if (key < kend) {
-      const Vec<T> kv = load_vec<T>(kb + (int64_t)key * D + t * 8);
+  i32x4 kr[KPW / 4];
+  uint32_t vr[KPW];
 #pragma unroll
-      for (int e = 0; e < 8; ++e) s += qv.v[e] * kv.v[e];
+  for (int it = 0; it < KPW / 4; ++it) {
+    const int key = kw + it * 4 + kg;
+    kr[it] = key < T_len ? *reinterpret_cast<const i32x4*>(kb + (int64_t)key * D + t * 8) : i32x4{0, 0, 0, 0};
+  }
+#pragma unroll
+  for (int k = 0; k < KPW; ++k)
+    vr[k] = kw + k < T_len ? *reinterpret_cast<const uint32_t*>(vb + (int64_t)(kw + k) * D + 2 * lane) : 0u;
+  float qf[G][8];
+#pragma unroll
+  for (int g = 0; g < G; ++g) {
+    const Vec<T> qv = load_vec<T>(q + b * qsb + (int64_t)(hk * G + g) * qsh + t * 8);
+#pragma unroll
+    for (int e = 0; e < 8; ++e) qf[g][e] = qv.v[e] * scale2;  // scores in log2 units
+  }
+#pragma unroll
+  for (int it = 0; it < KPW / 4; ++it) {
+    float kf[8];
+#pragma unroll
+    for (int w = 0; w < 4; ++w) {
+      const uint32_t x = (uint32_t)kr[it][w];
+      kf[2 * w] = to_f32<T>((u16)(x & 0xffffu));
+      kf[2 * w + 1] = to_f32<T>((u16)(x >> 16));
     }
-    s = group_sum<16>(s);
-    if (t == 0) sc[j] = key < kend ? s * scale : -INFINITY;
+    const int key = kw + it * 4 + kg;
+#pragma unroll
+    for (int g = 0; g < G; ++g) {
+      float sg = 0.f;
+#pragma unroll
+      for (int e = 0; e < 8; ++e) sg += qf[g][e] * kf[e];
+      sg = group_sum<16>(sg);
+      if (t == 0) sc[g][key - k0] = key < T_len ? sg : -INFINITY;
+    }
   }
   __syncthreads();
-  float m = fmaxf(sc[lane], sc[lane + 64]);
-  m = group_max<64>(m);
-  const float p0 = __expf(sc[lane] - m), p1 = __expf(sc[lane + 64] - m);
-  const float l = group_sum<64>(p0 + p1);
-  __syncthreads();
-  sc[lane] = p0;
-  sc[lane + 64] = p1;
-  __syncthreads();
-  float o[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
-  for (int it = 0; it < kChunk / 4; ++it) {
-    const int j = it * 4 + grp, key = k0 + j;
-    if (key < kend) {
-      const float p = sc[j];
-      const Vec<T> vv = load_vec<T>(vb + (int64_t)key * D + t * 8);
+  // softmax over the workgroup's 64 keys (lane = key), the same in every wave
+  float p[G], m[G], l[G];
 #pragma unroll
-      for (int e = 0; e < 8; ++e) o[e] += p * vv.v[e];
+  for (int g = 0; g < G; ++g) {
+    const float x = sc[g][lane];
+    float mx = x;
+#pragma unroll
+    for (int o = 1; o < 64; o <<= 1) mx = fmaxf(mx, __shfl_xor(mx, o, 64));
+    m[g] = mx;
+    p[g] = mx == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(x - mx);
+    l[g] = group_sum<64>(p[g]);
+  }
+  // P V over this wave's keys: lane owns dims 2*lane, 2*lane+1
+  float o[G][2];
+#pragma unroll
+  for (int g = 0; g < G; ++g) o[g][0] = o[g][1] = 0.f;
+#pragma unroll
+  for (int k = 0; k < KPW; ++k) {
+    const float v0 = to_f32<T>((u16)(vr[k] & 0xffffu)), v1 = to_f32<T>((u16)(vr[k] >> 16));
+#pragma unroll
+    for (int g = 0; g < G; ++g) {
+      const float pk = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, p[g]),
+                                                                           wave * KPW + k));
+      o[g][0] += pk * v0;
+      o[g][1] += pk * v1;
     }
   }
 #pragma unroll
-  for (int e = 0; e < 8; ++e) {
-    o[e] += __shfl_xor(o[e], 16, 64);
-    o[e] += __shfl_xor(o[e], 32, 64);
+  for (int g = 0; g < G; ++g) {
+    red_o[wave][g][2 * lane] = o[g][0];
+    red_o[wave][g][2 * lane + 1] = o[g][1];
   }
-  const int64_t pi = (int64_t)bh * splits + split;
-  if (grp == 0) {
+  __syncthreads();
+  const int64_t pbase = ((int64_t)bk * splits + split) * G;
+  for (int i = tid; i < G * D; i += 256) {
+    const int g = i / D, d = i % D;
+    opart[(pbase + g) * D + d] = red_o[0][g][d] + red_o[1][g][d] + red_o[2][g][d] + red_o[3][g][d];
+  }
+  if (tid == 0) {  // m and l are wave-uniform
 #pragma unroll
-    for (int e = 0; e < 8; ++e) opart[pi * D + t * 8 + e] = o[e];
-  }
-  if (lane == 0) {
-    mpart[pi] = m;
-    lpart[pi] = l;
+    for (int g = 0; g < G; ++g) {
+      mpart[pbase + g] = m[g];
+      lpart[pbase + g] = l[g];
+    }
   }
 }
 
-// out[b, h, :] = sum_j exp(m_j - M) o_j / sum_j exp(m_j - M) l_j over the splits (fixed order).
-template <typename T>
-__global__ __launch_bounds__(64) void decode_attn_merge(const float* __restrict__ opart,
-                                                        const float* __restrict__ mpart,
-                                                        const float* __restrict__ lpart, u16* __restrict__ out,
-                                                        int64_t osb, int64_t osh, int Hq, int splits) {
-  constexpr int D = 128;
-  const int bh = blockIdx.x, b = bh / Hq, h = bh % Hq, lane = threadIdx.x;
-  float M = -INFINITY;
-  for (int j = 0; j < splits; ++j) M = fmaxf(M, mpart[(int64_t)bh * splits + j]);
-  float den = 0.f, o0 = 0.f, o1 = 0.f;
-  for (int j = 0; j < splits; ++j) {
-    const int64_t pi = (int64_t)bh * splits + j;
-    if (mpart[pi] == -INFINITY) continue;  // empty split
-    const float w = __expf(mpart[pi] - M);
-    den += w * lpart[pi];
-    o0 += w * opart[pi * D + lane];
-    o1 += w * opart[pi * D + 64 + lane];
+// out[b, hq, :] = sum_j exp2(m_j - M) o_j / sum_j exp2(m_j - M) l_j over the splits, in fixed order.
+// One workgroup of 4 x 128 threads per (b, query head): the split weights go to LDS once, thread
+// group r sums the splits j = r mod 4 with all its loads in flight, and the 4 groups fold in LDS.
+template <typename T, int G>
+__global__ __launch_bounds__(512) void decode_merge_kernel(const float* __restrict__ opart,
+                                                           const float* __restrict__ mpart,
+                                                           const float* __restrict__ lpart, u16* __restrict__ out,
+                                                           int64_t osb, int64_t osh, int Hq, int splits) {
+  constexpr int D = 128, MAXS = 1024;
+  __shared__ float wgt[MAXS];
+  __shared__ float part[4][D];
+  __shared__ float red[16];
+  const int bh = blockIdx.x, b = bh / Hq, h = bh % Hq, bk = bh / G, g = bh % G;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  // global max and denominator over the splits (the whole workgroup, fixed reduction order)
+  float mx = -INFINITY;
+  for (int j = tid; j < splits; j += 512) mx = fmaxf(mx, mpart[((int64_t)bk * splits + j) * G + g]);
+  mx = group_max<64>(mx);
+  if (lane == 0) red[wave] = mx;
+  __syncthreads();
+  float M = red[0];
+#pragma unroll
+  for (int w = 1; w < 8; ++w) M = fmaxf(M, red[w]);
+  float den = 0.f;
+  for (int j = tid; j < splits; j += 512) {
+    const int64_t pj = ((int64_t)bk * splits + j) * G + g;
+    const float mj = mpart[pj];
+    const float w = mj == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(mj - M);  // split with no live key
+    wgt[j] = w;
+    den += w * lpart[pj];
   }
-  u16* orow = out + b * osb + h * osh;
-  orow[lane] = from_f32<T>(o0 / den);
-  orow[64 + lane] = from_f32<T>(o1 / den);
+  den = group_sum<64>(den);
+  __syncthreads();  // red[] reads done; wgt[] complete
+  if (lane == 0) red[8 + wave] = den;
+  const int r = tid >> 7, d = tid & 127;
+  float acc = 0.f;
+  for (int j0 = r; j0 < splits; j0 += 4 * 8) {
+    float x[8];
+#pragma unroll
+    for (int u = 0; u < 8; ++u) {
+      const int j = j0 + 4 * u;
+      x[u] = j < splits ? opart[(((int64_t)bk * splits + j) * G + g) * D + d] : 0.f;
+    }
+#pragma unroll
+    for (int u = 0; u < 8; ++u) {
+      const int j = j0 + 4 * u;
+      if (j < splits) acc += wgt[j] * x[u];
+    }
+  }
+  part[r][d] = acc;
+  __syncthreads();
+  if (tid < D) {
+    float tot = red[8];
+#pragma unroll
+    for (int w = 1; w < 8; ++w) tot += red[8 + w];
+    const float y = (part[0][tid] + part[1][tid]) + (part[2][tid] + part[3][tid]);
+    out[b * osb + (int64_t)h * osh + tid] = from_f32<T>(y / tot);
+  }
 }
 
 // ============================================================================ greedy select
@@ -263,34 +427,39 @@ __global__ void advance_kernel(int64_t* counter, int64_t by) { *counter += by; }
 
 bool al16(const void* p) { return ((uintptr_t)p & 15) == 0; }
 
-template <typename T, int M, int R>
-int gemv_launch(const void* x, int64_t ldx, const void* w, void* y, int64_t ldy, int64_t n, int64_t k,
-                hipStream_t s) {
-  gemv_kernel<T, M, R><<<(unsigned)((n + R - 1) / R), kThreads, 0, s>>>((const u16*)x, ldx, (const u16*)w, (u16*)y,
-                                                                         ldy, (int)n, (int)k);
+// Workspace: per (b, kv head, split, head of the group) 128 partial outputs, then the maxima, then
+// the sums.
+int64_t decode_splits(int64_t span) { return (span + kSplit - 1) / kSplit; }
+
+template <typename T, int G>
+int decode_g(dim3 grid, const void* q, int64_t qsb, int64_t qsh, const void* ck, const void* cv, int64_t ksb,
+             int64_t ksh, void* out, int64_t osb, int64_t osh, float* opart, float* mpart, float* lpart, int Hkv,
+             int T_len, const int64_t* len_dev, int capacity, int splits, float scale2, hipStream_t s) {
+  decode_attn_kernel<T, G><<<grid, 256, 0, s>>>((const u16*)q, qsb, qsh, (const u16*)ck, (const u16*)cv, ksb, ksh,
+                                                opart, mpart, lpart, Hkv, T_len, len_dev, capacity, splits, scale2);
+  decode_merge_kernel<T, G><<<grid.y * G, 512, 0, s>>>(opart, mpart, lpart, (u16*)out, osb, osh, Hkv * G, splits);
   return (int)hipGetLastError();
 }
 
-template <typename T, int M>
-int gemv_r(const void* x, int64_t ldx, const void* w, void* y, int64_t ldy, int64_t n, int64_t k, hipStream_t s) {
-  // Enough workgroups to keep every CU streaming: fewer rows per workgroup for narrow outputs.
-  if (n >= 8192) return gemv_launch<T, M, 4>(x, ldx, w, y, ldy, n, k, s);
-  if (n >= 4096) return gemv_launch<T, M, 2>(x, ldx, w, y, ldy, n, k, s);
-  return gemv_launch<T, M, 1>(x, ldx, w, y, ldy, n, k, s);
-}
-
 template <typename T>
-int gemv_m(int m, const void* x, int64_t ldx, const void* w, void* y, int64_t ldy, int64_t n, int64_t k,
-           hipStream_t s) {
-  switch (m) {
-    case 1: return gemv_r<T, 1>(x, ldx, w, y, ldy, n, k, s);
-    case 2: return gemv_r<T, 2>(x, ldx, w, y, ldy, n, k, s);
-    case 3: return gemv_r<T, 3>(x, ldx, w, y, ldy, n, k, s);
-    case 4: return gemv_r<T, 4>(x, ldx, w, y, ldy, n, k, s);
-    case 5: return gemv_r<T, 5>(x, ldx, w, y, ldy, n, k, s);
-    case 6: return gemv_r<T, 6>(x, ldx, w, y, ldy, n, k, s);
-    case 7: return gemv_r<T, 7>(x, ldx, w, y, ldy, n, k, s);
-    default: return gemv_r<T, 8>(x, ldx, w, y, ldy, n, k, s);
+int decode_t(int G, dim3 grid, const void* q, int64_t qsb, int64_t qsh, const void* ck, const void* cv, int64_t ksb,
+             int64_t ksh, void* out, int64_t osb, int64_t osh, float* opart, float* mpart, float* lpart, int Hkv,
+             int T_len, const int64_t* len_dev, int capacity, int splits, float scale2, hipStream_t s) {
+  switch (G) {
+#define Q3_DECODE_G(GG) \
+  case GG:              \
+    return decode_g<T, GG>(grid, q, qsb, qsh, ck, cv, ksb, ksh, out, osb, osh, opart, mpart, lpart, Hkv, T_len, len_dev, \
+                           capacity, splits, scale2, s);
+    Q3_DECODE_G(1)
+    Q3_DECODE_G(2)
+    Q3_DECODE_G(3)
+    Q3_DECODE_G(4)
+    Q3_DECODE_G(5)
+    Q3_DECODE_G(6)
+    Q3_DECODE_G(7)
+    Q3_DECODE_G(8)
+#undef Q3_DECODE_G
+    default: return Q3_ERR_INVALID;
   }
 }
 
@@ -300,10 +469,40 @@ extern "C" {
 
 int q3_gemv(int dtype, const void* x, int64_t ldx, const void* w, void* y, int64_t ldy, int64_t m, int64_t n,
             int64_t k, hipStream_t stream) {
-  Q3_REQUIRE((dtype == Q3_BF16 || dtype == Q3_F16) && x && w && y && m >= 1 && m <= 8 && n > 0 && k > 0);
-  Q3_REQUIRE(k % 8 == 0 && ldx % 8 == 0 && ldx >= k && ldy >= n && al16(x) && al16(w) && n < (1ll << 31));
-  if (dtype == Q3_BF16) return gemv_m<BF16>((int)m, x, ldx, w, y, ldy, n, k, stream);
-  return gemv_m<F16>((int)m, x, ldx, w, y, ldy, n, k, stream);
+  const void* ws[1] = {w};
+  void* ys[1] = {y};
+  const int64_t lds[1] = {ldy}, ns[1] = {n};
+  return q3_decode_linear(dtype, x, ldx, m, k, nullptr, 0.f, 0, 1, ws, ys, lds, ns, nullptr, 0, stream);
+}
+
+int q3_decode_linear(int dtype, const void* x, int64_t ldx, int64_t m, int64_t k, const void* norm_w, float eps,
+                     int mode, int nseg, const void* const* w, void* const* y, const int64_t* ldy, const int64_t* n,
+                     const void* res, int64_t ldres, hipStream_t stream) {
+  Q3_REQUIRE((dtype == Q3_BF16 || dtype == Q3_F16) && x && m >= 1 && m <= 16 && k > 0 && k % 8 == 0 &&
+             k < (1 << 30) && ldx % 8 == 0 && ldx >= k && al16(x) && (!norm_w || al16(norm_w)));
+  Q3_REQUIRE(w && y && ldy && n && nseg >= 1 && nseg <= 3 && (mode == 0 || mode == 1 || mode == 2));
+  Q3_REQUIRE(mode != 1 || (res && ldres >= 0));
+  Q3_REQUIRE(mode != 2 || (nseg == 2 && n[0] == n[1]));
+  DecArgs a{};
+  int64_t tiles = 0;
+  for (int i = 0; i < nseg; ++i) {
+    Q3_REQUIRE(w[i] && y[i] && al16(w[i]) && n[i] > 0 && n[i] < (1ll << 30) && ldy[i] >= n[i]);
+    const int t = (int)((n[i] + 15) / 16);
+    a.seg[i] = DecSeg{(const u16*)w[i], (u16*)y[i], ldy[i], (int)n[i], t};
+    if (mode != 2 || i == 0) tiles += t;
+  }
+  Q3_REQUIRE(tiles < (1ll << 31));
+  a.nseg = nseg;
+  a.x = (const u16*)x;
+  a.ldx = ldx;
+  a.M = (int)m;
+  a.K = (int)k;
+  a.nw = (const u16*)norm_w;
+  a.eps = eps;
+  a.res = (const u16*)res;
+  a.ldres = ldres;
+  if (dtype == Q3_BF16) return dlinear_t<BF16>(a, (int)tiles, mode, norm_w != nullptr, stream);
+  return dlinear_t<F16>(a, (int)tiles, mode, norm_w != nullptr, stream);
 }
 
 int q3_kv_append(int dtype, const void* k, const void* v, void* cache_k, void* cache_v, int64_t B, int64_t S,
@@ -319,9 +518,9 @@ int q3_kv_append(int dtype, const void* k, const void* v, void* cache_k, void* c
   return (int)hipGetLastError();
 }
 
-size_t q3_decode_attention_workspace_bytes(int64_t B, int64_t Hq, int64_t T_len) {
-  const int64_t splits = (T_len + kChunk - 1) / kChunk;
-  return (size_t)(B * Hq * splits) * (128 + 2) * sizeof(float);
+size_t q3_decode_attention_workspace_bytes(int64_t B, int64_t Hq, int64_t Hkv, int64_t T_len) {
+  if (B <= 0 || Hq <= 0 || Hkv <= 0 || T_len <= 0) return 0;
+  return (size_t)(B * Hq * decode_splits(T_len)) * (128 + 2) * sizeof(float);
 }
 
 int q3_decode_attention(int dtype, const void* q, int64_t qsb, int64_t qsh, const void* cache_k, const void* cache_v,
@@ -329,27 +528,22 @@ int q3_decode_attention(int dtype, const void* q, int64_t qsb, int64_t qsh, cons
                         int64_t Hq, int64_t Hkv, int64_t T_len, const int64_t* len_dev, int64_t capacity, int64_t D,
                         float scale, hipStream_t stream) {
   Q3_REQUIRE((dtype == Q3_BF16 || dtype == Q3_F16) && q && cache_k && cache_v && out && workspace && B > 0 &&
-             Hq > 0 && Hkv > 0 && Hq % Hkv == 0 && T_len > 0 && T_len <= capacity && D == 128 && B * Hq < 65536);
+             Hq > 0 && Hkv > 0 && Hq % Hkv == 0 && Hq / Hkv <= 8 && T_len > 0 && T_len <= capacity && D == 128 &&
+             B * Hkv < 65536 && (len_dev ? capacity : T_len) <= 1024 * kSplit);
+  Q3_REQUIRE(al16(q) && al16(cache_k) && al16(cache_v) && qsh % 8 == 0 && qsb % 8 == 0 && ksb % 8 == 0 && ksh % 8 == 0);
   // A device-resident length launches the fixed split count of the whole capacity (graph replay).
-  const int64_t splits = ((len_dev ? capacity : T_len) + kChunk - 1) / kChunk;
+  const int64_t splits = decode_splits(len_dev ? capacity : T_len);
   float* opart = (float*)workspace;
   float* mpart = opart + B * Hq * splits * 128;
   float* lpart = mpart + B * Hq * splits;
-  dim3 grid((unsigned)splits, (unsigned)(B * Hq));
-  if (dtype == Q3_BF16) {
-    decode_attn_partial<BF16><<<grid, 64, 0, stream>>>((const u16*)q, qsb, qsh, (const u16*)cache_k,
-                                                       (const u16*)cache_v, ksb, ksh, opart, mpart, lpart, (int)Hq,
-                                                       (int)Hkv, (int)T_len, len_dev, (int)capacity, (int)splits, scale);
-    decode_attn_merge<BF16><<<(unsigned)(B * Hq), 64, 0, stream>>>(opart, mpart, lpart, (u16*)out, osb, osh, (int)Hq,
-                                                                   (int)splits);
-  } else {
-    decode_attn_partial<F16><<<grid, 64, 0, stream>>>((const u16*)q, qsb, qsh, (const u16*)cache_k,
-                                                      (const u16*)cache_v, ksb, ksh, opart, mpart, lpart, (int)Hq,
-                                                      (int)Hkv, (int)T_len, len_dev, (int)capacity, (int)splits, scale);
-    decode_attn_merge<F16><<<(unsigned)(B * Hq), 64, 0, stream>>>(opart, mpart, lpart, (u16*)out, osb, osh, (int)Hq,
-                                                                  (int)splits);
-  }
-  return (int)hipGetLastError();
+  const dim3 grid((unsigned)splits, (unsigned)(B * Hkv));
+  const int G = (int)(Hq / Hkv);
+  const float scale2 = scale * 1.4426950408889634f;
+  if (dtype == Q3_BF16)
+    return decode_t<BF16>(G, grid, q, qsb, qsh, cache_k, cache_v, ksb, ksh, out, osb, osh, opart, mpart, lpart,
+                          (int)Hkv, (int)T_len, len_dev, (int)capacity, (int)splits, scale2, stream);
+  return decode_t<F16>(G, grid, q, qsb, qsh, cache_k, cache_v, ksb, ksh, out, osb, osh, opart, mpart, lpart, (int)Hkv,
+                       (int)T_len, len_dev, (int)capacity, (int)splits, scale2, stream);
 }
 
 size_t q3_greedy_select_workspace_bytes(int64_t batch) { return (size_t)batch * 64 * (sizeof(float) + sizeof(int)); }

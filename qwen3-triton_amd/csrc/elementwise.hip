@@ -10,8 +10,7 @@ namespace {
 
 constexpr int kBlock = 256;
 
-Q3_DEV float fast_exp(float x) { return __builtin_amdgcn_exp2f(x * 1.4426950408889634f); }
-Q3_DEV float sigmoid(float g) { return __builtin_amdgcn_rcpf(1.f + fast_exp(-g)); }
+Q3_DEV float sigmoid(float g) { return q3_sigmoid(g); }
 
 template <typename T> bool aligned16(const void* p) { return ((uintptr_t)p & 15) == 0; }
 

@@ -31,15 +31,6 @@ template <> Q3_DEV f32x16 mfma_32x32x16<F16>(bf16x8_t a, bf16x8_t b, f32x16 c) {
                                                  0, 0, 0);
 }
 
-template <typename T> Q3_DEV f32x4 mfma_16x16x32(bf16x8_t a, bf16x8_t b, f32x4 c);
-template <> Q3_DEV f32x4 mfma_16x16x32<BF16>(bf16x8_t a, bf16x8_t b, f32x4 c) {
-  return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
-}
-template <> Q3_DEV f32x4 mfma_16x16x32<F16>(bf16x8_t a, bf16x8_t b, f32x4 c) {
-  return __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(f16x8_t, a), __builtin_bit_cast(f16x8_t, b), c,
-                                                 0, 0, 0);
-}
-
 // Maps a linear workgroup id to (tile_m, tile_n): XCD-contiguous ranges, then GROUP-row raster.
 Q3_DEV void tile_coords(int bid, int tiles_m, int tiles_n, int& tm, int& tn) {
   constexpr int GROUP = 8;

@@ -2,6 +2,8 @@
 select, and forward-only norms.  Mirrors ``qwen3_triton/inference/kernels.py`` (names and call
 shapes); every op is a HIP kernel behind libq3hip.so.
 """
+import ctypes
+
 import torch
 
 from .. import _hip as H
@@ -36,7 +38,7 @@ def attention(q, cache_k, cache_v, start, *, split_decode=False, start_dev=None)
     if s == 1 and d == 128 and q.dtype in (torch.bfloat16, torch.float16):
         out = torch.empty_like(q)
         span = cap if start_dev is not None else total
-        ws = H.workspace(H.query("q3_decode_attention_workspace_bytes", b, hq, span), q.device)
+        ws = H.workspace(H.query("q3_decode_attention_workspace_bytes", b, hq, hkv, span), q.device)
         H.call("q3_decode_attention", H.code(q.dtype), q.data_ptr(), q.stride(0), q.stride(2), cache_k.data_ptr(),
                cache_v.data_ptr(), cache_k.stride(0), cache_k.stride(1), out.data_ptr(), out.stride(0),
                out.stride(2), ws.data_ptr(), b, hq, hkv, total, 0 if start_dev is None else start_dev.data_ptr(),
@@ -56,12 +58,48 @@ def linear(x, weight, *, gemv=True, accurate=False, sliced=False, prefill_tiling
     k = shape[-1]
     m = x.numel() // k
     n = weight.shape[0]
-    if gemv and m <= 8 and x.dtype in (torch.bfloat16, torch.float16) and x.is_contiguous() and \
+    if gemv and m <= DECODE_MAX_ROWS and x.dtype in (torch.bfloat16, torch.float16) and x.is_contiguous() and \
             weight.is_contiguous() and k % 8 == 0:
         y = torch.empty((*shape[:-1], n), device=x.device, dtype=x.dtype)
         H.call("q3_gemv", H.code(x.dtype), x.data_ptr(), k, weight.data_ptr(), y.data_ptr(), n, m, n, k, H.stream())
         return y
     return matmul(x.reshape(m, k), weight.t(), optimized=True).view(*shape[:-1], n)
+
+
+DECODE_MAX_ROWS = 16
+
+
+def decode_linear_ok(x, *weights):
+    """Whether the fused decode projection serves these operands (<= 16 token rows, 16-bit,
+    16-byte aligned rows)."""
+    k = x.shape[-1]
+    return x.numel() // k <= DECODE_MAX_ROWS and x.dtype in (torch.bfloat16, torch.float16) and \
+        x.is_contiguous() and k % 8 == 0 and all(w.is_contiguous() and w.dtype == x.dtype for w in weights)
+
+
+def decode_linear(x, weights, *, norm_weight=None, eps=1e-6, mode=0, res=None):
+    """Decode-step projection of the <= 16 token rows of ``x`` [..., K] on the matrix cores, one
+    launch for: an optional RMSNorm of ``x`` (``norm_weight``), up to 3 weights sharing that input
+    (mode 0, returns a list), ``res + x W^T`` (mode 1) or ``silu(x Wg^T) * (x Wu^T)`` (mode 2,
+    ``weights = [Wg, Wu]``).  Replaces the reference's rms_norm + linear(s) + residual_add / swiglu
+    sequence of ``inference/model.py:117-137``."""
+    shape = x.shape
+    k = shape[-1]
+    m = x.numel() // k
+    outs = [torch.empty((*shape[:-1], w.shape[0]), device=x.device, dtype=x.dtype) for w in weights]
+    if mode == 2:
+        outs = outs[:1]
+    nseg = len(weights)
+    arr_p = ctypes.c_void_p * nseg
+    arr_i = ctypes.c_int64 * nseg
+    ws = arr_p(*[w.data_ptr() for w in weights])
+    ys = arr_p(*([o.data_ptr() for o in outs] + [outs[0].data_ptr()] * (nseg - len(outs))))
+    ldy = arr_i(*[w.shape[0] for w in weights])
+    ns = arr_i(*[w.shape[0] for w in weights])
+    H.call("q3_decode_linear", H.code(x.dtype), x.data_ptr(), k, m, k,
+           0 if norm_weight is None else norm_weight.data_ptr(), float(eps), mode, nseg, ws, ys, ldy, ns,
+           0 if res is None else res.data_ptr(), 0 if res is None else res.shape[-1], H.stream())
+    return outs if mode == 0 else outs[0]
 
 
 _EOS_CACHE = {}

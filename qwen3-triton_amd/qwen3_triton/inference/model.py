@@ -162,9 +162,26 @@ class TritonQwen3Inference(nn.Module):
         try:
             x = embedding(input_ids, self.model.embed_tokens.weight)
             cos, sin = self.model.rotary_emb(pos, torch.bfloat16)
+            fused = self.gemv and kernels.decode_linear_ok(x, self.lm_head.weight)
             for i, layer in enumerate(self.model.layers):
                 a = layer.self_attn
                 d = a.head_dim
+                if fused:  # decode step: norms, residual adds and SwiGLU ride in the projections
+                    q, k, v = kernels.decode_linear(x, [a.q_proj.weight, a.k_proj.weight, a.v_proj.weight],
+                                                    norm_weight=layer.input_layernorm.weight,
+                                                    eps=layer.input_layernorm.eps)
+                    q = kernels.norm_rope(q.view(b, s, a.num_heads, d), a.q_norm.weight, cos, sin, a.q_norm.eps)
+                    k = kernels.norm_rope(k.view(b, s, a.num_kv_heads, d), a.k_norm.weight, cos, sin, a.k_norm.eps)
+                    kernels.append(k, v.view(b, s, a.num_kv_heads, d), cache.keys[i], cache.values[i], start, start_dev)
+                    y = kernels.attention(q, cache.keys[i], cache.values[i], start, split_decode=self.split_decode,
+                                          start_dev=start_dev).reshape(b, s, -1)
+                    x = kernels.decode_linear(y, [a.o_proj.weight], mode=1, res=x)
+                    m = layer.mlp
+                    y = kernels.decode_linear(x, [m.gate_proj.weight, m.up_proj.weight], mode=2,
+                                              norm_weight=layer.post_attention_layernorm.weight,
+                                              eps=layer.post_attention_layernorm.eps)
+                    x = kernels.decode_linear(y, [m.down_proj.weight], mode=1, res=x)
+                    continue
                 h = kernels.rms_norm(x, layer.input_layernorm.weight, layer.input_layernorm.eps)
                 q = kernels.linear(h, a.q_proj.weight, gemv=self.gemv).view(b, s, a.num_heads, d)
                 k = kernels.linear(h, a.k_proj.weight, gemv=self.gemv).view(b, s, a.num_kv_heads, d)
@@ -183,10 +200,14 @@ class TritonQwen3Inference(nn.Module):
                 else:
                     y = gate_up_swiglu(h, m.gate_proj.weight, m.up_proj.weight, optimized=True)
                 x = residual_add(x, kernels.linear(y, m.down_proj.weight, gemv=self.gemv))
-            x = kernels.rms_norm(x, self.model.norm.weight, self.model.norm.eps)
             if logits_to_keep:
                 x = x[:, -logits_to_keep:, :].contiguous()
-            logits = kernels.linear(x, self.lm_head.weight, gemv=self.gemv)
+            if fused:
+                logits = kernels.decode_linear(x, [self.lm_head.weight], norm_weight=self.model.norm.weight,
+                                               eps=self.model.norm.eps)[0]
+            else:
+                x = kernels.rms_norm(x, self.model.norm.weight, self.model.norm.eps)
+                logits = kernels.linear(x, self.lm_head.weight, gemv=self.gemv)
             cache.length = start + s
         except BaseException:
             cache.valid = False

@@ -10,7 +10,7 @@ from qwen3_triton.inference import kernels as K
 pytestmark = pytest.mark.gpu
 
 
-@pytest.mark.parametrize("m", [1, 2, 5, 8])
+@pytest.mark.parametrize("m", [1, 2, 5, 8, 16])
 @pytest.mark.parametrize("n,k", [(4096, 4096), (1024, 4096), (4096, 12288), (151936, 4096), (37, 64), (5000, 520)])
 def test_gemv(m, n, k):
     print(f"gemv m={m} n={n} k={k}", flush=True)
@@ -22,6 +22,36 @@ def test_gemv(m, n, k):
     assert max_rel(y, e) <= 8e-3
     y2 = K.linear(x.cuda(), w.cuda())
     assert torch.equal(y, y2)  # deterministic
+
+
+@pytest.mark.parametrize("m", [1, 5, 16])
+@pytest.mark.parametrize("k", [4096, 688, 256, 12288])
+@pytest.mark.parametrize("norm", [False, True])
+def test_decode_linear_modes(m, k, norm):
+    """Fused decode projection against the unfused fp64 math with the same rounding points:
+    xn = bf16(rmsnorm(x)); mode 0 three segments; mode 1 res + bf16(y); mode 2 silu(bf16 g) bf16(u)."""
+    print(f"decode_linear m={m} k={k} norm={norm}", flush=True)
+    gen = seeded(m * 7 + k + int(norm))
+    dt = torch.bfloat16
+    x = randn(m, k, gen=gen, dtype=dt)
+    nw = (1.0 + 0.1 * randn(k, gen=gen)).to(dt)
+    ws = [randn(n, k, gen=gen, dtype=dt, scale=0.02) for n in (1000, 200, 200)]
+    res = randn(m, 1000, gen=gen, dtype=dt)
+    xn = O.rms_norm_reference(x, nw, 1e-6, dtype=torch.float64).to(dt) if norm else x
+    kw = dict(norm_weight=nw.cuda() if norm else None, eps=1e-6)
+    ys = K.decode_linear(x.cuda(), [w.cuda() for w in ws], **kw)
+    for y, w in zip(ys, ws):
+        assert max_rel(y, xn.double() @ w.double().t()) <= 1e-2
+    y1 = K.decode_linear(x.cuda(), [ws[0].cuda()], mode=1, res=res.cuda(), **kw)
+    e1 = res.double() + (xn.double() @ ws[0].double().t()).to(dt).double()
+    assert max_rel(y1, e1) <= 1e-2
+    g, u = ws[1], ws[2]
+    y2 = K.decode_linear(x.cuda(), [g.cuda(), u.cuda()], mode=2, **kw)
+    eg = (xn.double() @ g.double().t()).to(dt)
+    eu = (xn.double() @ u.double().t()).to(dt)
+    e2 = O.swiglu_reference(eg, eu, dtype=torch.float64)
+    assert max_rel(y2, e2) <= 2e-2
+    assert torch.equal(y2, K.decode_linear(x.cuda(), [g.cuda(), u.cuda()], mode=2, **kw))  # deterministic
 
 
 def test_kv_append():
@@ -37,7 +67,8 @@ def test_kv_append():
 
 
 @pytest.mark.parametrize("b,hq,hk,t", [(1, 32, 8, 1), (1, 32, 8, 2048), (8, 32, 8, 1100), (2, 4, 2, 129),
-                                       (1, 32, 8, 2304)])
+                                       (1, 32, 8, 2304), (1, 8, 8, 300), (2, 24, 8, 70), (1, 16, 2, 500),
+                                       (3, 32, 8, 64), (1, 32, 8, 65)])
 def test_decode_attention(b, hq, hk, t):
     gen = seeded(t)
     cap = t + 5
@@ -47,6 +78,23 @@ def test_decode_attention(b, hq, hk, t):
     out = K.attention(q.cuda(), kk.cuda(), vv.cuda(), t - 1)
     e = O.scaled_dot_product_attention_reference(q.transpose(1, 2), kk[:, :, :t], vv[:, :, :t])
     assert max_rel(out.transpose(1, 2), e) <= 2e-2
+
+
+def test_decode_attention_lengths():
+    """Back-to-back calls of several lengths, device length (whole-capacity launch) against host
+    length."""
+    gen = seeded(77)
+    b, hq, hk, cap = 2, 32, 8, 700
+    kk = randn(b, hk, cap, 128, gen=gen, dtype=torch.bfloat16).cuda()
+    vv = randn(b, hk, cap, 128, gen=gen, dtype=torch.bfloat16).cuda()
+    for t in (650, 1, 129, 700):
+        q = randn(b, 1, hq, 128, gen=gen, dtype=torch.bfloat16)
+        e = O.scaled_dot_product_attention_reference(q.transpose(1, 2), kk[:, :, :t].cpu(), vv[:, :, :t].cpu())
+        out = K.attention(q.cuda(), kk, vv, t - 1)
+        assert max_rel(out.transpose(1, 2), e) <= 2e-2
+        dev = torch.tensor([t - 1], dtype=torch.int64, device="cuda")
+        out2 = K.attention(q.cuda(), kk, vv, 0, start_dev=dev)
+        assert max_rel(out2.transpose(1, 2), e) <= 2e-2
 
 
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
