@@ -211,6 +211,19 @@ int q3_decode_attention(int dtype, const void* q, int64_t qsb, int64_t qsh, cons
                         int64_t ksb, int64_t ksh, void* out, int64_t osb, int64_t osh, void* workspace, int64_t B,
                         int64_t Hq, int64_t Hkv, int64_t T_len, const int64_t* len_dev, int64_t capacity, int64_t D,
                         float scale, hipStream_t stream);
+/* Decode step attention with the per-token prologue fused in: q [B,Hq,D] and the new token's k, v
+ * [B,Hkv,D] are raw projections.  Each workgroup applies QK-norm (q_norm_w / k_norm_w, eps) and RoPE
+ * (cos/sin [B,D] rows of the token's position, batch stride csb) to its query heads; the workgroup
+ * whose split holds the token's position writes the normed+roped k and raw v into the caches there and
+ * uses them directly.  Same geometry, workspace and results (bit for bit) as q3_norm_rope_fwd on q and
+ * k, then q3_kv_append, then q3_decode_attention.  Replaces, in one launch pair:
+ * inference/model.py:122-125 (norm_rope q/k, cache append, attention for s == 1). */
+int q3_decode_step_attention(int dtype, const void* q, int64_t qsb, int64_t qsh, const void* k, const void* v,
+                             int64_t kvsb, int64_t kvsh, const void* q_norm_w, const void* k_norm_w, float eps,
+                             const void* cos, const void* sin, int64_t csb, void* cache_k, void* cache_v, int64_t ksb,
+                             int64_t ksh, void* out, int64_t osb, int64_t osh, void* workspace, int64_t B, int64_t Hq,
+                             int64_t Hkv, int64_t T_len, const int64_t* len_dev, int64_t capacity, int64_t D,
+                             float scale, hipStream_t stream);
 /* Greedy step: token[b] = argmax logits[b, :vocab] (lowest index on ties), pad if done[b]; writes
  * ids[b, p] (ids may be NULL; p = pos, plus *pos_dev when pos_dev is non-NULL), next[b],
  * done[b] |= token in eos[0:n_eos].

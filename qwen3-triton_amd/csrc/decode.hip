@@ -1,5 +1,7 @@
 // Single-GPU greedy decode: small-M GEMV, KV-cache append, split-KV decode attention and the
 // greedy argmax/select step.  All four are bound by HBM traffic (weights, cache, logits).
+#include <type_traits>
+
 #include "common.h"
 
 namespace {
@@ -9,11 +11,11 @@ constexpr int kThreads = 256;
 // ============================================================================ decode linear
 // y_s[m, n] = epilogue(sum_k xn[m, k] W_s[n, k]) for M <= 16 token rows (a decode step), on matrix
 // cores: v_mfma_f32_16x16x32 with the token rows as the A operand (rows >= M are zero) and 16 weight
-// rows as the B operand.  The weights stream straight into registers: per 128-wide k block, lane l
-// (row n = l % 16, quarter kq = l / 16) loads the 64 contiguous bytes W[n][kb + 32 kq, +32) and feeds
-// them to the 4 MFMA k-steps of the block (k-step s takes its 8 k at kb + 32 kq + 8 s); the token
-// fragments use the same k order, which the sum does not see.  A workgroup owns 16 output rows and
-// its 4 waves take interleaved k blocks; the partial 16 x 16 tiles fold in LDS in fixed order.
+// rows as the B operand.  The weights stream straight into registers: per 128-wide k block, k-step c
+// takes k in [kb + 32 c, +32) and lane l (row n = l % 16, quarter kq = l / 16) loads its 8 k at
+// kb + 32 c + 8 kq, so each load instruction reads 64 contiguous bytes of 16 rows.  A workgroup owns
+// 16 output rows and its NW waves take interleaved k blocks, P blocks in flight per wave (all loads
+// issued before the block's MFMAs); the partial 16 x 16 tiles fold in LDS in fixed order.
 //   * NORM: xn = x * rsqrt(mean(x^2) + eps) * norm_w (RMSNorm of the input rows, recomputed per
 //     workgroup from the M rows of x, rounded to the storage type like the standalone kernel);
 //   * MODE 0: y = acc;  MODE 1: y = res + T(acc) (residual add);  MODE 2: segments 0 and 1 are the
@@ -39,11 +41,11 @@ struct DecArgs {
   int64_t ldres;
 };
 
-template <typename T, int MODE, bool NORM>
-__global__ __launch_bounds__(256) void dlinear_kernel(DecArgs a) {
+template <typename T, int MODE, bool NORM, int NW, int P>
+__global__ __launch_bounds__(NW * 64) void dlinear_kernel(DecArgs a) {
   constexpr int NB = MODE == 2 ? 2 : 1;  // weight tiles per workgroup (gate + up)
   __shared__ float inv_s[16];
-  __shared__ f32x4 red[4][NB][64];
+  __shared__ f32x4 red[NW][NB][64];
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   int tile = blockIdx.x, s = 0;
   if constexpr (MODE != 2) {
@@ -54,7 +56,7 @@ __global__ __launch_bounds__(256) void dlinear_kernel(DecArgs a) {
   const int r = lane & 15, kq = lane >> 4;  // r: token row (A) and weight row (B) of this lane
 
   if constexpr (NORM) {
-    for (int m = wave; m < M; m += 4) {
+    for (int m = wave; m < M; m += NW) {
       const u16* xr = a.x + m * a.ldx;
       float ss = 0.f;
       for (int c = lane; c < K / 8; c += 64) {
@@ -69,52 +71,64 @@ __global__ __launch_bounds__(256) void dlinear_kernel(DecArgs a) {
   }
   const bool xrow = r < M;
   const float inv = NORM && xrow ? inv_s[r] : 1.f;
-  const u16* xr = a.x + (xrow ? r : 0) * a.ldx + 32 * kq;
+  const u16* xr = a.x + (xrow ? r : 0) * a.ldx + 8 * kq;
   const u16* wr[NB];
 #pragma unroll
   for (int j = 0; j < NB; ++j)
-    wr[j] = a.seg[MODE == 2 ? j : s].w + (int64_t)min(n0 + r, sg.n - 1) * K + 32 * kq;
+    wr[j] = a.seg[MODE == 2 ? j : s].w + (int64_t)min(n0 + r, sg.n - 1) * K + 8 * kq;
 
   f32x4 acc[NB];
 #pragma unroll
   for (int j = 0; j < NB; ++j) acc[j] = f32x4{0.f, 0.f, 0.f, 0.f};
 
-  // One 128-wide k block; `guard` bounds each 16-byte chunk by K (the ragged last block).
-  auto block = [&](int kb, bool guard) {
-    i32x4 wv[NB][4], xv[4], nv[4];
+  // Q blocks of 128 k at kb[0..Q): all loads first, then the MFMAs.  `guard` bounds each 16-byte
+  // chunk by K (the ragged last block).
+  auto blocks = [&](auto qc, const int* kb, bool guard) {
+    constexpr int Q = decltype(qc)::value;
+    i32x4 wv[Q][NB][4], xv[Q][4], nv[Q][4];
 #pragma unroll
-    for (int c = 0; c < 4; ++c) {
-      const int k = kb + 32 * kq + 8 * c;
-      const bool ok = !guard || k < K;
+    for (int p = 0; p < Q; ++p)
 #pragma unroll
-      for (int j = 0; j < NB; ++j) wv[j][c] = ok ? *reinterpret_cast<const i32x4*>(wr[j] + kb + 8 * c) : i32x4{0, 0, 0, 0};
-      xv[c] = ok && xrow ? *reinterpret_cast<const i32x4*>(xr + kb + 8 * c) : i32x4{0, 0, 0, 0};
-      if constexpr (NORM) nv[c] = ok ? *reinterpret_cast<const i32x4*>(a.nw + k) : i32x4{0, 0, 0, 0};
-    }
+      for (int c = 0; c < 4; ++c) {
+        const int k = kb[p] + 32 * c + 8 * kq;
+        const bool ok = !guard || k < K;
 #pragma unroll
-    for (int c = 0; c < 4; ++c) {
-      i32x4 xf = xv[c];
-      if constexpr (NORM) {
-#pragma unroll
-        for (int w = 0; w < 4; ++w) {
-          const uint32_t xx = (uint32_t)xv[c][w], ww = (uint32_t)nv[c][w];
-          const float lo = to_f32<T>((u16)(xx & 0xffffu)) * inv * to_f32<T>((u16)(ww & 0xffffu));
-          const float hi = to_f32<T>((u16)(xx >> 16)) * inv * to_f32<T>((u16)(ww >> 16));
-          xf[w] = (int)pack2<T>(lo, hi);
-        }
+        for (int j = 0; j < NB; ++j)
+          wv[p][j][c] = ok ? *reinterpret_cast<const i32x4*>(wr[j] + kb[p] + 32 * c) : i32x4{0, 0, 0, 0};
+        xv[p][c] = ok && xrow ? *reinterpret_cast<const i32x4*>(xr + kb[p] + 32 * c) : i32x4{0, 0, 0, 0};
+        if constexpr (NORM) nv[p][c] = ok ? *reinterpret_cast<const i32x4*>(a.nw + k) : i32x4{0, 0, 0, 0};
       }
 #pragma unroll
-      for (int j = 0; j < NB; ++j)
-        acc[j] = mfma_16x16x32<T>(__builtin_bit_cast(bf16x8_t, xf), __builtin_bit_cast(bf16x8_t, wv[j][c]), acc[j]);
-    }
+    for (int p = 0; p < Q; ++p)
+#pragma unroll
+      for (int c = 0; c < 4; ++c) {
+        i32x4 xf = xv[p][c];
+        if constexpr (NORM) {
+#pragma unroll
+          for (int w = 0; w < 4; ++w) {
+            const uint32_t xx = (uint32_t)xv[p][c][w], ww = (uint32_t)nv[p][c][w];
+            const float lo = to_f32<T>((u16)(xx & 0xffffu)) * inv * to_f32<T>((u16)(ww & 0xffffu));
+            const float hi = to_f32<T>((u16)(xx >> 16)) * inv * to_f32<T>((u16)(ww >> 16));
+            xf[w] = (int)pack2<T>(lo, hi);
+          }
+        }
+#pragma unroll
+        for (int j = 0; j < NB; ++j)
+          acc[j] = mfma_16x16x32<T>(__builtin_bit_cast(bf16x8_t, xf), __builtin_bit_cast(bf16x8_t, wv[p][j][c]), acc[j]);
+      }
   };
   const int nfull = K / 128, nblk = (K + 127) / 128;
   int b = wave;
-  for (; b + 4 < nfull; b += 8) {  // two blocks per step: more loads in flight
-    block(b * 128, false);
-    block((b + 4) * 128, false);
+  for (; b + (P - 1) * NW < nfull; b += P * NW) {  // P blocks in flight per wave
+    int kb[P];
+#pragma unroll
+    for (int p = 0; p < P; ++p) kb[p] = (b + p * NW) * 128;
+    blocks(std::integral_constant<int, P>{}, kb, false);
   }
-  for (; b < nblk; b += 4) block(b * 128, b >= nfull);
+  for (; b < nblk; b += NW) {
+    const int kb[1] = {b * 128};
+    blocks(std::integral_constant<int, 1>{}, kb, b >= nfull);
+  }
 
 #pragma unroll
   for (int j = 0; j < NB; ++j) red[wave][j][lane] = acc[j];
@@ -123,7 +137,9 @@ __global__ __launch_bounds__(256) void dlinear_kernel(DecArgs a) {
   float v[NB][4];
 #pragma unroll
   for (int j = 0; j < NB; ++j) {
-    const f32x4 t = ((red[0][j][lane] + red[1][j][lane]) + red[2][j][lane]) + red[3][j][lane];
+    f32x4 t = red[0][j][lane];
+#pragma unroll
+    for (int w = 1; w < NW; ++w) t += red[w][j][lane];
 #pragma unroll
     for (int e = 0; e < 4; ++e) v[j][e] = t[e];
   }
@@ -144,9 +160,11 @@ __global__ __launch_bounds__(256) void dlinear_kernel(DecArgs a) {
   }
 }
 
+// 4 waves x 2 k blocks in flight per wave: the best of {4, 8, 16} waves x {2, 4} blocks measured on
+// MI355X over the Qwen3-8B decode projections.
 template <typename T, int MODE, bool NORM>
 int dlinear_launch(const DecArgs& a, int tiles, hipStream_t s) {
-  dlinear_kernel<T, MODE, NORM><<<(unsigned)tiles, 256, 0, s>>>(a);
+  dlinear_kernel<T, MODE, NORM, 4, 2><<<(unsigned)tiles, 4 * 64, 0, s>>>(a);
   return (int)hipGetLastError();
 }
 
@@ -192,40 +210,111 @@ __global__ __launch_bounds__(kThreads) void kv_append_kernel(const u16* __restri
 // 4 waves fold through LDS.  A second kernel merges the splits in fixed order (deterministic).
 constexpr int kSplit = 64;
 
-template <typename T, int G>
-__global__ __launch_bounds__(256) void decode_attn_kernel(const u16* __restrict__ q, int64_t qsb, int64_t qsh,
-                                                          const u16* __restrict__ ck, const u16* __restrict__ cv,
-                                                          int64_t ksb, int64_t ksh, float* __restrict__ opart,
-                                                          float* __restrict__ mpart, float* __restrict__ lpart,
-                                                          int Hkv, int T_len, const int64_t* len_dev, int capacity,
-                                                          int splits, float scale2) {
+struct DecAttnArgs {
+  const u16* q;  // [B, Hq, D] at strides (qsb, qsh)
+  int64_t qsb, qsh;
+  u16* ck;
+  u16* cv;  // caches [.., capacity, D] at strides (ksb, ksh)
+  int64_t ksb, ksh;
+  float* opart;
+  float* mpart;
+  float* lpart;
+  int Hkv, T_len, capacity, splits;
+  const int64_t* len_dev;
+  float scale2;
+  // FUSED: q and the new token's k, v are raw projections; QK-norm + RoPE and the cache append
+  // happen here.
+  const u16* k;
+  const u16* v;  // [B, Hkv, D] at strides (kvsb, kvsh)
+  int64_t kvsb, kvsh;
+  const u16* qw;
+  const u16* kw;
+  float eps;
+  const u16* cs;
+  const u16* sn;  // [B, D] rotary tables of the token's position, batch stride csb
+  int64_t csb;
+};
+
+// RMSNorm over the 128 dims held by a 16-lane row (8 per lane) times the norm weight, then the
+// rotate-half RoPE with the partner dims 64 away (lane t ^ 8: DPP row_ror:8), rounded to the storage
+// type exactly like the standalone QK-norm + RoPE kernel.
+template <typename T>
+Q3_DEV void norm_rope8(float (&x)[8], const u16* w, const u16* cs, const u16* sn, int t, float eps) {
+  float ss = 0.f;
+#pragma unroll
+  for (int e = 0; e < 8; ++e) ss += x[e] * x[e];
+  const float inv = rsqrtf(group_sum<16>(ss) * (1.f / 128.f) + eps);
+  const Vec<T> wv = load_vec<T>(w + t * 8), cv = load_vec<T>(cs + t * 8), sv = load_vec<T>(sn + t * 8);
+  const float sign = t < 8 ? -1.f : 1.f;
+#pragma unroll
+  for (int e = 0; e < 8; ++e) {
+    const float n = x[e] * inv * wv.v[e];
+    const float np = __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, n), 0x128, 0xF, 0xF,
+                                                                        true));
+    x[e] = to_f32<T>(from_f32<T>(n * cv.v[e] + sign * np * sv.v[e]));
+  }
+}
+
+template <typename T, int G, bool FUSED>
+__global__ __launch_bounds__(256) void decode_attn_kernel(DecAttnArgs a) {
   constexpr int D = 128, KPW = kSplit / 4;  // keys per wave
   __shared__ float sc[G][kSplit];
   __shared__ float red_o[4][G][D];
-  const int split = blockIdx.x, bk = blockIdx.y, b = bk / Hkv, hk = bk % Hkv;
+  const int split = blockIdx.x, bk = blockIdx.y, b = bk / a.Hkv, hk = bk % a.Hkv;
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, t = lane & 15, kg = lane >> 4;
   // len_dev holds the cache length before this token: the token itself is at that position.
-  if (len_dev) T_len = min((int)*len_dev + 1, capacity);
+  const int pos = a.len_dev ? (int)*a.len_dev : a.T_len - 1;
+  const int T_len = a.len_dev ? min(pos + 1, a.capacity) : a.T_len;
   const int k0 = split * kSplit, kw = k0 + wave * KPW;
+  const bool own = FUSED && pos >= k0 && pos < k0 + kSplit && pos < a.capacity;  // this split holds the token
 
-  const u16* kb = ck + b * ksb + hk * ksh;
-  const u16* vb = cv + b * ksb + hk * ksh;
+  u16* kb = a.ck + b * a.ksb + hk * a.ksh;
+  u16* vb = a.cv + b * a.ksb + hk * a.ksh;
   i32x4 kr[KPW / 4];
   uint32_t vr[KPW];
 #pragma unroll
   for (int it = 0; it < KPW / 4; ++it) {
     const int key = kw + it * 4 + kg;
-    kr[it] = key < T_len ? *reinterpret_cast<const i32x4*>(kb + (int64_t)key * D + t * 8) : i32x4{0, 0, 0, 0};
+    kr[it] = key < T_len && !(own && key == pos) ? *reinterpret_cast<const i32x4*>(kb + (int64_t)key * D + t * 8)
+                                                 : i32x4{0, 0, 0, 0};
   }
 #pragma unroll
   for (int k = 0; k < KPW; ++k)
-    vr[k] = kw + k < T_len ? *reinterpret_cast<const uint32_t*>(vb + (int64_t)(kw + k) * D + 2 * lane) : 0u;
+    vr[k] = kw + k < T_len && !(own && kw + k == pos)
+                ? *reinterpret_cast<const uint32_t*>(vb + (int64_t)(kw + k) * D + 2 * lane)
+                : 0u;
+  if constexpr (FUSED) {
+    if (own) {  // the new token: k = rope(norm(k_raw)), v raw; into the cache and into this step
+      const u16* cs = a.cs + b * a.csb;
+      const u16* sn = a.sn + b * a.csb;
+      const Vec<T> kv = load_vec<T>(a.k + b * a.kvsb + hk * a.kvsh + t * 8);
+      float kn[8];
+#pragma unroll
+      for (int e = 0; e < 8; ++e) kn[e] = kv.v[e];
+      norm_rope8<T>(kn, a.kw, cs, sn, t, a.eps);
+      i32x4 kp;
+#pragma unroll
+      for (int w = 0; w < 4; ++w) kp[w] = (int)pack2<T>(kn[2 * w], kn[2 * w + 1]);
+#pragma unroll
+      for (int it = 0; it < KPW / 4; ++it)
+        if (kw + it * 4 + kg == pos) kr[it] = kp;
+      const uint32_t vp = *reinterpret_cast<const uint32_t*>(a.v + b * a.kvsb + hk * a.kvsh + 2 * lane);
+#pragma unroll
+      for (int k = 0; k < KPW; ++k)
+        if (kw + k == pos) vr[k] = vp;
+      if (wave == 0 && kg == 0) *reinterpret_cast<i32x4*>(kb + (int64_t)pos * D + t * 8) = kp;
+      if (wave == 0) *reinterpret_cast<uint32_t*>(vb + (int64_t)pos * D + 2 * lane) = vp;
+    }
+  }
   float qf[G][8];
 #pragma unroll
   for (int g = 0; g < G; ++g) {
-    const Vec<T> qv = load_vec<T>(q + b * qsb + (int64_t)(hk * G + g) * qsh + t * 8);
+    const Vec<T> qv = load_vec<T>(a.q + b * a.qsb + (int64_t)(hk * G + g) * a.qsh + t * 8);
 #pragma unroll
-    for (int e = 0; e < 8; ++e) qf[g][e] = qv.v[e] * scale2;  // scores in log2 units
+    for (int e = 0; e < 8; ++e) qf[g][e] = qv.v[e];
+    if constexpr (FUSED) norm_rope8<T>(qf[g], a.qw, a.cs + b * a.csb, a.sn + b * a.csb, t, a.eps);
+#pragma unroll
+    for (int e = 0; e < 8; ++e) qf[g][e] *= a.scale2;  // scores in log2 units
   }
 #pragma unroll
   for (int it = 0; it < KPW / 4; ++it) {
@@ -280,16 +369,16 @@ __global__ __launch_bounds__(256) void decode_attn_kernel(const u16* __restrict_
     red_o[wave][g][2 * lane + 1] = o[g][1];
   }
   __syncthreads();
-  const int64_t pbase = ((int64_t)bk * splits + split) * G;
+  const int64_t pbase = ((int64_t)bk * a.splits + split) * G;
   for (int i = tid; i < G * D; i += 256) {
     const int g = i / D, d = i % D;
-    opart[(pbase + g) * D + d] = red_o[0][g][d] + red_o[1][g][d] + red_o[2][g][d] + red_o[3][g][d];
+    a.opart[(pbase + g) * D + d] = red_o[0][g][d] + red_o[1][g][d] + red_o[2][g][d] + red_o[3][g][d];
   }
   if (tid == 0) {  // m and l are wave-uniform
 #pragma unroll
     for (int g = 0; g < G; ++g) {
-      mpart[pbase + g] = m[g];
-      lpart[pbase + g] = l[g];
+      a.mpart[pbase + g] = m[g];
+      a.lpart[pbase + g] = l[g];
     }
   }
 }
@@ -431,36 +520,58 @@ bool al16(const void* p) { return ((uintptr_t)p & 15) == 0; }
 // the sums.
 int64_t decode_splits(int64_t span) { return (span + kSplit - 1) / kSplit; }
 
-template <typename T, int G>
-int decode_g(dim3 grid, const void* q, int64_t qsb, int64_t qsh, const void* ck, const void* cv, int64_t ksb,
-             int64_t ksh, void* out, int64_t osb, int64_t osh, float* opart, float* mpart, float* lpart, int Hkv,
-             int T_len, const int64_t* len_dev, int capacity, int splits, float scale2, hipStream_t s) {
-  decode_attn_kernel<T, G><<<grid, 256, 0, s>>>((const u16*)q, qsb, qsh, (const u16*)ck, (const u16*)cv, ksb, ksh,
-                                                opart, mpart, lpart, Hkv, T_len, len_dev, capacity, splits, scale2);
-  decode_merge_kernel<T, G><<<grid.y * G, 512, 0, s>>>(opart, mpart, lpart, (u16*)out, osb, osh, Hkv * G, splits);
+template <typename T, int G, bool FUSED>
+int decode_g(const DecAttnArgs& a, dim3 grid, void* out, int64_t osb, int64_t osh, hipStream_t s) {
+  decode_attn_kernel<T, G, FUSED><<<grid, 256, 0, s>>>(a);
+  decode_merge_kernel<T, G><<<grid.y * G, 512, 0, s>>>(a.opart, a.mpart, a.lpart, (u16*)out, osb, osh, a.Hkv * G,
+                                                       a.splits);
   return (int)hipGetLastError();
 }
 
-template <typename T>
-int decode_t(int G, dim3 grid, const void* q, int64_t qsb, int64_t qsh, const void* ck, const void* cv, int64_t ksb,
-             int64_t ksh, void* out, int64_t osb, int64_t osh, float* opart, float* mpart, float* lpart, int Hkv,
-             int T_len, const int64_t* len_dev, int capacity, int splits, float scale2, hipStream_t s) {
+template <typename T, bool FUSED>
+int decode_t(int G, const DecAttnArgs& a, dim3 grid, void* out, int64_t osb, int64_t osh, hipStream_t s) {
   switch (G) {
-#define Q3_DECODE_G(GG) \
-  case GG:              \
-    return decode_g<T, GG>(grid, q, qsb, qsh, ck, cv, ksb, ksh, out, osb, osh, opart, mpart, lpart, Hkv, T_len, len_dev, \
-                           capacity, splits, scale2, s);
-    Q3_DECODE_G(1)
-    Q3_DECODE_G(2)
-    Q3_DECODE_G(3)
-    Q3_DECODE_G(4)
-    Q3_DECODE_G(5)
-    Q3_DECODE_G(6)
-    Q3_DECODE_G(7)
-    Q3_DECODE_G(8)
-#undef Q3_DECODE_G
+    case 1: return decode_g<T, 1, FUSED>(a, grid, out, osb, osh, s);
+    case 2: return decode_g<T, 2, FUSED>(a, grid, out, osb, osh, s);
+    case 3: return decode_g<T, 3, FUSED>(a, grid, out, osb, osh, s);
+    case 4: return decode_g<T, 4, FUSED>(a, grid, out, osb, osh, s);
+    case 5: return decode_g<T, 5, FUSED>(a, grid, out, osb, osh, s);
+    case 6: return decode_g<T, 6, FUSED>(a, grid, out, osb, osh, s);
+    case 7: return decode_g<T, 7, FUSED>(a, grid, out, osb, osh, s);
+    case 8: return decode_g<T, 8, FUSED>(a, grid, out, osb, osh, s);
     default: return Q3_ERR_INVALID;
   }
+}
+
+// Shared validation and workspace carving of both decode attention entry points.
+int decode_attn_setup(DecAttnArgs& a, dim3& grid, int dtype, const void* q, int64_t qsb, int64_t qsh,
+                      const void* cache_k, const void* cache_v, int64_t ksb, int64_t ksh, const void* out,
+                      void* workspace, int64_t B, int64_t Hq, int64_t Hkv, int64_t T_len, const int64_t* len_dev,
+                      int64_t capacity, int64_t D, float scale) {
+  Q3_REQUIRE((dtype == Q3_BF16 || dtype == Q3_F16) && q && cache_k && cache_v && out && workspace && B > 0 &&
+             Hq > 0 && Hkv > 0 && Hq % Hkv == 0 && Hq / Hkv <= 8 && T_len > 0 && T_len <= capacity && D == 128 &&
+             B * Hkv < 65536 && (len_dev ? capacity : T_len) <= 1024 * kSplit);
+  Q3_REQUIRE(al16(q) && al16(cache_k) && al16(cache_v) && qsh % 8 == 0 && qsb % 8 == 0 && ksb % 8 == 0 && ksh % 8 == 0);
+  // A device-resident length launches the fixed split count of the whole capacity (graph replay).
+  const int64_t splits = decode_splits(len_dev ? capacity : T_len);
+  a.q = (const u16*)q;
+  a.qsb = qsb;
+  a.qsh = qsh;
+  a.ck = (u16*)cache_k;
+  a.cv = (u16*)cache_v;
+  a.ksb = ksb;
+  a.ksh = ksh;
+  a.opart = (float*)workspace;
+  a.mpart = a.opart + B * Hq * splits * 128;
+  a.lpart = a.mpart + B * Hq * splits;
+  a.Hkv = (int)Hkv;
+  a.T_len = (int)T_len;
+  a.capacity = (int)capacity;
+  a.splits = (int)splits;
+  a.len_dev = len_dev;
+  a.scale2 = scale * 1.4426950408889634f;
+  grid = dim3((unsigned)splits, (unsigned)(B * Hkv));
+  return 0;
 }
 
 }  // namespace
@@ -527,23 +638,42 @@ int q3_decode_attention(int dtype, const void* q, int64_t qsb, int64_t qsh, cons
                         int64_t ksb, int64_t ksh, void* out, int64_t osb, int64_t osh, void* workspace, int64_t B,
                         int64_t Hq, int64_t Hkv, int64_t T_len, const int64_t* len_dev, int64_t capacity, int64_t D,
                         float scale, hipStream_t stream) {
-  Q3_REQUIRE((dtype == Q3_BF16 || dtype == Q3_F16) && q && cache_k && cache_v && out && workspace && B > 0 &&
-             Hq > 0 && Hkv > 0 && Hq % Hkv == 0 && Hq / Hkv <= 8 && T_len > 0 && T_len <= capacity && D == 128 &&
-             B * Hkv < 65536 && (len_dev ? capacity : T_len) <= 1024 * kSplit);
-  Q3_REQUIRE(al16(q) && al16(cache_k) && al16(cache_v) && qsh % 8 == 0 && qsb % 8 == 0 && ksb % 8 == 0 && ksh % 8 == 0);
-  // A device-resident length launches the fixed split count of the whole capacity (graph replay).
-  const int64_t splits = decode_splits(len_dev ? capacity : T_len);
-  float* opart = (float*)workspace;
-  float* mpart = opart + B * Hq * splits * 128;
-  float* lpart = mpart + B * Hq * splits;
-  const dim3 grid((unsigned)splits, (unsigned)(B * Hkv));
+  DecAttnArgs a{};
+  dim3 grid;
+  const int rc = decode_attn_setup(a, grid, dtype, q, qsb, qsh, cache_k, cache_v, ksb, ksh, out, workspace, B, Hq, Hkv,
+                                   T_len, len_dev, capacity, D, scale);
+  if (rc) return rc;
   const int G = (int)(Hq / Hkv);
-  const float scale2 = scale * 1.4426950408889634f;
-  if (dtype == Q3_BF16)
-    return decode_t<BF16>(G, grid, q, qsb, qsh, cache_k, cache_v, ksb, ksh, out, osb, osh, opart, mpart, lpart,
-                          (int)Hkv, (int)T_len, len_dev, (int)capacity, (int)splits, scale2, stream);
-  return decode_t<F16>(G, grid, q, qsb, qsh, cache_k, cache_v, ksb, ksh, out, osb, osh, opart, mpart, lpart, (int)Hkv,
-                       (int)T_len, len_dev, (int)capacity, (int)splits, scale2, stream);
+  if (dtype == Q3_BF16) return decode_t<BF16, false>(G, a, grid, out, osb, osh, stream);
+  return decode_t<F16, false>(G, a, grid, out, osb, osh, stream);
+}
+
+int q3_decode_step_attention(int dtype, const void* q, int64_t qsb, int64_t qsh, const void* k, const void* v,
+                             int64_t kvsb, int64_t kvsh, const void* q_norm_w, const void* k_norm_w, float eps,
+                             const void* cos, const void* sin, int64_t csb, void* cache_k, void* cache_v, int64_t ksb,
+                             int64_t ksh, void* out, int64_t osb, int64_t osh, void* workspace, int64_t B, int64_t Hq,
+                             int64_t Hkv, int64_t T_len, const int64_t* len_dev, int64_t capacity, int64_t D,
+                             float scale, hipStream_t stream) {
+  DecAttnArgs a{};
+  dim3 grid;
+  const int rc = decode_attn_setup(a, grid, dtype, q, qsb, qsh, cache_k, cache_v, ksb, ksh, out, workspace, B, Hq, Hkv,
+                                   T_len, len_dev, capacity, D, scale);
+  if (rc) return rc;
+  Q3_REQUIRE(k && v && q_norm_w && k_norm_w && cos && sin && al16(k) && al16(v) && al16(q_norm_w) &&
+             al16(k_norm_w) && al16(cos) && al16(sin) && kvsb % 8 == 0 && kvsh % 8 == 0 && csb % 8 == 0);
+  a.k = (const u16*)k;
+  a.v = (const u16*)v;
+  a.kvsb = kvsb;
+  a.kvsh = kvsh;
+  a.qw = (const u16*)q_norm_w;
+  a.kw = (const u16*)k_norm_w;
+  a.eps = eps;
+  a.cs = (const u16*)cos;
+  a.sn = (const u16*)sin;
+  a.csb = csb;
+  const int G = (int)(Hq / Hkv);
+  if (dtype == Q3_BF16) return decode_t<BF16, true>(G, a, grid, out, osb, osh, stream);
+  return decode_t<F16, true>(G, a, grid, out, osb, osh, stream);
 }
 
 size_t q3_greedy_select_workspace_bytes(int64_t batch) { return (size_t)batch * 64 * (sizeof(float) + sizeof(int)); }

@@ -50,6 +50,26 @@ def attention(q, cache_k, cache_v, start, *, split_decode=False, start_dev=None)
     return o.transpose(1, 2)
 
 
+def decode_step_attention(q, k, v, q_norm_w, k_norm_w, eps, cos, sin, cache_k, cache_v, start, start_dev=None):
+    """One decode step's attention from the raw projections q [B,1,Hq,D], k, v [B,1,Hkv,D]: QK-norm,
+    RoPE (cos/sin [B,1,D] at the token's position), cache append and split-KV attention in one
+    kernel pair (``inference/model.py:122-125``).  Returns [B,1,Hq,D]."""
+    b, s, hq, d = q.shape
+    hkv, cap = cache_k.shape[1], cache_k.shape[2]
+    if s != 1 or d != 128:
+        raise ValueError("decode_step_attention takes one token with head_dim 128")
+    out = torch.empty_like(q)
+    total = start + 1
+    span = cap if start_dev is not None else total
+    ws = H.workspace(H.query("q3_decode_attention_workspace_bytes", b, hq, hkv, span), q.device)
+    H.call("q3_decode_step_attention", H.code(q.dtype), q.data_ptr(), q.stride(0), q.stride(2), k.data_ptr(),
+           v.data_ptr(), k.stride(0), k.stride(2), q_norm_w.data_ptr(), k_norm_w.data_ptr(), float(eps),
+           cos.data_ptr(), sin.data_ptr(), cos.stride(0), cache_k.data_ptr(), cache_v.data_ptr(), cache_k.stride(0),
+           cache_k.stride(1), out.data_ptr(), out.stride(0), out.stride(2), ws.data_ptr(), b, hq, hkv, total,
+           0 if start_dev is None else start_dev.data_ptr(), cap, d, d ** -0.5, H.stream())
+    return out
+
+
 def linear(x, weight, *, gemv=True, accurate=False, sliced=False, prefill_tiling=False, reference_accumulation=False):
     """``inference/kernels.py:129``: Y = X W^T; M <= 8 rows stream the weights through the GEMV
     kernel, larger M use the matrix-core GEMM.  The SM86 accumulation-order switches are accepted

@@ -170,11 +170,19 @@ class TritonQwen3Inference(nn.Module):
                     q, k, v = kernels.decode_linear(x, [a.q_proj.weight, a.k_proj.weight, a.v_proj.weight],
                                                     norm_weight=layer.input_layernorm.weight,
                                                     eps=layer.input_layernorm.eps)
-                    q = kernels.norm_rope(q.view(b, s, a.num_heads, d), a.q_norm.weight, cos, sin, a.q_norm.eps)
-                    k = kernels.norm_rope(k.view(b, s, a.num_kv_heads, d), a.k_norm.weight, cos, sin, a.k_norm.eps)
-                    kernels.append(k, v.view(b, s, a.num_kv_heads, d), cache.keys[i], cache.values[i], start, start_dev)
-                    y = kernels.attention(q, cache.keys[i], cache.values[i], start, split_decode=self.split_decode,
-                                          start_dev=start_dev).reshape(b, s, -1)
+                    q = q.view(b, s, a.num_heads, d)
+                    k = k.view(b, s, a.num_kv_heads, d)
+                    v = v.view(b, s, a.num_kv_heads, d)
+                    if s == 1 and d == 128 and a.q_norm.eps == a.k_norm.eps:
+                        y = kernels.decode_step_attention(q, k, v, a.q_norm.weight, a.k_norm.weight, a.q_norm.eps,
+                                                          cos, sin, cache.keys[i], cache.values[i], start,
+                                                          start_dev).reshape(b, s, -1)
+                    else:
+                        q = kernels.norm_rope(q, a.q_norm.weight, cos, sin, a.q_norm.eps)
+                        k = kernels.norm_rope(k, a.k_norm.weight, cos, sin, a.k_norm.eps)
+                        kernels.append(k, v, cache.keys[i], cache.values[i], start, start_dev)
+                        y = kernels.attention(q, cache.keys[i], cache.values[i], start,
+                                              split_decode=self.split_decode, start_dev=start_dev).reshape(b, s, -1)
                     x = kernels.decode_linear(y, [a.o_proj.weight], mode=1, res=x)
                     m = layer.mlp
                     y = kernels.decode_linear(x, [m.gate_proj.weight, m.up_proj.weight], mode=2,

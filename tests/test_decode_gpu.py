@@ -97,6 +97,37 @@ def test_decode_attention_lengths():
         assert max_rel(out2.transpose(1, 2), e) <= 2e-2
 
 
+@pytest.mark.parametrize("b,hq,hk,t,dev", [(1, 32, 8, 2048, False), (1, 32, 8, 2048, True), (8, 32, 8, 1100, True),
+                                           (2, 4, 2, 64, False), (2, 16, 2, 65, True), (1, 8, 8, 1, False)])
+def test_decode_step_attention_matches_unfused(b, hq, hk, t, dev):
+    """QK-norm + RoPE + cache append + attention in one kernel pair: bit-identical output and caches
+    to norm_rope, append and decode attention run separately."""
+    print(f"decode_step_attention b={b} hq={hq} hk={hk} t={t} dev={dev}", flush=True)
+    gen = seeded(t + hq)
+    cap = t + 7
+    dt = torch.bfloat16
+    q = randn(b, 1, hq, 128, gen=gen, dtype=dt).cuda()
+    k = randn(b, 1, hk, 128, gen=gen, dtype=dt).cuda()
+    v = randn(b, 1, hk, 128, gen=gen, dtype=dt).cuda()
+    qw = (1 + 0.1 * randn(128, gen=gen)).to(dt).cuda()
+    kw = (1 + 0.1 * randn(128, gen=gen)).to(dt).cuda()
+    ck0 = randn(b, hk, cap, 128, gen=gen, dtype=dt).cuda()
+    cv0 = randn(b, hk, cap, 128, gen=gen, dtype=dt).cuda()
+    from qwen3_triton.kernels import _ops
+    inv = O.rope_inv_freq(1e6, 128)
+    cos, sin = _ops.rope_tables(torch.full((b, 1), t - 1, dtype=torch.int64, device="cuda"), inv.cuda(), dt)
+    start_dev = torch.tensor([t - 1], dtype=torch.int64, device="cuda") if dev else None
+    ck1, cv1 = ck0.clone(), cv0.clone()
+    qn = K.norm_rope(q, qw, cos, sin, 1e-6)
+    kn = K.norm_rope(k, kw, cos, sin, 1e-6)
+    K.append(kn, v, ck1, cv1, t - 1)
+    e = K.attention(qn, ck1, cv1, t - 1)
+    ck2, cv2 = ck0.clone(), cv0.clone()
+    y = K.decode_step_attention(q, k, v, qw, kw, 1e-6, cos, sin, ck2, cv2, 0 if dev else t - 1, start_dev)
+    assert torch.equal(ck2, ck1) and torch.equal(cv2, cv1)
+    assert torch.equal(y, e)
+
+
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
 def test_greedy_select_ties_pad_eos(dtype):
     v = 151936
