@@ -28,6 +28,12 @@ for p in (ROOT, os.path.join(ROOT, "qwen3-triton_amd")):
 
 PEAK_BF16_TFLOPS = 2500.0   # MI355X dense bf16 matrix-core peak
 PEAK_HBM_GBS = 8000.0       # MI355X HBM3E
+# HBM bytes per GEMM launch of the layer step, from two rocprofv3 counter passes over
+# `bench.py --pmc-probe` (FETCH_SIZE x 2.000 and WRITE_SIZE x 1.000: the factors that make a 1 GiB
+# device copy read 1 GiB), averaged over the step's 21 GEMM launches.  Re-measure with those two
+# passes (rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE -- python bench.py --pmc-probe) when the GEMM
+# kernels change.
+GEMM_TRAFFIC_BYTES_PER_LAUNCH = 685.9e6 + 101.1e6
 
 
 def qwen3_8b_config(layers):
@@ -231,7 +237,20 @@ def main():
     ap.add_argument("--no-layer", action="store_true", help="skip the decoder-layer step (profiling decode)")
     ap.add_argument("--decode-tokens", type=int, default=256)
     ap.add_argument("--decode-batches", default="1,8", help="comma list of decode batches among 1 and 8")
+    ap.add_argument("--pmc-probe", action="store_true",
+                    help="run one warm-up + one decoder-layer step and a 1 GiB device copy, then exit (the "
+                         "workload of the FETCH_SIZE / WRITE_SIZE counter passes behind roofline.traffic)")
     args = ap.parse_args()
+    if args.pmc_probe:
+        import torch
+        decoder_layer_bench(1, 1)
+        src = torch.empty(1 << 29, device="cuda", dtype=torch.bfloat16).fill_(1.0)   # 1 GiB
+        dst = torch.empty_like(src)
+        for _ in range(2):
+            dst.copy_(src)   # calibration: reads and writes exactly 1 GiB
+        torch.cuda.synchronize()
+        log("pmc probe done")
+        return
     if args.gpus != 1:
         print("bench.py measures one MI355X: this build has no multi-GPU path (collectives are out of scope); "
               "run with --gpus 1", file=sys.stderr)
@@ -266,9 +285,9 @@ def main():
         "data": "synthetic (random N(0,0.02) weights, N(0,1) hidden states and upstream gradients)",
         "config": {"workload": "qwen3-8b decoder layer fwd+bwd (config #4 layer)", "model": "Qwen3-8B layer",
                    "global_batch": 4, "seq_len": 2048, "tokens_per_step": layer["tokens"], "parallelism": "none"},
-        "roofline": {"bound": "mfma", "kernel": "gemm_nt_kernel (bf16 MFMA GEMM)",
+        "roofline": {"bound": "mfma", "kernel": "gemm_nt_v4_kernel (bf16 MFMA GEMM)",
                      "achieved": round(layer["gemm_tflops"], 1), "peak": PEAK_BF16_TFLOPS, "unit": "TFLOP/s",
-                     "frac": round(layer["gemm_tflops"] / PEAK_BF16_TFLOPS, 4), "traffic": None,
+                     "frac": round(layer["gemm_tflops"] / PEAK_BF16_TFLOPS, 4), "traffic": GEMM_TRAFFIC_BYTES_PER_LAUNCH,
                      "launches_per_step": layer["gemm_launches"] // args.steps,
                      "flops_per_launch": layer["gemm_flops_per_step"] / max(1, layer["gemm_launches"] // args.steps)},
         "step_roofline": {"algorithmic_tflop_per_step": round(layer["algorithmic_tflops_per_step"], 3),
