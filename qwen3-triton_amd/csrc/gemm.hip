@@ -16,6 +16,8 @@
 //
 // K % 64 != 0: gemm_nt_kernel, a register-staged 256 x 128 x 64 tile with padded LDS rows and
 // v_mfma_f32_32x32x16 (the k tail is zero-filled).
+#include <type_traits>
+
 #include "common.h"
 
 namespace {
@@ -155,28 +157,37 @@ template <int N> Q3_DEV void ring_sync() {
 }
 
 // ---------------------------------------------------------------- v4: register-lean 16x16x32 pipeline
-// 128-byte LDS rows (BK = 64) with swizzle swz(r) = (r & 7) ^ ((r >> 3) & 1): it depends on r mod 16
-// only, and any 16 consecutive rows reading one logical 16-byte chunk hit 16 distinct (bank half,
-// chunk) slots of the 64-bank LDS -- conflict free.  Because every 16x16x32 fragment starts on a
-// multiple of 16 rows, all fragments of a wave share one swizzle: a fragment address is one
-// per-k-step base register plus an immediate offset, which leaves room for a fenced double buffer
-// of fragments (reads of k-step ks+1 in flight during the MFMAs of ks, the first reads of tile
-// kt+1 during the last MFMAs of tile kt) at two waves per SIMD.
-Q3_DEV int swz16(int r) { return (r & 7) ^ ((r >> 3) & 1); }
+// 128-byte LDS rows (BK = 64) with the 16-byte chunk swizzle swz(r) = r & 7.  A 16x16x32 fragment
+// read has lanes 16q..16q+15 on 16 consecutive rows at one logical chunk; measured on MI355X this
+// swizzle reads such fragments conflict free (~139 TB/s of LDS reads per chip in a read-only loop),
+// while (r & 7) ^ ((r >> 3) & 1) or (r ^ (r >> 3)) & 7 conflict two ways (~76 TB/s).  Because every
+// fragment starts on a multiple of 8 rows, all fragments of a wave share one swizzle: a fragment
+// address is one per-k-step base register plus an immediate offset, which leaves room for a fenced
+// double buffer of fragments (reads of k-step ks+1 in flight during the MFMAs of ks, the first
+// reads of tile kt+1 during the last MFMAs of tile kt) at two waves per SIMD.
+Q3_DEV int swz8(int r) { return r & 7; }
+// 64-byte rows (BK = 32, 4 chunks): (r >> 1) & 3 is the conflict-free choice for the same read
+// pattern (~133 TB/s; r & 3, (r >> 2) & 3 and the XOR mixes of them ~75 TB/s).
+Q3_DEV int swz4(int r) { return (r >> 1) & 3; }
+template <int CPR> Q3_DEV int gemm_swz(int r) {
+  if constexpr (CPR == 8) return swz8(r);
+  else return swz4(r);
+}
 
-template <typename T, typename O, int BM, int BN, int WM, int WN, int STAGES, bool EVEN>
+template <typename T, typename O, int BM, int BN, int WM, int WN, int BK, int STAGES, bool EVEN>
 __global__ __launch_bounds__(WM * WN * 64) void gemm_nt_v4_kernel(const u16* __restrict__ A,
                                                                   const u16* __restrict__ B,
                                                                   typename O::storage* __restrict__ C, int M, int N,
                                                                   int K, int64_t lda, int64_t ldb, int64_t ldc,
                                                                   float alpha, int accumulate, int vec_store) {
-  constexpr int BK = 64, NW = WM * WN, ROWB = BK * 2, CPR = 8, RPL = 8;
+  static_assert(BK == 64 || BK == 32, "k tile");
+  constexpr int NW = WM * WN, ROWB = BK * 2, CPR = BK / 8, RPL = 64 / CPR;
   constexpr int TMW = BM / WM, TNW = BN / WN, FM = TMW / 16, FN = TNW / 16;
   constexpr int RG = (BM + BN) / RPL;
   static_assert(RG % NW == 0 && (BM / RPL) % NW == 0, "row groups must split evenly over the waves");
   constexpr int LPW = RG / NW, A_LOADS = (BM / RPL) / NW;
   constexpr int STAGE = (BM + BN) * BK;  // elements
-  constexpr int KS = BK / 32;            // 2 k-steps per tile
+  constexpr int KS = BK / 32;            // k-steps of 32 per tile
   __shared__ __attribute__((aligned(1024))) u16 lds[STAGES * STAGE];
 
   int tm, tn;
@@ -186,24 +197,18 @@ __global__ __launch_bounds__(WM * WN * 64) void gemm_nt_v4_kernel(const u16* __r
   const int wm = wave / WN, wn = wave % WN;
   const int wave_u = __builtin_amdgcn_readfirstlane(wave);
 
-  // ---- global -> LDS: row R of the [A; B] stage, logical chunk c lands at physical c ^ swz16(R).
-  // Row groups of 8 rows; the swizzle repeats every 2 groups, so one lane offset per group parity.
-  uint32_t offa[2], offb[2];
+  // ---- global -> LDS: row R of the [A; B] stage, logical chunk c lands at physical c ^ swz8(R).
+  // Row groups of 8 rows, so the swizzle (hence the lane offset) is the same for every group.
+  const int csrc = (lane % CPR) ^ gemm_swz<CPR>(lane / CPR);  // logical chunk this lane fetches (row = lane / CPR)
+  const uint32_t offa = (uint32_t)(((lane / CPR) * lda + csrc * 8) * 2);
+  const uint32_t offb = (uint32_t)(((lane / CPR) * ldb + csrc * 8) * 2);
   const u16* src[EVEN ? 1 : LPW];
-#pragma unroll
-  for (int par = 0; par < 2; ++par) {
-    const int R = par * RPL + lane / CPR;
-    const int c = (lane % CPR) ^ swz16(R);
-    offa[par] = (uint32_t)(((lane / CPR) * lda + c * 8) * 2);
-    offb[par] = (uint32_t)(((lane / CPR) * ldb + c * 8) * 2);
-  }
   if constexpr (!EVEN) {
 #pragma unroll
     for (int i = 0; i < LPW; ++i) {
       const int R = (wave + NW * i) * RPL + lane / CPR;
-      const int c = (lane % CPR) ^ swz16(R);
-      if (R < BM) src[i] = A + (int64_t)min(m0 + R, M - 1) * lda + c * 8;
-      else src[i] = B + (int64_t)min(n0 + R - BM, N - 1) * ldb + c * 8;
+      if (R < BM) src[i] = A + (int64_t)min(m0 + R, M - 1) * lda + csrc * 8;
+      else src[i] = B + (int64_t)min(n0 + R - BM, N - 1) * ldb + csrc * 8;
     }
   }
   auto issue = [&](int stage, int k0) {
@@ -213,9 +218,9 @@ __global__ __launch_bounds__(WM * WN * 64) void gemm_nt_v4_kernel(const u16* __r
       const void* g;
       if constexpr (EVEN) {
         if (i < A_LOADS)
-          g = reinterpret_cast<const char*>(A + (int64_t)(m0 + rg * RPL) * lda + k0) + offa[rg & 1];
+          g = reinterpret_cast<const char*>(A + (int64_t)(m0 + rg * RPL) * lda + k0) + offa;
         else
-          g = reinterpret_cast<const char*>(B + (int64_t)(n0 + rg * RPL - BM) * ldb + k0) + offb[rg & 1];
+          g = reinterpret_cast<const char*>(B + (int64_t)(n0 + rg * RPL - BM) * ldb + k0) + offb;
       } else {
         g = src[i] + k0;
       }
@@ -225,7 +230,7 @@ __global__ __launch_bounds__(WM * WN * 64) void gemm_nt_v4_kernel(const u16* __r
   };
 
   // ---- LDS -> fragments.  Lane l reads row (fragment base + l % 16), logical chunk ks*4 + l/16.
-  const int quarter = lane >> 4, sw = swz16(lane & 15);
+  const int quarter = lane >> 4, sw = gemm_swz<CPR>(lane & 15);
   uint32_t va[KS], vb[KS];
 #pragma unroll
   for (int ks = 0; ks < KS; ++ks) {
@@ -257,33 +262,47 @@ __global__ __launch_bounds__(WM * WN * 64) void gemm_nt_v4_kernel(const u16* __r
   else ring_sync<0>();
   if (STAGES - 1 < nk) issue(STAGES - 1, (STAGES - 1) * BK);
   load(0, 0, 0);
-  for (int kt = 0; kt < nk; ++kt) {
+  // One tile: each k-step first reads the next step's fragments into the other buffer (the next
+  // tile's first step after the barrier that makes that tile resident and frees this tile's stage
+  // for the ring refill), then runs its MFMAs.  CUR is the buffer holding step 0's fragments: with
+  // an odd number of steps per tile it alternates, so tiles go in pairs to keep it a constant.
+  auto tile = [&](int kt, auto cur_c) {
+    constexpr int CUR = decltype(cur_c)::value;
     const int stage = kt % STAGES;
-    // k-step 0: fragments of step 1 in flight during its MFMAs.  Step 0's fragments were read
-    // during the previous tile's last MFMAs; waiting for them here (already landed) keeps the
-    // outstanding-read count within what the LDS counter tracks, so the MFMAs below need no wait.
-    __builtin_amdgcn_sched_barrier(0);
-    __builtin_amdgcn_s_waitcnt((15) | (7 << 4) | (0 << 8) | (3 << 14));  // lgkmcnt(0)
-    load(stage, 1, 1);
-    __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-    for (int i = 0; i < FM; ++i)
+    for (int ks = 0; ks < KS; ++ks) {
+      const int b = (CUR + ks) & 1;
+      __builtin_amdgcn_sched_barrier(0);
+      if (ks + 1 < KS) {
+        // Step ks's fragments landed long ago: waiting for them keeps the outstanding-read count
+        // within what the LDS counter tracks, so the MFMAs below need no wait.
+        __builtin_amdgcn_s_waitcnt((15) | (7 << 4) | (0 << 8) | (3 << 14));  // lgkmcnt(0)
+        load(stage, b ^ 1, ks + 1);
+      } else {
+        // Tile kt+1 resident; every wave done with tile kt.  Runs on the last tile too (re-reading a
+        // resident stage) so the LDS counter state is the same on every path into the MFMAs.
+        if (kt + STAGES - 1 < nk) ring_sync<(STAGES - 2) * LPW>();
+        else ring_sync<0>();
+        if (kt + STAGES < nk) issue(stage, (kt + STAGES) * BK);
+        load((kt + 1) % STAGES, b ^ 1, 0);
+      }
+      __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-      for (int j = 0; j < FN; ++j) acc[i][j] = mfma_16x16x32<T>(bfr[0][j], af[0][i], acc[i][j]);
-    __builtin_amdgcn_sched_barrier(0);
-    // k-step 1: make tile kt+1 resident, refill the ring, read its first fragments.  The barrier
-    // and the fragment reads run on the last tile too (re-reading a resident stage), so the LDS
-    // counter state is the same on every path into the MFMAs below.
-    if (kt + STAGES - 1 < nk) ring_sync<(STAGES - 2) * LPW>();
-    else ring_sync<0>();
-    if (kt + STAGES < nk) issue(stage, (kt + STAGES) * BK);
-    load((kt + 1) % STAGES, 0, 0);
-    __builtin_amdgcn_sched_barrier(0);
+      for (int i = 0; i < FM; ++i)
 #pragma unroll
-    for (int i = 0; i < FM; ++i)
-#pragma unroll
-      for (int j = 0; j < FN; ++j) acc[i][j] = mfma_16x16x32<T>(bfr[1][j], af[1][i], acc[i][j]);
-    __builtin_amdgcn_sched_barrier(0);
+        for (int j = 0; j < FN; ++j) acc[i][j] = mfma_16x16x32<T>(bfr[b][j], af[b][i], acc[i][j]);
+      __builtin_amdgcn_sched_barrier(0);
+    }
+  };
+  if constexpr (KS % 2 == 0) {
+    for (int kt = 0; kt < nk; ++kt) tile(kt, std::integral_constant<int, 0>{});
+  } else {
+    int kt = 0;
+    for (; kt + 1 < nk; kt += 2) {
+      tile(kt, std::integral_constant<int, 0>{});
+      tile(kt + 1, std::integral_constant<int, 1>{});
+    }
+    if (kt < nk) tile(kt, std::integral_constant<int, 0>{});
   }
 
   // ---- epilogue: lane owns row m and 4 consecutive columns of each 16x16 block (C^T layout)
@@ -332,12 +351,12 @@ __global__ __launch_bounds__(WM * WN * 64) void gemm_nt_v4_kernel(const u16* __r
   }
 }
 
-template <typename T, typename O, int BM, int BN, int WM, int WN, int ST, bool EVEN>
+template <typename T, typename O, int BM, int BN, int WM, int WN, int ST, bool EVEN, int BK = 64>
 int launch_v4(const void* A, int64_t lda, const void* B, int64_t ldb, void* C, int64_t ldc, int64_t M, int64_t N,
               int64_t K, float alpha, int acc, hipStream_t s) {
   const int64_t tiles = ((M + BM - 1) / BM) * ((N + BN - 1) / BN);
   const int vec = (ldc % 4 == 0) && (((uintptr_t)C & (O::vec == 4 ? 15 : 7)) == 0);
-  gemm_nt_v4_kernel<T, O, BM, BN, WM, WN, ST, EVEN><<<(unsigned)tiles, WM * WN * 64, 0, s>>>(
+  gemm_nt_v4_kernel<T, O, BM, BN, WM, WN, BK, ST, EVEN><<<(unsigned)tiles, WM * WN * 64, 0, s>>>(
       (const u16*)A, (const u16*)B, (typename O::storage*)C, (int)M, (int)N, (int)K, lda, ldb, ldc, alpha, acc, vec);
   return (int)hipGetLastError();
 }
@@ -456,6 +475,11 @@ extern "C" int q3_gemm_nt_variant(int variant, const void* A, int64_t lda, const
     case 2: return launch_v4<BF16, BF16, 256, 256, 4, 2, 2, false>(A, lda, B, ldb, C, ldc, M, N, K, 1.f, 0, s);
     case 3: return launch_v4<BF16, BF16, 256, 128, 2, 2, 3, true>(A, lda, B, ldb, C, ldc, M, N, K, 1.f, 0, s);
     case 4: return launch_v4<BF16, BF16, 128, 128, 2, 2, 4, true>(A, lda, B, ldb, C, ldc, M, N, K, 1.f, 0, s);
+    case 5: return launch_v4<BF16, BF16, 256, 256, 4, 2, 4, true, 32>(A, lda, B, ldb, C, ldc, M, N, K, 1.f, 0, s);
+    case 6: return launch_v4<BF16, BF16, 256, 256, 4, 2, 5, true, 32>(A, lda, B, ldb, C, ldc, M, N, K, 1.f, 0, s);
+    case 7: return launch_v4<BF16, BF16, 256, 256, 2, 4, 4, true, 32>(A, lda, B, ldb, C, ldc, M, N, K, 1.f, 0, s);
+    case 8: return launch_v4<BF16, BF16, 256, 128, 2, 2, 6, true, 32>(A, lda, B, ldb, C, ldc, M, N, K, 1.f, 0, s);
+    case 9: return launch_v4<BF16, BF16, 128, 128, 2, 2, 8, true, 32>(A, lda, B, ldb, C, ldc, M, N, K, 1.f, 0, s);
     default: return Q3_ERR_INVALID;
   }
 }
