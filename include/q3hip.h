@@ -129,9 +129,11 @@ int q3_gemm_strided(int in_dtype, int out_dtype, const void* A, int64_t sam, int
  * layouts are taken in place).  Lk >= Lq; query i attends keys j <= i + (Lk - Lq); query head h
  * uses KV head h/(Hq/Hkv).  LSE and delta are [B,Hq,Lq] fp32 (natural-log LSE; delta =
  * rowsum(O*dO) is backward scratch).  On the matrix-core path (q3_attention_mfma_supported) the
- * caller also passes sequence-contiguous copies [B,H,D,ld] (ld >= L, ld % 8 == 0, zero pad) made by
+ * caller also passes sequence-major copies [B,H,D,ld] (ld >= L, ld % 16 == 0, zero pad) made by
  * q3_attention_seq_major: vt of V (forward), qt of Q, kt of K and dot of dO (backward), and every
- * row must be 16-byte aligned.  Other dtypes/head sizes run a SIMT path that ignores them.
+ * row must be 16-byte aligned.  Within every 16-position block of such a row the positions are
+ * stored in the order 0-3, 8-11, 4-7, 12-15 (the operand order of the matrix-core kernels).
+ * Other dtypes/head sizes run a SIMT path that ignores them.
  * Replaces: kernels/attention.py:20-50 + attention_kernels.py:9-253 (_attention_forward_kernel,
  *           _attention_delta_kernel, _attention_dq_kernel, _attention_dkdv_fused_kernel,
  *           _attention_kv_head_reduce_kernel), kernels/attention_precision.py:14-182,

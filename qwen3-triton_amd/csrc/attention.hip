@@ -44,16 +44,6 @@ Q3_DEV i32x4 ld16(const u16* p) { return *reinterpret_cast<const i32x4*>(p); }
 Q3_DEV void st16(u16* p, i32x4 v) { *reinterpret_cast<i32x4*>(p) = v; }
 Q3_DEV bf16x8_t as_frag(i32x4 v) { return __builtin_bit_cast(bf16x8_t, v); }
 
-// A-operand fragment whose 8 k-slots are the keys {c16 + 4g .. +3} and {c16 + 8 + 4g .. +3} of a
-// sequence-contiguous row (g = lane / 32): the permutation produced by the accumulator layout.
-Q3_DEV bf16x8_t perm_frag(const u16* row, int c16, int g) {
-  typedef __attribute__((__vector_size__(2 * sizeof(int)))) int i32x2;
-  const i32x2 lo = *reinterpret_cast<const i32x2*>(row + c16 + 4 * g);
-  const i32x2 hi = *reinterpret_cast<const i32x2*>(row + c16 + 8 + 4 * g);
-  i32x4 v = {lo[0], lo[1], hi[0], hi[1]};
-  return as_frag(v);
-}
-
 // Pack 8 accumulator values (v0..v0+7 of one 32x32 tile) into a B-operand fragment.
 template <typename T> Q3_DEV bf16x8_t pack8(const f32x16& a, int v0) {
   i32x4 r;
@@ -80,7 +70,7 @@ struct Lay {
 template <int CPR> Q3_DEV int chunk_swz(int r) {
   if constexpr (CPR == 16) return r & 15;
   else if constexpr (CPR == 8) return (r ^ (r >> 3)) & 7;
-  else return ((r >> 1) ^ (r >> 3)) & 3;
+  else return ((r >> 2) ^ (r >> 5)) & 3;
 }
 
 template <typename T, int D>
@@ -215,12 +205,9 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2, 2))
 #pragma unroll
       for (int dt = 0; dt < DT; ++dt) {
         const int r = dt * 32 + (lane & 31);
-        const int sw = chunk_swz<CPV>(r);
         const char* row = vbase + r * BN * 2;
-        typedef __attribute__((__vector_size__(2 * sizeof(int)))) int i32x2;
-        const i32x2 lo = *reinterpret_cast<const i32x2*>(row + (((2 * c) ^ sw) << 4) + 8 * g);
-        const i32x2 hi = *reinterpret_cast<const i32x2*>(row + (((2 * c + 1) ^ sw) << 4) + 8 * g);
-        const i32x4 v4 = {lo[0], lo[1], hi[0], hi[1]};
+        // keys {16c + 4g .. +3, 16c + 8 + 4g .. +3}: one 16-byte chunk of the permuted V^T row
+        const i32x4 v4 = *reinterpret_cast<const i32x4*>(row + (((2 * c + g) ^ chunk_swz<CPV>(r)) << 4));
         oacc[dt] = mma<T>(as_frag(v4), pb, oacc[dt]);
       }
     }
@@ -386,12 +373,8 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2, 2))
 #pragma unroll
         for (int dt = 0; dt < DT; ++dt) {
           const int r = dt * 32 + (lane & 31);
-          const int sw = chunk_swz<CPV>(r);
           const char* row = tb + r * BN * 2;
-          typedef __attribute__((__vector_size__(2 * sizeof(int)))) int i32x2;
-          const i32x2 lo = *reinterpret_cast<const i32x2*>(row + (((2 * c) ^ sw) << 4) + 8 * g);
-          const i32x2 hi = *reinterpret_cast<const i32x2*>(row + (((2 * c + 1) ^ sw) << 4) + 8 * g);
-          const i32x4 v4 = {lo[0], lo[1], hi[0], hi[1]};
+          const i32x4 v4 = *reinterpret_cast<const i32x4*>(row + (((2 * c + g) ^ chunk_swz<CPV>(r)) << 4));
           dq[dt] = mma<T>(as_frag(v4), db, dq[dt]);
         }
       }
@@ -524,12 +507,8 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(OCC, O
 #pragma unroll
       for (int dt = 0; dt < DT; ++dt) {
         const int r = dt * 32 + (lane & 31);
-        const int sw = chunk_swz<CPQ>(r);
-        typedef __attribute__((__vector_size__(2 * sizeof(int)))) int i32x2;
-        const int olo = r * BM * 2 + (((2 * c) ^ sw) << 4) + 8 * g, ohi = r * BM * 2 + (((2 * c + 1) ^ sw) << 4) + 8 * g;
-        const i32x2 a0 = *reinterpret_cast<const i32x2*>(dtb + olo), a1 = *reinterpret_cast<const i32x2*>(dtb + ohi);
-        const i32x2 b0 = *reinterpret_cast<const i32x2*>(qtb + olo), b1 = *reinterpret_cast<const i32x2*>(qtb + ohi);
-        const i32x4 va = {a0[0], a0[1], a1[0], a1[1]}, vb4 = {b0[0], b0[1], b1[0], b1[1]};
+        const int o = r * BM * 2 + (((2 * c + g) ^ chunk_swz<CPQ>(r)) << 4);
+        const i32x4 va = *reinterpret_cast<const i32x4*>(dtb + o), vb4 = *reinterpret_cast<const i32x4*>(qtb + o);
         dv[dt] = mma<T>(as_frag(va), pb, dv[dt]);
         dk[dt] = mma<T>(as_frag(vb4), dsb, dk[dt]);
       }
@@ -698,8 +677,13 @@ __global__ __launch_bounds__(kThreads) void attn_bwd_dkdv_simt(const typename T:
 }
 
 // ============================================================================ sequence-major copy
-// y[(b*H + h)*D + d][s] = x[b*sb + h*sh + s*ss + d] for s < L, 0 for L <= s < ldy: the
-// sequence-contiguous operand copies of the matrix-core path.  64 x 64 (position x d) LDS tiles.
+// y[(b*H + h)*D + d][p] = x[b*sb + h*sh + perm16(p)*ss + d] (0 where perm16(p) >= L): the
+// sequence-contiguous operand copies of the matrix-core path, with the 4-position groups 1 and 2
+// of every 16-position block swapped.  A lane's operand slice of such a row -- positions
+// {16c + 4g .. +3} and {16c + 8 + 4g .. +3}, the order in which the 32x32 accumulator layout hands
+// over P and dS -- is then one contiguous 16-byte chunk (8 + 8 bytes would read at half rate).
+// 64 x 64 (position x d) LDS tiles.
+Q3_DEV int perm16(int p) { return p ^ ((((p >> 2) ^ (p >> 3)) & 1) * 12); }
 __global__ __launch_bounds__(kThreads) void seq_major_kernel(const u16* __restrict__ x, Lay xl, u16* __restrict__ y,
                                                              int64_t ldy, int H, int L, int D) {
   __shared__ u16 tile[64][66];
@@ -715,7 +699,7 @@ __global__ __launch_bounds__(kThreads) void seq_major_kernel(const u16* __restri
   u16* yb = y + (int64_t)bh * D * ldy;
   for (int c = ty; c < 64; c += 4) {
     const int d = d0 + c, s = s0 + tx;
-    if (d < D && s < ldy) yb[(int64_t)d * ldy + s] = tile[tx][c];
+    if (d < D && s < ldy) yb[(int64_t)d * ldy + s] = tile[perm16(tx)][c];
   }
 }
 
@@ -802,7 +786,7 @@ int q3_attention_mfma_supported(int dtype, int64_t d) {
 int q3_attention_seq_major(int dtype, const void* x, int64_t sb, int64_t sh, int64_t ss, void* y, int64_t ldy,
                            int64_t B, int64_t H, int64_t L, int64_t D, hipStream_t stream) {
   Q3_REQUIRE((dtype == Q3_BF16 || dtype == Q3_F16) && x && y && B > 0 && H > 0 && L > 0 && D > 0 && ldy >= L &&
-             B * H < 65536 && (D + 63) / 64 < 65536);
+             ldy % 16 == 0 && B * H < 65536 && (D + 63) / 64 < 65536);
   dim3 grid((unsigned)((ldy + 63) / 64), (unsigned)((D + 63) / 64), (unsigned)(B * H));
   seq_major_kernel<<<grid, kThreads, 0, stream>>>((const u16*)x, Lay{sb, sh, ss}, (u16*)y, ldy, (int)H, (int)L,
                                                   (int)D);
@@ -817,7 +801,7 @@ int q3_attention_fwd(int dtype, const void* q, int64_t qsb, int64_t qsh, int64_t
   const Lay ql{qsb, qsh, qss}, kl{ksb, ksh, kss};
   const int b = (int)B, hq = (int)Hq, hkv = (int)Hkv, lq = (int)Lq, lk = (int)Lk;
   if (q3_attention_mfma_supported(dtype, D)) {
-    Q3_REQUIRE(vt && ldvt >= Lk && ldvt % 8 == 0 && lay_ok(q, ql) && lay_ok(k, kl) && lay_ok(o, ql) && al16(vt));
+    Q3_REQUIRE(vt && ldvt >= Lk && ldvt % 16 == 0 && lay_ok(q, ql) && lay_ok(k, kl) && lay_ok(o, ql) && al16(vt));
     const int ld = (int)ldvt;
     if (dtype == Q3_BF16) return Q3_ATTN_D(BF16, fwd_mfma, q, ql, k, kl, vt, o, lse, b, hq, hkv, lq, lk, ld, scale, stream);
     return Q3_ATTN_D(F16, fwd_mfma, q, ql, k, kl, vt, o, lse, b, hq, hkv, lq, lk, ld, scale, stream);
@@ -843,7 +827,7 @@ int q3_attention_bwd(int dtype, const void* q, int64_t qsb, int64_t qsh, int64_t
   else rc = delta_t<F32>(o, dout, ql, delta, B * Hq * Lq, hq, lq, d, stream);
   if (rc) return rc;
   if (q3_attention_mfma_supported(dtype, D)) {
-    Q3_REQUIRE(qt && kt && dot && ldqt >= Lq && ldkt >= Lk && ldqt % 8 == 0 && ldkt % 8 == 0 && lay_ok(q, ql) &&
+    Q3_REQUIRE(qt && kt && dot && ldqt >= Lq && ldkt >= Lk && ldqt % 16 == 0 && ldkt % 16 == 0 && lay_ok(q, ql) &&
                lay_ok(dout, ql) && lay_ok(dq, ql) && lay_ok(k, kl) && lay_ok(v, kl) && lay_ok(dk, kl) &&
                lay_ok(dv, kl) && al16(qt) && al16(kt) && al16(dot));
     const int lq8 = (int)ldqt, lk8 = (int)ldkt;

@@ -161,7 +161,7 @@ def _bhsd_strides(t):
     return t.stride(0), t.stride(1), t.stride(2)
 
 
-def seq_major(x, pad_to=8):
+def seq_major(x, pad_to=16):
     """[B,H,L,D]-indexed view (any b/h/s strides) -> contiguous [B,H,D,Lp], Lp = L rounded up to
     ``pad_to``, zero pad (the sequence-contiguous operand copy of the matrix-core attention)."""
     b, h, l, d = x.shape

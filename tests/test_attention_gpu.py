@@ -137,3 +137,20 @@ def test_attention_strided_layouts_bshd_and_cache():
     ck, cv = cache_k.cuda(), cache_v.cuda()
     oq, _ = _ops.attention_fwd(qh[:, :, 30:].cuda(), ck[:, :, :40], cv[:, :, :40], 128 ** -0.5)
     assert max_rel(oq, O.scaled_dot_product_attention_reference(qh[:, :, 30:], kh, vh)) <= 2e-2
+
+
+@pytest.mark.parametrize("l", [1, 15, 16, 100, 2048])
+def test_seq_major_layout(l):
+    """Sequence-major operand copy: [B,H,L,D] -> [B,H,D,Lp] (Lp = L rounded up to 16, zero pad) with the
+    4-position groups 1 and 2 of every 16-block swapped; bit-exact."""
+    from qwen3_triton.kernels import _ops
+    x = torch.randn(2, 3, l, 128, generator=seeded(l), dtype=torch.float32).to(torch.bfloat16)
+    y = _ops.seq_major(x.cuda()).cpu()
+    lp = -(-l // 16) * 16
+    assert y.shape == (2, 3, 128, lp)
+    ref = torch.zeros(2, 3, 128, lp, dtype=torch.bfloat16)
+    ref[..., :l] = x.transpose(2, 3)
+    p = torch.arange(lp)
+    src = p ^ ((((p >> 2) ^ (p >> 3)) & 1) * 12)
+    assert torch.equal(y, ref[..., src])
+
