@@ -462,11 +462,15 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(OCC, O
       }
       __builtin_amdgcn_global_load_lds(src, (__attribute__((address_space(3))) void*)(lds + dst), 16, 0, 0);
     }
-    if (tid < BM) {
-      const int qq = q0 + tid;
-      float* side = reinterpret_cast<float*>(lds + stage * STAGE + 4 * QB);
-      side[tid] = qq < Lq ? LSE[bh * Lq + qq] * kLog2e : 0.f;
-      side[BM + tid] = qq < Lq ? Delta[bh * Lq + qq] : 0.f;
+    // lse (lanes 0..31) and delta (lanes 32..63) of the tile's queries, straight into LDS like the
+    // operand tiles (a plain load + LDS store would stall wave 0 for a memory round trip per tile);
+    // queries past Lq read a clamped row and are masked where used.
+    static_assert(BM == 32, "side vector layout");
+    if (wave == 0) {
+      const int qq = min(q0 + (lane & 31), Lq - 1);
+      const float* src = (lane < 32 ? LSE : Delta) + bh * Lq + qq;
+      __builtin_amdgcn_global_load_lds(src, (__attribute__((address_space(3))) void*)(lds + stage * STAGE + 4 * QB),
+                                       4, 0, 0);
     }
   };
 
@@ -495,7 +499,7 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(OCC, O
 #pragma unroll
     for (int v = 0; v < 16; ++v) {
       const int r = acc_row(v, lane), qq = q0 + r;
-      float p = __builtin_amdgcn_exp2f(s[v] * scale2 - side[r]);
+      float p = __builtin_amdgcn_exp2f(s[v] * scale2 - side[r] * kLog2e);
       if (!full) p = (qq < Lq && kj <= qq + off) ? p : 0.f;
       s[v] = p;
       ds[v] = p * (dp[v] - side[BM + r]);
