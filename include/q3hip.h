@@ -80,7 +80,21 @@ int q3_swiglu_fwd(int dtype, const void* g, const void* u, void* y, int64_t n, h
 int q3_swiglu_bwd(int dtype, const void* g, const void* u, const void* dy, void* dg, void* du, int64_t n,
                   hipStream_t stream);
 
+/* SwiGLU backward on [rows, cols] blocks at their own row strides (gate and up halves of one
+ * [rows, 2*cols] buffer, as the reference's silu_and_mul input).  Same math as q3_swiglu_bwd.
+ * Replaces: ops/triton/silu_and_mul.py:20-121 (strided [..., 2d] form), kernels/mlp_precision.py:36-48. */
+int q3_swiglu_bwd_2d(int dtype, const void* g, int64_t ldg, const void* u, int64_t ldu, const void* dy, int64_t lddy,
+                     void* dg, int64_t lddg, void* du, int64_t lddu, int64_t rows, int64_t cols, hipStream_t stream);
+
 /* ------------------------------------------------------------------ elementwise / data movement */
+/* y[r * ldy + c] = x[r * ldx + c] for r < rows, c < cols (bit copy between strided blocks).
+ * No counterpart in the reference (it concatenates with torch); used to pack gradients side by side. */
+int q3_copy2d(int dtype, const void* x, int64_t ldx, void* y, int64_t ldy, int64_t rows, int64_t cols,
+              hipStream_t stream);
+/* y[c * ldy + r] = x[r * ldx + c] for r < rows, c < cols; writes nothing else (so it can fill a column
+ * block of a wider matrix).  Replaces: the .t().contiguous() operand copies of kernels/linear.py:45-105. */
+int q3_transpose2d(int dtype, const void* x, int64_t ldx, void* y, int64_t ldy, int64_t rows, int64_t cols,
+                   hipStream_t stream);
 /* c = a + b (fp32 add).  Replaces kernels/residual.py:6-30. */
 int q3_add(int dtype, const void* a, const void* b, void* c, int64_t n, hipStream_t stream);
 /* y = convert(x).  Replaces kernels/attention.py:11-20 (cast_tensor). */

@@ -260,6 +260,100 @@ __global__ __launch_bounds__(kBlock) void transpose16_kernel(const u16* __restri
   }
 }
 
+// ---------------------------------------------------------------- row-strided variants
+// The same element maps on [rows, cols] blocks whose rows sit at their own strides, so gate/up (or
+// q/k/v) results can live side by side in one [rows, 2 cols] buffer.  16-byte vectors when cols and
+// every stride are multiples of 8 elements and the pointers 16-byte aligned, else scalar.
+template <typename T>
+__global__ __launch_bounds__(kBlock) void swiglu_bwd2d_kernel(const typename T::storage* __restrict__ g, int64_t ldg,
+                                                              const typename T::storage* __restrict__ u, int64_t ldu,
+                                                              const typename T::storage* __restrict__ dy,
+                                                              int64_t lddy, typename T::storage* __restrict__ dg,
+                                                              int64_t lddg, typename T::storage* __restrict__ du,
+                                                              int64_t lddu, int64_t rows, int64_t cols, int vec) {
+  const int V = vec ? T::vec : 1;
+  const int64_t per = cols / V, n = rows * per;
+  const int64_t stride = (int64_t)gridDim.x * kBlock;
+  for (int64_t i = (int64_t)blockIdx.x * kBlock + threadIdx.x; i < n; i += stride) {
+    const int64_t r = i / per, c = (i % per) * V;
+    if (vec) {
+      Vec<T> gv = load_vec<T>(g + r * ldg + c), uv = load_vec<T>(u + r * ldu + c), dv = load_vec<T>(dy + r * lddy + c);
+      Vec<T> og, ou;
+#pragma unroll
+      for (int e = 0; e < T::vec; ++e) {
+        const float s = sigmoid(gv.v[e]);
+        og.v[e] = dv.v[e] * uv.v[e] * s * (1.f + gv.v[e] * (1.f - s));
+        ou.v[e] = dv.v[e] * gv.v[e] * s;
+      }
+      store_vec<T>(dg + r * lddg + c, og);
+      store_vec<T>(du + r * lddu + c, ou);
+    } else {
+      const float gg = to_f32<T>(g[r * ldg + c]), uu = to_f32<T>(u[r * ldu + c]), d = to_f32<T>(dy[r * lddy + c]);
+      const float sg = sigmoid(gg);
+      dg[r * lddg + c] = from_f32<T>(d * uu * sg * (1.f + gg * (1.f - sg)));
+      du[r * lddu + c] = from_f32<T>(d * gg * sg);
+    }
+  }
+}
+
+template <typename S>
+__global__ __launch_bounds__(kBlock) void copy2d_kernel(const S* __restrict__ x, int64_t ldx, S* __restrict__ y,
+                                                        int64_t ldy, int64_t rows, int64_t cols, int vec) {
+  constexpr int V = 16 / sizeof(S);
+  const int64_t per = vec ? cols / V : cols, n = rows * per;
+  const int64_t stride = (int64_t)gridDim.x * kBlock;
+  for (int64_t i = (int64_t)blockIdx.x * kBlock + threadIdx.x; i < n; i += stride) {
+    const int64_t r = i / per, c = i % per;
+    if (vec)
+      *reinterpret_cast<i32x4*>(y + r * ldy + c * V) = *reinterpret_cast<const i32x4*>(x + r * ldx + c * V);
+    else
+      y[r * ldy + c] = x[r * ldx + c];
+  }
+}
+
+// y[c * ldy + r] = x[r * ldx + c] for r < rows, c < cols; nothing else is written.  16-bit vector
+// path: the 8x8 register-block kernel above with an input row stride (rows % 8 == 0 so no block
+// reaches past the last row).
+__global__ __launch_bounds__(kBlock) void transpose2d16_kernel(const u16* __restrict__ x, int64_t ldx,
+                                                               u16* __restrict__ y, int64_t ldy, int64_t rows,
+                                                               int64_t cols) {
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int64_t r = (int64_t)blockIdx.y * 64 + 8 * (lane >> 3);
+  const int64_t c = (int64_t)blockIdx.x * 256 + wave * 64 + 8 * (lane & 7);
+  if (c >= cols || r >= rows) return;
+  uint32_t in[8][4];
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    const i32x4 v = *reinterpret_cast<const i32x4*>(x + (r + i) * ldx + c);
+#pragma unroll
+    for (int w = 0; w < 4; ++w) in[i][w] = (uint32_t)v[w];
+  }
+  u16* yb = y + c * ldy + r;
+#pragma unroll
+  for (int j = 0; j < 8; ++j) {
+    const int w = j >> 1, sh = (j & 1) * 16;
+    i32x4 o;
+#pragma unroll
+    for (int k = 0; k < 4; ++k)
+      o[k] = (int)(((in[2 * k][w] >> sh) & 0xffffu) | (((in[2 * k + 1][w] >> sh) & 0xffffu) << 16));
+    *reinterpret_cast<i32x4*>(yb + (int64_t)j * ldy) = o;
+  }
+}
+
+template <typename S>
+__global__ __launch_bounds__(kBlock) void transpose2d_scalar_kernel(const S* __restrict__ x, int64_t ldx,
+                                                                    S* __restrict__ y, int64_t ldy, int64_t rows,
+                                                                    int64_t cols) {
+  __shared__ S tile[64][65];
+  const int64_t r0 = (int64_t)blockIdx.y * 64, c0 = (int64_t)blockIdx.x * 64;
+  const int tx = threadIdx.x & 63, ty = threadIdx.x >> 6;
+  for (int r = ty; r < 64; r += 4)
+    if (r0 + r < rows && c0 + tx < cols) tile[r][tx] = x[(r0 + r) * ldx + c0 + tx];
+  __syncthreads();
+  for (int c = ty; c < 64; c += 4)
+    if (c0 + c < cols && r0 + tx < rows) y[(c0 + c) * ldy + r0 + tx] = tile[tx][c];
+}
+
 // ---------------------------------------------------------------- embedding
 template <typename T>
 __global__ __launch_bounds__(kBlock) void embedding_fwd_kernel(const void* __restrict__ ids, int ids64,
@@ -432,6 +526,57 @@ int q3_swiglu_bwd(int dtype, const void* g, const void* u, const void* dy, void*
                   hipStream_t stream) {
   Q3_REQUIRE(dtype_ok(dtype) && g && u && dy && dg && du && n > 0);
   return Q3_DISPATCH(dtype, swiglu_bwd_t, g, u, dy, dg, du, n, stream);
+}
+
+int q3_swiglu_bwd_2d(int dtype, const void* g, int64_t ldg, const void* u, int64_t ldu, const void* dy, int64_t lddy,
+                     void* dg, int64_t lddg, void* du, int64_t lddu, int64_t rows, int64_t cols, hipStream_t stream) {
+  Q3_REQUIRE(dtype_ok(dtype) && g && u && dy && dg && du && rows > 0 && cols > 0 && ldg >= cols && ldu >= cols &&
+             lddy >= cols && lddg >= cols && lddu >= cols);
+  const int64_t V = dtype == Q3_F32 ? 4 : 8;
+  const bool vec = cols % V == 0 && ldg % V == 0 && ldu % V == 0 && lddy % V == 0 && lddg % V == 0 && lddu % V == 0 &&
+                   aligned16<u16>(g) && aligned16<u16>(u) && aligned16<u16>(dy) && aligned16<u16>(dg) &&
+                   aligned16<u16>(du);
+  const unsigned grid = q3_grid_for(rows * (vec ? cols / V : cols), kBlock);
+#define Q3_SWB2(T, S)                                                                                          \
+  swiglu_bwd2d_kernel<T><<<grid, kBlock, 0, stream>>>((const S*)g, ldg, (const S*)u, ldu, (const S*)dy, lddy, \
+                                                      (S*)dg, lddg, (S*)du, lddu, rows, cols, vec ? 1 : 0)
+  if (dtype == Q3_BF16) Q3_SWB2(BF16, u16);
+  else if (dtype == Q3_F16) Q3_SWB2(F16, u16);
+  else Q3_SWB2(F32, float);
+#undef Q3_SWB2
+  return (int)hipGetLastError();
+}
+
+int q3_copy2d(int dtype, const void* x, int64_t ldx, void* y, int64_t ldy, int64_t rows, int64_t cols,
+              hipStream_t stream) {
+  Q3_REQUIRE(dtype_ok(dtype) && x && y && rows > 0 && cols > 0 && ldx >= cols && ldy >= cols);
+  const int64_t esz = dtype == Q3_F32 ? 4 : 2, V = 16 / esz;
+  const bool vec = cols % V == 0 && ldx % V == 0 && ldy % V == 0 && aligned16<u16>(x) && aligned16<u16>(y);
+  const unsigned grid = q3_grid_for(rows * (vec ? cols / V : cols), kBlock);
+  if (esz == 4)
+    copy2d_kernel<uint32_t><<<grid, kBlock, 0, stream>>>((const uint32_t*)x, ldx, (uint32_t*)y, ldy, rows, cols, vec);
+  else
+    copy2d_kernel<u16><<<grid, kBlock, 0, stream>>>((const u16*)x, ldx, (u16*)y, ldy, rows, cols, vec);
+  return (int)hipGetLastError();
+}
+
+int q3_transpose2d(int dtype, const void* x, int64_t ldx, void* y, int64_t ldy, int64_t rows, int64_t cols,
+                   hipStream_t stream) {
+  Q3_REQUIRE(dtype_ok(dtype) && x && y && rows > 0 && cols > 0 && ldx >= cols && ldy >= rows &&
+             (rows + 63) / 64 < 65536);
+  if (dtype != Q3_F32 && cols % 8 == 0 && rows % 8 == 0 && ldx % 8 == 0 && ldy % 8 == 0 && aligned16<u16>(x) &&
+      aligned16<u16>(y)) {
+    dim3 g16((unsigned)((cols + 255) / 256), (unsigned)((rows + 63) / 64));
+    transpose2d16_kernel<<<g16, kBlock, 0, stream>>>((const u16*)x, ldx, (u16*)y, ldy, rows, cols);
+    return (int)hipGetLastError();
+  }
+  dim3 grid((unsigned)((cols + 63) / 64), (unsigned)((rows + 63) / 64));
+  if (dtype == Q3_F32)
+    transpose2d_scalar_kernel<uint32_t><<<grid, kBlock, 0, stream>>>((const uint32_t*)x, ldx, (uint32_t*)y, ldy, rows,
+                                                                     cols);
+  else
+    transpose2d_scalar_kernel<u16><<<grid, kBlock, 0, stream>>>((const u16*)x, ldx, (u16*)y, ldy, rows, cols);
+  return (int)hipGetLastError();
 }
 
 int q3_add(int dtype, const void* a, const void* b, void* c, int64_t n, hipStream_t stream) {

@@ -37,6 +37,9 @@ SIGNATURES: dict[str, tuple] = {
     "q3_rope_apply": (_i32, [_i32, _p, _p, _p, _p, _i64, _i64, _i64, _i64, _i32, _i32, _p]),
     "q3_swiglu_fwd": (_i32, [_i32, _p, _p, _p, _i64, _p]),
     "q3_swiglu_bwd": (_i32, [_i32, _p, _p, _p, _p, _p, _i64, _p]),
+    "q3_swiglu_bwd_2d": (_i32, [_i32, _p, _i64, _p, _i64, _p, _i64, _p, _i64, _p, _i64, _i64, _i64, _p]),
+    "q3_copy2d": (_i32, [_i32, _p, _i64, _p, _i64, _i64, _i64, _p]),
+    "q3_transpose2d": (_i32, [_i32, _p, _i64, _p, _i64, _i64, _i64, _p]),
     "q3_add": (_i32, [_i32, _p, _p, _p, _i64, _p]),
     "q3_cast": (_i32, [_i32, _i32, _p, _p, _i64, _p]),
     "q3_fill": (_i32, [_i32, _p, _f32, _i64, _p]),

@@ -93,6 +93,42 @@ def swiglu_bwd(g, u, dy):
     return dg, du
 
 
+def _rows_strided(t):
+    return t.ndim == 2 and t.stride(1) == 1
+
+
+def swiglu_bwd_into(g, u, dy, dg, du):
+    """SwiGLU backward on [rows, cols] operands whose rows may sit at their own strides (dg and du can
+    be the two halves of one [rows, 2*cols] buffer)."""
+    for t in (g, u, dy, dg, du):
+        if not _rows_strided(t) or t.shape != g.shape:
+            raise ValueError("matching [rows, cols] row-strided operands required")
+    r, c = g.shape
+    H.call("q3_swiglu_bwd_2d", H.code(g.dtype), g.data_ptr(), g.stride(0), u.data_ptr(), u.stride(0), dy.data_ptr(),
+           dy.stride(0), dg.data_ptr(), dg.stride(0), du.data_ptr(), du.stride(0), r, c, H.stream())
+    return dg, du
+
+
+def copy_into(src, dst):
+    """dst[:, :] = src for [rows, cols] blocks at their own row strides."""
+    if not (_rows_strided(src) and _rows_strided(dst)) or src.shape != dst.shape or src.dtype != dst.dtype:
+        raise ValueError("matching [rows, cols] row-strided operands required")
+    H.call("q3_copy2d", H.code(src.dtype), src.data_ptr(), src.stride(0), dst.data_ptr(), dst.stride(0),
+           src.shape[0], src.shape[1], H.stream())
+    return dst
+
+
+def transpose_into(src, dst):
+    """dst = src^T for src [R, C] and dst [C, R] at their own row strides; dst may be a column block of
+    a wider matrix (nothing outside it is written)."""
+    r, c = src.shape
+    if not (_rows_strided(src) and _rows_strided(dst)) or dst.shape != (c, r) or src.dtype != dst.dtype:
+        raise ValueError("[R, C] source and [C, R] row-strided destination required")
+    H.call("q3_transpose2d", H.code(src.dtype), src.data_ptr(), src.stride(0), dst.data_ptr(), dst.stride(0), r, c,
+           H.stream())
+    return dst
+
+
 def add(a, b, out=None):
     c = torch.empty_like(a) if out is None else out
     H.call("q3_add", H.code(a.dtype), a.data_ptr(), b.data_ptr(), c.data_ptr(), a.numel(), H.stream())

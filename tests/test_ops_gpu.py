@@ -161,6 +161,27 @@ def test_residual_cast_fill_transpose(dtype):
 
 
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
+@pytest.mark.parametrize("r,c", [(64, 256), (8192, 1024), (72, 40), (37, 50)])
+def test_strided_data_movement(r, c, dtype):
+    """q3_transpose2d into a column block of a wider matrix writes nothing else; q3_copy2d and the
+    row-strided SwiGLU backward match their contiguous forms bit for bit."""
+    gen = seeded(r + c)
+    x = torch.randn(r, c, generator=gen).to(dtype).cuda()
+    wide = torch.full((c, 3 * r), 7.0, dtype=dtype, device="cuda")
+    _ops.transpose_into(x, wide[:, r:2 * r])
+    assert torch.equal(wide[:, r:2 * r].cpu(), x.t().cpu())
+    assert bool((wide[:, :r] == 7).all()) and bool((wide[:, 2 * r:] == 7).all())
+    dst = torch.full((r, 2 * c), 5.0, dtype=dtype, device="cuda")
+    _ops.copy_into(x, dst[:, c:])
+    assert torch.equal(dst[:, c:].cpu(), x.cpu()) and bool((dst[:, :c] == 5).all())
+    g, u, dy = (torch.randn(r, c, generator=gen).to(dtype).cuda() for _ in range(3))
+    eg, eu = _ops.swiglu_bwd(g, u, dy)
+    both = torch.empty(r, 2 * c, dtype=dtype, device="cuda")
+    _ops.swiglu_bwd_into(g, u, dy, both[:, :c], both[:, c:])
+    assert torch.equal(both[:, :c].cpu(), eg.cpu()) and torch.equal(both[:, c:].cpu(), eu.cpu())
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
 @pytest.mark.parametrize("batch,r,c,pad", [(1, 8192, 4096, 1), (2, 67, 136, 8), (1, 70, 264, 64), (3, 5, 8, 16),
                                            (1, 2048, 1024, 8), (2, 67, 130, 1)])
 def test_transpose_shapes(batch, r, c, pad, dtype):
