@@ -1,7 +1,8 @@
 """Training components (the reference's "precision" path), ``qwen3_triton/components.py:1-54``.
 
 ``HFOrderNorm`` / ``Attention`` / ``MLP`` / ``DecoderLayer`` / ``Backbone`` keep the reference's
-module structure and option switches: ``norm_rope_fusion`` selects the fused per-head RMSNorm +
+module structure and option switches (the q/k/v projections keep their own parameters and run
+through one shared-input projection op whose backward is a single dX GEMM): ``norm_rope_fusion`` selects the fused per-head RMSNorm +
 RoPE kernel, ``mlp_fusion`` the gate/up + SwiGLU op.  The reference's SM86 rounding-order options
 (``precision_options``) are accepted and select nothing on gfx950.
 """
@@ -10,6 +11,7 @@ import torch
 from ._model import TritonAttention, TritonDecoderLayer, TritonMLP, TritonNorm, TritonQwen3Model
 from .kernels.activation import swiglu
 from .kernels.attention import causal_attention_bshd
+from .kernels.linear import shared_input_projections
 from .kernels.math_precision import norm_rope, rms_norm
 from .kernels.mlp_precision import gate_up_swiglu
 from .kernels.rotary import apply_rotary
@@ -31,9 +33,11 @@ class Attention(TritonAttention):
         b, s, _ = x.shape
         d = self.head_dim
         cos, sin = positions
-        q = self.q_proj(x).view(b, s, self.num_heads, d)
-        k = self.k_proj(x).view(b, s, self.num_kv_heads, d)
-        v = self.v_proj(x).view(b, s, self.num_kv_heads, d)
+        q, k, v = shared_input_projections(x, [self.q_proj.weight, self.k_proj.weight, self.v_proj.weight],
+                                           optimized=self.q_proj.options.linear_optimized)
+        q = q.view(b, s, self.num_heads, d)
+        k = k.view(b, s, self.num_kv_heads, d)
+        v = v.view(b, s, self.num_kv_heads, d)
         if getattr(self.options, 'norm_rope_fusion', False):
             q = norm_rope(q, self.q_norm.weight, cos, sin, self.q_norm.eps)
             k = norm_rope(k, self.k_norm.weight, cos, sin, self.k_norm.eps)

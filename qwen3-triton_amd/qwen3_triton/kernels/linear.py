@@ -98,3 +98,61 @@ class _Linear(torch.autograd.Function):
 def linear(x, weight, *, optimized=False):
     """``kernels/linear.py:104``."""
     return _Linear.apply(x, weight, optimized)
+
+
+class _SharedInputProjections(torch.autograd.Function):
+    """Y_i = X W_i^T for several weights sharing one input (the q/k/v projections).  Forward runs
+    one GEMM per weight; backward packs the output gradients side by side, so dX = [dY_0 | dY_1 | ...]
+    [W_0; W_1; ...] is a single matrix-core GEMM (one rounding, no partial sums added afterwards), X is
+    transposed once, and one GEMM produces every weight gradient as a row block."""
+
+    @staticmethod
+    def forward(ctx, x, *weights):
+        flat = x.view(-1, x.shape[-1])
+        outs = [matmul(flat, w.t()).view(*x.shape[:-1], w.shape[0]) for w in weights]
+        ctx.save_for_backward(flat, *weights)
+        ctx.shape = x.shape
+        return tuple(outs)
+
+    @staticmethod
+    def backward(ctx, *grads):
+        flat, *weights = ctx.saved_tensors
+        m, k = flat.shape
+        ns = [w.shape[0] for w in weights]
+        nt = sum(ns)
+        dev, dt = flat.device, flat.dtype
+        dcat = torch.empty((m, nt), device=dev, dtype=dt)
+        wt = torch.empty((k, nt), device=dev, dtype=dt)
+        col = 0
+        for gr, w, n in zip(grads, weights, ns):
+            blk = dcat[:, col:col + n]
+            if gr is None:
+                blk.zero_()
+            else:
+                _ops.copy_into(gr.contiguous().view(m, n), blk)
+            _ops.transpose_into(w, wt[:, col:col + n])
+            col += n
+        dx = torch.empty((m, k), device=dev, dtype=dt)
+        gemm_nt_into(dcat, nt, wt, nt, dx, m, k, nt)
+        dct = _ops.transpose_into(dcat, torch.empty((nt, m), device=dev, dtype=dt))
+        xt = _ops.transpose_into(flat, torch.empty((k, m), device=dev, dtype=dt))
+        dw = torch.empty((nt, k), device=dev, dtype=dt)
+        gemm_nt_into(dct, m, xt, m, dw, nt, k, m)
+        dws, row = [], 0
+        for n in ns:
+            dws.append(dw[row:row + n])
+            row += n
+        return (dx.view(ctx.shape), *dws)
+
+
+def shared_input_projections(x, weights, *, optimized=False):
+    """[X W_i^T for W_i in weights]; the fused backward needs 16-bit contiguous operands with every
+    dimension a multiple of 8, otherwise each projection is an ordinary ``linear``."""
+    ok = x.dtype in (torch.bfloat16, torch.float16) and x.is_contiguous() and x.shape[-1] % 8 == 0 and \
+        (x.numel() // x.shape[-1]) % 8 == 0 and \
+        all(w.dtype == x.dtype and w.is_contiguous() and w.ndim == 2 and w.shape[1] == x.shape[-1] and
+            w.shape[0] % 8 == 0 for w in weights)
+    if not ok:
+        return [linear(x, w, optimized=optimized) for w in weights]
+    return list(_SharedInputProjections.apply(x, *weights))
+

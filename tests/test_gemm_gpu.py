@@ -76,3 +76,27 @@ def test_linear_autograd(dtype):
     for a, e in ((y, yr), (dx, ex), (dw, ew)):
         assert max_rel(a, e) < tol
         assert cosine(a, e) > 0.999
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
+def test_shared_input_projections_autograd(dtype):
+    """q/k/v-style projections sharing one input: outputs and all gradients against fp64 autograd
+    (bf16 takes the packed single-GEMM backward, fp32 the per-projection path)."""
+    from qwen3_triton.kernels.linear import shared_input_projections
+    gen = seeded(12)
+    x = randn(2, 40, 256, gen=gen, dtype=dtype)
+    ws = [randn(n, 256, gen=gen, dtype=dtype, scale=0.05) for n in (256, 64, 64)]
+    dys = [randn(2, 40, n, gen=gen, dtype=dtype) for n in (256, 64, 64)]
+    xd = x.cuda().requires_grad_()
+    wd = [w.cuda().requires_grad_() for w in ws]
+    ys = shared_input_projections(xd, wd)
+    grads = torch.autograd.grad(ys, [xd, *wd], [d.cuda() for d in dys])
+    xr = x.double().requires_grad_()
+    wr = [w.double().requires_grad_() for w in ws]
+    yr = [xr @ w.t() for w in wr]
+    er = torch.autograd.grad(yr, [xr, *wr], [d.double() for d in dys])
+    tol = 2e-2 if dtype == torch.bfloat16 else 1e-5
+    for a, e in zip(list(ys) + list(grads), yr + list(er)):
+        assert max_rel(a, e) < tol
+        assert cosine(a, e) > 0.999
+
