@@ -67,6 +67,22 @@ struct Lay {
 // workgroups fit per CU); LDS rows are unpadded and XOR-swizzled by 16-byte chunk so every MFMA
 // operand read is bank-conflict free.  Tiles entirely below the causal diagonal skip the mask, and
 // the output rescale is skipped when no lane's running max moved.
+// Ring-buffer wait: let the tile that is about to be read land while up to `younger` later tiles of
+// PER loads each stay in flight (vmcnt(younger * PER)), then a workgroup barrier that waits only for
+// LDS reads -- __syncthreads()' release fence would drain every in-flight tile (vmcnt(0)).
+template <int PER> Q3_DEV void ring_wait(int younger) {
+  switch (younger) {
+    case 0: __builtin_amdgcn_s_waitcnt((0 & 15) | (7 << 4) | (0 << 8)); break;
+    case 1: __builtin_amdgcn_s_waitcnt(((PER) & 15) | (((PER) >> 4) << 14) | (7 << 4) | (0 << 8)); break;
+    case 2: __builtin_amdgcn_s_waitcnt(((2 * PER) & 15) | (((2 * PER) >> 4) << 14) | (7 << 4) | (0 << 8)); break;
+    default: __builtin_amdgcn_s_waitcnt(((3 * PER) & 15) | (((3 * PER) >> 4) << 14) | (7 << 4) | (0 << 8)); break;
+  }
+  static_assert(3 * PER < 64, "vmcnt range");
+  asm volatile("" ::: "memory");
+  __builtin_amdgcn_s_barrier();
+  asm volatile("" ::: "memory");
+}
+
 template <int CPR> Q3_DEV int chunk_swz(int r) {
   if constexpr (CPR == 16) return r & 15;
   else if constexpr (CPR == 8) return (r ^ (r >> 3)) & 7;
@@ -90,7 +106,8 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2, 2))
   const int nqt = (Lq + 127) / 128;
   const int qt = nqt - 1 - (int)blockIdx.x;
   const int bh = blockIdx.y, b = bh / Hq, h = bh % Hq, hk = h / (Hq / Hkv);
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, g = lane >> 5;
+  const int tid = threadIdx.x, lane = tid & 63, g = lane >> 5;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform: scalar branches
   const int off = Lk - Lq;
   const int q0 = qt * 128 + wave * 32;
   const int qi = q0 + (lane & 31);
@@ -277,7 +294,8 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2, 2))
   const int nqt = (Lq + 127) / 128;
   const int qt = nqt - 1 - (int)blockIdx.y;  // longest query tiles first
   const int bh = blockIdx.x, b = bh / Hq, h = bh % Hq, hk = h / (Hq / Hkv);
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, g = lane >> 5;
+  const int tid = threadIdx.x, lane = tid & 63, g = lane >> 5;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform: scalar branches
   const int off = Lk - Lq;
   const int q0 = qt * 128 + wave * 32;
   const int qi = q0 + (lane & 31);
@@ -396,7 +414,7 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2, 2))
   }
 }
 
-template <typename T, int D, int OCC>
+template <typename T, int D, int OCC, int STAGES>
 __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(OCC, OCC))) void attn_bwd_dkdv_v2(
     const u16* __restrict__ Q, Lay ql, const u16* __restrict__ K, const u16* __restrict__ V, Lay kl,
     const u16* __restrict__ Qt, const u16* __restrict__ dO, const u16* __restrict__ dOt,
@@ -409,11 +427,12 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(OCC, O
   static_assert(NLOADS % 4 == 0, "loads split over 4 waves");
   constexpr int LPW = NLOADS / 4;
   constexpr int QB = BM * D * 2, STAGE = 4 * QB + 2 * BM * 4;
-  __shared__ __attribute__((aligned(1024))) char lds[2 * STAGE];
+  __shared__ __attribute__((aligned(1024))) char lds[STAGES * STAGE];
 
   const int kt = (int)blockIdx.y;  // smallest key tiles (the most query tiles) first
   const int bk = blockIdx.x, b = bk / Hkv, hk = bk % Hkv, ratio = Hq / Hkv;
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, g = lane >> 5;
+  const int tid = threadIdx.x, lane = tid & 63, g = lane >> 5;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform: scalar branches
   const int off = Lk - Lq;
   const int k0w = kt * 128 + wave * 32;
   const int kj = k0w + (lane & 31);
@@ -474,14 +493,19 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(OCC, O
     }
   };
 
-  if (total > 0) issue(0, 0);
+  // STAGES-deep ring: tiles u+1 .. u+STAGES-1 are in flight while tile u is computed.  Wave 0 issues
+  // one more load per tile (the lse/delta vector) than the others.
+#pragma unroll
+  for (int st = 0; st < STAGES - 1; ++st)
+    if (st < total) issue(st, st);
   for (int u = 0; u < total; ++u) {
-    __builtin_amdgcn_s_waitcnt((0 & 15) | (7 << 4) | (15 << 8));  // vmcnt(0)
-    __syncthreads();
-    if (u + 1 < total) issue((u + 1) & 1, u + 1);
+    const int younger = min(STAGES - 2, total - 1 - u);
+    if (wave == 0) ring_wait<LPW + 1>(younger);
+    else ring_wait<LPW>(younger);
+    if (u + STAGES - 1 < total) issue((u + STAGES - 1) % STAGES, u + STAGES - 1);
     const int q0 = qstart + (u % nq) * BM;
     if (min(q0 + BM - 1, Lq - 1) + off < k0w) continue;  // no query of the tile sees the wave's keys
-    const char* qb = lds + (u & 1) * STAGE;
+    const char* qb = lds + (u % STAGES) * STAGE;
     const char* db = qb + QB;
     const char* qtb = qb + 2 * QB;
     const char* dtb = qb + 3 * QB;
@@ -730,7 +754,8 @@ int bwd_mfma(const void* q, Lay ql, const void* k, const void* v, Lay kl, const 
                                                    (const u16*)kt, (const u16*)dout, lse, delta, (u16*)dq, Hq, Hkv,
                                                    Lq, Lk, ldkt, scale, scale * kLog2e);
   dim3 g2((unsigned)(B * Hkv), (unsigned)((Lk + 127) / 128));
-  attn_bwd_dkdv_v2<T, D, (D > 64 ? 1 : 2)><<<g2, kThreads, 0, s>>>((const u16*)q, ql, (const u16*)k, (const u16*)v, kl,
+  // D = 128: one workgroup per CU either way (registers), so a 4-deep ring costs no occupancy.
+  attn_bwd_dkdv_v2<T, D, (D > 64 ? 1 : 2), (D > 64 ? 4 : 2)><<<g2, kThreads, 0, s>>>((const u16*)q, ql, (const u16*)k, (const u16*)v, kl,
                                                   (const u16*)qt, (const u16*)dout, (const u16*)dot, lse, delta,
                                                   (u16*)dk, (u16*)dv, Hq, Hkv, Lq, Lk, ldqt, scale, scale * kLog2e);
   return (int)hipGetLastError();
