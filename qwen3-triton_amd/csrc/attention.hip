@@ -83,6 +83,9 @@ template <int PER> Q3_DEV void ring_wait(int younger) {
   asm volatile("" ::: "memory");
 }
 
+// LDS destination pointer of a direct-to-LDS load
+typedef __attribute__((address_space(3))) void* lds_vp;
+
 template <int CPR> Q3_DEV int chunk_swz(int r) {
   if constexpr (CPR == 16) return r & 15;
   else if constexpr (CPR == 8) return (r ^ (r >> 3)) & 7;
@@ -452,6 +455,22 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(OCC, O
   const int nq = (Lq - qstart + BM - 1) / BM;  // query tiles per head
   const int total = ratio * nq;
 
+  // D = 128, full query tile (q0 + BM <= Lq): load i (0, 1) of each operand covers rows
+  // wl * RPK + lane / CPK (wl = wave + 4 i) of Q and dO, rows wl * RPQ + lane / CPQ of Q^T and dO^T;
+  // per-lane byte offsets precomputed here, wave-uniform tile bases added per tile.
+  auto qoff = [&](int i) {
+    const int r = (wave + 4 * i) * RPK + lane / CPK;
+    return (uint32_t)(((int64_t)r * ql.s + ((lane % CPK) ^ chunk_swz<CPK>(r)) * 8) * 2);
+  };
+  auto toff = [&](int i) {
+    const int r = (wave + 4 * i) * RPQ + lane / CPQ;
+    return (uint32_t)(((int64_t)r * ldqt + ((lane % CPQ) ^ chunk_swz<CPQ>(r)) * 8) * 2);
+  };
+  // 32-bit lane offsets: bounded strides keep them exact
+  const bool kFast = D == 128 && ldqt < (1 << 24) && ql.s < (1 << 24);
+  static_assert(D != 128 || (QLOADS == 8 && TLOADS == 8 && LPW == 8), "load schedule of the D = 128 tile");
+  const uint32_t qo0 = qoff(0), qo1 = qoff(1), to0 = toff(0), to1 = toff(1);
+
   // tile u = (head hh, query tile): operands Q, dO rows and Q^T, dO^T columns, plus lse/delta
   auto issue = [&](int stage, int u) {
     const int hh = u / nq, q0 = qstart + (u % nq) * BM;
@@ -461,25 +480,43 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(OCC, O
     const u16* dOb = dO + b * ql.b + h * ql.h;
     const u16* Qtb = Qt + bh * D * ldqt;
     const u16* dOtb = dOt + bh * D * ldqt;
+    if (kFast && q0 + BM <= Lq) {
+      const char* qs = reinterpret_cast<const char*>(Qb + (int64_t)q0 * ql.s);
+      const char* ds = reinterpret_cast<const char*>(dOb + (int64_t)q0 * ql.s);
+      const char* qts = reinterpret_cast<const char*>(Qtb + q0);
+      const char* dts = reinterpret_cast<const char*>(dOtb + q0);
 #pragma unroll
-    for (int i = 0; i < LPW; ++i) {
-      const int w = wave + 4 * i;
-      const void* src;
-      int dst;
-      if (w < 2 * QLOADS) {
-        const int which = w / QLOADS, wl = w % QLOADS;
-        const int r = wl * RPK + lane / CPK;
-        const int c = (lane % CPK) ^ chunk_swz<CPK>(r);
-        src = (which ? dOb : Qb) + (int64_t)min(q0 + r, Lq - 1) * ql.s + c * 8;
-        dst = stage * STAGE + which * QB + wl * RPK * D * 2;
-      } else {
-        const int which = (w - 2 * QLOADS) / TLOADS, wl = (w - 2 * QLOADS) % TLOADS;
-        const int r = wl * RPQ + lane / CPQ;
-        const int c = (lane % CPQ) ^ chunk_swz<CPQ>(r);
-        src = (which ? dOtb : Qtb) + (int64_t)r * ldqt + min(q0 + c * 8, ldqt - 8);
-        dst = stage * STAGE + (2 + which) * QB + wl * RPQ * BM * 2;
+      for (int i = 0; i < 2; ++i) {
+        const int wl = wave + 4 * i;
+        const uint32_t qo = i ? qo1 : qo0, to = i ? to1 : to0;
+        __builtin_amdgcn_global_load_lds(qs + qo, (lds_vp)(lds + stage * STAGE + wl * RPK * D * 2), 16, 0, 0);
+        __builtin_amdgcn_global_load_lds(ds + qo, (lds_vp)(lds + stage * STAGE + QB + wl * RPK * D * 2), 16, 0, 0);
+        __builtin_amdgcn_global_load_lds(qts + to, (lds_vp)(lds + stage * STAGE + 2 * QB + wl * RPQ * BM * 2), 16,
+                                         0, 0);
+        __builtin_amdgcn_global_load_lds(dts + to, (lds_vp)(lds + stage * STAGE + 3 * QB + wl * RPQ * BM * 2), 16,
+                                         0, 0);
       }
-      __builtin_amdgcn_global_load_lds(src, (__attribute__((address_space(3))) void*)(lds + dst), 16, 0, 0);
+    } else {
+#pragma unroll
+      for (int i = 0; i < LPW; ++i) {
+        const int w = wave + 4 * i;
+        const void* src;
+        int dst;
+        if (w < 2 * QLOADS) {
+          const int which = w / QLOADS, wl = w % QLOADS;
+          const int r = wl * RPK + lane / CPK;
+          const int c = (lane % CPK) ^ chunk_swz<CPK>(r);
+          src = (which ? dOb : Qb) + (int64_t)min(q0 + r, Lq - 1) * ql.s + c * 8;
+          dst = stage * STAGE + which * QB + wl * RPK * D * 2;
+        } else {
+          const int which = (w - 2 * QLOADS) / TLOADS, wl = (w - 2 * QLOADS) % TLOADS;
+          const int r = wl * RPQ + lane / CPQ;
+          const int c = (lane % CPQ) ^ chunk_swz<CPQ>(r);
+          src = (which ? dOtb : Qtb) + (int64_t)r * ldqt + min(q0 + c * 8, ldqt - 8);
+          dst = stage * STAGE + (2 + which) * QB + wl * RPQ * BM * 2;
+        }
+        __builtin_amdgcn_global_load_lds(src, (lds_vp)(lds + dst), 16, 0, 0);
+      }
     }
     // lse (lanes 0..31) and delta (lanes 32..63) of the tile's queries, straight into LDS like the
     // operand tiles (a plain load + LDS store would stall wave 0 for a memory round trip per tile);
@@ -488,8 +525,7 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(OCC, O
     if (wave == 0) {
       const int qq = min(q0 + (lane & 31), Lq - 1);
       const float* src = (lane < 32 ? LSE : Delta) + bh * Lq + qq;
-      __builtin_amdgcn_global_load_lds(src, (__attribute__((address_space(3))) void*)(lds + stage * STAGE + 4 * QB),
-                                       4, 0, 0);
+      __builtin_amdgcn_global_load_lds(src, (lds_vp)(lds + stage * STAGE + 4 * QB), 4, 0, 0);
     }
   };
 
@@ -520,13 +556,25 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(OCC, O
     }
     const bool full = k0w + 31 <= q0 + off && q0 + BM - 1 < Lq;
     f32x16 ds;
+    if (full) {
 #pragma unroll
-    for (int v = 0; v < 16; ++v) {
-      const int r = acc_row(v, lane), qq = q0 + r;
-      float p = __builtin_amdgcn_exp2f(s[v] * scale2 - side[r] * kLog2e);
-      if (!full) p = (qq < Lq && kj <= qq + off) ? p : 0.f;
-      s[v] = p;
-      ds[v] = p * (dp[v] - side[BM + r]);
+      for (int v = 0; v < 16; ++v) {
+        const int r = acc_row(v, lane);
+        const float p = __builtin_amdgcn_exp2f(s[v] * scale2 - side[r] * kLog2e);
+        s[v] = p;
+        ds[v] = p * (dp[v] - side[BM + r]);
+      }
+    } else {
+      // query q0 + r is kept when r in [lo, hi): at or after the lane's key (causal) and inside Lq
+      const int lo = kj - off - q0, hi = Lq - q0;
+#pragma unroll
+      for (int v = 0; v < 16; ++v) {
+        const int r = acc_row(v, lane);
+        float p = __builtin_amdgcn_exp2f(s[v] * scale2 - side[r] * kLog2e);
+        p = (r >= lo && r < hi) ? p : 0.f;
+        s[v] = p;
+        ds[v] = p * (dp[v] - side[BM + r]);
+      }
     }
 #pragma unroll
     for (int c = 0; c < BM / 16; ++c) {
