@@ -15,7 +15,8 @@ def ref(a, b):
 
 @pytest.mark.parametrize("m,n,k", [(32, 32, 16), (256, 128, 64), (300, 200, 8), (1, 4096, 4096), (8, 1024, 4096),
                                    (513, 687, 688), (2048, 1024, 4096), (64, 151936 // 16, 256), (1000, 3000, 128),
-                                   (8192, 4096, 4096), (4096, 12288, 640), (8192, 1024, 192), (333, 4100, 4160)])
+                                   (8192, 4096, 4096), (4096, 12288, 640), (8192, 1024, 192), (333, 4100, 4160),
+                                   (4353, 4100, 1024), (2050, 4000, 512)])
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
 def test_gemm_nt_shapes(m, n, k, dtype):
     print(f"gemm_nt {m}x{n}x{k} {dtype}", flush=True)
@@ -43,6 +44,24 @@ def test_gemm_alpha_accumulate_and_ldc():
     e[:, :90] += 0.5 * ref(a, b.t())
     assert max_rel(out, e) < 1e-5
     assert torch.equal(out[:, 90:].cpu(), c0[:, 90:])  # columns beyond N untouched
+
+
+@pytest.mark.parametrize("m,n", [(4352, 4096), (4353, 4100), (2050, 4000)])
+def test_gemm_persistent_accumulate(m, n):
+    """More output tiles than CUs: workgroups stream several tiles (EVEN and edge-clamped paths)
+    and accumulate into an fp32 output with a row pitch wider than N."""
+    print(f"gemm_nt accumulate {m}x{n}", flush=True)
+    gen = seeded(m + n)
+    k = 256
+    a = randn(m, k, gen=gen, dtype=torch.bfloat16)
+    b = randn(n, k, gen=gen, dtype=torch.bfloat16)
+    c0 = randn(m, n + 8, gen=gen)
+    out = c0.clone().cuda()
+    gemm_nt_into(a.cuda(), k, b.cuda(), k, out, m, n, k, alpha=2.0, accumulate=True)
+    e = c0.double().clone()
+    e[:, :n] += 2.0 * ref(a, b.t())
+    assert max_rel(out, e) < 1e-5
+    assert torch.equal(out[:, n:].cpu(), c0[:, n:])
 
 
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
