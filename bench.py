@@ -30,10 +30,10 @@ PEAK_BF16_TFLOPS = 2500.0   # MI355X dense bf16 matrix-core peak
 PEAK_HBM_GBS = 8000.0       # MI355X HBM3E
 # HBM bytes per GEMM launch of the layer step, from two rocprofv3 counter passes over
 # `bench.py --pmc-probe` (FETCH_SIZE x 2.000 and WRITE_SIZE x 1.000: the factors that make a 1 GiB
-# device copy read 1 GiB), averaged over the step's 21 GEMM launches.  Re-measure with those two
+# device copy read 1 GiB), averaged over the step's 15 GEMM launches.  Re-measure with those two
 # passes (rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE -- python bench.py --pmc-probe) when the GEMM
 # kernels change.
-GEMM_TRAFFIC_BYTES_PER_LAUNCH = 685.9e6 + 101.1e6
+GEMM_TRAFFIC_BYTES_PER_LAUNCH = 948.1e6 + 118.5e6
 
 
 def qwen3_8b_config(layers):
@@ -45,12 +45,14 @@ def qwen3_8b_config(layers):
 
 
 class GemmTimer:
-    """Wraps the matrix-core GEMM launcher: records a HIP event pair on the launching stream around
-    every GEMM of the timed region, with its algorithmic FLOPs (2*M*N*K)."""
+    """Wraps the matrix-core GEMM launcher in every module that calls it: records a HIP event pair on
+    the launching stream around every GEMM of the timed region, with its algorithmic FLOPs
+    (2*M*N*K)."""
 
-    def __init__(self, linear_module):
-        self.mod = linear_module
-        self.orig = linear_module.gemm_nt_into
+    def __init__(self, modules):
+        self.mods = [m for m in modules if hasattr(m, "gemm_nt_into")]
+        self.orig = self.mods[0].gemm_nt_into
+        assert all(m.gemm_nt_into is self.orig for m in self.mods)
         self.records = []
         self.active = False
 
@@ -67,11 +69,13 @@ class GemmTimer:
             e.record()
             self.records.append((s, e, 2.0 * m * n * k))
 
-        self.mod.gemm_nt_into = timed
+        for m in self.mods:
+            m.gemm_nt_into = timed
         return self
 
     def __exit__(self, *exc):
-        self.mod.gemm_nt_into = self.orig
+        for m in self.mods:
+            m.gemm_nt_into = self.orig
 
     def summary(self):
         ms = sum(s.elapsed_time(e) for s, e, _ in self.records)
@@ -84,7 +88,7 @@ def decoder_layer_bench(steps, warmup):
     import torch
     from qwen3_triton.components import DecoderLayer
     from qwen3_triton.configuration import OptimizationOptions
-    from qwen3_triton.kernels import linear as linear_mod
+    from qwen3_triton.kernels import linear as linear_mod, mlp_precision, lm_head_ce
     from qwen3_triton.kernels.rotary import rotary_tables
     from qwen3_triton._model import rope_theta
 
@@ -116,7 +120,7 @@ def decoder_layer_bench(steps, warmup):
     for _ in range(warmup):
         step()
     torch.cuda.synchronize()
-    with GemmTimer(linear_mod) as gt:
+    with GemmTimer([linear_mod, mlp_precision, lm_head_ce]) as gt:
         gt.active = True
         start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
         torch.cuda.synchronize()
