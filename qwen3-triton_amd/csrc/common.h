@@ -56,9 +56,9 @@ template <> Q3_DEV uint32_t pack2<BF16>(float lo, float hi) { return pack_bf16x2
 // One 16-byte vector unpacked to fp32: VEC = 8 for 16-bit types, 4 for fp32.
 template <typename T> struct Vec { float v[T::vec]; };
 
-template <typename T> Q3_DEV Vec<T> load_vec(const typename T::storage* p) {
+// 16 bytes of storage (T::vec elements) as floats.
+template <typename T> Q3_DEV Vec<T> unpack_vec(i32x4 raw) {
   Vec<T> r;
-  i32x4 raw = *reinterpret_cast<const i32x4*>(p);
   if constexpr (T::vec == 4) {
 #pragma unroll
     for (int i = 0; i < 4; ++i) r.v[i] = __int_as_float(raw[i]);
@@ -71,6 +71,9 @@ template <typename T> Q3_DEV Vec<T> load_vec(const typename T::storage* p) {
     }
   }
   return r;
+}
+template <typename T> Q3_DEV Vec<T> load_vec(const typename T::storage* p) {
+  return unpack_vec<T>(*reinterpret_cast<const i32x4*>(p));
 }
 template <typename T> Q3_DEV void store_vec(typename T::storage* p, const Vec<T>& r) {
   i32x4 raw;

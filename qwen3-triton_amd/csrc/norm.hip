@@ -84,30 +84,39 @@ __global__ __launch_bounds__(kBlock) void rmsnorm_bwd_kernel(const typename T::s
   const int nvec = h / V;
   const int t = threadIdx.x % TPR, g = threadIdx.x / TPR;
   const float inv_h = 1.f / (float)h;
+  // Operands stay packed (16 bytes per vector) until used, and every load of a row is issued before
+  // any is consumed: rows past the end and vectors past h re-read a valid vector, and their terms
+  // are masked where they are used.
   float acc[MAXV][V];
-  Vec<T> wv[MAXV];
+  i32x4 wv[MAXV];
 #pragma unroll
   for (int j = 0; j < MAXV; ++j) {
     const int vi = j * TPR + t;
-    if (vi < nvec) wv[j] = load_vec<T>(w + (int64_t)vi * V);
+    wv[j] = *reinterpret_cast<const i32x4*>(w + (int64_t)(vi < nvec ? vi : 0) * V);
 #pragma unroll
     for (int e = 0; e < V; ++e) acc[j][e] = 0.f;
   }
   for (int64_t base = (int64_t)blockIdx.x * RPB; base < rows; base += (int64_t)gridDim.x * RPB) {
     const int64_t row = base + g;
     const bool valid = row < rows;
-    Vec<T> xv[MAXV], gv[MAXV];
-    float ss = 0.f, dot = 0.f;
+    const int64_t rc = valid ? row : rows - 1;
+    i32x4 xr[MAXV], gr[MAXV];
 #pragma unroll
     for (int j = 0; j < MAXV; ++j) {
       const int vi = j * TPR + t;
-      if (valid && vi < nvec) {
-        xv[j] = load_vec<T>(x + row * h + (int64_t)vi * V);
-        gv[j] = load_vec<T>(dy + row * h + (int64_t)vi * V);
+      const int64_t off = rc * h + (int64_t)(vi < nvec ? vi : 0) * V;
+      xr[j] = *reinterpret_cast<const i32x4*>(x + off);
+      gr[j] = *reinterpret_cast<const i32x4*>(dy + off);
+    }
+    float ss = 0.f, dot = 0.f;
+#pragma unroll
+    for (int j = 0; j < MAXV; ++j) {
+      if (j * TPR + t < nvec) {
+        const Vec<T> xv = unpack_vec<T>(xr[j]), gv = unpack_vec<T>(gr[j]), wf = unpack_vec<T>(wv[j]);
 #pragma unroll
         for (int e = 0; e < V; ++e) {
-          ss += xv[j].v[e] * xv[j].v[e];
-          dot += gv[j].v[e] * wv[j].v[e] * xv[j].v[e];
+          ss += xv.v[e] * xv.v[e];
+          dot += gv.v[e] * wf.v[e] * xv.v[e];
         }
       }
     }
@@ -119,11 +128,12 @@ __global__ __launch_bounds__(kBlock) void rmsnorm_bwd_kernel(const typename T::s
     for (int j = 0; j < MAXV; ++j) {
       const int vi = j * TPR + t;
       if (valid && vi < nvec) {
+        const Vec<T> xv = unpack_vec<T>(xr[j]), gv = unpack_vec<T>(gr[j]), wf = unpack_vec<T>(wv[j]);
         Vec<T> o;
 #pragma unroll
         for (int e = 0; e < V; ++e) {
-          o.v[e] = gv[j].v[e] * wv[j].v[e] * inv - xv[j].v[e] * c;
-          acc[j][e] += gv[j].v[e] * xv[j].v[e] * inv;
+          o.v[e] = gv.v[e] * wf.v[e] * inv - xv.v[e] * c;
+          acc[j][e] += gv.v[e] * xv.v[e] * inv;
         }
         store_vec<T>(dx + row * h + (int64_t)vi * V, o);
       }
