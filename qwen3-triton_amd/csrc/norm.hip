@@ -41,18 +41,26 @@ __global__ __launch_bounds__(kBlock) void rmsnorm_fwd_kernel(const typename T::s
   const int nvec = h / V;
   const int t = threadIdx.x % TPR, g = threadIdx.x / TPR;
   const float inv_h = 1.f / (float)h;
+  // Every load of a row is issued before any is consumed (packed operands; rows past the end and
+  // vectors past h re-read a valid vector whose terms are masked).
   for (int64_t base = (int64_t)blockIdx.x * RPB; base < rows; base += (int64_t)gridDim.x * RPB) {
     const int64_t row = base + g;
     const bool valid = row < rows;
-    Vec<T> xv[MAXV];
+    const int64_t rc = valid ? row : rows - 1;
+    i32x4 xr[MAXV], wr[MAXV];
+#pragma unroll
+    for (int j = 0; j < MAXV; ++j) {
+      const int vi = j * TPR + t, vc = vi < nvec ? vi : 0;
+      xr[j] = *reinterpret_cast<const i32x4*>(x + rc * h + (int64_t)vc * V);
+      wr[j] = *reinterpret_cast<const i32x4*>(w + (int64_t)vc * V);
+    }
     float ss = 0.f;
 #pragma unroll
     for (int j = 0; j < MAXV; ++j) {
-      const int vi = j * TPR + t;
-      if (valid && vi < nvec) {
-        xv[j] = load_vec<T>(x + row * h + (int64_t)vi * V);
+      if (j * TPR + t < nvec) {
+        const Vec<T> xv = unpack_vec<T>(xr[j]);
 #pragma unroll
-        for (int e = 0; e < V; ++e) ss += xv[j].v[e] * xv[j].v[e];
+        for (int e = 0; e < V; ++e) ss += xv.v[e] * xv.v[e];
       }
     }
     const float inv = rsqrtf(row_sum<TPR>(ss, red) * inv_h + eps);
@@ -60,9 +68,10 @@ __global__ __launch_bounds__(kBlock) void rmsnorm_fwd_kernel(const typename T::s
     for (int j = 0; j < MAXV; ++j) {
       const int vi = j * TPR + t;
       if (valid && vi < nvec) {
-        Vec<T> wv = load_vec<T>(w + (int64_t)vi * V), o;
+        const Vec<T> xv = unpack_vec<T>(xr[j]), wv = unpack_vec<T>(wr[j]);
+        Vec<T> o;
 #pragma unroll
-        for (int e = 0; e < V; ++e) o.v[e] = xv[j].v[e] * inv * wv.v[e];
+        for (int e = 0; e < V; ++e) o.v[e] = xv.v[e] * inv * wv.v[e];
         store_vec<T>(y + row * h + (int64_t)vi * V, o);
       }
     }
@@ -169,13 +178,16 @@ __global__ __launch_bounds__(kBlock) void colsum_level_kernel(const float* __res
   __shared__ float fold[4][64];
   const int c = blockIdx.x * 64 + (threadIdx.x & 63), grp = threadIdx.x >> 6;
   const int r0 = blockIdx.y * 64 + grp * 16;
+  // all 16 loads in flight at once (clamped indices, masked terms), summed in row order
+  const int cc = c < h ? c : h - 1;
+  float v[16];
+#pragma unroll
+  for (int i = 0; i < 16; ++i) v[i] = in[(int64_t)min(r0 + i, rows - 1) * h + cc];
   float s = 0.f;
   if (c < h) {
 #pragma unroll
-    for (int i = 0; i < 16; ++i) {
-      const int r = r0 + i;
-      if (r < rows) s += in[(int64_t)r * h + c];
-    }
+    for (int i = 0; i < 16; ++i)
+      if (r0 + i < rows) s += v[i];
   }
   fold[grp][threadIdx.x & 63] = s;
   __syncthreads();
