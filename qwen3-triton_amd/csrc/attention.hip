@@ -268,6 +268,27 @@ __global__ __launch_bounds__(kThreads) void attn_delta_kernel(const typename T::
   if (lane_id() == 0) delta[row] = s;
 }
 
+// Vectorised delta: LPR = D / 8 lanes per row, 16 bytes of O and dO per lane (one row per LPR-lane
+// group, 64 / LPR rows per wave); the row sum is a DPP reduction over the group.
+template <typename T, int LPR>
+__global__ __launch_bounds__(kThreads) void attn_delta_vec_kernel(const typename T::storage* __restrict__ O,
+                                                                  const typename T::storage* __restrict__ dO,
+                                                                  Lay ql, float* __restrict__ delta, int64_t rows,
+                                                                  int H, int L) {
+  constexpr int RPW = 64 / LPR;
+  const int lane = lane_id(), sub = lane % LPR;
+  const int64_t row = ((int64_t)blockIdx.x * (kThreads / 64) + (threadIdx.x >> 6)) * RPW + lane / LPR;
+  const int64_t rc = row < rows ? row : rows - 1;
+  const int64_t b = rc / ((int64_t)H * L), h = (rc / L) % H, q = rc % L;
+  const int64_t base = b * ql.b + h * ql.h + q * ql.s + sub * 8;
+  const Vec<T> o = load_vec<T>(O + base), g = load_vec<T>(dO + base);
+  float s = 0.f;
+#pragma unroll
+  for (int e = 0; e < 8; ++e) s += o.v[e] * g.v[e];
+  s = group_sum<LPR>(s);
+  if (sub == 0 && row < rows) delta[row] = s;
+}
+
 // ============================================================================ backward (MFMA)
 // dQ kernel -- workgroup: 4 waves x 32 queries of one (b, h).  Per 64-key tile: S^T = K Q^T,
 // dP^T = V dO^T, dS = P (dP - delta), dQ^T += Kt dS^T.
@@ -836,6 +857,19 @@ int bwd_simt(const void* q, Lay ql, const void* k, const void* v, Lay kl, const 
 template <typename T>
 int delta_t(const void* o, const void* dout, Lay ql, float* delta, int64_t rows, int H, int L, int D, hipStream_t s) {
   typedef typename T::storage S;
+  const bool vec = T::vec == 8 && (D == 128 || D == 64 || D == 32) && ql.b % 8 == 0 && ql.h % 8 == 0 &&
+                   ql.s % 8 == 0 && ((uintptr_t)o & 15) == 0 && ((uintptr_t)dout & 15) == 0;
+  if (vec) {
+    const int lpr = D / 8, rpb = (kThreads / 64) * (64 / lpr);
+    const unsigned grid = (unsigned)((rows + rpb - 1) / rpb);
+    if (lpr == 16)
+      attn_delta_vec_kernel<T, 16><<<grid, kThreads, 0, s>>>((const S*)o, (const S*)dout, ql, delta, rows, H, L);
+    else if (lpr == 8)
+      attn_delta_vec_kernel<T, 8><<<grid, kThreads, 0, s>>>((const S*)o, (const S*)dout, ql, delta, rows, H, L);
+    else
+      attn_delta_vec_kernel<T, 4><<<grid, kThreads, 0, s>>>((const S*)o, (const S*)dout, ql, delta, rows, H, L);
+    return (int)hipGetLastError();
+  }
   attn_delta_kernel<T><<<(unsigned)((rows + 3) / 4), kThreads, 0, s>>>((const S*)o, (const S*)dout, ql, delta, rows, H,
                                                                        L, D);
   return (int)hipGetLastError();
