@@ -226,6 +226,44 @@ def decode_bench(batch, prompt, new_tokens):
             "hbm_frac": round(step_bytes / (per_step_ms * 1e-3) / 1e9 / PEAK_HBM_GBS, 4)}
 
 
+def lm_head_ce_bench(steps=3, warmup=1):
+    """Fused LM-head + causal CE of config #4: hidden [4, 2048, 4096] N(0,1), W [151936, 4096]
+    N(0, 0.02), labels uniform over the vocabulary with 5 % set to -100 (seed 3); forward + backward
+    (backward recomputes each chunk's logits: 4 x the forward's 2*T*H*V FLOPs)."""
+    import torch
+    from qwen3_triton.kernels.lm_head_ce import lm_head_cross_entropy
+    b, s, h, v = 4, 2048, 4096, 151936
+    gen = torch.Generator(device="cuda").manual_seed(3)
+    x = torch.randn(b, s, h, device="cuda", dtype=torch.bfloat16, generator=gen).requires_grad_()
+    w = (torch.randn(v, h, device="cuda", dtype=torch.bfloat16, generator=gen) * 0.02).requires_grad_()
+    labels = torch.randint(0, v, (b, s), device="cuda", generator=gen)
+    drop = torch.rand(b, s, device="cuda", generator=gen) < 0.05
+    labels = torch.where(drop, torch.full_like(labels, -100), labels)
+
+    def step():
+        x.grad = None
+        w.grad = None
+        lm_head_cross_entropy(x, w, labels).backward()
+
+    for _ in range(warmup):
+        step()
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for _ in range(steps):
+        step()
+    e1.record()
+    torch.cuda.synchronize()
+    ms = e0.elapsed_time(e1) / steps
+    flops = 4 * 2.0 * b * s * h * v
+    del x, w
+    torch.cuda.empty_cache()
+    return {"tokens": b * s, "vocab": v, "ms_per_step": round(ms, 3), "tokens_per_s": round(b * s / (ms * 1e-3), 1),
+            "algorithmic_tflop_per_step": round(flops / 1e12, 2),
+            "achieved_tflops": round(flops / (ms * 1e-3) / 1e12, 1),
+            "frac": round(flops / (ms * 1e-3) / 1e12 / PEAK_BF16_TFLOPS, 4)}
+
+
 def log(msg):
     print(f"[bench] {msg}", file=sys.stderr, flush=True)
 
@@ -239,6 +277,7 @@ def main():
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-decode", action="store_true")
     ap.add_argument("--no-layer", action="store_true", help="skip the decoder-layer step (profiling decode)")
+    ap.add_argument("--no-lm-head", action="store_true", help="skip the fused LM-head + CE step")
     ap.add_argument("--decode-tokens", type=int, default=256)
     ap.add_argument("--decode-batches", default="1,8", help="comma list of decode batches among 1 and 8")
     ap.add_argument("--pmc-probe", action="store_true",
@@ -298,6 +337,9 @@ def main():
                           "achieved_tflops": round(layer["step_tflops"], 1),
                           "frac": round(layer["step_tflops"] / PEAK_BF16_TFLOPS, 4)},
     }
+    if not args.no_lm_head:
+        log("fused LM-head CE fwd+bwd")
+        result["lm_head_ce"] = lm_head_ce_bench()
     if not args.no_decode:
         log("decode")
         try:
