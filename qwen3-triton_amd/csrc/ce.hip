@@ -43,8 +43,7 @@ __global__ __launch_bounds__(kThreads) void ce_stats_kernel(const typename T::st
   const typename T::storage* row = z + r * ld;
   float m = -INFINITY, s = 0.f;
   const int64_t nv = vec_ok ? n / V : 0;
-  for (int64_t i = threadIdx.x; i < nv; i += kThreads) {
-    const Vec<T> x = load_vec<T>(row + i * V);
+  auto fold = [&](const Vec<T>& x) {
     float vm = x.v[0];
 #pragma unroll
     for (int e = 1; e < V; ++e) vm = fmaxf(vm, x.v[e]);
@@ -52,7 +51,16 @@ __global__ __launch_bounds__(kThreads) void ce_stats_kernel(const typename T::st
 #pragma unroll
     for (int e = 0; e < V; ++e) vs += __expf(x.v[e] - vm);
     lse_combine(m, s, vm, vs);
+  };
+  int64_t i = threadIdx.x;
+  for (; i + 3 * kThreads < nv; i += 4 * kThreads) {  // four 16-byte loads in flight
+    Vec<T> x[4];
+#pragma unroll
+    for (int u = 0; u < 4; ++u) x[u] = load_vec<T>(row + (i + u * kThreads) * V);
+#pragma unroll
+    for (int u = 0; u < 4; ++u) fold(x[u]);
   }
+  for (; i < nv; i += kThreads) fold(load_vec<T>(row + i * V));
   for (int64_t i = nv * V + threadIdx.x; i < n; i += kThreads) lse_combine(m, s, to_f32<T>(row[i]), 1.f);
 #pragma unroll
   for (int o = 1; o < 64; o <<= 1) {
@@ -132,7 +140,8 @@ __global__ __launch_bounds__(kThreads) void ce_grad_kernel(const typename T::sto
                                                            const float* __restrict__ count,
                                                            const float* __restrict__ up,
                                                            typename O::storage* __restrict__ dz, int64_t ldo,
-                                                           int64_t rows, int64_t vocab, int64_t ignore) {
+                                                           int64_t rows, int64_t vocab, int64_t ignore,
+                                                           int vec_ok) {
   const int64_t r = blockIdx.x;
   const int64_t t = tgt[r];
   const bool valid = t != ignore && t >= 0 && t < vocab;
@@ -140,7 +149,44 @@ __global__ __launch_bounds__(kThreads) void ce_grad_kernel(const typename T::sto
   const float l = lse[r];
   const typename T::storage* row = z + r * ld;
   typename O::storage* out = dz + r * ldo;
-  for (int64_t c = (int64_t)blockIdx.y * kThreads + threadIdx.x; c < n; c += (int64_t)gridDim.y * kThreads) {
+  // 8 columns per thread: 16-byte loads and stores (vec_ok: 16-byte aligned rows of both buffers)
+  const int64_t n8 = vec_ok ? n / 8 : 0;
+  for (int64_t i = (int64_t)blockIdx.y * kThreads + threadIdx.x; i < n8; i += (int64_t)gridDim.y * kThreads) {
+    const int64_t c = i * 8;
+    float zv[8];
+    if constexpr (T::vec == 8) {
+      const Vec<T> a = load_vec<T>(row + c);
+#pragma unroll
+      for (int e = 0; e < 8; ++e) zv[e] = a.v[e];
+    } else {
+      const Vec<T> a = load_vec<T>(row + c), b = load_vec<T>(row + c + 4);
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        zv[e] = a.v[e];
+        zv[4 + e] = b.v[e];
+      }
+    }
+    float pv[8];
+#pragma unroll
+    for (int e = 0; e < 8; ++e)
+      pv[e] = valid ? (__expf(zv[e] - l) - ((c + e + col0 == t) ? 1.f : 0.f)) * scale : 0.f;
+    if constexpr (O::vec == 8) {
+      Vec<O> o;
+#pragma unroll
+      for (int e = 0; e < 8; ++e) o.v[e] = pv[e];
+      store_vec<O>(out + c, o);
+    } else {
+      Vec<O> o0, o1;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        o0.v[e] = pv[e];
+        o1.v[e] = pv[4 + e];
+      }
+      store_vec<O>(out + c, o0);
+      store_vec<O>(out + c + 4, o1);
+    }
+  }
+  for (int64_t c = n8 * 8 + (int64_t)blockIdx.y * kThreads + threadIdx.x; c < n; c += (int64_t)gridDim.y * kThreads) {
     const float p = valid ? __expf(to_f32<T>(row[c]) - l) - ((c + col0 == t) ? 1.f : 0.f) : 0.f;
     out[c] = from_f32<O>(p * scale);
   }
@@ -161,11 +207,12 @@ template <typename T, typename O>
 int grad_t2(const void* z, int64_t ld, int64_t n, int64_t col0, const int64_t* tgt, const float* lse,
             const float* count, const float* up, void* dz, int64_t ldo, int64_t rows, int64_t vocab, int64_t ignore,
             hipStream_t st) {
-  int64_t gx = (n + kThreads - 1) / kThreads;
+  const int vec = ((uintptr_t)z % 16 == 0) && ((uintptr_t)dz % 16 == 0) && ld % 8 == 0 && ldo % 8 == 0;
+  int64_t gx = (n + 8 * kThreads - 1) / (8 * kThreads);
   if (gx > 64) gx = 64;
   ce_grad_kernel<T, O><<<dim3((unsigned)rows, (unsigned)gx), kThreads, 0, st>>>(
       (const typename T::storage*)z, ld, n, col0, tgt, lse, count, up, (typename O::storage*)dz, ldo, rows, vocab,
-      ignore);
+      ignore, vec);
   return (int)hipGetLastError();
 }
 
