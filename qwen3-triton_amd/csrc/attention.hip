@@ -800,6 +800,40 @@ __global__ __launch_bounds__(kThreads) void seq_major_kernel(const u16* __restri
   }
 }
 
+// Vectorised form (D % 64 == 0, 16-byte aligned rows): a wave covers 64 output positions x 64 d;
+// lane (dc = lane % 8, sg = lane / 8) loads the 8 source rows of output positions p0 .. p0 + 7
+// (p0 = 8 sg, rows perm16(p)) at d0 + 8 dc .. + 7 (16 bytes each), transposes the 8 x 8 block in
+// registers and writes 8 d rows x 16 bytes.  Loads are 128-byte row segments, stores 128-byte runs.
+__global__ __launch_bounds__(kThreads) void seq_major_vec_kernel(const u16* __restrict__ x, Lay xl,
+                                                                 u16* __restrict__ y, int64_t ldy, int H, int L,
+                                                                 int D) {
+  const int bh = blockIdx.z, b = bh / H, h = bh % H;
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int dc = lane & 7, sg = lane >> 3;
+  const int p0 = (blockIdx.x * 4 + wave) * 64 + 8 * sg, d = blockIdx.y * 64 + 8 * dc;
+  if (p0 >= ldy) return;
+  const u16* xb = x + b * xl.b + h * xl.h + d;
+  uint32_t in[8][4];
+#pragma unroll
+  for (int j = 0; j < 8; ++j) {
+    const int src = perm16(p0 + j);
+    i32x4 v = {0, 0, 0, 0};
+    if (src < L) v = *reinterpret_cast<const i32x4*>(xb + (int64_t)src * xl.s);
+#pragma unroll
+    for (int w = 0; w < 4; ++w) in[j][w] = (uint32_t)v[w];
+  }
+  u16* yb = y + (int64_t)bh * D * ldy + (int64_t)d * ldy + p0;
+#pragma unroll
+  for (int e = 0; e < 8; ++e) {  // output row d + e: positions p0 .. p0 + 7
+    const int w = e >> 1, sh = (e & 1) * 16;
+    i32x4 o;
+#pragma unroll
+    for (int k = 0; k < 4; ++k)
+      o[k] = (int)(((in[2 * k][w] >> sh) & 0xffffu) | (((in[2 * k + 1][w] >> sh) & 0xffffu) << 16));
+    *reinterpret_cast<i32x4*>(yb + (int64_t)e * ldy) = o;
+  }
+}
+
 // ============================================================================ host dispatch
 bool dtype_ok(int dt) { return dt == Q3_F32 || dt == Q3_F16 || dt == Q3_BF16; }
 
@@ -898,6 +932,13 @@ int q3_attention_seq_major(int dtype, const void* x, int64_t sb, int64_t sh, int
                            int64_t B, int64_t H, int64_t L, int64_t D, hipStream_t stream) {
   Q3_REQUIRE((dtype == Q3_BF16 || dtype == Q3_F16) && x && y && B > 0 && H > 0 && L > 0 && D > 0 && ldy >= L &&
              ldy % 16 == 0 && B * H < 65536 && (D + 63) / 64 < 65536);
+  if (D % 64 == 0 && ((uintptr_t)x & 15) == 0 && ((uintptr_t)y & 15) == 0 && sb % 8 == 0 && sh % 8 == 0 &&
+      ss % 8 == 0) {
+    dim3 grid((unsigned)((ldy + 255) / 256), (unsigned)(D / 64), (unsigned)(B * H));
+    seq_major_vec_kernel<<<grid, kThreads, 0, stream>>>((const u16*)x, Lay{sb, sh, ss}, (u16*)y, ldy, (int)H,
+                                                        (int)L, (int)D);
+    return (int)hipGetLastError();
+  }
   dim3 grid((unsigned)((ldy + 63) / 64), (unsigned)((D + 63) / 64), (unsigned)(B * H));
   seq_major_kernel<<<grid, kThreads, 0, stream>>>((const u16*)x, Lay{sb, sh, ss}, (u16*)y, ldy, (int)H, (int)L,
                                                   (int)D);

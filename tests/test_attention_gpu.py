@@ -140,15 +140,24 @@ def test_attention_strided_layouts_bshd_and_cache():
 
 
 @pytest.mark.parametrize("l", [1, 15, 16, 100, 2048])
-def test_seq_major_layout(l):
+@pytest.mark.parametrize("d,layout", [(128, "bhsd"), (64, "bshd"), (32, "bhsd"), (128, "bshd")])
+def test_seq_major_layout(l, d, layout):
     """Sequence-major operand copy: [B,H,L,D] -> [B,H,D,Lp] (Lp = L rounded up to 16, zero pad) with the
-    4-position groups 1 and 2 of every 16-block swapped; bit-exact."""
+    4-position groups 1 and 2 of every 16-block swapped; bit-exact, for contiguous and [B,S,H,D] views
+    (vector path for D % 64 == 0, element path otherwise)."""
     from qwen3_triton.kernels import _ops
-    x = torch.randn(2, 3, l, 128, generator=seeded(l), dtype=torch.float32).to(torch.bfloat16)
-    y = _ops.seq_major(x.cuda()).cpu()
+    print(f"seq_major l={l} d={d} {layout}", flush=True)
+    if layout == "bhsd":
+        x = torch.randn(2, 3, l, d, generator=seeded(l), dtype=torch.float32).to(torch.bfloat16)
+        xd = x.cuda()
+    else:
+        xs = torch.randn(2, l, 3, d, generator=seeded(l), dtype=torch.float32).to(torch.bfloat16)
+        x = xs.transpose(1, 2)
+        xd = xs.cuda().transpose(1, 2)
+    y = _ops.seq_major(xd).cpu()
     lp = -(-l // 16) * 16
-    assert y.shape == (2, 3, 128, lp)
-    ref = torch.zeros(2, 3, 128, lp, dtype=torch.bfloat16)
+    assert y.shape == (2, 3, d, lp)
+    ref = torch.zeros(2, 3, d, lp, dtype=torch.bfloat16)
     ref[..., :l] = x.transpose(2, 3)
     p = torch.arange(lp)
     src = p ^ ((((p >> 2) ^ (p >> 3)) & 1) * 12)
