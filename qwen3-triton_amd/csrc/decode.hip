@@ -160,11 +160,14 @@ __global__ __launch_bounds__(NW * 64) void dlinear_kernel(DecArgs a) {
   }
 }
 
-// 4 waves x 2 k blocks in flight per wave: the best of {4, 8, 16} waves x {2, 4} blocks measured on
-// MI355X over the Qwen3-8B decode projections.
+// Waves per workgroup x k blocks in flight per wave, per mode: measured on MI355X inside the captured
+// Qwen3-8B decode step (B1 and B8) over {2, 4, 8, 16} waves x {1, 2, 4} blocks, each projection
+// kind separately: the normed Q/K/V (and LM head) 8 x 2; O and down (+ residual) 8 x 1; gate/up +
+// SwiGLU 8 x 1.
 template <typename T, int MODE, bool NORM>
 int dlinear_launch(const DecArgs& a, int tiles, hipStream_t s) {
-  dlinear_kernel<T, MODE, NORM, 4, 2><<<(unsigned)tiles, 4 * 64, 0, s>>>(a);
+  constexpr int NW = 8, P = MODE == 0 ? 2 : 1;
+  dlinear_kernel<T, MODE, NORM, NW, P><<<(unsigned)tiles, NW * 64, 0, s>>>(a);
   return (int)hipGetLastError();
 }
 
