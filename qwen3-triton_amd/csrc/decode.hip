@@ -241,13 +241,14 @@ struct DecAttnArgs {
 // RMSNorm over the 128 dims held by a 16-lane row (8 per lane) times the norm weight, then the
 // rotate-half RoPE with the partner dims 64 away (lane t ^ 8: DPP row_ror:8), rounded to the storage
 // type exactly like the standalone QK-norm + RoPE kernel.
+// w, cs, sn: this lane's 8 elements (t * 8 ..) of the norm weight and the rotary tables, packed.
 template <typename T>
-Q3_DEV void norm_rope8(float (&x)[8], const u16* w, const u16* cs, const u16* sn, int t, float eps) {
+Q3_DEV void norm_rope8(float (&x)[8], i32x4 w, i32x4 cs, i32x4 sn, int t, float eps) {
   float ss = 0.f;
 #pragma unroll
   for (int e = 0; e < 8; ++e) ss += x[e] * x[e];
   const float inv = rsqrtf(group_sum<16>(ss) * (1.f / 128.f) + eps);
-  const Vec<T> wv = load_vec<T>(w + t * 8), cv = load_vec<T>(cs + t * 8), sv = load_vec<T>(sn + t * 8);
+  const Vec<T> wv = unpack_vec<T>(w), cv = unpack_vec<T>(cs), sv = unpack_vec<T>(sn);
   const float sign = t < 8 ? -1.f : 1.f;
 #pragma unroll
   for (int e = 0; e < 8; ++e) {
@@ -265,57 +266,72 @@ __global__ __launch_bounds__(256) void decode_attn_kernel(DecAttnArgs a) {
   __shared__ float red_o[4][G][D];
   const int split = blockIdx.x, bk = blockIdx.y, b = bk / a.Hkv, hk = bk % a.Hkv;
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, t = lane & 15, kg = lane >> 4;
-  // len_dev holds the cache length before this token: the token itself is at that position.
-  const int pos = a.len_dev ? (int)*a.len_dev : a.T_len - 1;
-  const int T_len = a.len_dev ? min(pos + 1, a.capacity) : a.T_len;
+  // Every global load is issued before any is used: the cache rows of this split are read
+  // unconditionally (rows up to the capacity exist; rows at or past the length, and the new token's
+  // own row, are replaced below), together with q, the new token's k/v and the norm/rotary tables.
   const int k0 = split * kSplit, kw = k0 + wave * KPW;
-  const bool own = FUSED && pos >= k0 && pos < k0 + kSplit && pos < a.capacity;  // this split holds the token
-
   u16* kb = a.ck + b * a.ksb + hk * a.ksh;
   u16* vb = a.cv + b * a.ksb + hk * a.ksh;
   i32x4 kr[KPW / 4];
   uint32_t vr[KPW];
 #pragma unroll
-  for (int it = 0; it < KPW / 4; ++it) {
-    const int key = kw + it * 4 + kg;
-    kr[it] = key < T_len && !(own && key == pos) ? *reinterpret_cast<const i32x4*>(kb + (int64_t)key * D + t * 8)
-                                                 : i32x4{0, 0, 0, 0};
-  }
+  for (int it = 0; it < KPW / 4; ++it)
+    kr[it] = *reinterpret_cast<const i32x4*>(kb + (int64_t)min(kw + it * 4 + kg, a.capacity - 1) * D + t * 8);
 #pragma unroll
   for (int k = 0; k < KPW; ++k)
-    vr[k] = kw + k < T_len && !(own && kw + k == pos)
-                ? *reinterpret_cast<const uint32_t*>(vb + (int64_t)(kw + k) * D + 2 * lane)
-                : 0u;
+    vr[k] = *reinterpret_cast<const uint32_t*>(vb + (int64_t)min(kw + k, a.capacity - 1) * D + 2 * lane);
+  i32x4 qraw[G];
+#pragma unroll
+  for (int g = 0; g < G; ++g)
+    qraw[g] = *reinterpret_cast<const i32x4*>(a.q + b * a.qsb + (int64_t)(hk * G + g) * a.qsh + t * 8);
+  i32x4 kraw = {0, 0, 0, 0}, qwv = {0, 0, 0, 0}, kwv = {0, 0, 0, 0}, csv = {0, 0, 0, 0}, snv = {0, 0, 0, 0};
+  uint32_t vraw = 0u;
+  if constexpr (FUSED) {
+    kraw = *reinterpret_cast<const i32x4*>(a.k + b * a.kvsb + hk * a.kvsh + t * 8);
+    vraw = *reinterpret_cast<const uint32_t*>(a.v + b * a.kvsb + hk * a.kvsh + 2 * lane);
+    qwv = *reinterpret_cast<const i32x4*>(a.qw + t * 8);
+    kwv = *reinterpret_cast<const i32x4*>(a.kw + t * 8);
+    csv = *reinterpret_cast<const i32x4*>(a.cs + b * a.csb + t * 8);
+    snv = *reinterpret_cast<const i32x4*>(a.sn + b * a.csb + t * 8);
+  }
+  // len_dev holds the cache length before this token: the token itself is at that position.
+  const int pos = a.len_dev ? (int)*a.len_dev : a.T_len - 1;
+  const int T_len = a.len_dev ? min(pos + 1, a.capacity) : a.T_len;
+  const bool own = FUSED && pos >= k0 && pos < k0 + kSplit && pos < a.capacity;  // this split holds the token
+#pragma unroll
+  for (int it = 0; it < KPW / 4; ++it)
+    if (kw + it * 4 + kg >= T_len || (own && kw + it * 4 + kg == pos)) kr[it] = i32x4{0, 0, 0, 0};
+#pragma unroll
+  for (int k = 0; k < KPW; ++k)
+    if (kw + k >= T_len || (own && kw + k == pos)) vr[k] = 0u;
+
   if constexpr (FUSED) {
     if (own) {  // the new token: k = rope(norm(k_raw)), v raw; into the cache and into this step
-      const u16* cs = a.cs + b * a.csb;
-      const u16* sn = a.sn + b * a.csb;
-      const Vec<T> kv = load_vec<T>(a.k + b * a.kvsb + hk * a.kvsh + t * 8);
+      const Vec<T> kv = unpack_vec<T>(kraw);
       float kn[8];
 #pragma unroll
       for (int e = 0; e < 8; ++e) kn[e] = kv.v[e];
-      norm_rope8<T>(kn, a.kw, cs, sn, t, a.eps);
+      norm_rope8<T>(kn, kwv, csv, snv, t, a.eps);
       i32x4 kp;
 #pragma unroll
       for (int w = 0; w < 4; ++w) kp[w] = (int)pack2<T>(kn[2 * w], kn[2 * w + 1]);
 #pragma unroll
       for (int it = 0; it < KPW / 4; ++it)
         if (kw + it * 4 + kg == pos) kr[it] = kp;
-      const uint32_t vp = *reinterpret_cast<const uint32_t*>(a.v + b * a.kvsb + hk * a.kvsh + 2 * lane);
 #pragma unroll
       for (int k = 0; k < KPW; ++k)
-        if (kw + k == pos) vr[k] = vp;
+        if (kw + k == pos) vr[k] = vraw;
       if (wave == 0 && kg == 0) *reinterpret_cast<i32x4*>(kb + (int64_t)pos * D + t * 8) = kp;
-      if (wave == 0) *reinterpret_cast<uint32_t*>(vb + (int64_t)pos * D + 2 * lane) = vp;
+      if (wave == 0) *reinterpret_cast<uint32_t*>(vb + (int64_t)pos * D + 2 * lane) = vraw;
     }
   }
   float qf[G][8];
 #pragma unroll
   for (int g = 0; g < G; ++g) {
-    const Vec<T> qv = load_vec<T>(a.q + b * a.qsb + (int64_t)(hk * G + g) * a.qsh + t * 8);
+    const Vec<T> qv = unpack_vec<T>(qraw[g]);
 #pragma unroll
     for (int e = 0; e < 8; ++e) qf[g][e] = qv.v[e];
-    if constexpr (FUSED) norm_rope8<T>(qf[g], a.qw, a.cs + b * a.csb, a.sn + b * a.csb, t, a.eps);
+    if constexpr (FUSED) norm_rope8<T>(qf[g], qwv, csv, snv, t, a.eps);
 #pragma unroll
     for (int e = 0; e < 8; ++e) qf[g][e] *= a.scale2;  // scores in log2 units
   }
