@@ -416,9 +416,17 @@ __global__ __launch_bounds__(512) void decode_merge_kernel(const float* __restri
   __shared__ float red[16];
   const int bh = blockIdx.x, b = bh / Hq, h = bh % Hq, bk = bh / G, g = bh % G;
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int r = tid >> 7, d = tid & 127;
+  // First iterations' loads up front (clamped indices, masked where used), so one memory latency
+  // covers the max, the weights and the first block of partial outputs.
+  const int64_t p0 = ((int64_t)bk * splits + min(tid, splits - 1)) * G + g;
+  const float m0 = mpart[p0], l0 = lpart[p0];
+  float x0[8];
+#pragma unroll
+  for (int u = 0; u < 8; ++u) x0[u] = opart[(((int64_t)bk * splits + min(r + 4 * u, splits - 1)) * G + g) * D + d];
   // global max and denominator over the splits (the whole workgroup, fixed reduction order)
-  float mx = -INFINITY;
-  for (int j = tid; j < splits; j += 512) mx = fmaxf(mx, mpart[((int64_t)bk * splits + j) * G + g]);
+  float mx = tid < splits ? m0 : -INFINITY;
+  for (int j = tid + 512; j < splits; j += 512) mx = fmaxf(mx, mpart[((int64_t)bk * splits + j) * G + g]);
   mx = group_max<64>(mx);
   if (lane == 0) red[wave] = mx;
   __syncthreads();
@@ -428,22 +436,21 @@ __global__ __launch_bounds__(512) void decode_merge_kernel(const float* __restri
   float den = 0.f;
   for (int j = tid; j < splits; j += 512) {
     const int64_t pj = ((int64_t)bk * splits + j) * G + g;
-    const float mj = mpart[pj];
+    const float mj = j == tid ? m0 : mpart[pj];
     const float w = mj == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(mj - M);  // split with no live key
     wgt[j] = w;
-    den += w * lpart[pj];
+    den += w * (j == tid ? l0 : lpart[pj]);
   }
   den = group_sum<64>(den);
   __syncthreads();  // red[] reads done; wgt[] complete
   if (lane == 0) red[8 + wave] = den;
-  const int r = tid >> 7, d = tid & 127;
   float acc = 0.f;
   for (int j0 = r; j0 < splits; j0 += 4 * 8) {
     float x[8];
 #pragma unroll
     for (int u = 0; u < 8; ++u) {
       const int j = j0 + 4 * u;
-      x[u] = j < splits ? opart[(((int64_t)bk * splits + j) * G + g) * D + d] : 0.f;
+      x[u] = j0 == r ? x0[u] : j < splits ? opart[(((int64_t)bk * splits + j) * G + g) * D + d] : 0.f;
     }
 #pragma unroll
     for (int u = 0; u < 8; ++u) {
