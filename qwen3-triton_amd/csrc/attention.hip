@@ -451,7 +451,13 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(OCC, O
   static_assert(NLOADS % 4 == 0, "loads split over 4 waves");
   constexpr int LPW = NLOADS / 4;
   constexpr int QB = BM * D * 2, STAGE = 4 * QB + 2 * BM * 4;
-  __shared__ __attribute__((aligned(1024))) char lds[STAGES * STAGE];
+  // D = 128: the V fragments of each wave's 32 keys live in a wave-private LDS block instead of
+  // registers (the two 128-register accumulators and the K fragments fill the VGPRs; with V also
+  // resident the compiler parked it in AGPRs and copied it back, and had no registers left to
+  // prefetch LDS operands).  Each lane reads back exactly the 16-byte chunks it wrote.
+  constexpr bool VLDS = D == 128;
+  constexpr int VBYTES = VLDS ? 4 * 32 * D * 2 : 16;
+  __shared__ __attribute__((aligned(1024))) char lds[STAGES * STAGE + VBYTES];
 
   const int kt = (int)blockIdx.y;  // smallest key tiles (the most query tiles) first
   const int bk = blockIdx.x, b = bk / Hkv, hk = bk % Hkv, ratio = Hq / Hkv;
@@ -462,12 +468,19 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(OCC, O
   const int kj = k0w + (lane & 31);
   const int64_t krow = b * kl.b + hk * kl.h + (int64_t)min(kj, Lk - 1) * kl.s;
 
-  bf16x8_t kf[KS], vf[KS];
+  bf16x8_t kf[KS], vf[VLDS ? 1 : KS];
+  char* vblk = lds + STAGES * STAGE + wave * 32 * D * 2 + (lane & 31) * D * 2;  // this lane's key row
+  auto voff = [&](int ks) { return ((2 * ks + g) ^ chunk_swz<CPK>(lane & 31)) << 4; };
 #pragma unroll
   for (int ks = 0; ks < KS; ++ks) {
     kf[ks] = as_frag(ld16(K + krow + ks * 16 + g * 8));
-    vf[ks] = as_frag(ld16(V + krow + ks * 16 + g * 8));
+    if constexpr (VLDS) *reinterpret_cast<i32x4*>(vblk + voff(ks)) = ld16(V + krow + ks * 16 + g * 8);
+    else vf[ks] = as_frag(ld16(V + krow + ks * 16 + g * 8));
   }
+  auto vfrag = [&](int ks) {
+    if constexpr (VLDS) return as_frag(*(const volatile __attribute__((address_space(3))) i32x4*)(vblk + voff(ks)));
+    else return vf[ks];
+  };
   f32x16 dk[DT], dv[DT];
 #pragma unroll
   for (int i = 0; i < DT; ++i) dk[i] = dv[i] = zero16();
@@ -569,11 +582,31 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(OCC, O
     const float* side = reinterpret_cast<const float*>(qb + 4 * QB);
     f32x16 s = zero16(), dp = zero16();
     const int qr = lane & 31, qsw = chunk_swz<CPK>(qr);
+    // Operand fragments one k-step ahead: step ks+1's LDS reads are issued before step ks's MFMAs
+    // (scheduling fences keep the order), so a read's latency overlaps the previous MFMAs.
+    auto qoffs = [&](int ks) { return qr * D * 2 + (((ks * 2 + g) ^ qsw) << 4); };
+    // volatile: the reads keep program order (prologue before prefetch), so each wait covers
+    // exactly the fragments the next MFMAs use
+    auto rd = [](const char* p) { return *(const volatile __attribute__((address_space(3))) i32x4*)(p); };
+    i32x4 fq[2], fd[2];
+    bf16x8_t fv[2];
+    fq[0] = rd(qb + qoffs(0));
+    fd[0] = rd(db + qoffs(0));
+    fv[0] = vfrag(0);
+    __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
     for (int ks = 0; ks < KS; ++ks) {
-      const int o = qr * D * 2 + (((ks * 2 + g) ^ qsw) << 4);
-      s = mma<T>(as_frag(*reinterpret_cast<const i32x4*>(qb + o)), kf[ks], s);
-      dp = mma<T>(as_frag(*reinterpret_cast<const i32x4*>(db + o)), vf[ks], dp);
+      const int cur = ks & 1;
+      if (ks + 1 < KS) {
+        fq[cur ^ 1] = rd(qb + qoffs(ks + 1));
+        fd[cur ^ 1] = rd(db + qoffs(ks + 1));
+        fv[cur ^ 1] = vfrag(ks + 1);
+      }
+      if (ks + 1 < KS) __builtin_amdgcn_s_waitcnt((15) | (7 << 4) | (3 << 8) | (3 << 14));  // lgkmcnt(3)
+      __builtin_amdgcn_sched_barrier(0);
+      s = mma<T>(as_frag(fq[cur]), kf[ks], s);
+      dp = mma<T>(as_frag(fd[cur]), fv[cur], dp);
+      __builtin_amdgcn_sched_barrier(0);
     }
     const bool full = k0w + 31 <= q0 + off && q0 + BM - 1 < Lq;
     f32x16 ds;
@@ -597,18 +630,33 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(OCC, O
         ds[v] = p * (dp[v] - side[BM + r]);
       }
     }
+    // dV^T += dO^T P and dK^T += Q^T dS over the tile's 32 queries: (c, dt) pairs in order, the next
+    // pair's two fragments read before the current pair's MFMAs.
+    const bf16x8_t pk[2] = {pack8<T>(s, 0), pack8<T>(s, 8)};
+    const bf16x8_t dk8[2] = {pack8<T>(ds, 0), pack8<T>(ds, 8)};
+    auto toffs = [&](int c, int dt) {
+      const int r = dt * 32 + (lane & 31);
+      return r * BM * 2 + (((2 * c + g) ^ chunk_swz<CPQ>(r)) << 4);
+    };
+    constexpr int NP = (BM / 16) * DT;
+    i32x4 fa[2], fb[2];
+    fa[0] = rd(dtb + toffs(0, 0));
+    fb[0] = rd(qtb + toffs(0, 0));
+    __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-    for (int c = 0; c < BM / 16; ++c) {
-      const bf16x8_t pb = pack8<T>(s, c * 8);
-      const bf16x8_t dsb = pack8<T>(ds, c * 8);
-#pragma unroll
-      for (int dt = 0; dt < DT; ++dt) {
-        const int r = dt * 32 + (lane & 31);
-        const int o = r * BM * 2 + (((2 * c + g) ^ chunk_swz<CPQ>(r)) << 4);
-        const i32x4 va = *reinterpret_cast<const i32x4*>(dtb + o), vb4 = *reinterpret_cast<const i32x4*>(qtb + o);
-        dv[dt] = mma<T>(as_frag(va), pb, dv[dt]);
-        dk[dt] = mma<T>(as_frag(vb4), dsb, dk[dt]);
+    for (int pi = 0; pi < NP; ++pi) {
+      const int c = pi / DT, dt = pi % DT, cur = pi & 1;
+      if (pi + 1 < NP) {
+        const int o = toffs((pi + 1) / DT, (pi + 1) % DT);
+        fa[cur ^ 1] = rd(dtb + o);
+        fb[cur ^ 1] = rd(qtb + o);
       }
+      // the pair's fragments landed; the next pair's two reads may still be in flight
+      if (pi + 1 < NP) __builtin_amdgcn_s_waitcnt((15) | (7 << 4) | (2 << 8) | (3 << 14));  // lgkmcnt(2)
+      __builtin_amdgcn_sched_barrier(0);
+      dv[dt] = mma<T>(as_frag(fa[cur]), pk[c], dv[dt]);
+      dk[dt] = mma<T>(as_frag(fb[cur]), dk8[c], dk[dt]);
+      __builtin_amdgcn_sched_barrier(0);
     }
   }
   if (kj < Lk) {
@@ -857,8 +905,8 @@ int bwd_mfma(const void* q, Lay ql, const void* k, const void* v, Lay kl, const 
                                                    (const u16*)kt, (const u16*)dout, lse, delta, (u16*)dq, Hq, Hkv,
                                                    Lq, Lk, ldkt, scale, scale * kLog2e);
   dim3 g2((unsigned)(B * Hkv), (unsigned)((Lk + 127) / 128));
-  // D = 128: one workgroup per CU either way (registers), so a 4-deep ring costs no occupancy.
-  attn_bwd_dkdv_v2<T, D, (D > 64 ? 1 : 2), (D > 64 ? 4 : 2)><<<g2, kThreads, 0, s>>>((const u16*)q, ql, (const u16*)k, (const u16*)v, kl,
+  // D = 128: one workgroup per CU either way (registers); a 3-deep ring plus the V block fits the LDS.
+  attn_bwd_dkdv_v2<T, D, (D > 64 ? 1 : 2), (D > 64 ? 3 : 2)><<<g2, kThreads, 0, s>>>((const u16*)q, ql, (const u16*)k, (const u16*)v, kl,
                                                   (const u16*)qt, (const u16*)dout, (const u16*)dot, lse, delta,
                                                   (u16*)dk, (u16*)dv, Hq, Hkv, Lq, Lk, ldqt, scale, scale * kLog2e);
   return (int)hipGetLastError();
