@@ -286,11 +286,23 @@ __global__ __launch_bounds__(WM * WN * 64) void gemm_nt_v4_kernel(const u16* __r
         if (kt + STAGES < nk) issue(stage, (kt + STAGES) * BK);
         load((kt + 1) % STAGES, b ^ 1, 0);
       }
-      __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
       for (int i = 0; i < FM; ++i)
 #pragma unroll
         for (int j = 0; j < FN; ++j) acc[i][j] = mfma_16x16x32<T>(bfr[b][j], af[b][i], acc[i][j]);
+      // Spread the step's memory instructions through its MFMAs: one ring refill load per MFMA, then
+      // one fragment read per MFMA (all eight waves issuing their reads and refills in one burst
+      // right after the barrier queued them behind each other; measured 3-5 % faster).
+#pragma unroll
+      for (int q = 0; q < LPW; ++q) {
+        __builtin_amdgcn_sched_group_barrier(0x020, 1, 0);  // VMEM read
+        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // MFMA
+      }
+#pragma unroll
+      for (int q = 0; q < FM + FN; ++q) {
+        __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);  // DS read
+        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // MFMA
+      }
       __builtin_amdgcn_sched_barrier(0);
     }
   };
