@@ -188,6 +188,16 @@ int q3_ce_finish(const float* m_part, const float* s_part, int nchunks, const fl
 int q3_ce_chunk_grad(int dtype, int out_dtype, const void* z, int64_t ld, int64_t n, int64_t col0, const int64_t* tgt,
                      const float* lse, const float* count, const float* up, void* dz, int64_t ldo, int64_t rows,
                      int64_t vocab, int64_t ignore_index, hipStream_t stream);
+/* The logits GEMM and q3_ce_chunk_grad in one kernel: z = A . B^T (A [M, K] token rows, B [N, K] the
+ * chunk's vocabulary rows starting at column col0; K % 64 == 0, 16-byte aligned K-contiguous rows) is
+ * formed in fp32 on the matrix cores and only dz (dtype, row stride lddz) is written, with the same
+ * expression as q3_ce_chunk_grad; up may be null (1).  The backward of the fused LM-head + CE.
+ * Replaces: kernels/loss.py:34-44,64-68 (_backward) together with the logits matmul of
+ * _model.py:131-132 (no single reference function). */
+int q3_gemm_nt_ce_grad(int dtype, const void* A, int64_t lda, const void* B, int64_t ldb, void* dz, int64_t lddz,
+                       int64_t M, int64_t N, int64_t K, int64_t col0, const int64_t* tgt, const float* lse,
+                       const float* count, const float* up, int64_t vocab, int64_t ignore_index,
+                       hipStream_t stream);
 
 /* ------------------------------------------------------------------ greedy decode
  * y[m, n] = sum_k x[m, k] * W[n, k] for m < M <= 16 (x rows at stride ldx, y rows at stride ldy),

@@ -174,12 +174,24 @@ template <int CPR> Q3_DEV int gemm_swz(int r) {
   else return swz4(r);
 }
 
-template <typename T, typename O, int BM, int BN, int WM, int WN, int BK, int STAGES, bool EVEN>
+// Cross-entropy gradient epilogue (EPI = 1): the tile is a chunk of logits z[m, col0 + n] and the
+// kernel stores dz = (exp(z - lse[m]) - [col0 + n == tgt[m]]) * (*up) / (*count) instead, 0 for rows
+// whose target is ignore_index or outside [0, vocab) (the fp32 logits never reach memory).
+struct CeEpi {
+  const int64_t* tgt;
+  const float* lse;
+  const float* count;
+  const float* up;
+  int64_t col0, vocab, ignore;
+};
+
+template <typename T, typename O, int BM, int BN, int WM, int WN, int BK, int STAGES, bool EVEN, int EPI = 0>
 __global__ __launch_bounds__(WM * WN * 64) void gemm_nt_v4_kernel(const u16* __restrict__ A,
                                                                   const u16* __restrict__ B,
                                                                   typename O::storage* __restrict__ C, int M, int N,
                                                                   int K, int64_t lda, int64_t ldb, int64_t ldc,
-                                                                  float alpha, int accumulate, int vec_store) {
+                                                                  float alpha, int accumulate, int vec_store,
+                                                                  CeEpi ce) {
   static_assert(BK == 64 || BK == 32, "k tile");
   constexpr int NW = WM * WN, ROWB = BK * 2, CPR = BK / 8, RPL = 64 / CPR;
   constexpr int TMW = BM / WM, TNW = BN / WN, FM = TMW / 16, FN = TNW / 16;
@@ -323,12 +335,25 @@ __global__ __launch_bounds__(WM * WN * 64) void gemm_nt_v4_kernel(const u16* __r
     const int row = m0 + wm * TMW + i * 16 + (lane & 15);
     if (row >= M) continue;
     typename O::storage* crow = C + (int64_t)row * ldc;
+    [[maybe_unused]] int64_t t = 0;
+    [[maybe_unused]] float lse = 0.f, scale = 0.f;
+    if constexpr (EPI == 1) {
+      t = ce.tgt[row];
+      lse = ce.lse[row];
+      const bool valid = t != ce.ignore && t >= 0 && t < ce.vocab;
+      scale = valid ? (ce.up ? *ce.up : 1.f) / *ce.count : 0.f;
+    }
 #pragma unroll
     for (int j = 0; j < FN; ++j) {
       const int col = n0 + wn * TNW + j * 16 + 4 * quarter;
       float r[4];
 #pragma unroll
-      for (int v = 0; v < 4; ++v) r[v] = alpha * acc[i][j][v];
+      for (int v = 0; v < 4; ++v) {
+        if constexpr (EPI == 1)
+          r[v] = scale != 0.f ? (__expf(acc[i][j][v] - lse) - ((col + v + ce.col0 == t) ? 1.f : 0.f)) * scale : 0.f;
+        else
+          r[v] = alpha * acc[i][j][v];
+      }
       if (vec_store && col + 3 < N) {
         if constexpr (O::vec == 4) {
           f32x4* p = reinterpret_cast<f32x4*>(crow + col);
@@ -363,14 +388,27 @@ __global__ __launch_bounds__(WM * WN * 64) void gemm_nt_v4_kernel(const u16* __r
   }
 }
 
-template <typename T, typename O, int BM, int BN, int WM, int WN, int ST, bool EVEN, int BK = 64>
+template <typename T, typename O, int BM, int BN, int WM, int WN, int ST, bool EVEN, int BK = 64, int EPI = 0>
 int launch_v4(const void* A, int64_t lda, const void* B, int64_t ldb, void* C, int64_t ldc, int64_t M, int64_t N,
-              int64_t K, float alpha, int acc, hipStream_t s) {
+              int64_t K, float alpha, int acc, hipStream_t s, CeEpi ce = CeEpi{}) {
   const int64_t tiles = ((M + BM - 1) / BM) * ((N + BN - 1) / BN);
   const int vec = (ldc % 4 == 0) && (((uintptr_t)C & (O::vec == 4 ? 15 : 7)) == 0);
-  gemm_nt_v4_kernel<T, O, BM, BN, WM, WN, BK, ST, EVEN><<<(unsigned)tiles, WM * WN * 64, 0, s>>>(
-      (const u16*)A, (const u16*)B, (typename O::storage*)C, (int)M, (int)N, (int)K, lda, ldb, ldc, alpha, acc, vec);
+  gemm_nt_v4_kernel<T, O, BM, BN, WM, WN, BK, ST, EVEN, EPI><<<(unsigned)tiles, WM * WN * 64, 0, s>>>(
+      (const u16*)A, (const u16*)B, (typename O::storage*)C, (int)M, (int)N, (int)K, lda, ldb, ldc, alpha, acc, vec,
+      ce);
   return (int)hipGetLastError();
+}
+
+// Tile choice of launch_nt's K % 64 == 0 path, with the cross-entropy gradient epilogue.
+template <typename T>
+int launch_ce_grad(const void* A, int64_t lda, const void* B, int64_t ldb, void* dz, int64_t lddz, int64_t M,
+                   int64_t N, int64_t K, const CeEpi& ce, hipStream_t s) {
+  if (((M + 255) / 256) * ((N + 255) / 256) >= 256) {
+    if (M % 256 == 0 && N % 256 == 0)
+      return launch_v4<T, T, 256, 256, 4, 2, 2, true, 64, 1>(A, lda, B, ldb, dz, lddz, M, N, K, 1.f, 0, s, ce);
+    return launch_v4<T, T, 256, 256, 4, 2, 2, false, 64, 1>(A, lda, B, ldb, dz, lddz, M, N, K, 1.f, 0, s, ce);
+  }
+  return launch_v4<T, T, 128, 128, 2, 2, 4, false, 64, 1>(A, lda, B, ldb, dz, lddz, M, N, K, 1.f, 0, s, ce);
 }
 
 // ---------------------------------------------------------------- strided SIMT fallback
@@ -507,6 +545,18 @@ int q3_gemm_nt(int in_dtype, int out_dtype, const void* A, int64_t lda, const vo
   Q3_REQUIRE(tiles < (1ll << 31));
   if (in_dtype == Q3_BF16) return nt_out<BF16>(out_dtype, A, lda, B, ldb, C, ldc, M, N, K, alpha, accumulate, stream);
   return nt_out<F16>(out_dtype, A, lda, B, ldb, C, ldc, M, N, K, alpha, accumulate, stream);
+}
+
+int q3_gemm_nt_ce_grad(int dtype, const void* A, int64_t lda, const void* B, int64_t ldb, void* dz, int64_t lddz,
+                       int64_t M, int64_t N, int64_t K, int64_t col0, const int64_t* tgt, const float* lse,
+                       const float* count, const float* up, int64_t vocab, int64_t ignore_index,
+                       hipStream_t stream) {
+  Q3_REQUIRE((dtype == Q3_BF16 || dtype == Q3_F16) && A && B && dz && tgt && lse && count);
+  Q3_REQUIRE(M > 0 && N > 0 && K > 0 && M < (1ll << 31) && N < (1ll << 31) && K < (1ll << 31) && K % 64 == 0);
+  Q3_REQUIRE(lda % 8 == 0 && ldb % 8 == 0 && lda >= K && ldb >= K && lddz >= N && al16(A) && al16(B));
+  const CeEpi ce{tgt, lse, count, up, col0, vocab, ignore_index};
+  if (dtype == Q3_BF16) return launch_ce_grad<BF16>(A, lda, B, ldb, dz, lddz, M, N, K, ce, stream);
+  return launch_ce_grad<F16>(A, lda, B, ldb, dz, lddz, M, N, K, ce, stream);
 }
 
 int q3_gemm_strided(int in_dtype, int out_dtype, const void* A, int64_t sam, int64_t sak, const void* B, int64_t sbk,

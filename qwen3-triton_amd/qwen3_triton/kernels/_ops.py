@@ -297,6 +297,15 @@ class CEState:
         return self.loss
 
 
+def gemm_ce_grad(x, w, col0, n, tgt, lse, count, up, dz, vocab, ignore_index):
+    """dz[:, :n] = CE gradient of the logits x . w[col0:col0+n]^T (matrix cores; fp32 logits stay in
+    registers).  x [T, H] and w [V, H] K-contiguous bf16/fp16, H % 64 == 0."""
+    t, h = x.shape
+    H.call("q3_gemm_nt_ce_grad", H.code(x.dtype), x.data_ptr(), x.stride(0), w[col0:].data_ptr(), w.stride(0),
+           dz.data_ptr(), dz.stride(0), t, n, h, col0, tgt.data_ptr(), lse.data_ptr(), count.data_ptr(),
+           0 if up is None else up.data_ptr(), vocab, int(ignore_index), H.stream())
+
+
 def ce_grad(z, ld, n, col0, tgt, lse, count, up, dz, ldo, vocab, ignore_index):
     rows = tgt.numel()
     H.call("q3_ce_chunk_grad", H.code(z.dtype), H.code(dz.dtype), z.data_ptr(), ld, n, col0, tgt.data_ptr(),

@@ -65,19 +65,23 @@ class _LMHeadCE(torch.autograd.Function):
         v, t, chunk = weight.shape[0], b * s, ctx.chunk
         x = hidden.view(t, h)
         up = dy.float().contiguous()
-        zbuf = torch.empty((t, chunk), device=x.device, dtype=torch.float32)
         dz = torch.empty((t, chunk), device=x.device, dtype=x.dtype)
         dx = torch.empty((t, h), device=x.device, dtype=torch.float32)
         dw = torch.empty_like(weight)
         mfma = _mfma_ok(x, weight) and t % 8 == 0
+        zbuf = None if (mfma and h % 64 == 0) else torch.empty((t, chunk), device=x.device, dtype=torch.float32)
         if mfma:
             wt = _ops.transpose_last2(weight, pad_to=8)   # [H, Vp]
             xt = _ops.transpose_last2(x)                  # [H, T]
+        fused = mfma and h % 64 == 0
         for c in range(-(-v // chunk)):
             c0 = c * chunk
             n = min(chunk, v - c0)
-            _chunk_logits(x, weight, c0, n, zbuf)
-            _ops.ce_grad(zbuf, chunk, n, c0, tgt, lse, count, up, dz, chunk, v, ctx.ignore)
+            if fused:   # logits GEMM with the CE-gradient epilogue: dz directly, no fp32 logits in memory
+                _ops.gemm_ce_grad(x, weight, c0, n, tgt, lse, count, up, dz, v, ctx.ignore)
+            else:
+                _chunk_logits(x, weight, c0, n, zbuf)
+                _ops.ce_grad(zbuf, chunk, n, c0, tgt, lse, count, up, dz, chunk, v, ctx.ignore)
             if mfma:
                 gemm_nt_into(dz, chunk, wt[:, c0:], wt.shape[1], dx, t, h, n, accumulate=c > 0)
                 dzt = _ops.transpose_last2(dz)            # [chunk, T]

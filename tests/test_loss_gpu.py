@@ -110,3 +110,31 @@ def test_lm_head_ce_config_shape_sampled_rows():
     pc *= (tall != -100).double()[:, None] / count
     edw = pc.t() @ x.view(-1, h).double()
     assert cosine(dw[vids.cuda()], edw) >= 0.999
+
+
+@pytest.mark.parametrize("t,h,n,col0,with_up", [(512, 256, 1000, 3000, True), (300, 128, 4096, 0, False),
+                                                (1024, 512, 2304, 8192, True)])
+def test_fused_ce_grad_gemm_matches_two_step(t, h, n, col0, with_up):
+    """The logits GEMM with the CE-gradient epilogue writes bit-for-bit the dz of the unfused path
+    (fp32 logits from the GEMM, then the CE gradient kernel), including ignored and out-of-range rows."""
+    print(f"fused ce grad t={t} h={h} n={n} col0={col0}", flush=True)
+    gen = seeded(t + n)
+    v = col0 + n + 17
+    x = randn(t, h, gen=gen, dtype=torch.bfloat16).cuda()
+    w = (randn(v, h, gen=gen) * 0.05).to(torch.bfloat16).cuda()
+    tgt = torch.randint(0, v, (t,), generator=gen)
+    tgt[::7] = -100                      # ignored
+    tgt[1::11] = col0 + torch.randint(0, n, (len(tgt[1::11]),), generator=gen)   # targets in this chunk
+    tgt[5] = v + 3                       # out of range: treated as ignored here
+    tgt = tgt.cuda()
+    lse = (randn(t, gen=gen) + 4.0).cuda()
+    count = torch.tensor([float((tgt != -100).sum())], device="cuda")
+    up = torch.tensor([0.75], device="cuda") if with_up else None
+    dz_fused = torch.full((t, n + 8), 7.0, device="cuda", dtype=torch.bfloat16)
+    _ops.gemm_ce_grad(x, w, col0, n, tgt, lse, count, up, dz_fused, v, -100)
+    z = torch.empty(t, n, device="cuda", dtype=torch.float32)
+    _chunk_logits(x, w, col0, n, z)
+    dz_ref = torch.empty(t, n, device="cuda", dtype=torch.bfloat16)
+    _ops.ce_grad(z, n, n, col0, tgt, lse, count, up, dz_ref, n, v, -100)
+    assert torch.equal(dz_fused[:, :n].cpu(), dz_ref.cpu())
+    assert torch.all(dz_fused[:, n:].float() == 7.0)          # columns past n untouched
