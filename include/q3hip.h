@@ -198,6 +198,16 @@ int q3_gemm_nt_ce_grad(int dtype, const void* A, int64_t lda, const void* B, int
                        int64_t M, int64_t N, int64_t K, int64_t col0, const int64_t* tgt, const float* lse,
                        const float* count, const float* up, int64_t vocab, int64_t ignore_index,
                        hipStream_t stream);
+/* The logits GEMM and q3_ce_chunk_stats in one kernel: z = A . B^T as above; per row and per group
+ * of 128 logit columns g (g = 0 .. ceil(N / 128) - 1), m_part[(part0 + g) * ldp + row] and
+ * s_part[...] receive the group's max and sum of exp(z - max), and pick[row] the logit of column
+ * tgt[row] - col0 when it lies in [0, N).  q3_ce_finish then merges all groups of all chunks as
+ * its nchunks partials.  The forward of the fused LM-head + CE.
+ * Replaces: kernels/loss.py:6-33,55-61 (_partials, _rows) together with the logits matmul of
+ * _model.py:131-132 (no single reference function). */
+int q3_gemm_nt_ce_stats(int dtype, const void* A, int64_t lda, const void* B, int64_t ldb, int64_t M, int64_t N,
+                        int64_t K, int64_t col0, const int64_t* tgt, float* m_part, float* s_part, float* pick,
+                        int64_t part0, int64_t ldp, hipStream_t stream);
 
 /* ------------------------------------------------------------------ greedy decode
  * y[m, n] = sum_k x[m, k] * W[n, k] for m < M <= 16 (x rows at stride ldx, y rows at stride ldy),

@@ -177,13 +177,27 @@ template <int CPR> Q3_DEV int gemm_swz(int r) {
 // Cross-entropy gradient epilogue (EPI = 1): the tile is a chunk of logits z[m, col0 + n] and the
 // kernel stores dz = (exp(z - lse[m]) - [col0 + n == tgt[m]]) * (*up) / (*count) instead, 0 for rows
 // whose target is ignore_index or outside [0, vocab) (the fp32 logits never reach memory).
+// Statistics epilogue (EPI = 2, 128 columns per wave): per row and 128-column group p (= part0 +
+// global column group of the tile), m_part[p * ldp + row] / s_part[...] get the group's max and
+// sum of exp(z - max), and pick[row] the logit of column tgt[row] - col0 when it lies in this chunk.
 struct CeEpi {
   const int64_t* tgt;
   const float* lse;
   const float* count;
   const float* up;
   int64_t col0, vocab, ignore;
+  float* m_part;
+  float* s_part;
+  float* pick;
+  int64_t part0, ldp;
 };
+
+Q3_DEV void lse_merge(float& m, float& s, float m2, float s2) {
+  const float mn = fmaxf(m, m2);
+  if (mn == -INFINITY) return;
+  s = s * __expf(m - mn) + s2 * __expf(m2 - mn);
+  m = mn;
+}
 
 template <typename T, typename O, int BM, int BN, int WM, int WN, int BK, int STAGES, bool EVEN, int EPI = 0>
 __global__ __launch_bounds__(WM * WN * 64) void gemm_nt_v4_kernel(const u16* __restrict__ A,
@@ -330,6 +344,41 @@ __global__ __launch_bounds__(WM * WN * 64) void gemm_nt_v4_kernel(const u16* __r
   }
 
   // ---- epilogue: lane owns row m and 4 consecutive columns of each 16x16 block (C^T layout)
+  if constexpr (EPI == 2) {
+    static_assert(TNW == 128, "one statistics partial per 128 columns");
+    const int64_t part = ce.part0 + (n0 + wn * TNW) / 128;
+#pragma unroll
+    for (int i = 0; i < FM; ++i) {
+      const int row = m0 + wm * TMW + i * 16 + (lane & 15);
+      const int64_t t = row < M ? ce.tgt[row] - ce.col0 : -1;  // target column within this chunk
+      float mx = -INFINITY;
+#pragma unroll
+      for (int j = 0; j < FN; ++j)
+#pragma unroll
+        for (int v = 0; v < 4; ++v)
+          if (n0 + wn * TNW + j * 16 + 4 * quarter + v < N) mx = fmaxf(mx, acc[i][j][v]);
+      float sm = 0.f;
+#pragma unroll
+      for (int j = 0; j < FN; ++j)
+#pragma unroll
+        for (int v = 0; v < 4; ++v) {
+          const int col = n0 + wn * TNW + j * 16 + 4 * quarter + v;
+          if (col < N) {
+            sm += mx == -INFINITY ? 0.f : __expf(acc[i][j][v] - mx);
+            if (col == t) ce.pick[row] = acc[i][j][v];
+          }
+        }
+      // the four lanes of a row (quarters) hold 32 columns each
+#pragma unroll
+      for (int o = 16; o < 64; o <<= 1) lse_merge(mx, sm, __shfl_xor(mx, o, 64), __shfl_xor(sm, o, 64));
+      // a group that starts past N (the second half of a ragged last tile) has no partial slot
+      if (quarter == 0 && row < M && n0 + wn * TNW < N) {
+        ce.m_part[part * ce.ldp + row] = mx;
+        ce.s_part[part * ce.ldp + row] = sm;
+      }
+    }
+    return;
+  }
 #pragma unroll
   for (int i = 0; i < FM; ++i) {
     const int row = m0 + wm * TMW + i * 16 + (lane & 15);
@@ -397,6 +446,15 @@ int launch_v4(const void* A, int64_t lda, const void* B, int64_t ldb, void* C, i
       (const u16*)A, (const u16*)B, (typename O::storage*)C, (int)M, (int)N, (int)K, lda, ldb, ldc, alpha, acc, vec,
       ce);
   return (int)hipGetLastError();
+}
+
+// 256 x 256 tiles (128 columns per wave) with the cross-entropy statistics epilogue.
+template <typename T>
+int launch_ce_stats(const void* A, int64_t lda, const void* B, int64_t ldb, int64_t M, int64_t N, int64_t K,
+                    const CeEpi& ce, hipStream_t s) {
+  if (M % 256 == 0 && N % 256 == 0)
+    return launch_v4<T, T, 256, 256, 4, 2, 2, true, 64, 2>(A, lda, B, ldb, nullptr, N, M, N, K, 1.f, 0, s, ce);
+  return launch_v4<T, T, 256, 256, 4, 2, 2, false, 64, 2>(A, lda, B, ldb, nullptr, N, M, N, K, 1.f, 0, s, ce);
 }
 
 // Tile choice of launch_nt's K % 64 == 0 path, with the cross-entropy gradient epilogue.
@@ -554,9 +612,20 @@ int q3_gemm_nt_ce_grad(int dtype, const void* A, int64_t lda, const void* B, int
   Q3_REQUIRE((dtype == Q3_BF16 || dtype == Q3_F16) && A && B && dz && tgt && lse && count);
   Q3_REQUIRE(M > 0 && N > 0 && K > 0 && M < (1ll << 31) && N < (1ll << 31) && K < (1ll << 31) && K % 64 == 0);
   Q3_REQUIRE(lda % 8 == 0 && ldb % 8 == 0 && lda >= K && ldb >= K && lddz >= N && al16(A) && al16(B));
-  const CeEpi ce{tgt, lse, count, up, col0, vocab, ignore_index};
+  const CeEpi ce{tgt, lse, count, up, col0, vocab, ignore_index, nullptr, nullptr, nullptr, 0, 0};
   if (dtype == Q3_BF16) return launch_ce_grad<BF16>(A, lda, B, ldb, dz, lddz, M, N, K, ce, stream);
   return launch_ce_grad<F16>(A, lda, B, ldb, dz, lddz, M, N, K, ce, stream);
+}
+
+int q3_gemm_nt_ce_stats(int dtype, const void* A, int64_t lda, const void* B, int64_t ldb, int64_t M, int64_t N,
+                        int64_t K, int64_t col0, const int64_t* tgt, float* m_part, float* s_part, float* pick,
+                        int64_t part0, int64_t ldp, hipStream_t stream) {
+  Q3_REQUIRE((dtype == Q3_BF16 || dtype == Q3_F16) && A && B && tgt && m_part && s_part && pick);
+  Q3_REQUIRE(M > 0 && N > 0 && K > 0 && M < (1ll << 31) && N < (1ll << 31) && K < (1ll << 31) && K % 64 == 0);
+  Q3_REQUIRE(lda % 8 == 0 && ldb % 8 == 0 && lda >= K && ldb >= K && ldp >= M && part0 >= 0 && al16(A) && al16(B));
+  const CeEpi ce{tgt, nullptr, nullptr, nullptr, col0, 0, 0, m_part, s_part, pick, part0, ldp};
+  if (dtype == Q3_BF16) return launch_ce_stats<BF16>(A, lda, B, ldb, M, N, K, ce, stream);
+  return launch_ce_stats<F16>(A, lda, B, ldb, M, N, K, ce, stream);
 }
 
 int q3_gemm_strided(int in_dtype, int out_dtype, const void* A, int64_t sam, int64_t sak, const void* B, int64_t sbk,

@@ -286,6 +286,14 @@ class CEState:
         H.call("q3_ce_chunk_stats", H.code(z.dtype), z.data_ptr(), ld, n, col0, tgt.data_ptr(),
                self.m[chunk].data_ptr(), self.s[chunk].data_ptr(), self.pick.data_ptr(), self.rows, H.stream())
 
+    def gemm_stats(self, part0, x, w, col0, n, tgt):
+        """Logits x . w[col0:col0+n]^T and their statistics in one matrix-core kernel: partials
+        part0 .. part0 + ceil(n / 128) - 1 (128 logit columns each) and the target logits."""
+        t, h = x.shape
+        H.call("q3_gemm_nt_ce_stats", H.code(x.dtype), x.data_ptr(), x.stride(0), w[col0:].data_ptr(), w.stride(0),
+               t, n, h, col0, tgt.data_ptr(), self.m.data_ptr(), self.s.data_ptr(), self.pick.data_ptr(), part0,
+               self.rows, H.stream())
+
     def finish(self, tgt, vocab, ignore_index, check=True):
         capturing = torch.cuda.is_current_stream_capturing()
         bad = None if (capturing or not check) else torch.zeros((), device=tgt.device, dtype=torch.int32)

@@ -46,13 +46,24 @@ class _LMHeadCE(torch.autograd.Function):
         tgt = _ops.ce_shift_labels(labels, ignore_index)
         chunk = min(chunk, v)
         nch = -(-v // chunk)
-        st = _ops.CEState(b * s, nch, hidden.device)
-        zbuf = torch.empty((b * s, chunk), device=hidden.device, dtype=torch.float32)
-        for c in range(nch):
-            c0 = c * chunk
-            n = min(chunk, v - c0)
-            _chunk_logits(x, weight, c0, n, zbuf)
-            st.stats(c, zbuf, chunk, n, c0, tgt)
+        if _mfma_ok(hidden, weight) and h % 64 == 0:
+            # logits GEMM with the statistics epilogue: one partial per 128 logit columns, no fp32
+            # logits in memory
+            groups = [-(-min(chunk, v - c * chunk) // 128) for c in range(nch)]
+            st = _ops.CEState(b * s, sum(groups), hidden.device)
+            part0 = 0
+            for c in range(nch):
+                c0 = c * chunk
+                st.gemm_stats(part0, x, weight, c0, min(chunk, v - c0), tgt)
+                part0 += groups[c]
+        else:
+            st = _ops.CEState(b * s, nch, hidden.device)
+            zbuf = torch.empty((b * s, chunk), device=hidden.device, dtype=torch.float32)
+            for c in range(nch):
+                c0 = c * chunk
+                n = min(chunk, v - c0)
+                _chunk_logits(x, weight, c0, n, zbuf)
+                st.stats(c, zbuf, chunk, n, c0, tgt)
         loss = st.finish(tgt, v, ignore_index)
         ctx.save_for_backward(hidden, weight, tgt, st.lse, st.count)
         ctx.ignore, ctx.chunk = ignore_index, chunk

@@ -138,3 +138,35 @@ def test_fused_ce_grad_gemm_matches_two_step(t, h, n, col0, with_up):
     _ops.ce_grad(z, n, n, col0, tgt, lse, count, up, dz_ref, n, v, -100)
     assert torch.equal(dz_fused[:, :n].cpu(), dz_ref.cpu())
     assert torch.all(dz_fused[:, n:].float() == 7.0)          # columns past n untouched
+
+
+@pytest.mark.parametrize("t,h,v,chunk", [(512, 256, 5000, 2048), (300, 128, 4096, 4096), (1024, 512, 9000, 4100),
+                                         (256, 64, 8576, 4096)])
+def test_fused_ce_stats_gemm_matches_two_step(t, h, v, chunk):
+    """The logits GEMM with the statistics epilogue (one partial per 128 logit columns) gives the same
+    lse and loss as fp32 logits + the chunk statistics kernel, to fp32 rounding of the merge order."""
+    print(f"fused ce stats t={t} h={h} v={v} chunk={chunk}", flush=True)
+    gen = seeded(t + v)
+    x = randn(t, h, gen=gen, dtype=torch.bfloat16).cuda()
+    w = (randn(v, h, gen=gen) * 0.05).to(torch.bfloat16).cuda()
+    tgt = torch.randint(0, v, (t,), generator=gen)
+    tgt[::9] = -100
+    tgt = tgt.cuda()
+    nch = -(-v // chunk)
+    groups = [-(-min(chunk, v - c * chunk) // 128) for c in range(nch)]
+    fused = _ops.CEState(t, sum(groups), x.device)
+    part0 = 0
+    for c in range(nch):
+        fused.gemm_stats(part0, x, w, c * chunk, min(chunk, v - c * chunk), tgt)
+        part0 += groups[c]
+    loss_f = fused.finish(tgt, v, -100).clone()
+    ref = _ops.CEState(t, nch, x.device)
+    z = torch.empty(t, chunk, device="cuda", dtype=torch.float32)
+    for c in range(nch):
+        n = min(chunk, v - c * chunk)
+        _chunk_logits(x, w, c * chunk, n, z)
+        ref.stats(c, z, chunk, n, c * chunk, tgt)
+    loss_r = ref.finish(tgt, v, -100).clone()
+    valid = (tgt != -100).cpu()
+    assert max_rel(fused.lse.cpu()[valid], ref.lse.cpu()[valid].double()) < 1e-6
+    assert abs(float(loss_f) - float(loss_r)) <= 1e-6 * abs(float(loss_r))
