@@ -76,23 +76,40 @@ class _LMHeadCE(torch.autograd.Function):
         v, t, chunk = weight.shape[0], b * s, ctx.chunk
         x = hidden.view(t, h)
         up = dy.float().contiguous()
-        dz = torch.empty((t, chunk), device=x.device, dtype=x.dtype)
-        dx = torch.empty((t, h), device=x.device, dtype=torch.float32)
         dw = torch.empty_like(weight)
         mfma = _mfma_ok(x, weight) and t % 8 == 0
-        zbuf = None if (mfma and h % 64 == 0) else torch.empty((t, chunk), device=x.device, dtype=torch.float32)
+        if mfma and h % 64 == 0:
+            # Every chunk's dz lands in one [T, Vp] buffer (Vp = V rounded up to 64, zero pad) written
+            # by the logits GEMM's CE-gradient epilogue; dW_c = dz_c^T . x per chunk, and dX = dz . W
+            # in one GEMM over the whole vocabulary at the end (bf16 out, no fp32 accumulation passes).
+            vp = -(-v // 64) * 64
+            wt = _ops.transpose_last2(weight, pad_to=64)  # [H, Vp]
+            xt = _ops.transpose_last2(x)                  # [H, T]
+            dz = torch.empty((t, vp), device=x.device, dtype=x.dtype)
+            if vp > v:
+                dz[:, v:].zero_()
+            dzt = torch.empty((chunk, t), device=x.device, dtype=x.dtype)
+            for c in range(-(-v // chunk)):
+                c0 = c * chunk
+                n = min(chunk, v - c0)
+                dzc = dz[:, c0:c0 + n]
+                _ops.gemm_ce_grad(x, weight, c0, n, tgt, lse, count, up, dzc, v, ctx.ignore)
+                _ops.transpose_into(dzc, dzt[:n])
+                gemm_nt_into(dzt, t, xt, t, dw[c0:c0 + n], n, h, t)
+            dx = torch.empty((t, h), device=x.device, dtype=x.dtype)
+            gemm_nt_into(dz, vp, wt, vp, dx, t, h, vp)
+            return dx.view(b, s, h), dw, None, None, None
+        zbuf = torch.empty((t, chunk), device=x.device, dtype=torch.float32)
+        dz = torch.empty((t, chunk), device=x.device, dtype=x.dtype)
+        dx = torch.empty((t, h), device=x.device, dtype=torch.float32)
         if mfma:
             wt = _ops.transpose_last2(weight, pad_to=8)   # [H, Vp]
             xt = _ops.transpose_last2(x)                  # [H, T]
-        fused = mfma and h % 64 == 0
         for c in range(-(-v // chunk)):
             c0 = c * chunk
             n = min(chunk, v - c0)
-            if fused:   # logits GEMM with the CE-gradient epilogue: dz directly, no fp32 logits in memory
-                _ops.gemm_ce_grad(x, weight, c0, n, tgt, lse, count, up, dz, v, ctx.ignore)
-            else:
-                _chunk_logits(x, weight, c0, n, zbuf)
-                _ops.ce_grad(zbuf, chunk, n, c0, tgt, lse, count, up, dz, chunk, v, ctx.ignore)
+            _chunk_logits(x, weight, c0, n, zbuf)
+            _ops.ce_grad(zbuf, chunk, n, c0, tgt, lse, count, up, dz, chunk, v, ctx.ignore)
             if mfma:
                 gemm_nt_into(dz, chunk, wt[:, c0:], wt.shape[1], dx, t, h, n, accumulate=c > 0)
                 dzt = _ops.transpose_last2(dz)            # [chunk, T]
