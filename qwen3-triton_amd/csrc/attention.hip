@@ -34,6 +34,8 @@ template <> Q3_DEV f32x16 mma<F16>(bf16x8_t a, bf16x8_t b, f32x16 c) {
                                                  0, 0);
 }
 
+template <typename T> Q3_DEV f32x4 mma16(bf16x8_t a, bf16x8_t b, f32x4 c) { return mfma_16x16x32<T>(a, b, c); }
+
 Q3_DEV f32x16 zero16() {
   f32x16 z;
 #pragma unroll
@@ -248,6 +250,344 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2, 2))
         *reinterpret_cast<i32x2*>(orow + d) = w;
       }
     if (g == 0) LSE[(int64_t)bh * Lq + qi] = (m + __log2f(l)) * kLn2;
+  }
+}
+
+// ============================================================================ forward, D = 128 (MFMA 16x16x32)
+// Workgroup: 8 waves sharing one KV head: wave w serves query head hk*GRP + (w % GH) (GH heads of
+// the GQA group per workgroup) and 32 query positions q0 .. q0+31 (8/GH position groups), so every
+// K/V tile in LDS feeds 256 query rows.  Scores are computed transposed, S^T = K Q^T, in 16x16
+// tiles: lane (G = lane/16, r16 = lane%16) owns queries q0 + r16 and q0 + 16 + r16 and holds 4 keys
+// of each 16-key tile.  Which K row feeds MFMA row r is chosen so that the two tiles of a 32-key
+// step hand over P in exactly the key order of a 16-byte chunk of the permuted V^T copy
+// (positions 0-3, 8-11, 4-7, 12-15 of every 16-block): P is the B operand of P.V as it comes out
+// of the exponentials.  Row statistics need one max over the 4 lanes of a query (gfx950
+// permlane16/32 swaps); the row sums stay per lane until the end.
+// Online softmax with a lazy rescale: the running max m (raw score units) moves only when a block
+// max exceeds it by more than 8 / scale2 (a factor 2^8 in p), so O is rarely rescaled; p <= 2^8
+// is exact in fp32 and in the bf16/fp16 P operand range.
+// Pipeline per 64-key block j: P(j-1).V(j-1) and S(j+1) = K(j+1).Q^T run on the matrix cores while
+// softmax(S(j)) runs on the VALU; steady-state blocks (unmasked, both neighbours present) are one
+// basic block of 8 fenced steps, each with 8 MFMAs, the next step's 4 operand fragments and one
+// part of the softmax.  K and V^T tiles go global -> LDS with direct-to-LDS loads into 2-stage
+// rings, issued one block ahead.
+Q3_DEV float xmax4(float x) {  // max over lanes {l, l^16, l^32, l^48}
+  auto a = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  x = __builtin_fmaxf(__uint_as_float(a[0]), __uint_as_float(a[1]));
+  auto c = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  return __builtin_fmaxf(__uint_as_float(c[0]), __uint_as_float(c[1]));
+}
+Q3_DEV float xsum4(float x) {  // sum over lanes {l, l^16, l^32, l^48}
+  auto a = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  x = __uint_as_float(a[0]) + __uint_as_float(a[1]);
+  auto c = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  return __uint_as_float(c[0]) + __uint_as_float(c[1]);
+}
+// LDS swizzles (16-byte chunk index XOR): K rows (16 chunks) by rows {0-7, 16-23} / {8-15, 24-31}
+// of each 32-row group, V^T rows (8 chunks) by row pair.
+Q3_DEV int kswz3(int r) { return (r & 7) | (((r >> 4) & 1) << 3); }
+Q3_DEV int vswz3(int r) { return (r >> 1) & 7; }
+
+template <typename T, int GH>
+__global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) void attn_fwd_v3(
+    const u16* __restrict__ Q, Lay ql, const u16* __restrict__ K, Lay kl, const u16* __restrict__ Vt,
+    u16* __restrict__ O, float* __restrict__ LSE, int Hq, int Hkv, int Lq, int Lk, int ldvt, float scale2) {
+  constexpr int D = 128, BN = 64, NW = 8, QT = 32 * (NW / GH);
+  constexpr int KST = BN * D * 2, VST = D * BN * 2;
+  __shared__ __attribute__((aligned(1024))) char lds[2 * KST + 2 * VST];
+  char* const kring = lds;
+  char* const vring = lds + 2 * KST;
+
+  const int nqt = (Lq + QT - 1) / QT;
+  const int qt = nqt - 1 - (int)blockIdx.y;  // longest query tiles first
+  const int tid = threadIdx.x, lane = tid & 63, G = lane >> 4, r16 = lane & 15;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int HB = Hq / GH, b = (int)blockIdx.x / HB, h = ((int)blockIdx.x % HB) * GH + wave % GH;
+  const int hk = h / (Hq / Hkv), bh = b * Hq + h;
+  const int off = Lk - Lq;
+  const int q0 = qt * QT + (wave / GH) * 32;
+  const u16* Qb = Q + b * ql.b + h * ql.h;
+  const u16* Kb = K + b * kl.b + hk * kl.h;
+  const u16* Vb = Vt + (int64_t)(b * Hkv + hk) * D * ldvt;
+
+  bf16x8_t qf[2][4];
+#pragma unroll
+  for (int u = 0; u < 2; ++u)
+#pragma unroll
+    for (int ks = 0; ks < 4; ++ks)
+      qf[u][ks] = as_frag(ld16(Qb + (int64_t)min(q0 + 16 * u + r16, Lq - 1) * ql.s + 32 * ks + 8 * G));
+
+  const int nb = (min(Lk, min(qt * QT + QT - 1, Lq - 1) + off + 1) + BN - 1) / BN;  // workgroup blocks
+  const int nbw = min(nb, (min(Lk, min(q0 + 31, Lq - 1) + off + 1) + BN - 1) / BN);  // this wave's
+  const int qfirst_w = q0 + off;
+  const int nfull = min(nbw, max(0, (qfirst_w + 1) / BN));  // blocks fully visible to the wave
+  const int qpos[2] = {q0 + r16 + off, q0 + 16 + r16 + off};
+
+  auto issueK = [&](int j) {  // 16 wave loads of 4 rows x 256 B, 2 per wave
+    const int k0 = j * BN;
+    char* base = kring + (j & 1) * KST;
+#pragma unroll
+    for (int i = 0; i < 16 / NW; ++i) {
+      const int w = wave + NW * i;
+      const int r = w * 4 + (lane >> 4);
+      const int c = (lane & 15) ^ kswz3(r);
+      const u16* src = Kb + (int64_t)min(k0 + r, Lk - 1) * kl.s + c * 8;
+      __builtin_amdgcn_global_load_lds(src, (lds_vp)(base + w * 1024), 16, 0, 0);
+    }
+  };
+  auto issueV = [&](int j) {  // 16 wave loads of 8 V^T rows x 128 B, 2 per wave
+    const int k0 = j * BN;
+    char* base = vring + (j & 1) * VST;
+#pragma unroll
+    for (int i = 0; i < 16 / NW; ++i) {
+      const int w = wave + NW * i;
+      const int r = w * 8 + (lane >> 3);
+      const int c = (lane & 7) ^ vswz3(r);
+      const u16* src = Vb + (int64_t)r * ldvt + min(k0 + c * 8, ldvt - 8);
+      __builtin_amdgcn_global_load_lds(src, (lds_vp)(base + w * 1024), 16, 0, 0);
+    }
+  };
+
+  // MFMA row r16 of key tile kt reads K row 32 (kt/2) + 8 (kt%2) + krow0 with
+  // krow0 = 4 ((r16/4) % 2) + 16 (r16/8) + r16 % 4; element i of that tile on lane group G is then
+  // key 32 (kt/2) + 8 (kt%2) + kbase + i, kbase = 4 (G % 2) + 16 (G / 2).  The K swizzle of every
+  // such row is r16, so one LDS offset per k-step; tile and stage offsets are immediates.
+  const int krow0 = 4 * ((r16 >> 2) & 1) + 16 * (r16 >> 3) + (r16 & 3);
+  const int kbase = 4 * (G & 1) + 16 * (G >> 1);
+  int koff[4];
+#pragma unroll
+  for (int ks = 0; ks < 4; ++ks) koff[ks] = krow0 * 256 + (((4 * ks + G) ^ r16) << 4);
+  int voff[2];
+#pragma unroll
+  for (int kc = 0; kc < 2; ++kc) voff[kc] = r16 * 128 + (((4 * kc + G) ^ vswz3(r16)) << 4);
+  constexpr int ktoff[4] = {0, 8 * 256, 32 * 256, 40 * 256};
+
+  f32x4 S[4][2];
+  i32x4 P[2][2];
+  f32x4 oacc[8][2];
+#pragma unroll
+  for (int dt = 0; dt < 8; ++dt)
+#pragma unroll
+    for (int u = 0; u < 2; ++u) oacc[dt][u] = f32x4{0.f, 0.f, 0.f, 0.f};
+  float m[2] = {-INFINITY, -INFINITY}, l[2] = {0.f, 0.f}, alpha[2] = {1.f, 1.f};
+  bool pend = false;
+  const float thr = 8.f / scale2;
+
+  auto qk = [&](int j) {
+    const char* kb = kring + (j & 1) * KST;
+#pragma unroll
+    for (int ks = 0; ks < 4; ++ks)
+#pragma unroll
+      for (int kt = 0; kt < 4; ++kt) {
+        const i32x4 a = *reinterpret_cast<const i32x4*>(kb + koff[ks] + ktoff[kt]);
+#pragma unroll
+        for (int u = 0; u < 2; ++u)
+          S[kt][u] = mma16<T>(as_frag(a), qf[u][ks], ks == 0 ? f32x4{0.f, 0.f, 0.f, 0.f} : S[kt][u]);
+      }
+  };
+  auto pv = [&](int j) {
+    const char* vb = vring + (j & 1) * VST;
+#pragma unroll
+    for (int dt = 0; dt < 8; ++dt)
+#pragma unroll
+      for (int kc = 0; kc < 2; ++kc) {
+        const i32x4 a = *reinterpret_cast<const i32x4*>(vb + voff[kc] + dt * 16 * 128);
+#pragma unroll
+        for (int u = 0; u < 2; ++u) oacc[dt][u] = mma16<T>(as_frag(a), as_frag(P[u][kc]), oacc[dt][u]);
+      }
+  };
+  auto rescale = [&]() {
+    if (pend) {
+#pragma unroll
+      for (int dt = 0; dt < 8; ++dt)
+#pragma unroll
+        for (int u = 0; u < 2; ++u)
+#pragma unroll
+          for (int i = 0; i < 4; ++i) oacc[dt][u][i] *= alpha[u];
+    }
+  };
+  // row max of S(j) for query tile u, then (after both) the lazy-rescale decision
+  auto rowmax = [&](int u) {
+    float x = __builtin_fmaxf(__builtin_fmaxf(S[0][u][0], S[0][u][1]), __builtin_fmaxf(S[0][u][2], S[0][u][3]));
+#pragma unroll
+    for (int kt = 1; kt < 4; ++kt)
+      x = __builtin_fmaxf(__builtin_fmaxf(x, __builtin_fmaxf(S[kt][u][0], S[kt][u][1])),
+                          __builtin_fmaxf(S[kt][u][2], S[kt][u][3]));
+    return xmax4(x);
+  };
+  float ms[2];
+  auto decide = [&](const float (&bm)[2]) {
+    bool need[2];
+#pragma unroll
+    for (int u = 0; u < 2; ++u) {
+      need[u] = bm[u] > m[u] + thr;
+      const float mn = need[u] ? bm[u] : m[u];
+      alpha[u] = __builtin_amdgcn_exp2f((m[u] - mn) * scale2);
+      l[u] *= alpha[u];
+      m[u] = mn;
+      ms[u] = mn == -INFINITY ? 0.f : mn * scale2;
+    }
+    pend = __any(need[0] || need[1]);
+  };
+  auto expo = [&](int u, int kt) {  // p = exp2(s * scale2 - m * scale2), summed per lane
+    float ps = 0.f;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      S[kt][u][i] = __builtin_amdgcn_exp2f(__builtin_fmaf(S[kt][u][i], scale2, -ms[u]));
+      ps += S[kt][u][i];
+    }
+    l[u] += ps;
+  };
+  auto pack = [&]() {
+#pragma unroll
+    for (int u = 0; u < 2; ++u)
+#pragma unroll
+      for (int c = 0; c < 2; ++c) {
+        i32x4 w;
+        w[0] = (int)pack2<T>(S[2 * c][u][0], S[2 * c][u][1]);
+        w[1] = (int)pack2<T>(S[2 * c][u][2], S[2 * c][u][3]);
+        w[2] = (int)pack2<T>(S[2 * c + 1][u][0], S[2 * c + 1][u][1]);
+        w[3] = (int)pack2<T>(S[2 * c + 1][u][2], S[2 * c + 1][u][3]);
+        P[u][c] = w;
+      }
+  };
+  auto softmax = [&](int j, bool mask) {
+    if (mask) {
+      const int qrel[2] = {qpos[0] - j * BN - kbase, qpos[1] - j * BN - kbase};
+#pragma unroll
+      for (int kt = 0; kt < 4; ++kt)
+#pragma unroll
+        for (int u = 0; u < 2; ++u)
+#pragma unroll
+          for (int i = 0; i < 4; ++i)
+            S[kt][u][i] = 32 * (kt >> 1) + 8 * (kt & 1) + i <= qrel[u] ? S[kt][u][i] : -INFINITY;
+    }
+    const float bm[2] = {rowmax(0), rowmax(1)};
+    decide(bm);
+#pragma unroll
+    for (int u = 0; u < 2; ++u)
+#pragma unroll
+      for (int kt = 0; kt < 4; ++kt) expo(u, kt);
+    pack();
+  };
+  // Steady state: steps 0-3 P(j-1).V(j-1) (d tiles 2s, 2s+1) beside max / rescale decision /
+  // exponentials of S(j); step 4 packs P(j); steps 4-7 S(j+1) = K(j+1).Q^T (k-step s-4).
+  auto fused = [&](int j) {
+    const char* vb = vring + ((j - 1) & 1) * VST;
+    const char* kb = kring + ((j + 1) & 1) * KST;
+    auto fetch = [&](int st, i32x4 (&F)[4]) {
+      if (st < 4) {
+#pragma unroll
+        for (int dd = 0; dd < 2; ++dd)
+#pragma unroll
+          for (int kc = 0; kc < 2; ++kc)
+            F[2 * dd + kc] = *reinterpret_cast<const i32x4*>(vb + voff[kc] + (2 * st + dd) * 16 * 128);
+      } else {
+#pragma unroll
+        for (int kt = 0; kt < 4; ++kt) F[kt] = *reinterpret_cast<const i32x4*>(kb + koff[st - 4] + ktoff[kt]);
+      }
+    };
+    i32x4 FB[2][4];
+    fetch(0, FB[0]);
+#pragma unroll
+    for (int st = 0; st < 8; ++st) {
+      i32x4 (&F)[4] = FB[st & 1];
+      if (st + 1 < 8) fetch(st + 1, FB[(st + 1) & 1]);
+      if (st == 0) {
+        const float bm[2] = {rowmax(0), rowmax(1)};
+        decide(bm);
+      } else if (st == 1) {
+        expo(0, 0), expo(0, 1), expo(0, 2);
+      } else if (st == 2) {
+        expo(0, 3), expo(1, 0), expo(1, 1);
+      } else if (st == 3) {
+        expo(1, 2), expo(1, 3);
+      } else if (st == 4) {
+        pack();
+      }
+      if (st < 4) {
+#pragma unroll
+        for (int dd = 0; dd < 2; ++dd)
+#pragma unroll
+          for (int kc = 0; kc < 2; ++kc)
+#pragma unroll
+            for (int u = 0; u < 2; ++u)
+              oacc[2 * st + dd][u] = mma16<T>(as_frag(F[2 * dd + kc]), as_frag(P[u][kc]), oacc[2 * st + dd][u]);
+      } else {
+        const int ks = st - 4;
+#pragma unroll
+        for (int kt = 0; kt < 4; ++kt)
+#pragma unroll
+          for (int u = 0; u < 2; ++u)
+            S[kt][u] = mma16<T>(as_frag(F[kt]), qf[u][ks], ks == 0 ? f32x4{0.f, 0.f, 0.f, 0.f} : S[kt][u]);
+      }
+      __builtin_amdgcn_sched_barrier(0);
+    }
+  };
+
+  // Block loop: the top of iteration j waits for K(j+1) and V(j-1) (issued one iteration earlier;
+  // the barrier needs no full drain since nothing younger is in flight), then refills the stages
+  // freed by iteration j-1.  The fused iterations form one contiguous range with a loop of its own
+  // (merging both paths into one loop body costs registers).
+  auto top = [&](int j) {
+    __builtin_amdgcn_s_waitcnt((0 & 15) | (7 << 4) | (0 << 8));  // vmcnt(0) lgkmcnt(0)
+    asm volatile("" ::: "memory");
+    __builtin_amdgcn_s_barrier();
+    asm volatile("" ::: "memory");
+    issueK(min(j + 2, nb - 1));
+    issueV(j);
+  };
+  auto generic = [&](int j) {
+    if (j >= 1 && j - 1 < nbw) {
+      rescale();
+      pv(j - 1);
+    }
+    if (j < nbw) softmax(j, j >= nfull);
+    if (j + 1 < nbw) qk(j + 1);
+  };
+  issueK(0);
+  if (nb > 1) issueK(1);
+  __builtin_amdgcn_s_waitcnt((0 & 15) | (7 << 4) | (0 << 8));
+  __syncthreads();
+  qk(0);
+  const int jf1 = max(1, min(nfull, nbw - 1));
+  top(0);
+  generic(0);
+  int j = 1;
+  for (; j < jf1; ++j) {
+    top(j);
+    rescale();
+    fused(j);
+  }
+  for (; j < nb; ++j) {
+    top(j);
+    generic(j);
+  }
+  __builtin_amdgcn_s_waitcnt((0 & 15) | (7 << 4) | (0 << 8));
+  __syncthreads();
+  if (nbw == nb) {
+    rescale();
+    pv(nb - 1);
+  }
+
+  // O^T accumulator: lane holds O[q0 + 16u + r16][16 dt + 4G + i]
+#pragma unroll
+  for (int u = 0; u < 2; ++u) {
+    const float lt = xsum4(l[u]);
+    const int qi = q0 + 16 * u + r16;
+    if (qi < Lq) {
+      const float inv = 1.f / lt;
+      u16* orow = O + b * ql.b + h * ql.h + (int64_t)qi * ql.s;
+#pragma unroll
+      for (int dt = 0; dt < 8; ++dt) {
+        typedef __attribute__((__vector_size__(2 * sizeof(int)))) int i32x2;
+        i32x2 w;
+        w[0] = (int)pack2<T>(oacc[dt][u][0] * inv, oacc[dt][u][1] * inv);
+        w[1] = (int)pack2<T>(oacc[dt][u][2] * inv, oacc[dt][u][3] * inv);
+        *reinterpret_cast<i32x2*>(orow + 16 * dt + 4 * G) = w;
+      }
+      if (G == 0) LSE[(int64_t)bh * Lq + qi] = (m[u] * scale2 + __log2f(lt)) * kLn2;
+    }
   }
 }
 
@@ -885,14 +1225,32 @@ __global__ __launch_bounds__(kThreads) void seq_major_vec_kernel(const u16* __re
 // ============================================================================ host dispatch
 bool dtype_ok(int dt) { return dt == Q3_F32 || dt == Q3_F16 || dt == Q3_BF16; }
 
+template <typename T, int GH>
+int fwd_v3(const void* q, Lay ql, const void* k, Lay kl, const void* vt, void* o, float* lse, int B, int Hq, int Hkv,
+           int Lq, int Lk, int ldvt, float scale, hipStream_t s) {
+  constexpr int QT = 32 * (8 / GH);
+  dim3 grid((unsigned)(B * Hq / GH), (unsigned)((Lq + QT - 1) / QT));
+  attn_fwd_v3<T, GH><<<grid, 512, 0, s>>>((const u16*)q, ql, (const u16*)k, kl, (const u16*)vt, (u16*)o, lse, Hq,
+                                          Hkv, Lq, Lk, ldvt, scale * kLog2e);
+  return (int)hipGetLastError();
+}
+
 template <typename T, int D>
 int fwd_mfma(const void* q, Lay ql, const void* k, Lay kl, const void* vt, void* o, float* lse, int B, int Hq,
              int Hkv, int Lq, int Lk, int ldvt, float scale, hipStream_t s) {
-  // Direct-to-LDS kernel: K rows and V^T rows are 16-byte aligned (checked by the caller).
-  dim3 grid((unsigned)((Lq + 127) / 128), (unsigned)(B * Hq));
-  attn_fwd_v2<T, D><<<grid, kThreads, 0, s>>>((const u16*)q, ql, (const u16*)k, kl, (const u16*)vt, (u16*)o, lse, Hq,
-                                               Hkv, Lq, Lk, ldvt, scale * kLog2e);
-  return (int)hipGetLastError();
+  if constexpr (D == 128) {
+    // 8-wave GQA workgroups: as many heads of the group per workgroup as divide it (4, 2 or 1)
+    const int grp = Hq / Hkv;
+    if (grp % 4 == 0) return fwd_v3<T, 4>(q, ql, k, kl, vt, o, lse, B, Hq, Hkv, Lq, Lk, ldvt, scale, s);
+    if (grp % 2 == 0) return fwd_v3<T, 2>(q, ql, k, kl, vt, o, lse, B, Hq, Hkv, Lq, Lk, ldvt, scale, s);
+    return fwd_v3<T, 1>(q, ql, k, kl, vt, o, lse, B, Hq, Hkv, Lq, Lk, ldvt, scale, s);
+  } else {
+    // Direct-to-LDS kernel: K rows and V^T rows are 16-byte aligned (checked by the caller).
+    dim3 grid((unsigned)((Lq + 127) / 128), (unsigned)(B * Hq));
+    attn_fwd_v2<T, D><<<grid, kThreads, 0, s>>>((const u16*)q, ql, (const u16*)k, kl, (const u16*)vt, (u16*)o, lse,
+                                                 Hq, Hkv, Lq, Lk, ldvt, scale * kLog2e);
+    return (int)hipGetLastError();
+  }
 }
 
 template <typename T, int D>
