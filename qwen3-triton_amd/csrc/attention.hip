@@ -591,6 +591,357 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
   }
 }
 
+// ============================================================================ backward, D = 128 (MFMA 16x16x32)
+// 8 bytes from LDS with the gfx950 transpose read: within each 16-lane group, lane j receives
+// element j % 4 of the 8-byte pieces addressed by lanes j / 4 + 4 k, k = 0..3.  Two such reads, by
+// lanes addressing rows k0 + i / 4 (+ 4) at columns m0 + 4 (i % 4), return the MFMA fragment
+// A[m0 + j][k0 .. k0 + 7] of a row-major [k][m] tile: the transposed operand without a copy.
+typedef short v4s_t __attribute__((ext_vector_type(4)));
+typedef __attribute__((__vector_size__(2 * sizeof(int)))) int i32x2;
+Q3_DEV i32x2 ldtr(const char* p) {
+  return __builtin_bit_cast(i32x2, __builtin_amdgcn_ds_read_tr16_b64_v4i16((__attribute__((address_space(3))) v4s_t*)p));
+}
+// 16-byte chunk swizzle of the 256-byte query rows of the dK/dV tiles: a bijection onto 0..15 of
+// the 16 rows a row-read pass touches ({0-3, 8-11, 16-19, 24-27}, +4), and distinct 32-byte bank
+// groups for the 8 rows of each half-wave pass of a transpose read.
+Q3_DEV int qswz3(int r) { return 2 * ((r & 3) | (((r >> 3) & 1) << 2)) + ((r >> 4) & 1); }
+
+// dK/dV -- workgroup: 4 waves x 32 keys of one (b, kv head), one wave per SIMD (the K/V fragments and
+// the dK/dV accumulators fill the registers); loops over the group's query heads and the 32-query
+// tiles at or after the keys, Q/dO tiles and lse/delta through a 4-stage direct-to-LDS ring.  Per
+// tile: S = Q K^T and dP = dO V^T (Q/dO row fragments from LDS, K/V fragments in registers),
+// P = exp2(S s - lse), dS = P (dP - delta), then dV^T += dO^T P and dK^T += Q^T dS with dO^T and Q^T
+// read from the same LDS tiles by transpose reads (no sequence-major copies).  MFMA row r16 of query
+// tile t reads query 8 (r16/4) + 4 t + r16 % 4, so lane group G holds queries 8 G .. 8 G + 7 of each
+// key: P and dS pack straight into the B operands.  Deterministic: the group's heads accumulate in
+// registers.
+template <typename T>
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) void attn_bwd_dkdv_v3(
+    const u16* __restrict__ Q, Lay ql, const u16* __restrict__ K, const u16* __restrict__ V, Lay kl,
+    const u16* __restrict__ dO, const float* __restrict__ LSE, const float* __restrict__ Delta,
+    u16* __restrict__ dK, u16* __restrict__ dV, int Hq, int Hkv, int Lq, int Lk, float scale, float scale2) {
+  constexpr int D = 128, BM = 32, ST = 4;
+  constexpr int TB = BM * D * 2;              // one operand tile (8 KB)
+  constexpr int STAGE = 2 * TB + 2 * BM * 4;  // Q, dO, lse, delta
+  __shared__ __attribute__((aligned(1024))) char lds[ST * STAGE];
+
+  const int kt = (int)blockIdx.y;  // smallest key tiles (most query tiles) first
+  const int bk = blockIdx.x, b = bk / Hkv, hk = bk % Hkv, ratio = Hq / Hkv;
+  const int tid = threadIdx.x, lane = tid & 63, G = lane >> 4, r16 = lane & 15;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int off = Lk - Lq;
+  const int k0w = kt * 128 + wave * 32;
+
+  // K^T / V^T B operands: lane (G, r16) holds key k0w + 16 c + r16, dims 32 ks + 8 G .. + 7
+  bf16x8_t kf[2][4], vf[2][4];
+#pragma unroll
+  for (int c = 0; c < 2; ++c) {
+    const int64_t row = b * kl.b + hk * kl.h + (int64_t)min(k0w + 16 * c + r16, Lk - 1) * kl.s;
+#pragma unroll
+    for (int ks = 0; ks < 4; ++ks) {
+      kf[c][ks] = as_frag(ld16(K + row + 32 * ks + 8 * G));
+      vf[c][ks] = as_frag(ld16(V + row + 32 * ks + 8 * G));
+    }
+  }
+  f32x4 dk[8][2], dv[8][2];
+#pragma unroll
+  for (int d = 0; d < 8; ++d)
+#pragma unroll
+    for (int c = 0; c < 2; ++c) dk[d][c] = dv[d][c] = f32x4{0.f, 0.f, 0.f, 0.f};
+
+  const int qstart = max(0, kt * 128 - off) / BM * BM;
+  const int nq = (Lq - qstart + BM - 1) / BM;  // query tiles per head
+  const int total = ratio * nq;
+
+  auto issue = [&](int u) {  // Q and dO: 8 wave loads each (4 rows x 256 B), 2 per wave; wave 0: lse/delta
+    const int hh = u / nq, q0 = qstart + (u % nq) * BM;
+    const int h = hk * ratio + hh;
+    const int64_t bh = (int64_t)b * Hq + h;
+    const u16* Qb = Q + b * ql.b + h * ql.h;
+    const u16* dOb = dO + b * ql.b + h * ql.h;
+    char* base = lds + (u % ST) * STAGE;
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+      const int w = wave + 4 * i;
+      const int r = 4 * w + (lane >> 4);
+      const int c = (lane & 15) ^ qswz3(r);
+      const int64_t src = (int64_t)min(q0 + r, Lq - 1) * ql.s + c * 8;
+      __builtin_amdgcn_global_load_lds(Qb + src, (lds_vp)(base + w * 1024), 16, 0, 0);
+      __builtin_amdgcn_global_load_lds(dOb + src, (lds_vp)(base + TB + w * 1024), 16, 0, 0);
+    }
+    if (wave == 0) {  // lse (lanes 0..31) and delta (32..63) of the tile's queries; past Lq clamped
+      const int qq = min(q0 + (lane & 31), Lq - 1);
+      const float* src = (lane < 32 ? LSE : Delta) + bh * Lq + qq;
+      __builtin_amdgcn_global_load_lds(src, (lds_vp)(base + 2 * TB), 4, 0, 0);
+    }
+  };
+
+  // row reads: query row qrow0 (+ 4 t), chunk 4 ks + G; transpose reads: group G, lane i of read h
+  // addresses query row 8 G + 4 h + i / 4, bytes 32 dt + 8 (i % 4)
+  const int qrow0 = 8 * (r16 >> 2) + (r16 & 3);
+  int roff[4];
+#pragma unroll
+  for (int ks = 0; ks < 4; ++ks) roff[ks] = qrow0 * 256 + (((4 * ks + G) ^ qswz3(qrow0)) << 4);
+  auto tr_addr = [&](int h, int dt) {
+    const int row = 8 * G + 4 * h + (r16 >> 2);
+    const int byte = 32 * dt + 8 * (r16 & 3);
+    return row * 256 + ((((byte >> 4) ^ qswz3(row)) << 4) | (byte & 15));
+  };
+
+#pragma unroll
+  for (int st = 0; st < ST - 1; ++st)
+    if (st < total) issue(st);
+  for (int u = 0; u < total; ++u) {
+    {  // ring: tile u landed, up to ST - 2 younger tiles (4 loads per wave, 5 for wave 0) in flight
+      const int younger = max(0, min(ST - 2, total - 1 - u));
+      const int n = younger * (wave == 0 ? 5 : 4);
+      if (n >= 10) __builtin_amdgcn_s_waitcnt((10 & 15) | (7 << 4) | (0 << 8));
+      else if (n >= 8) __builtin_amdgcn_s_waitcnt((8 & 15) | (7 << 4) | (0 << 8));
+      else if (n >= 5) __builtin_amdgcn_s_waitcnt((5 & 15) | (7 << 4) | (0 << 8));
+      else if (n >= 4) __builtin_amdgcn_s_waitcnt((4 & 15) | (7 << 4) | (0 << 8));
+      else __builtin_amdgcn_s_waitcnt((0 & 15) | (7 << 4) | (0 << 8));
+      asm volatile("" ::: "memory");
+      __builtin_amdgcn_s_barrier();
+      asm volatile("" ::: "memory");
+      if (u + ST - 1 < total) issue(u + ST - 1);
+    }
+    const int q0 = qstart + (u % nq) * BM;
+    if (min(q0 + BM - 1, Lq - 1) + off < k0w) continue;  // no query of the tile sees the wave's keys
+    const char* qb = lds + (u % ST) * STAGE;
+    const char* db = qb + TB;
+    const float* side = reinterpret_cast<const float*>(qb + 2 * TB);
+
+    f32x4 s[2][2], dp[2][2];  // [query tile t][key tile c]
+#pragma unroll
+    for (int ks = 0; ks < 4; ++ks) {
+      i32x4 qa[2], da[2];
+#pragma unroll
+      for (int t = 0; t < 2; ++t) {
+        qa[t] = *reinterpret_cast<const i32x4*>(qb + roff[ks] + 4 * t * 256);
+        da[t] = *reinterpret_cast<const i32x4*>(db + roff[ks] + 4 * t * 256);
+      }
+#pragma unroll
+      for (int t = 0; t < 2; ++t)
+#pragma unroll
+        for (int c = 0; c < 2; ++c) {
+          s[t][c] = mma16<T>(as_frag(qa[t]), kf[c][ks], ks == 0 ? f32x4{0.f, 0.f, 0.f, 0.f} : s[t][c]);
+          dp[t][c] = mma16<T>(as_frag(da[t]), vf[c][ks], ks == 0 ? f32x4{0.f, 0.f, 0.f, 0.f} : dp[t][c]);
+        }
+    }
+    const bool mask = !(k0w + 31 <= q0 + off && q0 + BM - 1 < Lq);
+    const f32x4 l0 = *reinterpret_cast<const f32x4*>(side + 8 * G);
+    const f32x4 l1 = *reinterpret_cast<const f32x4*>(side + 8 * G + 4);
+    const f32x4 d0 = *reinterpret_cast<const f32x4*>(side + BM + 8 * G);
+    const f32x4 d1 = *reinterpret_cast<const f32x4*>(side + BM + 8 * G + 4);
+    i32x4 pp[2], dd[2];
+#pragma unroll
+    for (int c = 0; c < 2; ++c) {
+      float pv[8], dsv[8];
+#pragma unroll
+      for (int t = 0; t < 2; ++t)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          float p = __builtin_amdgcn_exp2f(__builtin_fmaf(s[t][c][i], scale2, -(t ? l1[i] : l0[i]) * kLog2e));
+          if (mask) {
+            const int q = q0 + 8 * G + 4 * t + i;
+            p = (k0w + 16 * c + r16 <= q + off && q < Lq) ? p : 0.f;
+          }
+          pv[4 * t + i] = p;
+          dsv[4 * t + i] = p * (dp[t][c][i] - (t ? d1[i] : d0[i]));
+        }
+#pragma unroll
+      for (int w = 0; w < 4; ++w) {
+        pp[c][w] = (int)pack2<T>(pv[2 * w], pv[2 * w + 1]);
+        dd[c][w] = (int)pack2<T>(dsv[2 * w], dsv[2 * w + 1]);
+      }
+    }
+#pragma unroll
+    for (int dt = 0; dt < 8; ++dt) {
+      const i32x2 q0v = ldtr(qb + tr_addr(0, dt)), q1v = ldtr(qb + tr_addr(1, dt));
+      const i32x2 d0v = ldtr(db + tr_addr(0, dt)), d1v = ldtr(db + tr_addr(1, dt));
+      const i32x4 aq = {q0v[0], q0v[1], q1v[0], q1v[1]}, ad = {d0v[0], d0v[1], d1v[0], d1v[1]};
+#pragma unroll
+      for (int c = 0; c < 2; ++c) {
+        dv[dt][c] = mma16<T>(as_frag(ad), as_frag(pp[c]), dv[dt][c]);
+        dk[dt][c] = mma16<T>(as_frag(aq), as_frag(dd[c]), dk[dt][c]);
+      }
+    }
+  }
+
+  // dK^T / dV^T accumulators: lane holds [d = 16 dt + 4 G + i][key = k0w + 16 c + r16]
+#pragma unroll
+  for (int c = 0; c < 2; ++c) {
+    const int kj = k0w + 16 * c + r16;
+    if (kj >= Lk) continue;
+    const int64_t row = b * kl.b + hk * kl.h + (int64_t)kj * kl.s;
+#pragma unroll
+    for (int dt = 0; dt < 8; ++dt) {
+      i32x2 wk, wv;
+      wk[0] = (int)pack2<T>(dk[dt][c][0] * scale, dk[dt][c][1] * scale);
+      wk[1] = (int)pack2<T>(dk[dt][c][2] * scale, dk[dt][c][3] * scale);
+      wv[0] = (int)pack2<T>(dv[dt][c][0], dv[dt][c][1]);
+      wv[1] = (int)pack2<T>(dv[dt][c][2], dv[dt][c][3]);
+      *reinterpret_cast<i32x2*>(dK + row + 16 * dt + 4 * G) = wk;
+      *reinterpret_cast<i32x2*>(dV + row + 16 * dt + 4 * G) = wv;
+    }
+  }
+}
+
+// dQ -- workgroup: 8 waves sharing one KV head, as the forward (GH query heads of the group x 8/GH
+// groups of 32 query positions), 64-key blocks of K, V (rows) and K^T (the sequence-major copy)
+// through a 2-stage direct-to-LDS ring.  Per block: S^T = K Q^T, dP^T = V dO^T (Q, dO fragments in
+// registers), P^T = exp2(S^T s - lse), dS^T = P^T (dP^T - delta), dQ^T += K^T dS^T; the K/V row
+// mapping of the forward makes dS^T the B operand of the K^T product as it comes out.
+template <typename T, int GH>
+__global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) void attn_bwd_dq_v3(
+    const u16* __restrict__ Q, Lay ql, const u16* __restrict__ K, const u16* __restrict__ V, Lay kl,
+    const u16* __restrict__ Kt, const u16* __restrict__ dO, const float* __restrict__ LSE,
+    const float* __restrict__ Delta, u16* __restrict__ dQ, int Hq, int Hkv, int Lq, int Lk, int ldkt, float scale,
+    float scale2) {
+  constexpr int D = 128, BN = 64, NW = 8, QT = 32 * (NW / GH);
+  constexpr int KST = BN * D * 2;  // one 64 x 128 tile
+  constexpr int STAGE = 3 * KST;   // K, V, K^T
+  __shared__ __attribute__((aligned(1024))) char lds[2 * STAGE];
+
+  const int nqt = (Lq + QT - 1) / QT;
+  const int qt = nqt - 1 - (int)blockIdx.y;  // longest query tiles first
+  const int tid = threadIdx.x, lane = tid & 63, G = lane >> 4, r16 = lane & 15;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int HB = Hq / GH, b = (int)blockIdx.x / HB, h = ((int)blockIdx.x % HB) * GH + wave % GH;
+  const int hk = h / (Hq / Hkv), bh = b * Hq + h;
+  const int off = Lk - Lq;
+  const int q0 = qt * QT + (wave / GH) * 32;
+  const u16* Kb = K + b * kl.b + hk * kl.h;
+  const u16* Vb = V + b * kl.b + hk * kl.h;
+  const u16* Ktb = Kt + (int64_t)(b * Hkv + hk) * D * ldkt;
+
+  bf16x8_t qf[2][4], df[2][4];
+  float lse2[2], dlt[2];
+#pragma unroll
+  for (int u = 0; u < 2; ++u) {
+    const int qi = min(q0 + 16 * u + r16, Lq - 1);
+    const int64_t row = b * ql.b + h * ql.h + (int64_t)qi * ql.s;
+#pragma unroll
+    for (int ks = 0; ks < 4; ++ks) {
+      qf[u][ks] = as_frag(ld16(Q + row + 32 * ks + 8 * G));
+      df[u][ks] = as_frag(ld16(dO + row + 32 * ks + 8 * G));
+    }
+    lse2[u] = LSE[(int64_t)bh * Lq + qi] * kLog2e;
+    dlt[u] = Delta[(int64_t)bh * Lq + qi];
+  }
+
+  const int nb = (min(Lk, min(qt * QT + QT - 1, Lq - 1) + off + 1) + BN - 1) / BN;
+  const int nbw = min(nb, (min(Lk, min(q0 + 31, Lq - 1) + off + 1) + BN - 1) / BN);
+  const int nfull = min(nbw, max(0, (q0 + off + 1) / BN));  // blocks fully visible to the wave
+  const int qpos[2] = {q0 + r16 + off, q0 + 16 + r16 + off};
+
+  auto issue = [&](int j) {  // K, V: 16 wave loads each (4 rows x 256 B); K^T: 16 (8 rows x 128 B)
+    const int k0 = j * BN;
+    char* base = lds + (j & 1) * STAGE;
+#pragma unroll
+    for (int i = 0; i < 16 / NW; ++i) {
+      const int w = wave + NW * i;
+      const int r = w * 4 + (lane >> 4);
+      const int c = (lane & 15) ^ kswz3(r);
+      const int64_t src = (int64_t)min(k0 + r, Lk - 1) * kl.s + c * 8;
+      __builtin_amdgcn_global_load_lds(Kb + src, (lds_vp)(base + w * 1024), 16, 0, 0);
+      __builtin_amdgcn_global_load_lds(Vb + src, (lds_vp)(base + KST + w * 1024), 16, 0, 0);
+      const int rt = w * 8 + (lane >> 3);
+      const int ct = (lane & 7) ^ vswz3(rt);
+      __builtin_amdgcn_global_load_lds(Ktb + (int64_t)rt * ldkt + min(k0 + ct * 8, ldkt - 8),
+                                       (lds_vp)(base + 2 * KST + w * 1024), 16, 0, 0);
+    }
+  };
+
+  const int krow0 = 4 * ((r16 >> 2) & 1) + 16 * (r16 >> 3) + (r16 & 3);
+  const int kbase = 4 * (G & 1) + 16 * (G >> 1);
+  int koff[4];
+#pragma unroll
+  for (int ks = 0; ks < 4; ++ks) koff[ks] = krow0 * 256 + (((4 * ks + G) ^ r16) << 4);
+  int toff[2];
+#pragma unroll
+  for (int kc = 0; kc < 2; ++kc) toff[kc] = r16 * 128 + (((4 * kc + G) ^ vswz3(r16)) << 4);
+  constexpr int ktoff[4] = {0, 8 * 256, 32 * 256, 40 * 256};
+
+  f32x4 dq[8][2];
+#pragma unroll
+  for (int dt = 0; dt < 8; ++dt)
+#pragma unroll
+    for (int u = 0; u < 2; ++u) dq[dt][u] = f32x4{0.f, 0.f, 0.f, 0.f};
+
+  issue(0);
+  for (int j = 0; j < nb; ++j) {
+    __builtin_amdgcn_s_waitcnt((0 & 15) | (7 << 4) | (0 << 8));  // block j landed; nothing younger
+    asm volatile("" ::: "memory");
+    __builtin_amdgcn_s_barrier();
+    asm volatile("" ::: "memory");
+    if (j + 1 < nb) issue(j + 1);
+    if (j >= nbw) continue;
+    const char* kb = lds + (j & 1) * STAGE;
+    const char* vb = kb + KST;
+    const char* tb = kb + 2 * KST;
+    f32x4 S[4][2], DP[4][2];
+#pragma unroll
+    for (int ks = 0; ks < 4; ++ks)
+#pragma unroll
+      for (int kt = 0; kt < 4; ++kt) {
+        const i32x4 a = *reinterpret_cast<const i32x4*>(kb + koff[ks] + ktoff[kt]);
+        const i32x4 av = *reinterpret_cast<const i32x4*>(vb + koff[ks] + ktoff[kt]);
+#pragma unroll
+        for (int u = 0; u < 2; ++u) {
+          S[kt][u] = mma16<T>(as_frag(a), qf[u][ks], ks == 0 ? f32x4{0.f, 0.f, 0.f, 0.f} : S[kt][u]);
+          DP[kt][u] = mma16<T>(as_frag(av), df[u][ks], ks == 0 ? f32x4{0.f, 0.f, 0.f, 0.f} : DP[kt][u]);
+        }
+      }
+    const bool mask = j >= nfull;
+    i32x4 DS[2][2];
+#pragma unroll
+    for (int u = 0; u < 2; ++u) {
+      const int qrel = qpos[u] - j * BN - kbase;
+#pragma unroll
+      for (int kt = 0; kt < 4; ++kt)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          float p = __builtin_amdgcn_exp2f(__builtin_fmaf(S[kt][u][i], scale2, -lse2[u]));
+          if (mask) p = 32 * (kt >> 1) + 8 * (kt & 1) + i <= qrel ? p : 0.f;
+          S[kt][u][i] = p * (DP[kt][u][i] - dlt[u]);
+        }
+#pragma unroll
+      for (int c = 0; c < 2; ++c) {
+        i32x4 w;
+        w[0] = (int)pack2<T>(S[2 * c][u][0], S[2 * c][u][1]);
+        w[1] = (int)pack2<T>(S[2 * c][u][2], S[2 * c][u][3]);
+        w[2] = (int)pack2<T>(S[2 * c + 1][u][0], S[2 * c + 1][u][1]);
+        w[3] = (int)pack2<T>(S[2 * c + 1][u][2], S[2 * c + 1][u][3]);
+        DS[u][c] = w;
+      }
+    }
+#pragma unroll
+    for (int dt = 0; dt < 8; ++dt)
+#pragma unroll
+      for (int kc = 0; kc < 2; ++kc) {
+        const i32x4 a = *reinterpret_cast<const i32x4*>(tb + toff[kc] + dt * 16 * 128);
+#pragma unroll
+        for (int u = 0; u < 2; ++u) dq[dt][u] = mma16<T>(as_frag(a), as_frag(DS[u][kc]), dq[dt][u]);
+      }
+  }
+
+  // dQ^T accumulator: lane holds dQ[q0 + 16 u + r16][16 dt + 4 G + i]
+#pragma unroll
+  for (int u = 0; u < 2; ++u) {
+    const int qi = q0 + 16 * u + r16;
+    if (qi >= Lq) continue;
+    u16* row = dQ + b * ql.b + h * ql.h + (int64_t)qi * ql.s;
+#pragma unroll
+    for (int dt = 0; dt < 8; ++dt) {
+      i32x2 w;
+      w[0] = (int)pack2<T>(dq[dt][u][0] * scale, dq[dt][u][1] * scale);
+      w[1] = (int)pack2<T>(dq[dt][u][2] * scale, dq[dt][u][3] * scale);
+      *reinterpret_cast<i32x2*>(row + 16 * dt + 4 * G) = w;
+    }
+  }
+}
+
 // ============================================================================ backward: delta
 // delta[r] = sum_d O[r,d] * dO[r,d] (fp32), one wave per row.
 template <typename T>
@@ -1253,21 +1604,48 @@ int fwd_mfma(const void* q, Lay ql, const void* k, Lay kl, const void* vt, void*
   }
 }
 
+template <typename T, int GH>
+int bwd_dq_v3(const void* q, Lay ql, const void* k, const void* v, Lay kl, const void* kt, const void* dout,
+              const float* lse, const float* delta, void* dq, int B, int Hq, int Hkv, int Lq, int Lk, int ldkt,
+              float scale, hipStream_t s) {
+  constexpr int QT = 32 * (8 / GH);
+  dim3 g((unsigned)(B * Hq / GH), (unsigned)((Lq + QT - 1) / QT));
+  attn_bwd_dq_v3<T, GH><<<g, 512, 0, s>>>((const u16*)q, ql, (const u16*)k, (const u16*)v, kl, (const u16*)kt,
+                                          (const u16*)dout, lse, delta, (u16*)dq, Hq, Hkv, Lq, Lk, ldkt, scale,
+                                          scale * kLog2e);
+  return (int)hipGetLastError();
+}
+
 template <typename T, int D>
 int bwd_mfma(const void* q, Lay ql, const void* k, const void* v, Lay kl, const void* qt, const void* kt,
              const void* dout, const void* dot, const float* lse, const float* delta, void* dq, void* dk, void* dv,
              int B, int Hq, int Hkv, int Lq, int Lk, int ldqt, int ldkt, float scale, hipStream_t s) {
-  // Direct-to-LDS kernels need 16-byte aligned rows of every operand (checked by the caller).
-  dim3 g1((unsigned)(B * Hq), (unsigned)((Lq + 127) / 128));
-  attn_bwd_dq_v2<T, D, 1><<<g1, kThreads, 0, s>>>((const u16*)q, ql, (const u16*)k, (const u16*)v, kl,
-                                                   (const u16*)kt, (const u16*)dout, lse, delta, (u16*)dq, Hq, Hkv,
-                                                   Lq, Lk, ldkt, scale, scale * kLog2e);
-  dim3 g2((unsigned)(B * Hkv), (unsigned)((Lk + 127) / 128));
-  // D = 128: one workgroup per CU either way (registers); a 3-deep ring plus the V block fits the LDS.
-  attn_bwd_dkdv_v2<T, D, (D > 64 ? 1 : 2), (D > 64 ? 3 : 2)><<<g2, kThreads, 0, s>>>((const u16*)q, ql, (const u16*)k, (const u16*)v, kl,
-                                                  (const u16*)qt, (const u16*)dout, (const u16*)dot, lse, delta,
-                                                  (u16*)dk, (u16*)dv, Hq, Hkv, Lq, Lk, ldqt, scale, scale * kLog2e);
-  return (int)hipGetLastError();
+  if constexpr (D == 128) {
+    // dQ on 8-wave GQA workgroups (K^T copy), dK/dV with transpose reads (qt, dot unused)
+    const int grp = Hq / Hkv;
+    int rc;
+    if (grp % 4 == 0) rc = bwd_dq_v3<T, 4>(q, ql, k, v, kl, kt, dout, lse, delta, dq, B, Hq, Hkv, Lq, Lk, ldkt, scale, s);
+    else if (grp % 2 == 0)
+      rc = bwd_dq_v3<T, 2>(q, ql, k, v, kl, kt, dout, lse, delta, dq, B, Hq, Hkv, Lq, Lk, ldkt, scale, s);
+    else rc = bwd_dq_v3<T, 1>(q, ql, k, v, kl, kt, dout, lse, delta, dq, B, Hq, Hkv, Lq, Lk, ldkt, scale, s);
+    if (rc) return rc;
+    dim3 g2((unsigned)(B * Hkv), (unsigned)((Lk + 127) / 128));
+    attn_bwd_dkdv_v3<T><<<g2, 256, 0, s>>>((const u16*)q, ql, (const u16*)k, (const u16*)v, kl, (const u16*)dout, lse,
+                                           delta, (u16*)dk, (u16*)dv, Hq, Hkv, Lq, Lk, scale, scale * kLog2e);
+    return (int)hipGetLastError();
+  } else {
+    // Direct-to-LDS kernels need 16-byte aligned rows of every operand (checked by the caller).
+    dim3 g1((unsigned)(B * Hq), (unsigned)((Lq + 127) / 128));
+    attn_bwd_dq_v2<T, D, 1><<<g1, kThreads, 0, s>>>((const u16*)q, ql, (const u16*)k, (const u16*)v, kl,
+                                                     (const u16*)kt, (const u16*)dout, lse, delta, (u16*)dq, Hq, Hkv,
+                                                     Lq, Lk, ldkt, scale, scale * kLog2e);
+    dim3 g2((unsigned)(B * Hkv), (unsigned)((Lk + 127) / 128));
+    // D = 128: one workgroup per CU either way (registers); a 3-deep ring plus the V block fits the LDS.
+    attn_bwd_dkdv_v2<T, D, (D > 64 ? 1 : 2), (D > 64 ? 3 : 2)><<<g2, kThreads, 0, s>>>((const u16*)q, ql, (const u16*)k, (const u16*)v, kl,
+                                                    (const u16*)qt, (const u16*)dout, (const u16*)dot, lse, delta,
+                                                    (u16*)dk, (u16*)dv, Hq, Hkv, Lq, Lk, ldqt, scale, scale * kLog2e);
+    return (int)hipGetLastError();
+  }
 }
 
 template <typename T>
@@ -1385,9 +1763,11 @@ int q3_attention_bwd(int dtype, const void* q, int64_t qsb, int64_t qsh, int64_t
   else rc = delta_t<F32>(o, dout, ql, delta, B * Hq * Lq, hq, lq, d, stream);
   if (rc) return rc;
   if (q3_attention_mfma_supported(dtype, D)) {
-    Q3_REQUIRE(qt && kt && dot && ldqt >= Lq && ldkt >= Lk && ldqt % 16 == 0 && ldkt % 16 == 0 && lay_ok(q, ql) &&
-               lay_ok(dout, ql) && lay_ok(dq, ql) && lay_ok(k, kl) && lay_ok(v, kl) && lay_ok(dk, kl) &&
-               lay_ok(dv, kl) && al16(qt) && al16(kt) && al16(dot));
+    // D = 128 reads Q and dO transposed straight from LDS: qt / dot are not needed (may be null)
+    const bool need_qt = D != 128;
+    Q3_REQUIRE(kt && ldkt >= Lk && ldkt % 16 == 0 && lay_ok(q, ql) && lay_ok(dout, ql) && lay_ok(dq, ql) &&
+               lay_ok(k, kl) && lay_ok(v, kl) && lay_ok(dk, kl) && lay_ok(dv, kl) && al16(kt));
+    Q3_REQUIRE(!need_qt || (qt && dot && ldqt >= Lq && ldqt % 16 == 0 && al16(qt) && al16(dot)));
     const int lq8 = (int)ldqt, lk8 = (int)ldkt;
     if (dtype == Q3_BF16)
       return Q3_ATTN_D(BF16, bwd_mfma, q, ql, k, v, kl, qt, kt, dout, dot, lse, delta, dq, dk, dv, b, hq, hkv, lq, lk,

@@ -250,8 +250,11 @@ def attention_bwd(q, k, v, o, lse, do, scale):
     qt = kt = dot = None
     ldq = ldk = 0
     if attention_mfma(q.dtype, d):
-        qt, kt, dot = seq_major(q), seq_major(k), seq_major(do)
-        ldq, ldk = qt.shape[-1], kt.shape[-1]
+        kt = seq_major(k)
+        ldk = kt.shape[-1]
+        if d != 128:  # head_dim 128 reads Q and dO transposed in LDS
+            qt, dot = seq_major(q), seq_major(do)
+            ldq = qt.shape[-1]
     p = (lambda t: 0 if t is None else t.data_ptr())
     H.call("q3_attention_bwd", H.code(q.dtype), q.data_ptr(), *_bhsd_strides(q), k.data_ptr(), v.data_ptr(),
            *_bhsd_strides(k), o.data_ptr(), do.data_ptr(), lse.data_ptr(), p(qt), ldq, p(kt), ldk, p(dot),
