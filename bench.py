@@ -264,6 +264,111 @@ def lm_head_ce_bench(steps=3, warmup=1):
             "frac": round(flops / (ms * 1e-3) / 1e12 / PEAK_BF16_TFLOPS, 4)}
 
 
+def _event_ms(fn, reps):
+    import torch
+    fn()
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for _ in range(reps):
+        fn()
+    e1.record()
+    torch.cuda.synchronize()
+    return e0.elapsed_time(e1) / reps
+
+
+def attention_bench(reps=10):
+    """Config #3: GQA causal flash attention (32 query / 8 KV heads, head_dim 128, bf16, seed 2) at
+    B4 x S2048 and B1 x S8192.  Forward = the V^T copy + the flash kernel; backward = delta, the K^T
+    copy, dQ and dK/dV (the whole op as the autograd backward runs it).  Algorithmic work: causal
+    forward 2 * 2 * B * Hq * S^2 / 2 * D FLOP, backward 2.5 x that."""
+    import torch
+    from qwen3_triton.kernels import _ops
+    out = {}
+    gen = torch.Generator(device="cuda").manual_seed(2)
+    for b, s in ((4, 2048), (1, 8192)):
+        q = torch.randn(b, s, 32, 128, device="cuda", dtype=torch.bfloat16, generator=gen).transpose(1, 2)
+        k = torch.randn(b, s, 8, 128, device="cuda", dtype=torch.bfloat16, generator=gen).transpose(1, 2)
+        v = torch.randn(b, s, 8, 128, device="cuda", dtype=torch.bfloat16, generator=gen).transpose(1, 2)
+        do = torch.randn(b, s, 32, 128, device="cuda", dtype=torch.bfloat16, generator=gen).transpose(1, 2)
+        sc = 128 ** -0.5
+        o, lse = _ops.attention_fwd(q, k, v, sc)
+        f_ms = _event_ms(lambda: _ops.attention_fwd(q, k, v, sc), reps)
+        b_ms = _event_ms(lambda: _ops.attention_bwd(q, k, v, o, lse, do, sc), reps)
+        fwd_flops = 2 * 2 * b * 32 * s * s / 2 * 128
+        f_tf, b_tf = fwd_flops / (f_ms * 1e-3) / 1e12, 2.5 * fwd_flops / (b_ms * 1e-3) / 1e12
+        out[f"b{b}_s{s}"] = {"fwd_ms": round(f_ms, 4), "fwd_tflops": round(f_tf, 1),
+                             "fwd_frac": round(f_tf / PEAK_BF16_TFLOPS, 4), "bwd_ms": round(b_ms, 4),
+                             "bwd_tflops": round(b_tf, 1), "bwd_frac": round(b_tf / PEAK_BF16_TFLOPS, 4)}
+        del q, k, v, do, o, lse
+    torch.cuda.empty_cache()
+    return out
+
+
+def bandwidth_bench(reps=20):
+    """Config #2: the bandwidth-bound ops at Qwen3-8B shape, bf16 (seed 1): RMSNorm on [8192, 4096],
+    fused per-head QK-norm + RoPE on Q [8192, 32, 128] and K [8192, 8, 128], RoPE on Q, SwiGLU on
+    [8192, 12288].  Kernel launches on preallocated buffers; achieved = algorithmic HBM bytes (each
+    operand read or written once: x/y 2 B per element, plus weights and rotary tables) / time."""
+    import torch
+    from qwen3_triton import _hip as H
+    from qwen3_triton.kernels import _ops
+    gen = torch.Generator(device="cuda").manual_seed(1)
+    bf = torch.bfloat16
+    st = H.stream()
+    res = {}
+
+    def rec(name, ms, nbytes):
+        gbs = nbytes / (ms * 1e-3) / 1e9
+        res[name] = {"us": round(ms * 1e3, 2), "gb": round(nbytes / 1e9, 4), "gbs": round(gbs, 1),
+                     "frac": round(gbs / PEAK_HBM_GBS, 4)}
+
+    t, h = 8192, 4096
+    x = torch.randn(t, h, device="cuda", dtype=bf, generator=gen)
+    w = (1 + 0.1 * torch.randn(h, device="cuda", generator=gen)).to(bf)
+    y, dy, dx = torch.empty_like(x), torch.randn(t, h, device="cuda", dtype=bf, generator=gen), torch.empty_like(x)
+    dw = torch.empty_like(w)
+    ws = H.workspace(H.query("q3_rmsnorm_bwd_workspace_bytes", t, h), x.device)
+    rec("rmsnorm_fwd", _event_ms(lambda: H.call("q3_rmsnorm_fwd", H.BF16, x.data_ptr(), w.data_ptr(), y.data_ptr(), t,
+                                                h, 1e-6, st), reps), 2 * 2 * t * h)
+    rec("rmsnorm_bwd", _event_ms(lambda: H.call("q3_rmsnorm_bwd", H.BF16, x.data_ptr(), w.data_ptr(), dy.data_ptr(),
+                                                dx.data_ptr(), dw.data_ptr(), ws.data_ptr(), t, h, 1e-6, st), reps),
+        3 * 2 * t * h)
+    del x, y, dy, dx
+    pos = torch.arange(2048, device="cuda").repeat(4, 1)
+    inv = (1.0 / (1e6 ** (torch.arange(0, 128, 2, dtype=torch.float32) / 128))).cuda()
+    cos, sin = _ops.rope_tables(pos, inv, bf)
+    tab = 2 * 2 * t * 128
+    for name, heads in (("q", 32), ("k", 8)):
+        xq = torch.randn(4, 2048, heads, 128, device="cuda", dtype=bf, generator=gen)
+        wq = (1 + 0.1 * torch.randn(128, device="cuda", generator=gen)).to(bf)
+        yq, dyq, dxq, dwq = torch.empty_like(xq), torch.randn_like(xq), torch.empty_like(xq), torch.empty_like(wq)
+        wsq = H.workspace(H.query("q3_norm_rope_bwd_workspace_bytes", t, heads, 128), xq.device)
+        n = xq.numel()
+        rec(f"qk_norm_rope_fwd_{name}", _event_ms(lambda: H.call(
+            "q3_norm_rope_fwd", H.BF16, xq.data_ptr(), wq.data_ptr(), cos.data_ptr(), sin.data_ptr(), yq.data_ptr(), t,
+            heads, 128, 1e-6, st), reps), 2 * 2 * n + tab)
+        rec(f"qk_norm_rope_bwd_{name}", _event_ms(lambda: H.call(
+            "q3_norm_rope_bwd", H.BF16, xq.data_ptr(), wq.data_ptr(), cos.data_ptr(), sin.data_ptr(), dyq.data_ptr(),
+            dxq.data_ptr(), dwq.data_ptr(), wsq.data_ptr(), t, heads, 128, 1e-6, st), reps), 3 * 2 * n + tab)
+        if name == "q":
+            rec("rope_fwd_q", _event_ms(lambda: H.call("q3_rope_apply", H.BF16, xq.data_ptr(), cos.data_ptr(),
+                                                       sin.data_ptr(), yq.data_ptr(), 4, 2048, heads, 128, 0, 0, st),
+                                        reps), 2 * 2 * n + tab)
+        del xq, yq, dyq, dxq
+    g = torch.randn(t, 12288, device="cuda", dtype=bf, generator=gen)
+    u = torch.randn(t, 12288, device="cuda", dtype=bf, generator=gen)
+    dyg, yg, dg, du = torch.randn_like(g), torch.empty_like(g), torch.empty_like(g), torch.empty_like(g)
+    n = g.numel()
+    rec("swiglu_fwd", _event_ms(lambda: H.call("q3_swiglu_fwd", H.BF16, g.data_ptr(), u.data_ptr(), yg.data_ptr(), n,
+                                               st), reps), 3 * 2 * n)
+    rec("swiglu_bwd", _event_ms(lambda: H.call("q3_swiglu_bwd", H.BF16, g.data_ptr(), u.data_ptr(), dyg.data_ptr(),
+                                               dg.data_ptr(), du.data_ptr(), n, st), reps), 5 * 2 * n)
+    del g, u, dyg, yg, dg, du
+    torch.cuda.empty_cache()
+    return res
+
+
 def log(msg):
     print(f"[bench] {msg}", file=sys.stderr, flush=True)
 
@@ -278,6 +383,7 @@ def main():
     ap.add_argument("--no-decode", action="store_true")
     ap.add_argument("--no-layer", action="store_true", help="skip the decoder-layer step (profiling decode)")
     ap.add_argument("--no-lm-head", action="store_true", help="skip the fused LM-head + CE step")
+    ap.add_argument("--no-ops", action="store_true", help="skip the per-op attention / bandwidth measurements")
     ap.add_argument("--decode-tokens", type=int, default=256)
     ap.add_argument("--decode-batches", default="1,8", help="comma list of decode batches among 1 and 8")
     ap.add_argument("--pmc-probe", action="store_true",
@@ -337,6 +443,10 @@ def main():
                           "achieved_tflops": round(layer["step_tflops"], 1),
                           "frac": round(layer["step_tflops"] / PEAK_BF16_TFLOPS, 4)},
     }
+    if not args.no_ops:
+        log("attention (config #3) and bandwidth-bound ops (config #2)")
+        result["attention"] = attention_bench()
+        result["bandwidth_ops"] = bandwidth_bench()
     if not args.no_lm_head:
         log("fused LM-head CE fwd+bwd")
         result["lm_head_ce"] = lm_head_ce_bench()

@@ -144,7 +144,8 @@ int q3_gemm_strided(int in_dtype, int out_dtype, const void* A, int64_t sam, int
  * uses KV head h/(Hq/Hkv).  LSE and delta are [B,Hq,Lq] fp32 (natural-log LSE; delta =
  * rowsum(O*dO) is backward scratch).  On the matrix-core path (q3_attention_mfma_supported) the
  * caller also passes sequence-major copies [B,H,D,ld] (ld >= L, ld % 16 == 0, zero pad) made by
- * q3_attention_seq_major: vt of V (forward), qt of Q, kt of K and dot of dO (backward), and every
+ * q3_attention_seq_major: vt of V (forward), qt of Q, kt of K and dot of dO (backward; at head_dim
+ * 128 only kt is read -- Q and dO are read transposed in LDS -- and qt / dot may be null), and every
  * row must be 16-byte aligned.  Within every 16-position block of such a row the positions are
  * stored in the order 0-3, 8-11, 4-7, 12-15 (the operand order of the matrix-core kernels).
  * Other dtypes/head sizes run a SIMT path that ignores them.

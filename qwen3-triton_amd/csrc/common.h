@@ -87,6 +87,21 @@ template <typename T> Q3_DEV void store_vec(typename T::storage* p, const Vec<T>
   *reinterpret_cast<i32x4*>(p) = raw;
 }
 
+// ------------------------------------------------------------------ streaming access
+// Streaming operands are touched once: non-temporal loads and stores keep them out of the caches.
+Q3_DEV i32x4 ld_nt(const void* p) { return __builtin_nontemporal_load(reinterpret_cast<const i32x4*>(p)); }
+template <typename T> Q3_DEV void st_nt(typename T::storage* p, const Vec<T>& r) {
+  i32x4 raw;
+  if constexpr (T::vec == 4) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) raw[i] = __float_as_int(r.v[i]);
+  } else {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) raw[i] = (int)pack2<T>(r.v[2 * i], r.v[2 * i + 1]);
+  }
+  __builtin_nontemporal_store(raw, reinterpret_cast<i32x4*>(p));
+}
+
 // ------------------------------------------------------------------ matrix cores
 // D(16x16, fp32) += A(16x32) B(32x16), 16-bit inputs: lane l holds A[l % 16][8 (l / 16) + 0..7],
 // B[8 (l / 16) + 0..7][l % 16] and D[4 (l / 16) + 0..3][l % 16].

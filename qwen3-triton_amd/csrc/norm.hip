@@ -133,6 +133,10 @@ __global__ __launch_bounds__(kBlock) void rmsnorm_bwd_kernel(const typename T::s
     dot = row_sum<TPR>(dot, red);
     const float inv = rsqrtf(ss * inv_h + eps);
     const float c = inv * inv * inv * dot * inv_h;  // inv * (inv^2 * mean(g*w*x))
+    // The second pass unpacks the packed operands again: keeping the unpacked fp32 copies live across
+    // the reductions took the kernel to 356 VGPRs (one workgroup per CU, too few loads in flight).
+#pragma unroll
+    for (int j = 0; j < MAXV; ++j) asm volatile("" : "+v"(xr[j]), "+v"(gr[j]), "+v"(wv[j]));
 #pragma unroll
     for (int j = 0; j < MAXV; ++j) {
       const int vi = j * TPR + t;
@@ -360,40 +364,46 @@ __global__ __launch_bounds__(kBlock) void norm_rope_bwd_kernel(const typename T:
   float acc[V];
 #pragma unroll
   for (int e = 0; e < V; ++e) acc[e] = 0.f;
-  for (int64_t base = (int64_t)blockIdx.x * RPB; base < rows; base += (int64_t)gridDim.x * RPB) {
-    const int64_t row = base + g;
-    const bool valid = row < rows;
-    const int64_t tok = row / heads;
-    Vec<T> xv, gv, cv, sv;
-    if (valid) {
-      xv = load_vec<T>(x + row * D + t * V);
-      gv = load_vec<T>(dy + row * D + t * V);
-      cv = load_vec<T>(cs + tok * D + t * V);
-      sv = load_vec<T>(sn + tok * D + t * V);
-    } else {
+  // U rows per thread and iteration (RPB apart), every load issued before the first use at clamped
+  // row indices (rows past the end are masked at the store and in the dw sum).
+  constexpr int U = 4;
+  for (int64_t base = (int64_t)blockIdx.x * RPB * U; base < rows; base += (int64_t)gridDim.x * RPB * U) {
+    i32x4 xr[U], gr[U], cr[U], sr[U];
 #pragma unroll
-      for (int e = 0; e < V; ++e) xv.v[e] = gv.v[e] = cv.v[e] = sv.v[e] = 0.f;
+    for (int j = 0; j < U; ++j) {
+      const int64_t rc = min(base + j * RPB + g, rows - 1), tok = rc / heads;
+      xr[j] = *reinterpret_cast<const i32x4*>(x + rc * D + t * V);
+      gr[j] = *reinterpret_cast<const i32x4*>(dy + rc * D + t * V);
+      cr[j] = *reinterpret_cast<const i32x4*>(cs + tok * D + t * V);
+      sr[j] = *reinterpret_cast<const i32x4*>(sn + tok * D + t * V);
     }
-    float ss = 0.f, dot = 0.f;
-    float ng[V];
 #pragma unroll
-    for (int e = 0; e < V; ++e) {
-      const float gs_p = partner<TPR>(gv.v[e] * sv.v[e]);  // dy[p] * sin[p]
-      ng[e] = gv.v[e] * cv.v[e] + sign * gs_p;
-      ss += xv.v[e] * xv.v[e];
-      dot += ng[e] * wv.v[e] * xv.v[e];
-    }
-    ss = group_sum<TPR>(ss);
-    dot = group_sum<TPR>(dot);
-    const float inv = rsqrtf(ss * (1.f / D) + eps);
-    const float c = inv * inv * inv * dot * (1.f / D);
-    Vec<T> o;
+    for (int j = 0; j < U; ++j) {
+      const int64_t row = base + j * RPB + g;
+      const bool valid = row < rows;
+      const Vec<T> xv = unpack_vec<T>(xr[j]), gv = unpack_vec<T>(gr[j]), cv = unpack_vec<T>(cr[j]),
+                   sv = unpack_vec<T>(sr[j]);
+      float ss = 0.f, dot = 0.f;
+      float ng[V];
 #pragma unroll
-    for (int e = 0; e < V; ++e) {
-      o.v[e] = ng[e] * wv.v[e] * inv - xv.v[e] * c;
-      acc[e] += ng[e] * xv.v[e] * inv;
+      for (int e = 0; e < V; ++e) {
+        const float gs_p = partner<TPR>(gv.v[e] * sv.v[e]);  // dy[p] * sin[p]
+        ng[e] = gv.v[e] * cv.v[e] + sign * gs_p;
+        ss += xv.v[e] * xv.v[e];
+        dot += ng[e] * wv.v[e] * xv.v[e];
+      }
+      ss = group_sum<TPR>(ss);
+      dot = group_sum<TPR>(dot);
+      const float inv = rsqrtf(ss * (1.f / D) + eps);
+      const float c = inv * inv * inv * dot * (1.f / D);
+      Vec<T> o;
+#pragma unroll
+      for (int e = 0; e < V; ++e) {
+        o.v[e] = ng[e] * wv.v[e] * inv - xv.v[e] * c;
+        if (valid) acc[e] += ng[e] * xv.v[e] * inv;
+      }
+      if (valid) store_vec<T>(dx + row * D + t * V, o);
     }
-    if (valid) store_vec<T>(dx + row * D + t * V, o);
   }
   for (int gi = 0; gi < RPB; ++gi) {
     if (g == gi) {
