@@ -47,6 +47,15 @@ int q3_rmsnorm_fwd(int dtype, const void* x, const void* w, void* y, int64_t row
 size_t q3_rmsnorm_bwd_workspace_bytes(int64_t rows, int64_t h);
 int q3_rmsnorm_bwd(int dtype, const void* x, const void* w, const void* dy, void* dx, void* dw, void* workspace,
                    int64_t rows, int64_t h, float eps, hipStream_t stream);
+/* dx = dres + (the RMSNorm input gradient), the backward of a residual block's input x that feeds
+ * both the residual sum and the norm (y = x + f(norm(x))): the two gradients of x are summed in
+ * the same pass instead of by a separate add.  dres [rows, h], same dtype; dw and the workspace as
+ * q3_rmsnorm_bwd.  The norm's gradient is rounded to the storage type before the sum, as the
+ * separate add would see it.
+ * Replaces: kernels/norm.py:39-66 (_RMSNorm.backward) + kernels/residual.py:13-30 (_Residual.backward),
+ *           whose two gradients of x the reference sums in autograd. */
+int q3_rmsnorm_bwd_add(int dtype, const void* x, const void* w, const void* dy, const void* dres, void* dx, void* dw,
+                       void* workspace, int64_t rows, int64_t h, float eps, hipStream_t stream);
 
 /* ------------------------------------------------------------------ fused per-head RMSNorm + RoPE
  * x: [tokens, heads, d] (rows = tokens*heads); cos/sin: [tokens, d]; w: [d].

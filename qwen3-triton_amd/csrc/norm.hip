@@ -79,16 +79,19 @@ __global__ __launch_bounds__(kBlock) void rmsnorm_fwd_kernel(const typename T::s
 }
 
 // ---------------------------------------------------------------- RMSNorm backward (dx + dw partials)
-template <typename T, int TPR, int MAXV>
+// RES: dx = dres + (the norm's input gradient) -- the residual branch's gradient of the same input,
+// summed here instead of in a separate add.
+template <typename T, int TPR, int MAXV, bool RES>
 __global__ __launch_bounds__(kBlock) void rmsnorm_bwd_kernel(const typename T::storage* __restrict__ x,
                                                              const typename T::storage* __restrict__ w,
                                                              const typename T::storage* __restrict__ dy,
+                                                             const typename T::storage* __restrict__ dres,
                                                              typename T::storage* __restrict__ dx,
                                                              float* __restrict__ partial, int64_t rows, int h,
                                                              float eps) {
   constexpr int V = T::vec;
   constexpr int RPB = kBlock / TPR;
-  extern __shared__ float fold[];  // h floats
+  extern __shared__ float fold[];  // h floats, then the weight row (h storage elements)
   __shared__ float red[kBlock / 64];
   const int nvec = h / V;
   const int t = threadIdx.x % TPR, g = threadIdx.x / TPR;
@@ -96,32 +99,34 @@ __global__ __launch_bounds__(kBlock) void rmsnorm_bwd_kernel(const typename T::s
   // Operands stay packed (16 bytes per vector) until used, and every load of a row is issued before
   // any is consumed: rows past the end and vectors past h re-read a valid vector, and their terms
   // are masked where they are used.
+  // The weight row lives in LDS (read by both passes of every row), leaving the registers to the
+  // row operands in flight and the fp32 dW accumulators.
+  i32x4* wsh = reinterpret_cast<i32x4*>(fold + h);
+  for (int i = threadIdx.x; i < nvec; i += kBlock) wsh[i] = *reinterpret_cast<const i32x4*>(w + (int64_t)i * V);
+  __syncthreads();
   float acc[MAXV][V];
-  i32x4 wv[MAXV];
 #pragma unroll
-  for (int j = 0; j < MAXV; ++j) {
-    const int vi = j * TPR + t;
-    wv[j] = *reinterpret_cast<const i32x4*>(w + (int64_t)(vi < nvec ? vi : 0) * V);
+  for (int j = 0; j < MAXV; ++j)
 #pragma unroll
     for (int e = 0; e < V; ++e) acc[j][e] = 0.f;
-  }
   for (int64_t base = (int64_t)blockIdx.x * RPB; base < rows; base += (int64_t)gridDim.x * RPB) {
     const int64_t row = base + g;
     const bool valid = row < rows;
     const int64_t rc = valid ? row : rows - 1;
-    i32x4 xr[MAXV], gr[MAXV];
+    i32x4 xr[MAXV], gr[MAXV], rr[RES ? MAXV : 1];
 #pragma unroll
     for (int j = 0; j < MAXV; ++j) {
       const int vi = j * TPR + t;
       const int64_t off = rc * h + (int64_t)(vi < nvec ? vi : 0) * V;
       xr[j] = *reinterpret_cast<const i32x4*>(x + off);
       gr[j] = *reinterpret_cast<const i32x4*>(dy + off);
+      if constexpr (RES) rr[j] = *reinterpret_cast<const i32x4*>(dres + off);
     }
     float ss = 0.f, dot = 0.f;
 #pragma unroll
     for (int j = 0; j < MAXV; ++j) {
       if (j * TPR + t < nvec) {
-        const Vec<T> xv = unpack_vec<T>(xr[j]), gv = unpack_vec<T>(gr[j]), wf = unpack_vec<T>(wv[j]);
+        const Vec<T> xv = unpack_vec<T>(xr[j]), gv = unpack_vec<T>(gr[j]), wf = unpack_vec<T>(wsh[j * TPR + t]);
 #pragma unroll
         for (int e = 0; e < V; ++e) {
           ss += xv.v[e] * xv.v[e];
@@ -136,17 +141,26 @@ __global__ __launch_bounds__(kBlock) void rmsnorm_bwd_kernel(const typename T::s
     // The second pass unpacks the packed operands again: keeping the unpacked fp32 copies live across
     // the reductions took the kernel to 356 VGPRs (one workgroup per CU, too few loads in flight).
 #pragma unroll
-    for (int j = 0; j < MAXV; ++j) asm volatile("" : "+v"(xr[j]), "+v"(gr[j]), "+v"(wv[j]));
+    for (int j = 0; j < MAXV; ++j) asm volatile("" : "+v"(xr[j]), "+v"(gr[j]));
+    if constexpr (RES) {
+#pragma unroll
+      for (int j = 0; j < MAXV; ++j) asm volatile("" : "+v"(rr[j]));
+    }
 #pragma unroll
     for (int j = 0; j < MAXV; ++j) {
       const int vi = j * TPR + t;
       if (valid && vi < nvec) {
-        const Vec<T> xv = unpack_vec<T>(xr[j]), gv = unpack_vec<T>(gr[j]), wf = unpack_vec<T>(wv[j]);
+        const Vec<T> xv = unpack_vec<T>(xr[j]), gv = unpack_vec<T>(gr[j]), wf = unpack_vec<T>(wsh[vi]);
         Vec<T> o;
 #pragma unroll
         for (int e = 0; e < V; ++e) {
           o.v[e] = gv.v[e] * wf.v[e] * inv - xv.v[e] * c;
           acc[j][e] += gv.v[e] * xv.v[e] * inv;
+        }
+        if constexpr (RES) {  // the norm's gradient rounded as the standalone kernel rounds it, then added
+          const Vec<T> rv = unpack_vec<T>(rr[j]);
+#pragma unroll
+          for (int e = 0; e < V; ++e) o.v[e] = to_f32<T>(from_f32<T>(o.v[e])) + rv.v[e];
         }
         store_vec<T>(dx + row * h + (int64_t)vi * V, o);
       }
@@ -439,12 +453,16 @@ int launch_fwd(const void* x, const void* w, void* y, int64_t rows, int64_t h, f
 }
 
 template <typename T, int TPR, int MAXV>
-int launch_bwd(const void* x, const void* w, const void* dy, void* dx, void* dw, float* part, int64_t rows,
-               int64_t h, float eps, hipStream_t s) {
+int launch_bwd(const void* x, const void* w, const void* dy, const void* dres, void* dx, void* dw, float* part,
+               int64_t rows, int64_t h, float eps, hipStream_t s) {
   typedef typename T::storage S;
   const int64_t nb = bwd_blocks(rows, h);
-  rmsnorm_bwd_kernel<T, TPR, MAXV><<<(unsigned)nb, kBlock, h * sizeof(float), s>>>(
-      (const S*)x, (const S*)w, (const S*)dy, (S*)dx, part, rows, (int)h, eps);
+  if (dres)
+    rmsnorm_bwd_kernel<T, TPR, MAXV, true><<<(unsigned)nb, kBlock, h * (sizeof(float) + sizeof(S)), s>>>(
+        (const S*)x, (const S*)w, (const S*)dy, (const S*)dres, (S*)dx, part, rows, (int)h, eps);
+  else
+    rmsnorm_bwd_kernel<T, TPR, MAXV, false><<<(unsigned)nb, kBlock, h * (sizeof(float) + sizeof(S)), s>>>(
+        (const S*)x, (const S*)w, (const S*)dy, nullptr, (S*)dx, part, rows, (int)h, eps);
   colsum<T>(part, (S*)dw, (int)nb, (int)h, s);
   return (int)hipGetLastError();
 }
@@ -470,24 +488,29 @@ int rms_fwd_dispatch(const void* x, const void* w, void* y, int64_t rows, int64_
 }
 
 template <typename T>
-int rms_bwd_dispatch(const void* x, const void* w, const void* dy, void* dx, void* dw, float* part, int64_t rows,
-                     int64_t h, float eps, hipStream_t s) {
+int rms_bwd_dispatch(const void* x, const void* w, const void* dy, const void* dres, void* dx, void* dw, float* part,
+                     int64_t rows, int64_t h, float eps, hipStream_t s) {
   constexpr int V = T::vec;
   typedef typename T::storage S;
   const int64_t nvec = h / V;
   if (h % V == 0) {
-    if (nvec <= 8) return launch_bwd<T, 8, 1>(x, w, dy, dx, dw, part, rows, h, eps, s);
-    if (nvec <= 16) return launch_bwd<T, 16, 1>(x, w, dy, dx, dw, part, rows, h, eps, s);
-    if (nvec <= 32) return launch_bwd<T, 32, 1>(x, w, dy, dx, dw, part, rows, h, eps, s);
-    if (nvec <= 64) return launch_bwd<T, 64, 1>(x, w, dy, dx, dw, part, rows, h, eps, s);
-    if (nvec <= 64 * 4) return launch_bwd<T, 64, 4>(x, w, dy, dx, dw, part, rows, h, eps, s);
-    if (nvec <= 64 * 8) return launch_bwd<T, 64, 8>(x, w, dy, dx, dw, part, rows, h, eps, s);
-    if (nvec <= 256 * 4) return launch_bwd<T, 256, 4>(x, w, dy, dx, dw, part, rows, h, eps, s);
+    if (nvec <= 8) return launch_bwd<T, 8, 1>(x, w, dy, dres, dx, dw, part, rows, h, eps, s);
+    if (nvec <= 16) return launch_bwd<T, 16, 1>(x, w, dy, dres, dx, dw, part, rows, h, eps, s);
+    if (nvec <= 32) return launch_bwd<T, 32, 1>(x, w, dy, dres, dx, dw, part, rows, h, eps, s);
+    if (nvec <= 64) return launch_bwd<T, 64, 1>(x, w, dy, dres, dx, dw, part, rows, h, eps, s);
+    if (nvec <= 64 * 4) return launch_bwd<T, 64, 4>(x, w, dy, dres, dx, dw, part, rows, h, eps, s);
+    if (nvec <= 64 * 8) return launch_bwd<T, 64, 8>(x, w, dy, dres, dx, dw, part, rows, h, eps, s);
+    if (nvec <= 256 * 4) return launch_bwd<T, 256, 4>(x, w, dy, dres, dx, dw, part, rows, h, eps, s);
   }
   const int64_t gb = generic_blocks(rows, h);
   rownorm_generic_bwd<T><<<(unsigned)gb, kBlock, 0, s>>>((const S*)x, (const S*)w, nullptr, nullptr, (const S*)dy,
                                                          (S*)dx, part, rows, (int)h, 0, eps);
   colsum<T>(part, (S*)dw, (int)(4 * gb), (int)h, s);
+  if (dres) {  // the scalar path adds the residual gradient with the streaming add kernel
+    const int rc = (int)hipGetLastError();
+    if (rc) return rc;
+    return q3_add(T::code, dx, dres, dx, rows * h, s);
+  }
   return (int)hipGetLastError();
 }
 
@@ -585,7 +608,14 @@ int q3_rmsnorm_bwd(int dtype, const void* x, const void* w, const void* dy, void
                    int64_t rows, int64_t h, float eps, hipStream_t stream) {
   Q3_REQUIRE(dtype_ok(dtype) && x && w && dy && dx && dw && workspace && rows > 0 && h > 0 && eps > 0.f);
   Q3_REQUIRE(h <= 16384);  // LDS fold buffer of the vector path: h floats
-  return Q3_DISPATCH(dtype, rms_bwd_dispatch, x, w, dy, dx, dw, (float*)workspace, rows, h, eps, stream);
+  return Q3_DISPATCH(dtype, rms_bwd_dispatch, x, w, dy, nullptr, dx, dw, (float*)workspace, rows, h, eps, stream);
+}
+
+int q3_rmsnorm_bwd_add(int dtype, const void* x, const void* w, const void* dy, const void* dres, void* dx, void* dw,
+                       void* workspace, int64_t rows, int64_t h, float eps, hipStream_t stream) {
+  Q3_REQUIRE(dtype_ok(dtype) && x && w && dy && dres && dx && dw && workspace && rows > 0 && h > 0 && eps > 0.f);
+  Q3_REQUIRE(h <= 16384);
+  return Q3_DISPATCH(dtype, rms_bwd_dispatch, x, w, dy, dres, dx, dw, (float*)workspace, rows, h, eps, stream);
 }
 
 int q3_norm_rope_fwd(int dtype, const void* x, const void* w, const void* cos, const void* sin, void* y,

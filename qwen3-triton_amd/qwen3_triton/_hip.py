@@ -30,6 +30,7 @@ SIGNATURES: dict[str, tuple] = {
     "q3_rmsnorm_fwd": (_i32, [_i32, _p, _p, _p, _i64, _i64, _f32, _p]),
     "q3_rmsnorm_bwd_workspace_bytes": (_sz, [_i64, _i64]),
     "q3_rmsnorm_bwd": (_i32, [_i32, _p, _p, _p, _p, _p, _p, _i64, _i64, _f32, _p]),
+    "q3_rmsnorm_bwd_add": (_i32, [_i32, _p, _p, _p, _p, _p, _p, _p, _i64, _i64, _f32, _p]),
     "q3_norm_rope_fwd": (_i32, [_i32, _p, _p, _p, _p, _p, _i64, _i64, _i64, _f32, _p]),
     "q3_norm_rope_bwd_workspace_bytes": (_sz, [_i64, _i64, _i64]),
     "q3_norm_rope_bwd": (_i32, [_i32, _p, _p, _p, _p, _p, _p, _p, _p, _i64, _i64, _i64, _f32, _p]),

@@ -20,7 +20,7 @@ from .kernels.embedding import embedding
 from .kernels.linear import linear
 from .kernels.lm_head_ce import lm_head_cross_entropy
 from .kernels.loss import causal_cross_entropy
-from .kernels.norm import rms_norm
+from .kernels.norm import rms_norm, rms_norm_fork
 from .kernels.residual import residual_add
 from .kernels.rotary import apply_rotary, rotary_tables
 
@@ -145,8 +145,12 @@ class TritonDecoderLayer(nn.Module):
         self.post_attention_layernorm = TritonNorm(c.hidden_size, c.rms_norm_eps)
 
     def forward(self, x, position_embeddings):
-        x = residual_add(x, self.self_attn(self.input_layernorm(x), position_embeddings))
-        return residual_add(x, self.mlp(self.post_attention_layernorm(x)))
+        # x feeds both the residual sum and the norm: one fork node, so the backward sums the two
+        # gradients of x inside the RMSNorm backward kernel (``_model.py:60-108`` layer order).
+        x, h = rms_norm_fork(x, self.input_layernorm.weight, self.input_layernorm.eps)
+        x = residual_add(x, self.self_attn(h, position_embeddings))
+        x, h = rms_norm_fork(x, self.post_attention_layernorm.weight, self.post_attention_layernorm.eps)
+        return residual_add(x, self.mlp(h))
 
 
 class TritonQwen3Model(nn.Module):

@@ -38,6 +38,18 @@ def rmsnorm_bwd(x, w, dy, eps):
     return dx, dw
 
 
+def rmsnorm_bwd_add(x, w, dy, dres, eps):
+    """dx = dres + the RMSNorm input gradient (one kernel), dw."""
+    h = w.numel()
+    rows = x.numel() // h
+    dx = torch.empty_like(x)
+    dw = torch.empty_like(w)
+    ws = H.workspace(H.query("q3_rmsnorm_bwd_workspace_bytes", rows, h), x.device)
+    H.call("q3_rmsnorm_bwd_add", H.code(x.dtype), x.data_ptr(), w.data_ptr(), dy.data_ptr(), dres.data_ptr(),
+           dx.data_ptr(), dw.data_ptr(), ws.data_ptr(), rows, h, float(eps), H.stream())
+    return dx, dw
+
+
 def norm_rope_fwd(x, w, cos, sin, eps):
     """x [B,S,heads,D] (or [tokens,heads,D]); cos/sin [B,S,D]."""
     d, heads = x.shape[-1], x.shape[-2]

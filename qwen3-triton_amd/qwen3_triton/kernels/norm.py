@@ -35,3 +35,31 @@ class _RMSNorm(torch.autograd.Function):
 def rms_norm(x, weight, eps=1e-6, *, optimized=False):
     """``kernels/norm.py:65``."""
     return _RMSNorm.apply(x, weight, eps, optimized)
+
+
+class _RMSNormFork(torch.autograd.Function):
+    """The input of a residual block, x -> (x, rms_norm(x)), as one node: the residual branch's
+    gradient and the norm's input gradient of x are summed inside the backward kernel
+    (``q3_rmsnorm_bwd_add``) instead of by autograd with a separate add.  Same math as
+    ``rms_norm`` on the second output; the first is a view of x."""
+
+    @staticmethod
+    def forward(ctx, x, weight, eps):
+        y = _RMSNorm.forward(ctx, x, weight, eps, False)
+        return x.view_as(x), y
+
+    @staticmethod
+    def backward(ctx, dres, dy):
+        x, w = ctx.saved_tensors
+        if dy is None:
+            return dres, None, None
+        if dres is None:
+            dx, dw = _ops.rmsnorm_bwd(x, w, dy.contiguous(), ctx.eps)
+        else:
+            dx, dw = _ops.rmsnorm_bwd_add(x, w, dy.contiguous(), dres.contiguous(), ctx.eps)
+        return dx, dw, None
+
+
+def rms_norm_fork(x, weight, eps=1e-6):
+    """(x, rms_norm(x, weight, eps)) for a residual block ``x + f(rms_norm(x))``."""
+    return _RMSNormFork.apply(x, weight, eps)

@@ -7,7 +7,7 @@ import oracle as O
 from _util import cosine, max_rel, randn, seeded, tol_for
 
 from qwen3_triton.kernels import _ops
-from qwen3_triton.kernels.norm import rms_norm
+from qwen3_triton.kernels.norm import rms_norm, rms_norm_fork
 from qwen3_triton.kernels.norm_rope import norm_rope
 from qwen3_triton.kernels.rotary import apply_rotary, rotary_tables
 from qwen3_triton.kernels.activation import swiglu
@@ -55,6 +55,34 @@ def test_rmsnorm_fwd_bwd(shape, dtype):
     # deterministic: same inputs, bitwise-equal weight gradient
     _, dw2 = _grads(rms_norm(xd, wd, 1e-6), (xd, wd), dy.cuda())
     assert torch.equal(dw, dw2)
+
+
+@pytest.mark.parametrize("dtype", DTYPES)
+@pytest.mark.parametrize("shape", [(2, 7, 128), (3, 4096), (5, 24), (2, 3, 5120), (2, 8192), (1, 1, 10000)])
+def test_rmsnorm_fork_residual_gradient(shape, dtype):
+    """x -> (x, rms_norm(x)) feeding x + f(norm(x)): dx = g + norm_bwd(g * df) from one kernel
+    (q3_rmsnorm_bwd_add, the scalar path with its add for h = 10000), against the oracle."""
+    print(f"rmsnorm fork {shape} {dtype}", flush=True)
+    gen = seeded(3)
+    h = shape[-1]
+    x = randn(*shape, gen=gen, dtype=dtype)
+    w = randn(h, gen=gen, dtype=dtype, scale=0.1, shift=1.0)
+    g = randn(*shape, gen=gen, dtype=dtype)
+    c = randn(*shape, gen=gen, dtype=dtype)   # y = x + c * norm(x): the norm branch's upstream grad is g * c
+    xd, wd, cd = x.cuda().requires_grad_(), w.cuda().requires_grad_(), c.cuda()
+    xa, n = rms_norm_fork(xd, wd, 1e-6)
+    assert xa.data_ptr() == xd.data_ptr()
+    y = residual_add(xa, (n.float() * cd.float()).to(dtype))
+    dx, dw = _grads(y, (xd, wd), g.cuda())
+    gn = (g.double() * c.double()).to(dtype)
+    ex, ew = O.rms_norm_backward_reference(x, w, gn, 1e-6)
+    check(dx, (g.double() + ex.double()).to(dtype), dtype, "dx")
+    check(dw, ew, dtype, "dw")
+    # the fused kernel equals norm backward + residual add, bit for bit on the same inputs
+    dx1, dw1 = _ops.rmsnorm_bwd(xd.detach(), wd.detach(), gn.cuda(), 1e-6)
+    dx2, dw2 = _ops.rmsnorm_bwd_add(xd.detach(), wd.detach(), gn.cuda(), g.cuda(), 1e-6)
+    assert torch.equal(dw1, dw2)
+    assert torch.equal(_ops.add(dx1, g.cuda()), dx2)
 
 
 @pytest.mark.parametrize("dtype", DTYPES)
