@@ -84,7 +84,10 @@ __global__ __launch_bounds__(kThreads) void ce_stats_kernel(const typename T::st
 }
 
 // Merge the per-chunk (m, s) of each row (chunk-major arrays [nchunks][rows]), write lse and the
-// per-row loss; flag targets outside [0, vocab) that are not ignore_index.
+// per-row loss; flag targets outside [0, vocab) that are not ignore_index.  A workgroup takes
+// kFinRows rows; thread t folds the partials c = t / kFinRows (mod kFinSlices) of row t % kFinRows,
+// then the slices of each row merge in slice order (fixed partition and order: deterministic).
+constexpr int kFinRows = 16, kFinSlices = kThreads / kFinRows;
 __global__ __launch_bounds__(kThreads) void ce_finish_kernel(const float* __restrict__ m_part,
                                                              const float* __restrict__ s_part, int nchunks,
                                                              const float* __restrict__ pick,
@@ -92,10 +95,30 @@ __global__ __launch_bounds__(kThreads) void ce_finish_kernel(const float* __rest
                                                              float* __restrict__ lse, float* __restrict__ loss_rows,
                                                              int* __restrict__ bad, int64_t rows, int64_t vocab,
                                                              int64_t ignore) {
-  const int64_t r = (int64_t)blockIdx.x * kThreads + threadIdx.x;
-  if (r >= rows) return;
+  __shared__ float sm[kFinSlices][kFinRows], ss[kFinSlices][kFinRows];
+  const int lr = threadIdx.x % kFinRows, sl = threadIdx.x / kFinRows;
+  const int64_t r = (int64_t)blockIdx.x * kFinRows + lr;
+  const int64_t rc = r < rows ? r : rows - 1;
   float m = -INFINITY, s = 0.f;
-  for (int c = 0; c < nchunks; ++c) lse_combine(m, s, m_part[(int64_t)c * rows + r], s_part[(int64_t)c * rows + r]);
+  int c = sl;
+  for (; c + 3 * kFinSlices < nchunks; c += 4 * kFinSlices) {  // four partials in flight
+    float pm[4], ps[4];
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      pm[u] = m_part[(int64_t)(c + u * kFinSlices) * rows + rc];
+      ps[u] = s_part[(int64_t)(c + u * kFinSlices) * rows + rc];
+    }
+#pragma unroll
+    for (int u = 0; u < 4; ++u) lse_combine(m, s, pm[u], ps[u]);
+  }
+  for (; c < nchunks; c += kFinSlices) lse_combine(m, s, m_part[(int64_t)c * rows + rc], s_part[(int64_t)c * rows + rc]);
+  sm[sl][lr] = m;
+  ss[sl][lr] = s;
+  __syncthreads();
+  if (sl != 0 || r >= rows) return;
+  m = sm[0][lr];
+  s = ss[0][lr];
+  for (int k = 1; k < kFinSlices; ++k) lse_combine(m, s, sm[k][lr], ss[k][lr]);
   const float l = m + __logf(s);
   lse[r] = l;
   const int64_t t = tgt[r];
@@ -252,7 +275,7 @@ int q3_ce_finish(const float* m_part, const float* s_part, int nchunks, const fl
                  float* lse, float* loss_rows, int* bad, float* loss, float* count, int64_t rows, int64_t vocab,
                  int64_t ignore_index, hipStream_t stream) {
   Q3_REQUIRE(m_part && s_part && nchunks > 0 && pick && tgt && lse && loss_rows && loss && count && rows > 0);
-  ce_finish_kernel<<<(unsigned)((rows + kThreads - 1) / kThreads), kThreads, 0, stream>>>(
+  ce_finish_kernel<<<(unsigned)((rows + kFinRows - 1) / kFinRows), kThreads, 0, stream>>>(
       m_part, s_part, nchunks, pick, tgt, lse, loss_rows, bad, rows, vocab, ignore_index);
   ce_mean_kernel<<<1, kThreads, 0, stream>>>(loss_rows, tgt, rows, vocab, ignore_index, loss, count);
   return (int)hipGetLastError();
