@@ -55,22 +55,36 @@ __global__ __launch_bounds__(NW * 64) void dlinear_kernel(DecArgs a) {
   const int n0 = tile * 16, K = a.K, M = a.M;
   const int r = lane & 15, kq = lane >> 4;  // r: token row (A) and weight row (B) of this lane
 
-  if constexpr (NORM) {
-    // Sum of squares of each input row over the whole workgroup: thread t takes chunks t, t + NW*64,
-    // .. of every row, the loads of all rows issued before any is used (one memory latency).
-    __shared__ float part[NW][16];
-    float ss[16];
+  if (NORM && M > 4) {
+    // many rows: one wave per row (the rows' loads run in parallel across the waves)
+    for (int m = wave; m < M; m += NW) {
+      const u16* xr = a.x + m * a.ldx;
+      float ss = 0.f;
+      for (int c = lane; c < K / 8; c += 64) {
+        const Vec<T> v = load_vec<T>(xr + c * 8);
 #pragma unroll
-    for (int m = 0; m < 16; ++m) ss[m] = 0.f;
+        for (int e = 0; e < 8; ++e) ss += v.v[e] * v.v[e];
+      }
+      ss = group_sum<64>(ss);
+      if (lane == 0) inv_s[m] = rsqrtf(ss * (1.f / (float)K) + a.eps);
+    }
+    __syncthreads();
+  } else if constexpr (NORM) {
+    // few rows: the sum of squares of each row over the whole workgroup: thread t takes chunks t,
+    // t + NW*64, .. of every row, the loads of all rows issued before any is used.
+    __shared__ float part[NW][4];
+    float ss[4];
+#pragma unroll
+    for (int m = 0; m < 4; ++m) ss[m] = 0.f;
     for (int c0 = 0; c0 < K / 8; c0 += NW * 64) {
       const int c = min(c0 + tid, K / 8 - 1);
       const bool live = c0 + tid < K / 8;
-      i32x4 raw[16];
+      i32x4 raw[4];
 #pragma unroll
-      for (int m = 0; m < 16; ++m)
+      for (int m = 0; m < 4; ++m)
         if (m < M) raw[m] = *reinterpret_cast<const i32x4*>(a.x + m * a.ldx + c * 8);
 #pragma unroll
-      for (int m = 0; m < 16; ++m)
+      for (int m = 0; m < 4; ++m)
         if (m < M && live) {
           const Vec<T> v = unpack_vec<T>(raw[m]);
 #pragma unroll
@@ -78,7 +92,7 @@ __global__ __launch_bounds__(NW * 64) void dlinear_kernel(DecArgs a) {
         }
     }
 #pragma unroll
-    for (int m = 0; m < 16; ++m)
+    for (int m = 0; m < 4; ++m)
       if (m < M) {
         const float w = group_sum<64>(ss[m]);
         if (lane == 0) part[wave][m] = w;
