@@ -24,7 +24,7 @@ __all__ = [
     "lm_head_cross_entropy_reference",
     "embedding_backward_reference",
     "OracleConfig", "init_params", "decoder_layer_reference", "model_forward_reference",
-    "greedy_generate_reference", "argmax_lowest_reference",
+    "greedy_generate_reference", "argmax_lowest_reference", "cached_decode_reference",
 ]
 
 
@@ -376,3 +376,39 @@ def greedy_generate_reference(ids, p, cfg, max_new_tokens, *, eos=(), pad=0, dty
         if eos and bool(done.all()):
             break
     return out, torch.stack(margins, dim=1) if margins else torch.zeros(b, 0)
+
+
+def cached_decode_reference(prompt, p, cfg, steps, *, forced=None, dtype=torch.float32):
+    """Prefill + one-token-at-a-time decode through a K/V cache, ``inference/model.py:102-142,158-188``
+    (``_forward`` with ``cache.length`` as the RoPE / causal offset, ``logits_to_keep=1``).
+
+    The cache holds the already normed + rotated K and V of every position, so each step costs one
+    token's matrix products instead of a full recomputation.  ``forced`` [B, steps] (optional)
+    feeds fixed tokens instead of the greedy ones (teacher forcing), so a run can be compared step
+    by step with another run's logits.  Returns (greedy tokens [B, steps] chosen after each of the
+    ``steps`` forwards, last-position logits [B, steps, V]).  ``p`` should already be in ``dtype``
+    (converting a 150K-row embedding per call is slow); norm weights may be any dtype.
+    """
+    b, s = prompt.shape
+    caches = [dict() for _ in range(cfg.num_hidden_layers)]
+    inv = rope_inv_freq(cfg.rope_theta, cfg.head_dim)
+    emb = p["model.embed_tokens.weight"].to(dtype)
+    head = p["lm_head.weight"].to(dtype)
+    toks, logits_out = [], []
+    cur, start = prompt, 0
+    for step in range(steps):
+        n = cur.shape[1]
+        pos = torch.arange(start, start + n)[None, :].expand(b, n)
+        cos, sin = rotary_tables_reference(pos, inv, dtype=dtype)
+        x = emb[cur]
+        for l in range(cfg.num_hidden_layers):
+            x = decoder_layer_reference(x, p, f"model.layers.{l}.", cfg, cos, sin, start=start,
+                                        cache=caches[l], dtype=dtype)
+        x = rms_norm_reference(x[:, -1:], p["model.norm.weight"], cfg.rms_norm_eps, dtype=dtype)
+        last = (x @ head.T)[:, 0]
+        tok = argmax_lowest_reference(last)
+        toks.append(tok)
+        logits_out.append(last)
+        start += n
+        cur = (tok if forced is None else forced[:, step])[:, None]
+    return torch.stack(toks, dim=1), torch.stack(logits_out, dim=1)

@@ -8,15 +8,24 @@ from qwen3_triton.kernels import _ops
 from .attention import _validate
 
 
-def attention_backward_triton(q, k, v, grad_out, *, scale=None, lse=None):
-    """dQ, dK, dV of causal GQA attention.  The HIP backward needs O for delta = rowsum(O*dO), so
-    the forward is recomputed here (it also supplies LSE when none is given)."""
+def attention_backward_triton(q, k, v, grad_out, *, scale=None, lse=None, out=None):
+    """dQ, dK, dV of causal GQA attention ([B, H, S, D] operands).
+
+    The backward's softmax term needs delta = rowsum(O * dO) for every query row, and a row sum
+    over all keys cannot be formed tile by tile.  A caller that kept the forward output passes it
+    as ``out`` (with its ``lse``): then no forward work is repeated.  Without it one forward pass
+    supplies O (and LSE when ``lse`` is None).  This keyword is an addition to the reference
+    signature; the autograd path (``attention_triton_autograd``) always has O saved."""
     _validate(q, k, v, True)
     if grad_out.shape != q.shape:
         raise ValueError("invalid q/k/grad_out shapes")
     q, k, v, grad_out = (t.contiguous() for t in (q, k, v, grad_out))
     if scale is None:
         scale = 1.0 / math.sqrt(q.shape[-1])
-    out, lse_new = _ops.attention_fwd(q, k, v, scale)
-    lse = lse_new if lse is None else lse.contiguous()
-    return _ops.attention_bwd(q, k, v, out, lse, grad_out, scale)
+    if out is None or lse is None:
+        o, lse_new = _ops.attention_fwd(q, k, v, scale)
+        out = o if out is None else out
+        lse = lse_new if lse is None else lse
+    if out.shape != q.shape:
+        raise ValueError("out must have the shape of q")
+    return _ops.attention_bwd(q, k, v, out.contiguous(), lse.contiguous(), grad_out, scale)

@@ -13,6 +13,7 @@ from dataclasses import dataclass
 import torch
 from torch import nn
 
+from ._checkpoint import check_architecture, resolve_tied, rope_theta, scaled_rope  # noqa: F401
 from .kernels import _ops
 from .kernels.activation import swiglu
 from .kernels.attention import causal_attention_bshd
@@ -23,24 +24,6 @@ from .kernels.loss import causal_cross_entropy
 from .kernels.norm import rms_norm, rms_norm_fork
 from .kernels.residual import residual_add
 from .kernels.rotary import apply_rotary, rotary_tables
-
-
-def rope_theta(config):
-    """RoPE base of an HF Qwen3 config (``rope_theta``, or ``rope_parameters['rope_theta']`` in
-    newer transformers releases)."""
-    theta = getattr(config, 'rope_theta', None)
-    if theta is None:
-        theta = (getattr(config, 'rope_parameters', None) or {}).get('rope_theta', 10000.0)
-    return float(theta)
-
-
-def scaled_rope(config):
-    """True when the config asks for a RoPE scaling variant (anything but the default rotation)."""
-    for name in ('rope_scaling', 'rope_parameters'):
-        spec = getattr(config, name, None)
-        if spec and spec.get('rope_type', spec.get('type', 'default')) not in (None, 'default'):
-            return True
-    return False
 
 
 @dataclass(frozen=True)
@@ -165,49 +148,48 @@ class TritonQwen3Model(nn.Module):
 
     def forward(self, ids, position_ids=None):
         x = self.embed_tokens(ids)
-        if position_ids is None:
-            position_ids = _ops.positions(ids.shape[0], ids.shape[1], 0, ids.device)
-        if position_ids.shape == (1, ids.shape[1]) and ids.shape[0] != 1:
-            position_ids = position_ids.expand(ids.shape[0], -1).contiguous()
-        if position_ids.shape != ids.shape:
-            raise ValueError('position_ids must match batch and sequence')
-        positions = self.rotary_emb(position_ids, x.dtype)
+        positions = self.rotary_emb(self._positions_for(ids, position_ids), x.dtype)
         for layer in self.layers:
             x = layer(x, positions)
         return self.norm(x)
 
+    @staticmethod
+    def _positions_for(ids, position_ids):
+        """[B, S] int64 positions: 0..S-1 per row by default; one [1, S] row is shared by the batch."""
+        b, s = ids.shape
+        if position_ids is None:
+            return _ops.positions(b, s, 0, ids.device)
+        if tuple(position_ids.shape) == (1, s) and b > 1:
+            position_ids = position_ids.expand(b, s).contiguous()
+        if tuple(position_ids.shape) != (b, s):
+            raise ValueError(f'position_ids of shape {tuple(position_ids.shape)} do not match input_ids {(b, s)}')
+        return position_ids
+
 
 class TritonQwen3ForCausalLM(nn.Module):
     backbone_class = TritonQwen3Model
+    # HF forward features this dense causal-training model does not provide (no silent fallback).
+    _UNSUPPORTED_FORWARD = ('use_cache', 'past_key_values', 'attention_mask', 'output_attentions',
+                            'output_hidden_states', 'logits_to_keep')
 
     def __init__(self, config, options=None):
         super().__init__()
+        check_architecture(config)
         self.config = config
         self.options = options or ComputeOptions()
-        if config.model_type != 'qwen3':
-            raise ValueError('Official Qwen3 config required')
-        if config.hidden_act != 'silu' or config.attention_dropout != 0 or getattr(config, 'attention_bias', False):
-            raise ValueError('Only SiLU, zero dropout, bias-free Qwen3 supported')
-        if getattr(config, 'use_sliding_window', False) or scaled_rope(config):
-            raise ValueError('Sliding window and scaled RoPE are not implemented')
-        if config.head_dim % 2 or config.num_attention_heads % config.num_key_value_heads:
-            raise ValueError('Even rotary dimension and valid GQA required')
         self.model = self.backbone_class(config, self.options)
         self.lm_head = TritonLinear(config.hidden_size, config.vocab_size, config.initializer_range, self.options)
         self.tie_weights()
 
     def tie_weights(self):
+        """Share the embedding matrix as the LM head when the config ties them."""
         if self.config.tie_word_embeddings:
             self.lm_head.weight = self.model.embed_tokens.weight
 
     def load_hf_state_dict(self, state, *, assign=False):
-        state = dict(state)
-        if self.config.tie_word_embeddings and 'lm_head.weight' not in state:
-            state['lm_head.weight'] = state['model.embed_tokens.weight']
-        if self.config.tie_word_embeddings and not torch.equal(state['lm_head.weight'],
-                                                               state['model.embed_tokens.weight']):
-            raise ValueError('Checkpoint disagrees with tied embedding configuration')
-        result = self.load_state_dict(state, strict=True, assign=assign)
+        """Load official Qwen3 parameter names (strict); a tied checkpoint may omit the LM head."""
+        result = self.load_state_dict(resolve_tied(state, self.config.tie_word_embeddings), strict=True,
+                                      assign=assign)
         self.tie_weights()
         return result
 
@@ -215,20 +197,22 @@ class TritonQwen3ForCausalLM(nn.Module):
                 past_key_values=None, output_attentions=False, output_hidden_states=False, return_dict=True,
                 logits_to_keep=0):
         from transformers.modeling_outputs import CausalLMOutputWithPast
-        if use_cache or past_key_values is not None or attention_mask is not None or output_attentions or \
-                output_hidden_states or logits_to_keep:
-            raise ValueError('Only dense unpadded causal training without cache/extra outputs is implemented; '
-                             'no fallback')
+        asked = dict(use_cache=use_cache, past_key_values=past_key_values is not None,
+                     attention_mask=attention_mask is not None, output_attentions=output_attentions,
+                     output_hidden_states=output_hidden_states, logits_to_keep=logits_to_keep)
+        requested = [k for k in self._UNSUPPORTED_FORWARD if asked[k]]
+        if requested:
+            raise ValueError(f'dense unpadded causal training only; not implemented: {", ".join(requested)}')
         if input_ids.ndim != 2 or input_ids.dtype not in (torch.int32, torch.int64):
-            raise ValueError('Integer [B,S] input_ids required')
+            raise ValueError('input_ids must be an integer [batch, sequence] tensor')
         hidden = self.model(input_ids, position_ids)
+        logits = loss = None
         if labels is not None and self.options.fused_lm_head_loss:
             loss = lm_head_cross_entropy(hidden, self.lm_head.weight, labels)
-            logits = None
         else:
             logits = self.lm_head(hidden)
-            loss = causal_cross_entropy(logits, labels, optimized=self.options.loss_optimized) \
-                if labels is not None else None
-        if not return_dict:
-            return (loss, logits) if labels is not None else (logits,)
-        return CausalLMOutputWithPast(loss=loss, logits=logits)
+            if labels is not None:
+                loss = causal_cross_entropy(logits, labels, optimized=self.options.loss_optimized)
+        if return_dict:
+            return CausalLMOutputWithPast(loss=loss, logits=logits)
+        return (logits,) if labels is None else (loss, logits)

@@ -153,3 +153,29 @@ def rms_norm(x, weight, eps, *, reference_accumulation=False):
 def norm_rope(x, weight, cos, sin, eps):
     """``inference/kernels.py:188``: forward-only fused per-head RMSNorm + RoPE."""
     return _ops.norm_rope_fwd(x, weight, cos, sin, eps)
+
+
+def sliced_linear(x, weight):
+    """``inference/kernels.py:213``: Y = x W^T for ONE token row (decode GEMV).  The reference's
+    two-accumulator SM86 slicing is an accumulation-order choice; here it is the streaming decode
+    kernel."""
+    if x.numel() != x.shape[-1] or not x.is_contiguous() or not weight.is_contiguous():
+        raise ValueError('one contiguous token row and a row-major weight are required')
+    if x.dtype != torch.bfloat16 or weight.dtype != x.dtype or x.device != weight.device or not x.is_cuda or \
+            x.shape[-1] != weight.shape[1]:
+        raise ValueError('matching bf16 ROCm input and [N, K] weight required')
+    return linear(x, weight, gemv=True)
+
+
+def tiled_prefill_gate_up(x, gate_weight, up_weight):
+    """``inference/kernels.py:222``: silu(x Wg^T) * (x Wu^T) for a short prefill chunk, forward only
+    (the dual-weight GEMM of ``mlp_precision``; any row count, not only the reference's M = 65)."""
+    n, k = gate_weight.shape
+    if x.shape[-1] != k or up_weight.shape != gate_weight.shape:
+        raise ValueError('x [..., K] with matching [N, K] gate/up weights required')
+    if x.dtype != torch.bfloat16 or not x.is_cuda or \
+            any(t.device != x.device or t.dtype != x.dtype or not t.is_contiguous() for t in (x, gate_weight, up_weight)):
+        raise ValueError('matching contiguous bf16 ROCm inputs required')
+    from ..kernels.mlp_precision import gate_up_swiglu
+    with torch.no_grad():
+        return gate_up_swiglu(x, gate_weight, up_weight, optimized=True)

@@ -8,7 +8,8 @@ from pathlib import Path
 import torch
 from torch import nn
 
-from .._model import TritonQwen3ForCausalLM, rope_theta
+from .._checkpoint import read_checkpoint, resolve_tied, rope_theta
+from .._model import TritonQwen3ForCausalLM
 from ..configuration import OptimizationOptions
 from ..kernels import _ops
 from ..kernels.activation import swiglu
@@ -20,10 +21,11 @@ from . import kernels
 
 @dataclass
 class KVCache:
-    """Request-owned [layer][batch, KV-head, capacity, head-dim] storage (``inference/model.py:26-45``).
+    """Per-request key/value storage, one ``[batch, kv_heads, capacity, head_dim]`` bf16 tensor per
+    layer for keys and one for values (the reference's cache fields, ``inference/model.py:26-45``).
 
-    Only positions below ``length`` are readable; reset keeps the allocation and discards the
-    logical contents.  A failed forward invalidates the cache until an explicit reset."""
+    ``length`` positions are filled.  ``reset`` keeps the memory and forgets the contents.  A forward
+    that raises marks the cache invalid, and it stays unusable until ``reset``."""
     keys: list
     values: list
     capacity: int
@@ -34,11 +36,21 @@ class KVCache:
 
     @property
     def nbytes(self):
-        return sum(t.numel() * t.element_size() for t in self.keys + self.values)
+        return sum(t.numel() * t.element_size() for t in (*self.keys, *self.values))
 
     def reset(self):
-        self.length = 0
-        self.valid = True
+        self.length, self.valid = 0, True
+
+    def admit(self, owner, batch, tokens):
+        """Raise unless ``tokens`` more positions of ``batch`` rows fit this valid cache of ``owner``."""
+        problems = [what for bad, what in (
+            (self.owner is not owner, 'belongs to another model'),
+            (not self.valid, 'was invalidated by a failed forward (reset it)'),
+            (batch != self.batch_size, f'holds batch {self.batch_size}, not {batch}'),
+            (self.length + tokens > self.capacity,
+             f'has {self.capacity - self.length} free positions, {tokens} needed')) if bad]
+        if problems:
+            raise ValueError('KV cache ' + '; '.join(problems))
 
 
 class TritonQwen3Inference(nn.Module):
@@ -46,35 +58,29 @@ class TritonQwen3Inference(nn.Module):
                  reference_accumulation=False):
         super().__init__()
         if config.head_dim != 128:
-            raise ValueError('The qualified Qwen3 attention head dimension is 128')
+            raise ValueError('inference kernels are built for head_dim 128 (the Qwen3 attention head)')
+        # The parameters are created on the meta device: a checkpoint or random_init supplies them, so no
+        # throw-away initialisation of a multi-GB model happens on the host.
         with torch.device('meta'):
             core = TritonQwen3ForCausalLM(config, OptimizationOptions())
-        self.model = core.model
-        self.lm_head = core.lm_head
-        self.config = config
+        self.model, self.lm_head, self.config = core.model, core.lm_head, config
         self.gemv, self.split_decode = gemv, split_decode
         self._cache_owner = object()
-        try:
-            from transformers import GenerationConfig
-            self.generation_config = GenerationConfig.from_model_config(config)
-        except Exception:  # pragma: no cover - generation defaults only
-            self.generation_config = None
+        self.generation_config = _generation_config(config)
         self.eval()
 
     # ------------------------------------------------------------------ weights
     def load_hf_state_dict(self, state):
-        state = dict(state)
-        if self.config.tie_word_embeddings and 'lm_head.weight' not in state:
-            state['lm_head.weight'] = state['model.embed_tokens.weight']
-        if self.config.tie_word_embeddings and not torch.equal(state['lm_head.weight'],
-                                                               state['model.embed_tokens.weight']):
-            raise ValueError('Tied checkpoint weights disagree')
+        """Adopt bf16 tensors with official Qwen3 names (strict, no copies: ``assign``)."""
+        tied = self.config.tie_word_embeddings
+        state = resolve_tied(state, tied)
+        wrong = sorted(k for k, v in state.items() if v.dtype != torch.bfloat16 and not k.endswith('inv_freq'))
+        if wrong:
+            raise ValueError(f'bf16 inference weights required; {wrong[0]} is not bf16')
         self.load_state_dict(state, assign=True, strict=True)
-        if self.config.tie_word_embeddings:
+        if tied:
             self.lm_head.weight = self.model.embed_tokens.weight
-        if any(p.dtype != torch.bfloat16 for p in self.parameters()):
-            raise ValueError('BF16 inference checkpoint required')
-        self.model.rotary_emb.inv_freq = self._inv_freq()
+        self.model.rotary_emb.inv_freq = self._inv_freq().to(self.lm_head.weight.device)
         return self
 
     def _inv_freq(self):
@@ -95,49 +101,40 @@ class TritonQwen3Inference(nn.Module):
                 t = torch.empty(p.shape, dtype=torch.bfloat16, device=device)
                 t.normal_(0.0, std, generator=gen)
                 state[name] = t
-        model.load_hf_state_dict(state)
-        model.model.rotary_emb.inv_freq = model.model.rotary_emb.inv_freq.to(device)
-        return model
+        return model.load_hf_state_dict(state)
 
     @classmethod
     def from_pretrained(cls, path, *, device='cuda', **kw):
-        """Load local official safetensors (``inference/model.py:68-88``); no download."""
-        import json
-        from safetensors import safe_open
+        """A local Qwen3 safetensors checkpoint (``inference/model.py:68-88``): ``config.json``, an
+        optional ``generation_config.json``, and ``model.safetensors`` or the shards named by
+        ``model.safetensors.index.json``.  Tensors are read shard by shard straight onto ``device``;
+        nothing is downloaded."""
         from transformers import AutoConfig
         path = Path(path).resolve()
-        config = AutoConfig.from_pretrained(path, local_files_only=True)
-        model = cls(config, **kw)
-        index = path / 'model.safetensors.index.json'
-        shards = sorted(set(json.loads(index.read_text())['weight_map'].values())) if index.exists() \
-            else ['model.safetensors']
-        state = {}
-        for name in shards:
-            shard = (path / name).resolve()
-            if not shard.is_relative_to(path):
-                raise ValueError('Checkpoint shard escapes model directory')
-            with safe_open(shard, framework='pt', device='cpu') as f:
-                for key in f.keys():
-                    state[key] = f.get_tensor(key)
-        model.load_hf_state_dict(state)
-        del state
-        model.to(device=device)
-        return model
+        model = cls(AutoConfig.from_pretrained(path, local_files_only=True), **kw)
+        if (path / 'generation_config.json').is_file():
+            from transformers import GenerationConfig
+            model.generation_config = GenerationConfig.from_pretrained(path, local_files_only=True)
+        return model.load_hf_state_dict(read_checkpoint(path, device))
 
     @property
     def device(self):
         return self.lm_head.weight.device
 
     def new_cache(self, batch_size, max_length):
-        if type(batch_size) is not int or batch_size < 1 or type(max_length) is not int or \
-                not 1 <= max_length <= self.config.max_position_embeddings:
-            raise ValueError('Positive batch/capacity within max_position_embeddings required')
+        """An empty KV cache of ``max_length`` positions for ``batch_size`` rows on the model's device."""
+        c = self.config
+        if type(batch_size) is not int or batch_size < 1:
+            raise ValueError('batch_size must be a positive int')
+        if type(max_length) is not int or not 1 <= max_length <= c.max_position_embeddings:
+            raise ValueError(f'max_length must be an int in [1, {c.max_position_embeddings}]')
         if self.device.type != 'cuda':
-            raise ValueError('Load BF16 weights onto a ROCm device first')
-        shape = (batch_size, self.config.num_key_value_heads, max_length, self.config.head_dim)
-        keys = [torch.empty(shape, device=self.device, dtype=torch.bfloat16) for _ in self.model.layers]
-        values = [torch.empty(shape, device=self.device, dtype=torch.bfloat16) for _ in self.model.layers]
-        return KVCache(keys, values, max_length, batch_size, self._cache_owner)
+            raise ValueError('the weights are not on a ROCm device (load or move them first)')
+        shape = (batch_size, c.num_key_value_heads, max_length, c.head_dim)
+
+        def layer_buffers():
+            return [torch.empty(shape, device=self.device, dtype=torch.bfloat16) for _ in self.model.layers]
+        return KVCache(layer_buffers(), layer_buffers(), max_length, batch_size, self._cache_owner)
 
     # ------------------------------------------------------------------ forward
     def _forward(self, input_ids, cache, logits_to_keep, *, validate_ids=True, start_dev=None):
@@ -148,9 +145,7 @@ class TritonQwen3Inference(nn.Module):
         b, s = input_ids.shape
         if b < 1 or s < 1:
             raise ValueError('Nonempty batch/sequence required')
-        if cache.owner is not self._cache_owner or not cache.valid or b != cache.batch_size or \
-                cache.length + s > cache.capacity:
-            raise ValueError('Foreign, invalid, mismatched or exhausted KV cache')
+        cache.admit(self._cache_owner, b, s)
         if type(logits_to_keep) is not int or not 0 <= logits_to_keep <= s:
             raise ValueError('logits_to_keep must be 0 or within current sequence length')
         if validate_ids and not bool(((input_ids >= 0) & (input_ids < self.config.vocab_size)).all()):
@@ -276,6 +271,15 @@ class TritonQwen3Inference(nn.Module):
         return output[:, :s + step + 1].contiguous()
 
 
+def _generation_config(config):
+    """HF generation defaults (EOS / pad ids) derived from the model config, or None."""
+    try:
+        from transformers import GenerationConfig
+        return GenerationConfig.from_model_config(config)
+    except Exception:  # pragma: no cover - generation defaults only
+        return None
+
+
 class DecodeSession:
     """Greedy decoding with ONE captured HIP graph for the decode step, replayed at every position.
 
@@ -344,43 +348,93 @@ class DecodeSession:
 
 
 class CapturedGreedyRequest:
-    """A whole greedy request (prefill + fixed token budget, no early EOS) captured as one HIP
-    graph (``inference/model.py:191-225``).  Single-stream and non-reentrant; the returned tokens
-    alias request storage until the next replay."""
+    """A fixed-shape greedy request (prefill + ``max_new_tokens`` tokens, no early EOS) replayed from
+    HIP graphs, with the call contract of ``inference/model.py:191-225``: the constructor captures,
+    each call copies a prompt of the captured shape in and returns the [B, S + max_new_tokens]
+    tokens.  Single-stream and non-reentrant; the returned tensor aliases request storage until
+    the next call.
+
+    Two graphs serve any token budget: one for the prefill (embedding through the first greedy
+    token) and one decode step whose position-dependent kernels read the cache length from device
+    memory, replayed ``max_new_tokens - 1`` times.  The graph size is therefore fixed (about 36
+    layers x 8 kernels per graph for Qwen3-8B) whatever the budget.  Capturing the whole request as
+    one graph instead would grow with prompt and budget (~157 K kernel nodes for a 2048-token prompt
+    and 256 new tokens) and is not done.
+    """
 
     @torch.inference_mode()
     def __init__(self, model, input_ids, *, max_new_tokens):
         if type(max_new_tokens) is not int or max_new_tokens < 1:
-            raise ValueError('Positive fixed token budget required')
-        self.model = model
-        self.shape = tuple(input_ids.shape)
-        self.busy = False
+            raise ValueError('max_new_tokens must be a positive int (the fixed token budget)')
+        if input_ids.ndim != 2 or input_ids.device != model.device or \
+                input_ids.dtype not in (torch.int32, torch.int64) or min(input_ids.shape) < 1:
+            raise ValueError('a nonempty integer [B, S] prompt on the model device is required')
+        _check_vocab(model, input_ids)
+        b, s = input_ids.shape
+        self.model, self.shape, self.budget, self.busy = model, (b, s), max_new_tokens, False
         self.input = input_ids.clone()
-        if not bool(((self.input >= 0) & (self.input < model.config.vocab_size)).all()):
-            raise ValueError('Token ID outside vocabulary')
-        stream = torch.cuda.Stream(device=model.device)
-        stream.wait_stream(torch.cuda.current_stream(model.device))
-        with torch.cuda.stream(stream):
-            for _ in range(2):
-                model.generate(self.input, max_new_tokens=max_new_tokens, eos_token_id=[], pad_token_id=0)
-        torch.cuda.current_stream(model.device).wait_stream(stream)
-        self.graph = torch.cuda.CUDAGraph()
-        with torch.cuda.graph(self.graph, stream=stream):
-            self.output = model.generate(self.input, max_new_tokens=max_new_tokens, eos_token_id=[], pad_token_id=0)
+        dev = model.device
+        self.cache = model.new_cache(b, s + max_new_tokens)
+        self.output = torch.zeros((b, s + max_new_tokens), device=dev, dtype=torch.int64)
+        self.current = torch.zeros((b, 1), device=dev, dtype=torch.int64)
+        self.length = torch.zeros((1,), device=dev, dtype=torch.int64)
+        self.done = torch.zeros((b,), device=dev, dtype=torch.bool)
+        stream = torch.cuda.Stream(device=dev)
+        stream.wait_stream(torch.cuda.current_stream(dev))
+        with torch.cuda.stream(stream):   # one eager pass: workspaces and kernels are warm before capture
+            self._prefill()
+            if max_new_tokens > 1:
+                self._step()
+        self.prefill_graph = torch.cuda.CUDAGraph()
+        self.cache.reset()
+        with torch.cuda.graph(self.prefill_graph, stream=stream):
+            self._prefill()
+        self.step_graph = None
+        if max_new_tokens > 1:
+            self.step_graph = torch.cuda.CUDAGraph()
+            with torch.cuda.graph(self.step_graph, stream=stream):
+                self._step()
+        torch.cuda.current_stream(dev).wait_stream(stream)
+        self.cache.reset()
+
+    def _prefill(self):
+        """Prompt -> cache, first greedy token at position S; device length := S."""
+        b, s = self.shape
+        self.cache.length = 0
+        self.output[:, :s].copy_(self.input)
+        logits = self.model._forward(self.input, self.cache, 1, validate_ids=False).logits[:, 0, :]
+        self.done.zero_()
+        kernels.select(logits, self.output, self.current, self.done, s, (), 0)
+        self.length.zero_()
+        kernels.advance(self.length, s)
+
+    def _step(self):
+        """One cached token at the device-resident length L: token L+1 is written; L += 1."""
+        self.cache.length = self.shape[1]   # host-side bound checks only; positions come from self.length
+        logits = self.model._forward(self.current, self.cache, 1, validate_ids=False,
+                                     start_dev=self.length).logits[:, 0, :]
+        kernels.select(logits, self.output, self.current, self.done, 1, (), 0, position_dev=self.length)
+        kernels.advance(self.length, 1)
 
     @torch.inference_mode()
     def __call__(self, input_ids):
         if self.busy:
-            raise RuntimeError('Concurrent graph request reuse is unsupported')
+            raise RuntimeError('a CapturedGreedyRequest serves one call at a time')
         if tuple(input_ids.shape) != self.shape or input_ids.device != self.model.device or \
                 input_ids.dtype != self.input.dtype:
-            raise ValueError('Captured input shape/device/dtype differs')
+            raise ValueError(f'prompt must match the captured {self.shape} {self.input.dtype} on {self.model.device}')
         self.busy = True
         try:
-            if not bool(((input_ids >= 0) & (input_ids < self.model.config.vocab_size)).all()):
-                raise ValueError('Token ID outside vocabulary')
+            _check_vocab(self.model, input_ids)
             self.input.copy_(input_ids)
-            self.graph.replay()
+            self.prefill_graph.replay()
+            for _ in range(self.budget - 1):
+                self.step_graph.replay()
             return self.output
         finally:
             self.busy = False
+
+
+def _check_vocab(model, ids):
+    if not bool(((ids >= 0) & (ids < model.config.vocab_size)).all()):
+        raise ValueError('token id outside the vocabulary')

@@ -1,31 +1,50 @@
-"""Public Qwen3 training model and variant factory (``qwen3_triton/model.py:1-23``)."""
+"""Public Qwen3 training model and variant factory (``qwen3_triton/model.py:1-23``).
+
+``PrecisionQwen3ForCausalLM`` is the training model on the ``components`` modules.  It carries
+the reference's five precision switches as a tuple inside the options.  On gfx950 every kernel
+computes in fp32 and rounds once, so the switches are validated and recorded but select nothing.
+"""
 from dataclasses import fields, replace
 
 from ._model import TritonQwen3ForCausalLM
 from .components import Backbone, HFOrderNorm  # noqa: F401
 from .configuration import OptimizationOptions, options_for_variant
 
+PRECISION_SWITCHES = ('xor_sum', 'lse_fma', 'native_delta', 'native_dq', 'sum_fma')
+
+
+def _precision_items(precision_options):
+    """The five switches as an ordered tuple of (name, bool); all on when none are given."""
+    if precision_options is None:
+        return tuple((name, True) for name in PRECISION_SWITCHES)
+    given = dict(precision_options)
+    if sorted(given) != sorted(PRECISION_SWITCHES) or not all(type(v) is bool for v in given.values()):
+        raise ValueError(f'precision_options must give exactly the booleans {", ".join(PRECISION_SWITCHES)}')
+    return tuple((name, given[name]) for name in PRECISION_SWITCHES)
+
+
+def _optimization_options(options):
+    """``OptimizationOptions`` from None (every switch off), an ``OptimizationOptions``, or any object
+    whose like-named attributes are read (missing ones off)."""
+    if isinstance(options, OptimizationOptions):
+        return options
+    switches = [f.name for f in fields(OptimizationOptions) if f.name != 'precision_options']
+    return OptimizationOptions(**{name: bool(getattr(options, name, False)) for name in switches})
+
+
+def _is_8b_shape(config):
+    return (config.num_hidden_layers, config.hidden_size, config.head_dim) == (36, 4096, 128)
+
 
 class PrecisionQwen3ForCausalLM(TritonQwen3ForCausalLM):
     backbone_class = Backbone
 
     def __init__(self, config, options=None, *, precision_options=None, require_8b_shape=True):
-        if precision_options is None:
-            precision_options = dict(xor_sum=True, lse_fma=True, native_delta=True, native_dq=True, sum_fma=True)
-        if set(precision_options) != {'xor_sum', 'lse_fma', 'native_delta', 'native_dq', 'sum_fma'} or \
-                any(type(v) is not bool for v in precision_options.values()):
-            raise ValueError('Explicit five boolean precision options required')
-        if require_8b_shape and not (config.num_hidden_layers == 36 and config.hidden_size == 4096 and
-                                     config.head_dim == 128):
-            raise ValueError('The precision model is qualified for the Qwen3-8B shape only')
-        if options is None:
-            options = OptimizationOptions(**{f.name: False for f in fields(OptimizationOptions)
-                                             if f.name != 'precision_options'})
-        elif not isinstance(options, OptimizationOptions):
-            options = OptimizationOptions(**{f.name: getattr(options, f.name, False)
-                                             for f in fields(OptimizationOptions) if f.name != 'precision_options'})
-        options = replace(options, precision_options=tuple(precision_options.items()))
-        super().__init__(config, options)
+        switches = _precision_items(precision_options)
+        if require_8b_shape and not _is_8b_shape(config):
+            raise ValueError('the precision model is qualified for the Qwen3-8B shape (36 layers, hidden 4096, '
+                             'head_dim 128); pass require_8b_shape=False for other shapes')
+        super().__init__(config, replace(_optimization_options(options), precision_options=switches))
 
 
 def model_for_variant(config, name, *, precision_options=None):

@@ -74,6 +74,13 @@ def test_reference_entry_points_agree():
     g2 = torch.autograd.grad(attention_triton_autograd(*a), a, do.cuda())
     for x, y in zip(g1, g2):
         assert torch.equal(x, y)
+    g3 = attention_backward_triton(qd, kd, vd, do.cuda(), lse=lse, out=o1)   # saved O: no forward rerun
+    for x, y in zip(g3, g2):
+        assert torch.equal(x, y)
+    from qwen3_triton.kernels.attention_precision import candidate
+    assert torch.equal(candidate(qd, kd, vd), o1)
+    with pytest.raises(TypeError):
+        candidate(qd, kd, vd, lse_fma=1)
     with pytest.raises(NotImplementedError):
         attention_triton(qd, kd, vd, is_causal=False)
 

@@ -24,3 +24,50 @@ def test_cpu_tensors_are_rejected_no_fallback():
         silu_and_mul_triton(x, x)
     with pytest.raises(ValueError):
         apply_rotary(torch.randn(1, 2, 3, 4), torch.randn(1, 2, 4), torch.randn(1, 2, 4))
+
+
+def test_reference_api_modules_and_defaults():
+    """Names the reference exports on this path exist with its defaults."""
+    import inspect
+    from qwen3_triton.kernels import mlp, attention_precision
+    from qwen3_triton.inference import kernels as ik
+    assert callable(mlp.gate_up_swiglu) and callable(ik.sliced_linear) and callable(ik.tiled_prefill_gate_up)
+    sig = inspect.signature(attention_precision.candidate).parameters
+    assert {k: sig[k].default for k in ("lse_fma", "native_delta", "native_dq", "sum_fma", "xor_sum")} == \
+        dict(lse_fma=False, native_delta=False, native_dq=False, sum_fma=False, xor_sum=True)
+    assert attention_precision.f32(0.1) == 0.10000000149011612
+    assert attention_precision.f32(128 ** -0.5) != 128 ** -0.5
+
+
+def test_precision_model_option_validation():
+    from qwen3_triton.model import _optimization_options, _precision_items
+    from qwen3_triton.configuration import OptimizationOptions
+    import pytest
+    assert dict(_precision_items(None)) == dict(xor_sum=True, lse_fma=True, native_delta=True, native_dq=True,
+                                                sum_fma=True)
+    with pytest.raises(ValueError):
+        _precision_items(dict(xor_sum=True))
+    with pytest.raises(ValueError):
+        _precision_items(dict(xor_sum=1, lse_fma=True, native_delta=True, native_dq=True, sum_fma=True))
+    o = _optimization_options(None)
+    assert isinstance(o, OptimizationOptions) and not o.mlp_fusion and not o.linear_optimized
+
+
+def test_architecture_rules():
+    import pytest
+    from transformers import Qwen3Config
+    from qwen3_triton._checkpoint import check_architecture
+    check_architecture(Qwen3Config(head_dim=128))
+    for kw, what in [(dict(hidden_act="gelu"), "SiLU"), (dict(attention_bias=True), "bias"),
+                     (dict(num_attention_heads=6, num_key_value_heads=4), "GQA"),
+                     (dict(rope_scaling={"rope_type": "linear", "factor": 2.0}), "RoPE")]:
+        with pytest.raises(ValueError, match=what):
+            check_architecture(Qwen3Config(head_dim=128, **kw))
+
+
+def test_captured_request_rejects_bad_budgets_before_any_gpu_work():
+    import pytest
+    from qwen3_triton.inference import CapturedGreedyRequest
+    for budget in (0, -1, 2.0):
+        with pytest.raises(ValueError):
+            CapturedGreedyRequest(object(), None, max_new_tokens=budget)

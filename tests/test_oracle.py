@@ -254,3 +254,23 @@ def test_greedy_loop_matches_hf_generate():
         e = hf.generate(ids, max_new_tokens=6, do_sample=False, eos_token_id=None, pad_token_id=0)
     assert torch.equal(toks, e)
     assert margins.shape == (2, 6) and bool((margins >= 0).all())
+
+
+def test_cached_decode_matches_full_recomputation():
+    """The KV-cached oracle decode (prefill, then one token per step against the cache) equals the
+    full-recomputation greedy loop token for token, and every step's logits equal the last row of
+    a no-cache forward over the whole prefix (fp64); teacher forcing feeds the given tokens."""
+    cfg = O.OracleConfig(vocab_size=61, hidden_size=32, intermediate_size=40, num_hidden_layers=2,
+                         num_attention_heads=4, num_key_value_heads=2, head_dim=8)
+    p = {k: v.double() for k, v in O.init_params(cfg, seed=3, std=0.3).items()}
+    ids = torch.randint(0, 61, (3, 7), generator=g(43))
+    full, _ = O.greedy_generate_reference(ids, p, cfg, 5, dtype=D64)
+    toks, logits = O.cached_decode_reference(ids, p, cfg, 5, dtype=D64)
+    assert torch.equal(toks, full[:, 7:])
+    forced = torch.randint(0, 61, (3, 5), generator=g(44))
+    ftoks, flog = O.cached_decode_reference(ids, p, cfg, 5, forced=forced, dtype=D64)
+    seq = torch.cat([ids, forced], dim=1)
+    for t in range(5):
+        e, _ = O.model_forward_reference(seq[:, :7 + t], p, cfg, dtype=D64)
+        torch.testing.assert_close(flog[:, t], e[:, -1], rtol=1e-10, atol=1e-10)
+        assert torch.equal(ftoks[:, t], O.argmax_lowest_reference(e[:, -1]))
