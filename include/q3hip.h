@@ -28,6 +28,7 @@ extern "C" {
 
 #define Q3_OK 0
 #define Q3_ERR_INVALID 100000 /* arguments rejected before launch */
+#define Q3_ERR_SCRATCH 100001 /* request larger than a no-allocation entry point's fixed scratch */
 
 enum { Q3_F32 = 0, Q3_F16 = 1, Q3_BF16 = 2 };
 
@@ -270,6 +271,23 @@ int q3_decode_step_attention(int dtype, const void* q, int64_t qsb, int64_t qsh,
                              int64_t ksh, void* out, int64_t osb, int64_t osh, void* workspace, int64_t B, int64_t Hq,
                              int64_t Hkv, int64_t T_len, const int64_t* len_dev, int64_t capacity, int64_t D,
                              float scale, hipStream_t stream);
+/* q3_decode_step_attention without a workspace argument: the split partials go to a fixed
+ * Q3_NOALLOC_SCRATCH_BYTES (16 MiB) device array inside the library (one per GPU, kept until the
+ * process ends), so the call allocates nothing.  No counterpart in the reference: it is for callers that cannot allocate
+ * device memory (code under HIP graph capture, serving loops that forbid allocation).  The
+ * limit is q3_decode_attention_workspace_bytes(B, Hq, Hkv, span) <= Q3_NOALLOC_SCRATCH_BYTES, span =
+ * capacity when len_dev is given, else T_len (B 8 x Hq 32 fits a span of 8064 positions);
+ * larger requests return Q3_ERR_SCRATCH before any launch.  Every call on one GPU shares that
+ * GPU's array, so calls that overlap on one GPU (concurrent streams or threads) race; calls in
+ * one stream are ordered and safe.  Arguments and results otherwise as q3_decode_step_attention
+ * (bit-identical outputs). */
+#define Q3_NOALLOC_SCRATCH_BYTES ((size_t)16 << 20)
+int q3_decode_step_attention_noalloc(int dtype, const void* q, int64_t qsb, int64_t qsh, const void* k, const void* v,
+                                     int64_t kvsb, int64_t kvsh, const void* q_norm_w, const void* k_norm_w, float eps,
+                                     const void* cos, const void* sin, int64_t csb, void* cache_k, void* cache_v,
+                                     int64_t ksb, int64_t ksh, void* out, int64_t osb, int64_t osh, int64_t B,
+                                     int64_t Hq, int64_t Hkv, int64_t T_len, const int64_t* len_dev, int64_t capacity,
+                                     int64_t D, float scale, hipStream_t stream);
 /* Greedy step: token[b] = argmax logits[b, :vocab] (lowest index on ties), pad if done[b]; writes
  * ids[b, p] (ids may be NULL; p = pos, plus *pos_dev when pos_dev is non-NULL), next[b],
  * done[b] |= token in eos[0:n_eos].

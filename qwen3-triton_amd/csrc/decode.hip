@@ -1,5 +1,6 @@
 // Single-GPU greedy decode: small-M GEMV, KV-cache append, split-KV decode attention and the
 // greedy argmax/select step.  All four are bound by HBM traffic (weights, cache, logits).
+#include <mutex>
 #include <type_traits>
 
 #include "common.h"
@@ -737,6 +738,60 @@ int q3_decode_step_attention(int dtype, const void* q, int64_t qsb, int64_t qsh,
   const int G = (int)(Hq / Hkv);
   if (dtype == Q3_BF16) return decode_t<BF16, true>(G, a, grid, out, osb, osh, stream);
   return decode_t<F16, true>(G, a, grid, out, osb, osh, stream);
+}
+
+}  // extern "C"
+
+namespace {
+
+// Split partials of q3_decode_step_attention_noalloc live in this file-scope device array instead of
+// a caller workspace.  Each GPU holds its own copy (for the life of the process) at its own address.
+// In host code `scratch` only names the symbol: its device address, per device, comes from
+// hipGetSymbolAddress and is the only handle passed to kernels.
+constexpr size_t kScratchBytes = Q3_NOALLOC_SCRATCH_BYTES;
+static __device__ __align__(256) unsigned char scratch[kScratchBytes];
+
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mu;
+void* g_scratch_ptr[kMaxDevices] = {};
+
+// Device address of `scratch` on the current device, looked up once per device.
+int scratch_address(void** out) {
+  int dev = 0;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) return (int)e;
+  if (dev < 0 || dev >= kMaxDevices) return Q3_ERR_INVALID;
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (!g_scratch_ptr[dev]) {
+    void* p = nullptr;
+    e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (e != hipSuccess) return (int)e;
+    if (!p) return Q3_ERR_INVALID;
+    g_scratch_ptr[dev] = p;
+  }
+  *out = g_scratch_ptr[dev];
+  return 0;
+}
+
+}  // namespace
+
+extern "C" {
+
+int q3_decode_step_attention_noalloc(int dtype, const void* q, int64_t qsb, int64_t qsh, const void* k, const void* v,
+                                     int64_t kvsb, int64_t kvsh, const void* q_norm_w, const void* k_norm_w, float eps,
+                                     const void* cos, const void* sin, int64_t csb, void* cache_k, void* cache_v,
+                                     int64_t ksb, int64_t ksh, void* out, int64_t osb, int64_t osh, int64_t B,
+                                     int64_t Hq, int64_t Hkv, int64_t T_len, const int64_t* len_dev, int64_t capacity,
+                                     int64_t D, float scale, hipStream_t stream) {
+  // The partials (written in full by the split kernel before the merge reads them) must fit the array.
+  const int64_t span = len_dev ? capacity : T_len;
+  if (q3_decode_attention_workspace_bytes(B, Hq, Hkv, span) > kScratchBytes) return Q3_ERR_SCRATCH;
+  void* ws = nullptr;
+  const int rc = scratch_address(&ws);
+  if (rc) return rc;
+  return q3_decode_step_attention(dtype, q, qsb, qsh, k, v, kvsb, kvsh, q_norm_w, k_norm_w, eps, cos, sin, csb,
+                                  cache_k, cache_v, ksb, ksh, out, osb, osh, ws, B, Hq, Hkv, T_len, len_dev, capacity,
+                                  D, scale, stream);
 }
 
 size_t q3_greedy_select_workspace_bytes(int64_t batch) { return (size_t)batch * 64 * (sizeof(float) + sizeof(int)); }

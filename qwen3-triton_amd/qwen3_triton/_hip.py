@@ -73,6 +73,9 @@ SIGNATURES: dict[str, tuple] = {
     "q3_decode_step_attention": (_i32, [_i32, _p, _i64, _i64, _p, _p, _i64, _i64, _p, _p, _f32, _p, _p, _i64, _p, _p,
                                         _i64, _i64, _p, _i64, _i64, _p, _i64, _i64, _i64, _i64, _p, _i64, _i64, _f32,
                                         _p]),
+    "q3_decode_step_attention_noalloc": (_i32, [_i32, _p, _i64, _i64, _p, _p, _i64, _i64, _p, _p, _f32, _p, _p, _i64,
+                                                _p, _p, _i64, _i64, _p, _i64, _i64, _i64, _i64, _i64, _i64, _p, _i64,
+                                                _i64, _f32, _p]),
     "q3_greedy_select_workspace_bytes": (_sz, [_i64]),
     "q3_greedy_select": (_i32, [_i32, _p, _i64, _i64, _i64, _p, _p, _i64, _i64, _p, _p, _p, _p, _i32, _i64, _p]),
     "q3_advance": (_i32, [_p, _i64, _p]),

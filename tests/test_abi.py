@@ -46,3 +46,16 @@ def test_invalid_arguments_are_rejected_before_launch():
     assert lib.q3_swiglu_fwd(7, 1, 1, 1, 16, None) == 100000
     assert lib.q3_gemm_nt(0, 0, 16, 8, 16, 8, 16, 8, 1, 1, 8, 1.0, 0, None) == 100000  # fp32 in: not MFMA
     assert lib.q3_gemm_nt(2, 0, 16, 8, 16, 8, 16, 8, 1, 1, 12, 1.0, 0, None) == 100000  # K % 8 != 0
+
+
+def test_noalloc_decode_attention_rejects_oversize_before_any_gpu_call():
+    """The no-allocation decode attention refuses a request whose split partials exceed its fixed
+    scratch array (Q3_ERR_SCRATCH) before touching the device or any pointer."""
+    lib = H.load()
+    assert b"scratch" in lib.q3_error_string(100001)
+    limit = 16 << 20
+    assert H.query("q3_decode_attention_workspace_bytes", 8, 32, 8, 8064) <= limit
+    assert H.query("q3_decode_attention_workspace_bytes", 8, 32, 8, 8128) > limit
+    args = [2, None, 0, 0, None, None, 0, 0, None, None, 1e-6, None, None, 0, None, None, 0, 0, None, 0, 0,
+            8, 32, 8, 8128, None, 8128, 128, 0.088, None]
+    assert lib.q3_decode_step_attention_noalloc(*args) == 100001
