@@ -53,6 +53,9 @@ class GemmTimer:
         self.mods = [m for m in modules if hasattr(m, "gemm_nt_into")]
         self.orig = self.mods[0].gemm_nt_into
         assert all(m.gemm_nt_into is self.orig for m in self.mods)
+        # the gate/up GEMM with the SwiGLU epilogue (two weights, one launch)
+        self.gu_mods = [m for m in modules if hasattr(m, "gate_up_swiglu_into")]
+        self.gu_orig = self.gu_mods[0].gate_up_swiglu_into if self.gu_mods else None
         self.records = []
         self.active = False
 
@@ -69,13 +72,26 @@ class GemmTimer:
             e.record()
             self.records.append((s, e, 2.0 * m * n * k))
 
+        def timed_gu(x, wg, wu, g, u, y, m, n, k):
+            if not self.active:
+                return self.gu_orig(x, wg, wu, g, u, y, m, n, k)
+            s, e = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            s.record()
+            self.gu_orig(x, wg, wu, g, u, y, m, n, k)
+            e.record()
+            self.records.append((s, e, 2.0 * 2 * m * n * k))
+
         for m in self.mods:
             m.gemm_nt_into = timed
+        for m in self.gu_mods:
+            m.gate_up_swiglu_into = timed_gu
         return self
 
     def __exit__(self, *exc):
         for m in self.mods:
             m.gemm_nt_into = self.orig
+        for m in self.gu_mods:
+            m.gate_up_swiglu_into = self.gu_orig
 
     def summary(self):
         ms = sum(s.elapsed_time(e) for s, e, _ in self.records)

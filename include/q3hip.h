@@ -140,6 +140,17 @@ int q3_embedding_bwd(int dtype, const void* ids, int ids_is_int64, const void* d
  *           ops/triton/gate_up_swiglu.py:151-176 (_matmul_kernel). */
 int q3_gemm_nt(int in_dtype, int out_dtype, const void* A, int64_t lda, const void* B, int64_t ldb, void* C,
                int64_t ldc, int64_t M, int64_t N, int64_t K, float alpha, int accumulate, hipStream_t stream);
+/* Gate/up projections with the SwiGLU epilogue in one matrix-core GEMM: for x [M, K] and weights
+ * wg, wu [N, K] (K-contiguous rows, row stride ldw), stores G = x wg^T, U = x wu^T (each rounded to
+ * dtype) and Y = silu(G) * U computed from the rounded G and U (the same expression as
+ * q3_swiglu_fwd on the stored G, U), all [M, N] at row stride ldo.  One launch reads x and both
+ * weights once per tile.  M % 256 == 0, N % 128 == 0, K % 64 == 0, ldo % 8 == 0; every pointer
+ * 16-byte aligned.
+ * Replaces: kernels/mlp_precision.py:16-33 / kernels/mlp.py:14-33 (_gate_up: both K loops and the
+ * G, U, Y stores in one kernel), ops/triton/gate_up_swiglu.py:178-288. */
+int q3_gemm_gate_up_swiglu(int dtype, const void* x, int64_t ldx, const void* wg, const void* wu, int64_t ldw,
+                           void* g, void* u, void* y, int64_t ldo, int64_t M, int64_t N, int64_t K,
+                           hipStream_t stream);
 /* Same product for arbitrary element strides: A(m,k) = A[m*sam + k*sak], B(k,n) = B[k*sbk + n*sbn];
  * any dtype (fp32 included).  SIMT path for shapes the matrix-core kernel does not take.
  * Replaces: kernels/linear.py:13-42 (_gemm with arbitrary strides). */

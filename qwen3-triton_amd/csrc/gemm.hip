@@ -180,6 +180,11 @@ template <int CPR> Q3_DEV int gemm_swz(int r) {
 // Statistics epilogue (EPI = 2, 128 columns per wave): per row and 128-column group p (= part0 +
 // global column group of the tile), m_part[p * ldp + row] / s_part[...] get the group's max and
 // sum of exp(z - max), and pick[row] the logit of column tgt[row] - col0 when it lies in this chunk.
+// Gate/up epilogue (EPI = 3): the B operand is two weights, Wg (B) and Wu (b2), interleaved in
+// 16-row blocks (virtual B row r: block r / 16, even blocks from Wg, odd from Wu, weight row
+// (block / 2) * 16 + r % 16), so each lane holds the gate and up accumulators of the same output
+// element in neighbouring 16 x 16 fragments.  It stores G = bf16(x Wg^T), U = bf16(x Wu^T) and
+// Y = silu(G) * U computed from the rounded G and U (row stride ldc, C = Y).
 struct CeEpi {
   const int64_t* tgt;
   const float* lse;
@@ -190,6 +195,9 @@ struct CeEpi {
   float* s_part;
   float* pick;
   int64_t part0, ldp;
+  const u16* b2;
+  u16* g_out;
+  u16* u_out;
 };
 
 Q3_DEV void lse_merge(float& m, float& s, float m2, float s2) {
@@ -243,10 +251,15 @@ __global__ __launch_bounds__(WM * WN * 64) void gemm_nt_v4_kernel(const u16* __r
       const int rg = wave_u + NW * i;
       const void* g;
       if constexpr (EVEN) {
-        if (i < A_LOADS)
+        if (i < A_LOADS) {
           g = reinterpret_cast<const char*>(A + (int64_t)(m0 + rg * RPL) * lda + k0) + offa;
-        else
+        } else if constexpr (EPI == 3) {
+          const int vr = n0 + rg * RPL - BM, blk = vr >> 4;
+          const u16* w = (blk & 1) ? ce.b2 : B;
+          g = reinterpret_cast<const char*>(w + (int64_t)((blk >> 1) * 16 + (vr & 15)) * ldb + k0) + offb;
+        } else {
           g = reinterpret_cast<const char*>(B + (int64_t)(n0 + rg * RPL - BM) * ldb + k0) + offb;
+        }
       } else {
         g = src[i] + k0;
       }
@@ -344,6 +357,72 @@ __global__ __launch_bounds__(WM * WN * 64) void gemm_nt_v4_kernel(const u16* __r
   }
 
   // ---- epilogue: lane owns row m and 4 consecutive columns of each 16x16 block (C^T layout)
+  // Coalesced epilogue through LDS (16-bit outputs of full tiles): each wave rounds its tile into a
+  // private LDS block (16-byte chunks XOR-swizzled by row, conflict-free writes and reads), then
+  // stores whole rows with 16-byte stores instead of 8-byte pieces of 16 rows.
+  typedef __attribute__((__vector_size__(2 * sizeof(int)))) int i32x2;
+  [[maybe_unused]] char* wl = reinterpret_cast<char*>(lds) + wave_u * (TMW * TNW * 2);
+  // NC = columns of the staged tile (TNW, or TNW / 2 for one gate/up output)
+  [[maybe_unused]] auto stage = [&](auto nc_c, int i, int jc, uint32_t lo, uint32_t hi) {
+    constexpr int NC = decltype(nc_c)::value, CH = NC / 8;
+    const int r = i * 16 + (lane & 15);
+    const int c = (jc * 16 + 4 * quarter) >> 3;  // logical 16-byte chunk
+    const int sw = CH == 16 ? (r & 15) : ((r >> 1) & 7);
+    *reinterpret_cast<i32x2*>(wl + r * (NC * 2) + ((c ^ sw) << 4) + (quarter & 1) * 8) = i32x2{(int)lo, (int)hi};
+  };
+  [[maybe_unused]] auto flush = [&](auto nc_c, typename O::storage* dst, int64_t ld) {
+    constexpr int NC = decltype(nc_c)::value, CH = NC / 8, RPI = 64 / CH;  // rows per instruction
+    __builtin_amdgcn_s_waitcnt((15) | (7 << 4) | (0 << 8) | (3 << 14));  // this wave's staging writes
+    __builtin_amdgcn_wave_barrier();
+#pragma unroll
+    for (int q = 0; q < TMW / RPI; ++q) {
+      const int r = q * RPI + lane / CH, c = lane % CH;
+      const int sw = CH == 16 ? (r & 15) : ((r >> 1) & 7);
+      const i32x4 v = *reinterpret_cast<const i32x4*>(wl + r * (NC * 2) + ((c ^ sw) << 4));
+      *reinterpret_cast<i32x4*>(dst + (int64_t)r * ld + c * 8) = v;
+    }
+    __builtin_amdgcn_s_waitcnt((15) | (7 << 4) | (0 << 8) | (3 << 14));  // reads done before the block is reused
+    __builtin_amdgcn_wave_barrier();
+  };
+  if constexpr (EPI == 3) {
+    static_assert(FN % 2 == 0 && EVEN, "gate/up fragments come in (gate, up) pairs of full tiles");
+    static_assert(O::vec == 8, "16-bit outputs");
+    constexpr auto NC = std::integral_constant<int, TNW / 2>{};
+    __syncthreads();  // every wave is done with the operand ring
+    const int64_t o0 = (int64_t)(m0 + wm * TMW) * ldc + (n0 + wn * TNW) / 2;
+#pragma unroll
+    for (int out = 0; out < 3; ++out) {
+#pragma unroll
+      for (int i = 0; i < FM; ++i)
+#pragma unroll
+        for (int p = 0; p < FN / 2; ++p) {
+          float gq[4], uq[4], v[4];
+#pragma unroll
+          for (int e = 0; e < 4; ++e) {
+            gq[e] = to_f32<T>(from_f32<T>(acc[i][2 * p][e]));
+            uq[e] = to_f32<T>(from_f32<T>(acc[i][2 * p + 1][e]));
+            v[e] = out == 0 ? gq[e] : out == 1 ? uq[e] : gq[e] * q3_sigmoid(gq[e]) * uq[e];
+          }
+          stage(NC, i, p, pack2<T>(v[0], v[1]), pack2<T>(v[2], v[3]));
+        }
+      flush(NC, (out == 0 ? ce.g_out : out == 1 ? ce.u_out : C) + o0, ldc);
+    }
+    return;
+  }
+  if constexpr (EPI == 0 && EVEN && O::vec == 8) {
+    if (!accumulate && vec_store == 2) {
+      constexpr auto NC = std::integral_constant<int, TNW>{};
+      __syncthreads();  // every wave is done with the operand ring
+#pragma unroll
+      for (int i = 0; i < FM; ++i)
+#pragma unroll
+        for (int j = 0; j < FN; ++j)
+          stage(NC, i, j, pack2<O>(alpha * acc[i][j][0], alpha * acc[i][j][1]),
+                pack2<O>(alpha * acc[i][j][2], alpha * acc[i][j][3]));
+      flush(NC, C + (int64_t)(m0 + wm * TMW) * ldc + n0 + wn * TNW, ldc);
+      return;
+    }
+  }
   if constexpr (EPI == 2) {
     static_assert(TNW == 128, "one statistics partial per 128 columns");
     const int64_t part = ce.part0 + (n0 + wn * TNW) / 128;
@@ -441,7 +520,10 @@ template <typename T, typename O, int BM, int BN, int WM, int WN, int ST, bool E
 int launch_v4(const void* A, int64_t lda, const void* B, int64_t ldb, void* C, int64_t ldc, int64_t M, int64_t N,
               int64_t K, float alpha, int acc, hipStream_t s, CeEpi ce = CeEpi{}) {
   const int64_t tiles = ((M + BM - 1) / BM) * ((N + BN - 1) / BN);
-  const int vec = (ldc % 4 == 0) && (((uintptr_t)C & (O::vec == 4 ? 15 : 7)) == 0);
+  static_assert(BM * BN * 2 <= ST * (BM + BN) * BK * 2, "the LDS epilogue reuses the operand ring");
+  // 2: 16-byte row stores (the LDS epilogue), 1: 8-byte (16-bit) / 16-byte (fp32) stores, 0: scalar
+  const int vec = (ldc % 8 == 0 && ((uintptr_t)C & 15) == 0) ? 2
+                  : ((ldc % 4 == 0) && (((uintptr_t)C & (O::vec == 4 ? 15 : 7)) == 0)) ? 1 : 0;
   gemm_nt_v4_kernel<T, O, BM, BN, WM, WN, BK, ST, EVEN, EPI><<<(unsigned)tiles, WM * WN * 64, 0, s>>>(
       (const u16*)A, (const u16*)B, (typename O::storage*)C, (int)M, (int)N, (int)K, lda, ldb, ldc, alpha, acc, vec,
       ce);
@@ -467,6 +549,18 @@ int launch_ce_grad(const void* A, int64_t lda, const void* B, int64_t ldb, void*
     return launch_v4<T, T, 256, 256, 4, 2, 2, false, 64, 1>(A, lda, B, ldb, dz, lddz, M, N, K, 1.f, 0, s, ce);
   }
   return launch_v4<T, T, 128, 128, 2, 2, 4, false, 64, 1>(A, lda, B, ldb, dz, lddz, M, N, K, 1.f, 0, s, ce);
+}
+
+// Gate/up GEMM with the SwiGLU epilogue: 256 x 256 tiles of the interleaved [Wg; Wu] operand, so a
+// tile covers 256 rows x 128 output columns (M % 256 == 0, N % 128 == 0).
+template <typename T>
+int launch_gate_up(const void* X, int64_t ldx, const void* Wg, const void* Wu, int64_t ldw, void* G, void* U, void* Y,
+                   int64_t ldo, int64_t M, int64_t N, int64_t K, hipStream_t s) {
+  CeEpi e{};
+  e.b2 = (const u16*)Wu;
+  e.g_out = (u16*)G;
+  e.u_out = (u16*)U;
+  return launch_v4<T, T, 256, 256, 4, 2, 2, true, 64, 3>(X, ldx, Wg, ldw, Y, ldo, M, 2 * N, K, 1.f, 0, s, e);
 }
 
 // ---------------------------------------------------------------- strided SIMT fallback
@@ -626,6 +720,18 @@ int q3_gemm_nt_ce_stats(int dtype, const void* A, int64_t lda, const void* B, in
   const CeEpi ce{tgt, nullptr, nullptr, nullptr, col0, 0, 0, m_part, s_part, pick, part0, ldp};
   if (dtype == Q3_BF16) return launch_ce_stats<BF16>(A, lda, B, ldb, M, N, K, ce, stream);
   return launch_ce_stats<F16>(A, lda, B, ldb, M, N, K, ce, stream);
+}
+
+int q3_gemm_gate_up_swiglu(int dtype, const void* x, int64_t ldx, const void* wg, const void* wu, int64_t ldw,
+                           void* g, void* u, void* y, int64_t ldo, int64_t M, int64_t N, int64_t K,
+                           hipStream_t stream) {
+  Q3_REQUIRE((dtype == Q3_BF16 || dtype == Q3_F16) && x && wg && wu && g && u && y);
+  Q3_REQUIRE(M > 0 && N > 0 && K > 0 && M % 256 == 0 && N % 128 == 0 && K % 64 == 0 && M < (1ll << 31) &&
+             N < (1ll << 30) && K < (1ll << 31) && (M / 256) * (N / 128) < (1ll << 31));
+  Q3_REQUIRE(ldx % 8 == 0 && ldw % 8 == 0 && ldo % 8 == 0 && ldx >= K && ldw >= K && ldo >= N && al16(x) &&
+             al16(wg) && al16(wu) && al16(g) && al16(u) && al16(y));
+  if (dtype == Q3_BF16) return launch_gate_up<BF16>(x, ldx, wg, wu, ldw, g, u, y, ldo, M, N, K, stream);
+  return launch_gate_up<F16>(x, ldx, wg, wu, ldw, g, u, y, ldo, M, N, K, stream);
 }
 
 int q3_gemm_strided(int in_dtype, int out_dtype, const void* A, int64_t sam, int64_t sak, const void* B, int64_t sbk,

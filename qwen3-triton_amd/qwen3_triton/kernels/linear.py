@@ -40,6 +40,17 @@ def gemm_nt_into(a, lda, bnk, ldb, out, m, n, k, *, alpha=1.0, accumulate=False)
            out.data_ptr(), out.stride(0), m, n, k, float(alpha), int(accumulate), H.stream())
 
 
+def gate_up_swiglu_into(x, wg, wu, g, u, y, m, n, k):
+    """g = x wg^T, u = x wu^T, y = silu(g) * u in one matrix-core GEMM (M % 256 == 0, N % 128 == 0,
+    K % 64 == 0; contiguous [M, K] x and [N, K] weights, contiguous [M, N] outputs)."""
+    H.call("q3_gemm_gate_up_swiglu", H.code(x.dtype), x.data_ptr(), k, wg.data_ptr(), wu.data_ptr(), k,
+           g.data_ptr(), u.data_ptr(), y.data_ptr(), n, m, n, k, H.stream())
+
+
+def gate_up_fused_ok(x, m, n, k):
+    return x.dtype in (torch.bfloat16, torch.float16) and m % 256 == 0 and n % 128 == 0 and k % 64 == 0
+
+
 def matmul_into(a, b, out, *, alpha=1.0, accumulate=False):
     m, k = a.shape
     n = b.shape[1]

@@ -1,7 +1,9 @@
 """Gate/up projections + SwiGLU as one autograd op.
 
 Mirrors ``qwen3_triton/kernels/mlp_precision.py:16-66`` (``_GateUp`` / ``gate_up_swiglu``):
-forward G = X Wg^T, U = X Wu^T, Y = silu(G)*U, saving G and U; backward = SwiGLU backward,
+forward G = X Wg^T, U = X Wu^T, Y = silu(G)*U, saving G and U -- one matrix-core GEMM over both
+weights with the SwiGLU in its epilogue (``q3_gemm_gate_up_swiglu``) when M % 256 == 0 and
+N % 128 == 0, else two GEMMs and the SwiGLU kernel; backward = SwiGLU backward,
 dX = dG Wg + dU Wu (fp32 accumulation across both products, one rounding), dWg = dG^T X,
 dWu = dU^T X.  On the matrix cores the backward keeps dG and dU side by side in one [M, 2N]
 buffer, so dX is a single GEMM over K = 2N and both weight gradients come from one GEMM.
@@ -9,7 +11,7 @@ buffer, so dX is a single GEMM over K = 2N and both weight gradients come from o
 import torch
 
 from . import _ops
-from .linear import gemm_nt_into, matmul, matmul_into
+from .linear import gate_up_fused_ok, gate_up_swiglu_into, gemm_nt_into, matmul, matmul_into
 
 
 class _GateUp(torch.autograd.Function):
@@ -24,9 +26,14 @@ class _GateUp(torch.autograd.Function):
         if min(m, k, n) < 1:
             raise ValueError('Nonempty inputs required')
         flat = x.view(m, k)
-        g = matmul(flat, wg.t())
-        u = matmul(flat, wu.t())
-        y = _ops.swiglu_fwd(g, u)
+        if gate_up_fused_ok(x, m, n, k):
+            # one GEMM over both weights; the SwiGLU runs in its epilogue
+            g, u, y = (torch.empty((m, n), device=x.device, dtype=x.dtype) for _ in range(3))
+            gate_up_swiglu_into(flat, wg, wu, g, u, y, m, n, k)
+        else:
+            g = matmul(flat, wg.t())
+            u = matmul(flat, wu.t())
+            y = _ops.swiglu_fwd(g, u)
         ctx.save_for_backward(x, wg, wu, g, u)
         return y.view(*x.shape[:-1], n)
 

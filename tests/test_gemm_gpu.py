@@ -119,3 +119,34 @@ def test_shared_input_projections_autograd(dtype):
         assert max_rel(a, e) < tol
         assert cosine(a, e) > 0.999
 
+
+
+@pytest.mark.parametrize("m,n,k", [(256, 128, 64), (512, 384, 256), (1024, 1280, 448), (8192, 12288, 4096)])
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+def test_gate_up_swiglu_gemm(m, n, k, dtype):
+    """q3_gemm_gate_up_swiglu: G and U bit-equal to the plain GEMM of each weight (same tile and
+    k order), Y bit-equal to the SwiGLU kernel on them, and sampled rows against fp64."""
+    from qwen3_triton.kernels import _ops
+    from qwen3_triton.kernels.linear import gate_up_swiglu_into
+    import oracle as O
+    print(f"gate_up_swiglu {m}x{n}x{k} {dtype}", flush=True)
+    gen = seeded(m + n + k)
+    x = randn(m, k, gen=gen, dtype=dtype).cuda()
+    wg = randn(n, k, gen=gen, dtype=dtype, scale=0.05).cuda()
+    wu = randn(n, k, gen=gen, dtype=dtype, scale=0.05).cuda()
+    g, u, y = (torch.empty(m, n, device="cuda", dtype=dtype) for _ in range(3))
+    gate_up_swiglu_into(x, wg, wu, g, u, y, m, n, k)
+    g2, u2 = torch.empty_like(g), torch.empty_like(u)
+    gemm_nt_into(x, k, wg, k, g2, m, n, k)
+    gemm_nt_into(x, k, wu, k, u2, m, n, k)
+    if m * n >= 256 * 256 * 256:   # the plain GEMM picks the same 256 x 256 tile there
+        assert torch.equal(g, g2) and torch.equal(u, u2)
+    else:
+        assert max_rel(g, g2) <= 8e-3 and max_rel(u, u2) <= 8e-3
+    assert torch.equal(y, _ops.swiglu_fwd(g, u))
+    rows = torch.arange(0, m, max(1, m // 64))
+    xr = x[rows].cpu().double()
+    eg, eu = xr @ wg.cpu().double().t(), xr @ wu.cpu().double().t()
+    tol = 8e-3 if dtype == torch.bfloat16 else 1e-3
+    assert max_rel(g[rows], eg) <= tol and max_rel(u[rows], eu) <= tol
+    assert max_rel(y[rows], O.swiglu_reference(eg, eu, dtype=torch.float64)) <= 2 * tol
