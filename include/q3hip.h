@@ -213,12 +213,15 @@ int q3_ce_chunk_grad(int dtype, int out_dtype, const void* z, int64_t ld, int64_
 /* The logits GEMM and q3_ce_chunk_grad in one kernel: z = A . B^T (A [M, K] token rows, B [N, K] the
  * chunk's vocabulary rows starting at column col0; K % 64 == 0, 16-byte aligned K-contiguous rows) is
  * formed in fp32 on the matrix cores and only dz (dtype, row stride lddz) is written, with the same
- * expression as q3_ce_chunk_grad; up may be null (1).  The backward of the fused LM-head + CE.
+ * expression as q3_ce_chunk_grad; up may be null (1).  With dzt non-NULL the same values are also
+ * stored transposed, dzt[n * lddzt + m] = dz[m, n] (the operand of dW = dz^T . A), which needs
+ * M % 256 == 0, N % 256 == 0, (M / 256) * (N / 256) >= 256, lddz and lddzt multiples of 8 and
+ * 16-byte aligned dz, dzt.  The backward of the fused LM-head + CE.
  * Replaces: kernels/loss.py:34-44,64-68 (_backward) together with the logits matmul of
  * _model.py:131-132 (no single reference function). */
 int q3_gemm_nt_ce_grad(int dtype, const void* A, int64_t lda, const void* B, int64_t ldb, void* dz, int64_t lddz,
-                       int64_t M, int64_t N, int64_t K, int64_t col0, const int64_t* tgt, const float* lse,
-                       const float* count, const float* up, int64_t vocab, int64_t ignore_index,
+                       void* dzt, int64_t lddzt, int64_t M, int64_t N, int64_t K, int64_t col0, const int64_t* tgt,
+                       const float* lse, const float* count, const float* up, int64_t vocab, int64_t ignore_index,
                        hipStream_t stream);
 /* The logits GEMM and q3_ce_chunk_stats in one kernel: z = A . B^T as above; per row and per group
  * of 128 logit columns g (g = 0 .. ceil(N / 128) - 1), m_part[(part0 + g) * ldp + row] and

@@ -198,6 +198,8 @@ struct CeEpi {
   const u16* b2;
   u16* g_out;
   u16* u_out;
+  u16* zt;       // EPI 1: optional transposed copy of dz ([N][M] at row stride ldzt)
+  int64_t ldzt;
 };
 
 Q3_DEV void lse_merge(float& m, float& s, float m2, float s2) {
@@ -370,12 +372,13 @@ __global__ __launch_bounds__(WM * WN * 64) void gemm_nt_v4_kernel(const u16* __r
     const int sw = CH == 16 ? (r & 15) : ((r >> 1) & 7);
     *reinterpret_cast<i32x2*>(wl + r * (NC * 2) + ((c ^ sw) << 4) + (quarter & 1) * 8) = i32x2{(int)lo, (int)hi};
   };
-  [[maybe_unused]] auto flush = [&](auto nc_c, typename O::storage* dst, int64_t ld) {
+  [[maybe_unused]] auto flush = [&](auto nc_c, typename O::storage* dst, int64_t ld, auto nr_c) {
     constexpr int NC = decltype(nc_c)::value, CH = NC / 8, RPI = 64 / CH;  // rows per instruction
+    constexpr int NR = decltype(nr_c)::value;
     __builtin_amdgcn_s_waitcnt((15) | (7 << 4) | (0 << 8) | (3 << 14));  // this wave's staging writes
     __builtin_amdgcn_wave_barrier();
 #pragma unroll
-    for (int q = 0; q < TMW / RPI; ++q) {
+    for (int q = 0; q < NR / RPI; ++q) {
       const int r = q * RPI + lane / CH, c = lane % CH;
       const int sw = CH == 16 ? (r & 15) : ((r >> 1) & 7);
       const i32x4 v = *reinterpret_cast<const i32x4*>(wl + r * (NC * 2) + ((c ^ sw) << 4));
@@ -405,7 +408,7 @@ __global__ __launch_bounds__(WM * WN * 64) void gemm_nt_v4_kernel(const u16* __r
           }
           stage(NC, i, p, pack2<T>(v[0], v[1]), pack2<T>(v[2], v[3]));
         }
-      flush(NC, (out == 0 ? ce.g_out : out == 1 ? ce.u_out : C) + o0, ldc);
+      flush(NC, (out == 0 ? ce.g_out : out == 1 ? ce.u_out : C) + o0, ldc, std::integral_constant<int, TMW>{});
     }
     return;
   }
@@ -419,7 +422,52 @@ __global__ __launch_bounds__(WM * WN * 64) void gemm_nt_v4_kernel(const u16* __r
         for (int j = 0; j < FN; ++j)
           stage(NC, i, j, pack2<O>(alpha * acc[i][j][0], alpha * acc[i][j][1]),
                 pack2<O>(alpha * acc[i][j][2], alpha * acc[i][j][3]));
-      flush(NC, C + (int64_t)(m0 + wm * TMW) * ldc + n0 + wn * TNW, ldc);
+      flush(NC, C + (int64_t)(m0 + wm * TMW) * ldc + n0 + wn * TNW, ldc, std::integral_constant<int, TMW>{});
+      return;
+    }
+  }
+  if constexpr (EPI == 1 && EVEN && O::vec == 8) {
+    if (vec_store == 2) {
+      constexpr auto NC = std::integral_constant<int, TNW>{};
+      __syncthreads();  // every wave is done with the operand ring
+      uint32_t pk[FM][FN][2];
+#pragma unroll
+      for (int i = 0; i < FM; ++i) {
+        const int row = m0 + wm * TMW + i * 16 + (lane & 15);
+        const int64_t t = ce.tgt[row];
+        const float lse = ce.lse[row];
+        const bool valid = t != ce.ignore && t >= 0 && t < ce.vocab;
+        const float scale = valid ? (ce.up ? *ce.up : 1.f) / *ce.count : 0.f;
+#pragma unroll
+        for (int j = 0; j < FN; ++j) {
+          const int col = n0 + wn * TNW + j * 16 + 4 * quarter;
+          float r[4];
+#pragma unroll
+          for (int v = 0; v < 4; ++v)
+            r[v] = scale != 0.f ? (__expf(acc[i][j][v] - lse) - ((col + v + ce.col0 == t) ? 1.f : 0.f)) * scale : 0.f;
+          pk[i][j][0] = pack2<O>(r[0], r[1]);
+          pk[i][j][1] = pack2<O>(r[2], r[3]);
+          stage(NC, i, j, pk[i][j][0], pk[i][j][1]);
+        }
+      }
+      flush(NC, C + (int64_t)(m0 + wm * TMW) * ldc + n0 + wn * TNW, ldc, std::integral_constant<int, TMW>{});
+      if (ce.zt) {
+        // transposed block: TNW rows (columns of the tile) x TMW columns (its rows), 16-bit stores
+        // into 16-byte chunks swizzled as the row-major staging of a TMW-wide block
+        static_assert(TMW == 64, "transposed staging assumes 64-row wave tiles");
+#pragma unroll
+        for (int i = 0; i < FM; ++i)
+#pragma unroll
+          for (int j = 0; j < FN; ++j)
+#pragma unroll
+            for (int v = 0; v < 4; ++v) {
+              const int tr = j * 16 + 4 * quarter + v, tc = i * 16 + (lane & 15);
+              const u16 val = (u16)(pk[i][j][v >> 1] >> (16 * (v & 1)));
+              *reinterpret_cast<u16*>(wl + tr * (TMW * 2) + (((tc >> 3) ^ ((tr >> 1) & 7)) << 4) + (tc & 7) * 2) = val;
+            }
+        flush(std::integral_constant<int, TMW>{}, ce.zt + (int64_t)(n0 + wn * TNW) * ce.ldzt + m0 + wm * TMW, ce.ldzt,
+              std::integral_constant<int, TNW>{});
+      }
       return;
     }
   }
@@ -700,13 +748,18 @@ int q3_gemm_nt(int in_dtype, int out_dtype, const void* A, int64_t lda, const vo
 }
 
 int q3_gemm_nt_ce_grad(int dtype, const void* A, int64_t lda, const void* B, int64_t ldb, void* dz, int64_t lddz,
-                       int64_t M, int64_t N, int64_t K, int64_t col0, const int64_t* tgt, const float* lse,
-                       const float* count, const float* up, int64_t vocab, int64_t ignore_index,
+                       void* dzt, int64_t lddzt, int64_t M, int64_t N, int64_t K, int64_t col0, const int64_t* tgt,
+                       const float* lse, const float* count, const float* up, int64_t vocab, int64_t ignore_index,
                        hipStream_t stream) {
   Q3_REQUIRE((dtype == Q3_BF16 || dtype == Q3_F16) && A && B && dz && tgt && lse && count);
   Q3_REQUIRE(M > 0 && N > 0 && K > 0 && M < (1ll << 31) && N < (1ll << 31) && K < (1ll << 31) && K % 64 == 0);
   Q3_REQUIRE(lda % 8 == 0 && ldb % 8 == 0 && lda >= K && ldb >= K && lddz >= N && al16(A) && al16(B));
-  const CeEpi ce{tgt, lse, count, up, col0, vocab, ignore_index, nullptr, nullptr, nullptr, 0, 0};
+  // the transposed copy comes from the LDS epilogue of full 256 x 256 tiles with 16-byte row stores
+  Q3_REQUIRE(!dzt || (M % 256 == 0 && N % 256 == 0 && (M / 256) * (N / 256) >= 256 && lddz % 8 == 0 && al16(dz) &&
+                      lddzt % 8 == 0 && lddzt >= M && al16(dzt)));
+  CeEpi ce{tgt, lse, count, up, col0, vocab, ignore_index, nullptr, nullptr, nullptr, 0, 0};
+  ce.zt = (u16*)dzt;
+  ce.ldzt = lddzt;
   if (dtype == Q3_BF16) return launch_ce_grad<BF16>(A, lda, B, ldb, dz, lddz, M, N, K, ce, stream);
   return launch_ce_grad<F16>(A, lda, B, ldb, dz, lddz, M, N, K, ce, stream);
 }

@@ -61,8 +61,8 @@ SIGNATURES: dict[str, tuple] = {
     "q3_ce_chunk_stats": (_i32, [_i32, _p, _i64, _i64, _i64, _p, _p, _p, _p, _i64, _p]),
     "q3_ce_finish": (_i32, [_p, _p, _i32, _p, _p, _p, _p, _p, _p, _p, _i64, _i64, _i64, _p]),
     "q3_ce_chunk_grad": (_i32, [_i32, _i32, _p, _i64, _i64, _i64, _p, _p, _p, _p, _p, _i64, _i64, _i64, _i64, _p]),
-    "q3_gemm_nt_ce_grad": (_i32, [_i32, _p, _i64, _p, _i64, _p, _i64, _i64, _i64, _i64, _i64, _p, _p, _p, _p, _i64,
-                                  _i64, _p]),
+    "q3_gemm_nt_ce_grad": (_i32, [_i32, _p, _i64, _p, _i64, _p, _i64, _p, _i64, _i64, _i64, _i64, _i64, _p, _p, _p,
+                                  _p, _i64, _i64, _p]),
     "q3_gemm_nt_ce_stats": (_i32, [_i32, _p, _i64, _p, _i64, _i64, _i64, _i64, _i64, _p, _p, _p, _p, _i64, _i64,
                                    _p]),
     "q3_gemv": (_i32, [_i32, _p, _i64, _p, _p, _i64, _i64, _i64, _i64, _p]),

@@ -320,13 +320,21 @@ class CEState:
         return self.loss
 
 
-def gemm_ce_grad(x, w, col0, n, tgt, lse, count, up, dz, vocab, ignore_index):
+def gemm_ce_grad(x, w, col0, n, tgt, lse, count, up, dz, vocab, ignore_index, dzt=None):
     """dz[:, :n] = CE gradient of the logits x . w[col0:col0+n]^T (matrix cores; fp32 logits stay in
-    registers).  x [T, H] and w [V, H] K-contiguous bf16/fp16, H % 64 == 0."""
+    registers), and dzt[:n, :] = its transpose when given.  x [T, H] and w [V, H] K-contiguous
+    bf16/fp16, H % 64 == 0."""
     t, h = x.shape
     H.call("q3_gemm_nt_ce_grad", H.code(x.dtype), x.data_ptr(), x.stride(0), w[col0:].data_ptr(), w.stride(0),
-           dz.data_ptr(), dz.stride(0), t, n, h, col0, tgt.data_ptr(), lse.data_ptr(), count.data_ptr(),
+           dz.data_ptr(), dz.stride(0), 0 if dzt is None else dzt.data_ptr(), 0 if dzt is None else dzt.stride(0),
+           t, n, h, col0, tgt.data_ptr(), lse.data_ptr(), count.data_ptr(),
            0 if up is None else up.data_ptr(), vocab, int(ignore_index), H.stream())
+
+
+def ce_grad_transposed_ok(x, t, n, lddz, dz, dzt):
+    """Whether q3_gemm_nt_ce_grad can write the transposed dz copy for this chunk."""
+    return t % 256 == 0 and n % 256 == 0 and (t // 256) * (n // 256) >= 256 and lddz % 8 == 0 and \
+        dz.data_ptr() % 16 == 0 and dzt.stride(0) % 8 == 0 and dzt.data_ptr() % 16 == 0
 
 
 def ce_grad(z, ld, n, col0, tgt, lse, count, up, dz, ldo, vocab, ignore_index):

@@ -93,8 +93,12 @@ class _LMHeadCE(torch.autograd.Function):
                 c0 = c * chunk
                 n = min(chunk, v - c0)
                 dzc = dz[:, c0:c0 + n]
-                _ops.gemm_ce_grad(x, weight, c0, n, tgt, lse, count, up, dzc, v, ctx.ignore)
-                _ops.transpose_into(dzc, dzt[:n])
+                if _ops.ce_grad_transposed_ok(x, t, n, vp, dzc, dzt):
+                    # the CE-gradient GEMM stores dz and its transpose (the dW operand) itself
+                    _ops.gemm_ce_grad(x, weight, c0, n, tgt, lse, count, up, dzc, v, ctx.ignore, dzt=dzt[:n])
+                else:
+                    _ops.gemm_ce_grad(x, weight, c0, n, tgt, lse, count, up, dzc, v, ctx.ignore)
+                    _ops.transpose_into(dzc, dzt[:n])
                 gemm_nt_into(dzt, t, xt, t, dw[c0:c0 + n], n, h, t)
             dx = torch.empty((t, h), device=x.device, dtype=x.dtype)
             gemm_nt_into(dz, vp, wt, vp, dx, t, h, vp)

@@ -113,7 +113,8 @@ def test_lm_head_ce_config_shape_sampled_rows():
 
 
 @pytest.mark.parametrize("t,h,n,col0,with_up", [(512, 256, 1000, 3000, True), (300, 128, 4096, 0, False),
-                                                (1024, 512, 2304, 8192, True)])
+                                                (1024, 512, 2304, 8192, True), (8192, 256, 2048, 512, True),
+                                                (4096, 128, 4096, 0, False)])
 def test_fused_ce_grad_gemm_matches_two_step(t, h, n, col0, with_up):
     """The logits GEMM with the CE-gradient epilogue writes bit-for-bit the dz of the unfused path
     (fp32 logits from the GEMM, then the CE gradient kernel), including ignored and out-of-range rows."""
@@ -138,6 +139,14 @@ def test_fused_ce_grad_gemm_matches_two_step(t, h, n, col0, with_up):
     _ops.ce_grad(z, n, n, col0, tgt, lse, count, up, dz_ref, n, v, -100)
     assert torch.equal(dz_fused[:, :n].cpu(), dz_ref.cpu())
     assert torch.all(dz_fused[:, n:].float() == 7.0)          # columns past n untouched
+    if _ops.ce_grad_transposed_ok(x, t, n, n + 8, dz_fused, torch.empty(0, t + 8, device="cuda")):
+        # the same launch with the transposed copy: dz unchanged, dzt = dz^T, nothing past t written
+        dz2 = torch.full((t, n + 8), 7.0, device="cuda", dtype=torch.bfloat16)
+        dzt = torch.full((n, t + 8), 5.0, device="cuda", dtype=torch.bfloat16)
+        _ops.gemm_ce_grad(x, w, col0, n, tgt, lse, count, up, dz2, v, -100, dzt=dzt)
+        assert torch.equal(dz2, dz_fused)
+        assert torch.equal(dzt[:, :t], dz_ref.t())
+        assert torch.all(dzt[:, t:].float() == 5.0)
 
 
 @pytest.mark.parametrize("t,h,v,chunk", [(512, 256, 5000, 2048), (300, 128, 4096, 4096), (1024, 512, 9000, 4100),
