@@ -242,7 +242,8 @@ int q3_gemm_nt_ce_stats(int dtype, const void* A, int64_t lda, const void* B, in
 int q3_gemv(int dtype, const void* x, int64_t ldx, const void* w, void* y, int64_t ldy, int64_t m, int64_t n,
             int64_t k, hipStream_t stream);
 /* Fused decode-step projection for M <= 16 token rows (K % 8 == 0, 16-byte aligned rows):
- *   xn = norm_w ? RMSNorm(x) * norm_w (eps, rounded to dtype) : x
+ *   with norm_w, xn W^T means rsqrt(mean_k x[m, k]^2 + eps) * (dtype(x[m, :] * norm_w) W^T), the
+ *   RMSNorm's row scale applied to the fp32 dot product; without it, x W^T;
  *   mode 0: y_i[m, :n_i] = xn W_i^T for each of the nseg <= 3 segments (W_i [n_i, K], row-major);
  *   mode 1: y_0 = res + dtype(xn W_0^T)  (residual add; res rows at stride ldres, may alias y_0);
  *   mode 2: y_0 = silu(dtype(xn W_0^T)) * dtype(xn W_1^T)  (SwiGLU; nseg == 2, n_0 == n_1).

@@ -17,13 +17,15 @@ constexpr int kThreads = 256;
 // kb + 32 c + 8 kq, so each load instruction reads 64 contiguous bytes of 16 rows.  A workgroup owns
 // 16 output rows and its NW waves take interleaved k blocks, P blocks in flight per wave (all loads
 // issued before the block's MFMAs); the partial 16 x 16 tiles fold in LDS in fixed order.
-//   * NORM: xn = x * rsqrt(mean(x^2) + eps) * norm_w (RMSNorm of the input rows, recomputed per
-//     workgroup from the M rows of x, rounded to the storage type like the standalone kernel);
+//   * NORM: the RMSNorm of the input rows folded in: y = rsqrt(mean_k x[m, k]^2 + eps) *
+//     sum_k T(x[m, k] norm_w[k]) W[n, k] -- the row scale multiplies the fp32 dot product, and each
+//     workgroup accumulates the sums of squares from the x chunks it already streams (no separate
+//     normalisation pass before the weights);
 //   * MODE 0: y = acc;  MODE 1: y = res + T(acc) (residual add);  MODE 2: segments 0 and 1 are the
 //     gate and up weights, y_0 = silu(T(acc_gate)) * T(acc_up) (SwiGLU);
 //   * up to 3 weight segments share the input (the Q, K and V projections in one launch).
-// Rounding points match the unfused path (GEMV output, then residual / SwiGLU), and every output is
-// a fixed-order reduction: deterministic.
+// Rounding points: the GEMV output, then residual / SwiGLU, as the unfused path (which rounds the
+// normalised input before its GEMM instead); every output is a fixed-order reduction: deterministic.
 struct DecSeg {
   const u16* w;
   u16* y;
@@ -45,8 +47,8 @@ struct DecArgs {
 template <typename T, int MODE, bool NORM, int NW, int P>
 __global__ __launch_bounds__(NW * 64) void dlinear_kernel(DecArgs a) {
   constexpr int NB = MODE == 2 ? 2 : 1;  // weight tiles per workgroup (gate + up)
-  __shared__ float inv_s[16];
   __shared__ f32x4 red[NW][NB][64];
+  __shared__ float red_ss[NORM ? NW : 1][64];
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   int tile = blockIdx.x, s = 0;
   if constexpr (MODE != 2) {
@@ -56,59 +58,11 @@ __global__ __launch_bounds__(NW * 64) void dlinear_kernel(DecArgs a) {
   const int n0 = tile * 16, K = a.K, M = a.M;
   const int r = lane & 15, kq = lane >> 4;  // r: token row (A) and weight row (B) of this lane
 
-  if (NORM && M > 4) {
-    // many rows: one wave per row (the rows' loads run in parallel across the waves)
-    for (int m = wave; m < M; m += NW) {
-      const u16* xr = a.x + m * a.ldx;
-      float ss = 0.f;
-      for (int c = lane; c < K / 8; c += 64) {
-        const Vec<T> v = load_vec<T>(xr + c * 8);
-#pragma unroll
-        for (int e = 0; e < 8; ++e) ss += v.v[e] * v.v[e];
-      }
-      ss = group_sum<64>(ss);
-      if (lane == 0) inv_s[m] = rsqrtf(ss * (1.f / (float)K) + a.eps);
-    }
-    __syncthreads();
-  } else if constexpr (NORM) {
-    // few rows: the sum of squares of each row over the whole workgroup: thread t takes chunks t,
-    // t + NW*64, .. of every row, the loads of all rows issued before any is used.
-    __shared__ float part[NW][4];
-    float ss[4];
-#pragma unroll
-    for (int m = 0; m < 4; ++m) ss[m] = 0.f;
-    for (int c0 = 0; c0 < K / 8; c0 += NW * 64) {
-      const int c = min(c0 + tid, K / 8 - 1);
-      const bool live = c0 + tid < K / 8;
-      i32x4 raw[4];
-#pragma unroll
-      for (int m = 0; m < 4; ++m)
-        if (m < M) raw[m] = *reinterpret_cast<const i32x4*>(a.x + m * a.ldx + c * 8);
-#pragma unroll
-      for (int m = 0; m < 4; ++m)
-        if (m < M && live) {
-          const Vec<T> v = unpack_vec<T>(raw[m]);
-#pragma unroll
-          for (int e = 0; e < 8; ++e) ss[m] += v.v[e] * v.v[e];
-        }
-    }
-#pragma unroll
-    for (int m = 0; m < 4; ++m)
-      if (m < M) {
-        const float w = group_sum<64>(ss[m]);
-        if (lane == 0) part[wave][m] = w;
-      }
-    __syncthreads();
-    if (tid < M) {
-      float t = part[0][tid];
-#pragma unroll
-      for (int w = 1; w < NW; ++w) t += part[w][tid];
-      inv_s[tid] = rsqrtf(t * (1.f / (float)K) + a.eps);
-    }
-    __syncthreads();
-  }
   const bool xrow = r < M;
-  const float inv = NORM && xrow ? inv_s[r] : 1.f;
+  // NORM: y = inv[m] * sum_k (x[m, k] nw[k]) W[n, k] with inv[m] = rsqrt(mean_k x[m, k]^2 + eps): the
+  // per-row scale is applied after the dot product, and the sum of squares is accumulated from the
+  // same x chunks the MFMAs consume, so no separate normalisation pass precedes the weight stream.
+  float ssq = 0.f;
   const u16* xr = a.x + (xrow ? r : 0) * a.ldx + 8 * kq;
   const u16* wr[NB];
 #pragma unroll
@@ -145,9 +99,9 @@ __global__ __launch_bounds__(NW * 64) void dlinear_kernel(DecArgs a) {
 #pragma unroll
           for (int w = 0; w < 4; ++w) {
             const uint32_t xx = (uint32_t)xv[p][c][w], ww = (uint32_t)nv[p][c][w];
-            const float lo = to_f32<T>((u16)(xx & 0xffffu)) * inv * to_f32<T>((u16)(ww & 0xffffu));
-            const float hi = to_f32<T>((u16)(xx >> 16)) * inv * to_f32<T>((u16)(ww >> 16));
-            xf[w] = (int)pack2<T>(lo, hi);
+            const float x0 = to_f32<T>((u16)(xx & 0xffffu)), x1 = to_f32<T>((u16)(xx >> 16));
+            ssq += x0 * x0 + x1 * x1;
+            xf[w] = (int)pack2<T>(x0 * to_f32<T>((u16)(ww & 0xffffu)), x1 * to_f32<T>((u16)(ww >> 16)));
           }
         }
 #pragma unroll
@@ -170,6 +124,7 @@ __global__ __launch_bounds__(NW * 64) void dlinear_kernel(DecArgs a) {
 
 #pragma unroll
   for (int j = 0; j < NB; ++j) red[wave][j][lane] = acc[j];
+  if constexpr (NORM) red_ss[wave][lane] = ssq;
   __syncthreads();
   if (wave != 0) return;
   float v[NB][4];
@@ -180,6 +135,21 @@ __global__ __launch_bounds__(NW * 64) void dlinear_kernel(DecArgs a) {
     for (int w = 1; w < NW; ++w) t += red[w][j][lane];
 #pragma unroll
     for (int e = 0; e < 4; ++e) v[j][e] = t[e];
+  }
+  if constexpr (NORM) {
+    // lane (r, kq) holds row r's squares over its k chunks: fold the waves, then the 4 quarters
+    float t = red_ss[0][lane];
+#pragma unroll
+    for (int w = 1; w < NW; ++w) t += red_ss[w][lane];
+    t += __shfl_xor(t, 16, 64);
+    t += __shfl_xor(t, 32, 64);
+    const float inv_r = rsqrtf(t * (1.f / (float)K) + a.eps);  // row r's scale
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      const float inv_m = __shfl(inv_r, 4 * kq + e, 64);       // the scale of output row m = 4 kq + e
+#pragma unroll
+      for (int j = 0; j < NB; ++j) v[j][e] *= inv_m;
+    }
   }
   // lane holds D[m = 4 kq + e][n = r]
   const int n = n0 + r;

@@ -28,8 +28,9 @@ def test_gemv(m, n, k):
 @pytest.mark.parametrize("k", [4096, 688, 256, 12288])
 @pytest.mark.parametrize("norm", [False, True])
 def test_decode_linear_modes(m, k, norm):
-    """Fused decode projection against the unfused fp64 math with the same rounding points:
-    xn = bf16(rmsnorm(x)); mode 0 three segments; mode 1 res + bf16(y); mode 2 silu(bf16 g) bf16(u)."""
+    """Fused decode projection against the unfused fp64 math: xn = bf16(rmsnorm(x)) (the kernel
+    rounds x * norm_w instead and applies the row scale to the fp32 dot product: the same math up to
+    one bf16 rounding); mode 0 three segments; mode 1 res + bf16(y); mode 2 silu(bf16 g) bf16(u)."""
     print(f"decode_linear m={m} k={k} norm={norm}", flush=True)
     gen = seeded(m * 7 + k + int(norm))
     dt = torch.bfloat16
