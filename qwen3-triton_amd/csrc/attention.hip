@@ -710,7 +710,12 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
     const char* qb = lds + (u % ST) * STAGE;
     const char* db = qb + TB;
     const float* side = reinterpret_cast<const float*>(qb + 2 * TB);
+    const f32x4 l0 = *reinterpret_cast<const f32x4*>(side + 8 * G);
+    const f32x4 l1 = *reinterpret_cast<const f32x4*>(side + 8 * G + 4);
+    const f32x4 d0 = *reinterpret_cast<const f32x4*>(side + BM + 8 * G);
+    const f32x4 d1 = *reinterpret_cast<const f32x4*>(side + BM + 8 * G + 4);
 
+    // dP starts from -delta (its row constant), so the products leave dP - delta
     f32x4 s[2][2], dp[2][2];  // [query tile t][key tile c]
 #pragma unroll
     for (int ks = 0; ks < 4; ++ks) {
@@ -725,14 +730,10 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
 #pragma unroll
         for (int c = 0; c < 2; ++c) {
           s[t][c] = mma16<T>(as_frag(qa[t]), kf[c][ks], ks == 0 ? f32x4{0.f, 0.f, 0.f, 0.f} : s[t][c]);
-          dp[t][c] = mma16<T>(as_frag(da[t]), vf[c][ks], ks == 0 ? f32x4{0.f, 0.f, 0.f, 0.f} : dp[t][c]);
+          dp[t][c] = mma16<T>(as_frag(da[t]), vf[c][ks], ks == 0 ? -(t ? d1 : d0) : dp[t][c]);
         }
     }
     const bool mask = !(k0w + 31 <= q0 + off && q0 + BM - 1 < Lq);
-    const f32x4 l0 = *reinterpret_cast<const f32x4*>(side + 8 * G);
-    const f32x4 l1 = *reinterpret_cast<const f32x4*>(side + 8 * G + 4);
-    const f32x4 d0 = *reinterpret_cast<const f32x4*>(side + BM + 8 * G);
-    const f32x4 d1 = *reinterpret_cast<const f32x4*>(side + BM + 8 * G + 4);
     i32x4 pp[2], dd[2];
 #pragma unroll
     for (int c = 0; c < 2; ++c) {
@@ -747,7 +748,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
             p = (k0w + 16 * c + r16 <= q + off && q < Lq) ? p : 0.f;
           }
           pv[4 * t + i] = p;
-          dsv[4 * t + i] = p * (dp[t][c][i] - (t ? d1[i] : d0[i]));
+          dsv[4 * t + i] = p * dp[t][c][i];
         }
 #pragma unroll
       for (int w = 0; w < 4; ++w) {
@@ -890,7 +891,7 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
 #pragma unroll
         for (int u = 0; u < 2; ++u) {
           S[kt][u] = mma16<T>(as_frag(a), qf[u][ks], ks == 0 ? f32x4{0.f, 0.f, 0.f, 0.f} : S[kt][u]);
-          DP[kt][u] = mma16<T>(as_frag(av), df[u][ks], ks == 0 ? f32x4{0.f, 0.f, 0.f, 0.f} : DP[kt][u]);
+          DP[kt][u] = mma16<T>(as_frag(av), df[u][ks], ks == 0 ? f32x4{-dlt[u], -dlt[u], -dlt[u], -dlt[u]} : DP[kt][u]);
         }
       }
     const bool mask = j >= nfull;
@@ -904,7 +905,7 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
         for (int i = 0; i < 4; ++i) {
           float p = __builtin_amdgcn_exp2f(__builtin_fmaf(S[kt][u][i], scale2, -lse2[u]));
           if (mask) p = 32 * (kt >> 1) + 8 * (kt & 1) + i <= qrel ? p : 0.f;
-          S[kt][u][i] = p * (DP[kt][u][i] - dlt[u]);
+          S[kt][u][i] = p * DP[kt][u][i];  // DP started from -delta
         }
 #pragma unroll
       for (int c = 0; c < 2; ++c) {
