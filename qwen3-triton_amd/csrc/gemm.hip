@@ -247,26 +247,32 @@ __global__ __launch_bounds__(WM * WN * 64) void gemm_nt_v4_kernel(const u16* __r
       else src[i] = B + (int64_t)min(n0 + R - BM, N - 1) * ldb + csrc * 8;
     }
   }
-  auto issue = [&](int stage, int k0) {
+  // Full tiles (EVEN): the ring refill is issued on every tile, so the loop body is straight-line
+  // code and the refill loads interleave with the MFMAs; past the last k tile it re-reads a tile that
+  // was just consumed (L2-resident) into a stage that is never read again.
+  int kfill = 0;  // k of a tile already loaded: the data a refill past the last k tile re-reads
+  auto issue = [&](int stage, int k0) {  // k0 < 0: past the last k tile (EVEN only)
 #pragma unroll
     for (int i = 0; i < LPW; ++i) {
       const int rg = wave_u + NW * i;
-      const void* g;
+      u16* dst = lds + stage * STAGE + rg * RPL * BK;
       if constexpr (EVEN) {
+        const int kk = k0 < 0 ? kfill : k0;  // past the last k tile: refill with a resident tile's data
+        const void* g;
         if (i < A_LOADS) {
-          g = reinterpret_cast<const char*>(A + (int64_t)(m0 + rg * RPL) * lda + k0) + offa;
+          g = reinterpret_cast<const char*>(A + (int64_t)(m0 + rg * RPL) * lda + kk) + offa;
         } else if constexpr (EPI == 3) {
-          const int vr = n0 + rg * RPL - BM, blk = vr >> 4;
+          const int vr = rg * RPL - BM, blk = vr >> 4;  // virtual B row within the tile
           const u16* w = (blk & 1) ? ce.b2 : B;
-          g = reinterpret_cast<const char*>(w + (int64_t)((blk >> 1) * 16 + (vr & 15)) * ldb + k0) + offb;
+          g = reinterpret_cast<const char*>(w + (int64_t)(n0 / 2 + (blk >> 1) * 16 + (vr & 15)) * ldb + kk) + offb;
         } else {
-          g = reinterpret_cast<const char*>(B + (int64_t)(n0 + rg * RPL - BM) * ldb + k0) + offb;
+          g = reinterpret_cast<const char*>(B + (int64_t)(n0 + rg * RPL - BM) * ldb + kk) + offb;
         }
+        __builtin_amdgcn_global_load_lds(g, (__attribute__((address_space(3))) void*)dst, 16, 0, 0);
       } else {
-        g = src[i] + k0;
+        const void* g = src[i] + k0;
+        __builtin_amdgcn_global_load_lds(g, (__attribute__((address_space(3))) void*)dst, 16, 0, 0);
       }
-      __builtin_amdgcn_global_load_lds(g, (__attribute__((address_space(3))) void*)(lds + stage * STAGE + rg * RPL * BK),
-                                       16, 0, 0);
     }
   };
 
@@ -296,12 +302,19 @@ __global__ __launch_bounds__(WM * WN * 64) void gemm_nt_v4_kernel(const u16* __r
     for (int j = 0; j < FN; ++j) acc[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
 
   const int nk = K / BK;
+  if constexpr (EVEN) {  // every ring slot is always issued (past the end: zero-filling range misses)
 #pragma unroll
-  for (int st = 0; st < STAGES - 1; ++st)
-    if (st < nk) issue(st, st * BK);
-  if (nk - 1 >= STAGES - 2) ring_sync<(STAGES - 2) * LPW>();
-  else ring_sync<0>();
-  if (STAGES - 1 < nk) issue(STAGES - 1, (STAGES - 1) * BK);
+    for (int st = 0; st < STAGES - 1; ++st) issue(st, st < nk ? st * BK : -1);
+    ring_sync<(STAGES - 2) * LPW>();
+    issue(STAGES - 1, STAGES - 1 < nk ? (STAGES - 1) * BK : -1);
+  } else {
+#pragma unroll
+    for (int st = 0; st < STAGES - 1; ++st)
+      if (st < nk) issue(st, st * BK);
+    if (nk - 1 >= STAGES - 2) ring_sync<(STAGES - 2) * LPW>();
+    else ring_sync<0>();
+    if (STAGES - 1 < nk) issue(STAGES - 1, (STAGES - 1) * BK);
+  }
   load(0, 0, 0);
   // One tile: each k-step first reads the next step's fragments into the other buffer (the next
   // tile's first step after the barrier that makes that tile resident and frees this tile's stage
@@ -322,9 +335,15 @@ __global__ __launch_bounds__(WM * WN * 64) void gemm_nt_v4_kernel(const u16* __r
       } else {
         // Tile kt+1 resident; every wave done with tile kt.  Runs on the last tile too (re-reading a
         // resident stage) so the LDS counter state is the same on every path into the MFMAs.
-        if (kt + STAGES - 1 < nk) ring_sync<(STAGES - 2) * LPW>();
-        else ring_sync<0>();
-        if (kt + STAGES < nk) issue(stage, (kt + STAGES) * BK);
+        if constexpr (EVEN) {
+          ring_sync<(STAGES - 2) * LPW>();
+          kfill = kt * BK;
+          issue(stage, kt + STAGES < nk ? (kt + STAGES) * BK : -1);
+        } else {
+          if (kt + STAGES - 1 < nk) ring_sync<(STAGES - 2) * LPW>();
+          else ring_sync<0>();
+          if (kt + STAGES < nk) issue(stage, (kt + STAGES) * BK);
+        }
         load((kt + 1) % STAGES, b ^ 1, 0);
       }
 #pragma unroll
