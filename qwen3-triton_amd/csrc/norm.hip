@@ -6,7 +6,7 @@
 // DPP/swizzle butterfly inside the group (TPR <= 64) or wave butterflies + LDS (TPR = 256).
 // Weight gradients are accumulated per lane across the rows a workgroup visits, folded across the
 // workgroup in a fixed order, written as one fp32 partial row per workgroup, and summed over
-// workgroups by a fixed-shape column-sum tree: the result is bitwise deterministic.
+// workgroups by one fixed-order column-sum launch: the result is bitwise deterministic.
 #include "common.h"
 
 namespace {
@@ -186,46 +186,70 @@ __global__ __launch_bounds__(kBlock) void rmsnorm_bwd_kernel(const typename T::s
   for (int c = threadIdx.x; c < h; c += kBlock) partial[(int64_t)blockIdx.x * h + c] = fold[c];
 }
 
-// Column sums of an fp32 [R][h] partial matrix as a fixed-shape tree: a workgroup reduces a
-// 64-row x 64-column block (4 row groups of 16 rows, folded in order through LDS) into one row of
-// the next level.  Two levels cover R <= 4096.  Same inputs -> same summation order -> bitwise
-// reproducible results.
-template <typename O>
-__global__ __launch_bounds__(kBlock) void colsum_level_kernel(const float* __restrict__ in,
-                                                              typename O::storage* __restrict__ out, int rows, int h) {
-  __shared__ float fold[4][64];
-  const int c = blockIdx.x * 64 + (threadIdx.x & 63), grp = threadIdx.x >> 6;
-  const int r0 = blockIdx.y * 64 + grp * 16;
-  // all 16 loads in flight at once (clamped indices, masked terms), summed in row order
-  const int cc = c < h ? c : h - 1;
-  float v[16];
+// Column sums of an fp32 [R][h] partial matrix in one launch: a workgroup owns L * V columns
+// (L lanes of V consecutive columns) and 256 / L row groups; row group g sums rows g, g + 256 / L,
+// ... in order, then the groups fold through LDS as a fixed binary tree.  Same (R, h) -> same
+// summation order -> bitwise reproducible results.
+template <typename O, int L, int V>
+__global__ __launch_bounds__(kBlock) void colsum_kernel(const float* __restrict__ in,
+                                                        typename O::storage* __restrict__ out, int rows, int h) {
+  constexpr int RG = kBlock / L, W = L * V;
+  __shared__ float red[RG][W];
+  const int lc = threadIdx.x % L, g = threadIdx.x / L;
+  const int c0 = (blockIdx.x * L + lc) * V;
+  const int cc = c0 < h ? c0 : 0;
+  float s[V];
 #pragma unroll
-  for (int i = 0; i < 16; ++i) v[i] = in[(int64_t)min(r0 + i, rows - 1) * h + cc];
-  float s = 0.f;
-  if (c < h) {
+  for (int e = 0; e < V; ++e) s[e] = 0.f;
+  // 8 rows in flight per step (clamped indices, masked terms)
+  for (int r0 = g; r0 < rows; r0 += 8 * RG) {
+    float v[8][V];
 #pragma unroll
-    for (int i = 0; i < 16; ++i)
-      if (r0 + i < rows) s += v[i];
+    for (int i = 0; i < 8; ++i) {
+      const int64_t r = min(r0 + i * RG, rows - 1);
+      if constexpr (V == 4) {
+        const f32x4 x = *reinterpret_cast<const f32x4*>(in + r * h + cc);
+#pragma unroll
+        for (int e = 0; e < 4; ++e) v[i][e] = x[e];
+      } else {
+        v[i][0] = in[r * h + cc];
+      }
+    }
+#pragma unroll
+    for (int i = 0; i < 8; ++i)
+      if (r0 + i * RG < rows) {
+#pragma unroll
+        for (int e = 0; e < V; ++e) s[e] += v[i][e];
+      }
   }
-  fold[grp][threadIdx.x & 63] = s;
+#pragma unroll
+  for (int e = 0; e < V; ++e) red[g][lc * V + e] = s[e];
   __syncthreads();
-  if (grp == 0 && c < h) {
-    const int l = threadIdx.x & 63;
-    out[(int64_t)blockIdx.y * h + c] = from_f32<O>(((fold[0][l] + fold[1][l]) + fold[2][l]) + fold[3][l]);
+#pragma unroll
+  for (int half = RG / 2; half >= 1; half >>= 1) {
+    if (g < half) {
+#pragma unroll
+      for (int e = 0; e < V; ++e) red[g][lc * V + e] += red[g + half][lc * V + e];
+    }
+    __syncthreads();
+  }
+  if (g == 0 && c0 < h) {
+#pragma unroll
+    for (int e = 0; e < V; ++e) out[c0 + e] = from_f32<O>(red[0][lc * V + e]);
   }
 }
 
-// dw[c] = sum over the nb partial rows in `part`; `part` must have room for nb + ceil(nb/64) rows.
+// dw[c] = sum over the nb partial rows in `part`.
 template <typename T> void colsum(float* part, typename T::storage* dw, int nb, int h, hipStream_t s) {
-  const unsigned gx = (unsigned)((h + 63) / 64);
-  if (nb <= 64) {
-    colsum_level_kernel<T><<<dim3(gx, 1), kBlock, 0, s>>>(part, dw, nb, h);
-    return;
+  if (h % 4 == 0) {
+    if (h >= 1024) {
+      colsum_kernel<T, 4, 4><<<(unsigned)((h + 15) / 16), kBlock, 0, s>>>(part, dw, nb, h);
+    } else {
+      colsum_kernel<T, 1, 4><<<(unsigned)((h + 3) / 4), kBlock, 0, s>>>(part, dw, nb, h);
+    }
+  } else {
+    colsum_kernel<T, 4, 1><<<(unsigned)((h + 3) / 4), kBlock, 0, s>>>(part, dw, nb, h);
   }
-  const int r2 = (nb + 63) / 64;
-  float* level2 = part + (int64_t)nb * h;
-  colsum_level_kernel<F32><<<dim3(gx, (unsigned)r2), kBlock, 0, s>>>(part, level2, nb, h);
-  colsum_level_kernel<T><<<dim3(gx, 1), kBlock, 0, s>>>(level2, dw, r2, h);
 }
 
 // ---------------------------------------------------------------- generic (scalar) row kernels
@@ -601,7 +625,7 @@ int q3_rmsnorm_fwd(int dtype, const void* x, const void* w, void* y, int64_t row
 
 size_t q3_rmsnorm_bwd_workspace_bytes(int64_t rows, int64_t h) {
   const int64_t nb = bwd_blocks(rows, h);
-  return (size_t)(nb + (nb + 63) / 64) * (size_t)h * sizeof(float);
+  return (size_t)nb * (size_t)h * sizeof(float);
 }
 
 int q3_rmsnorm_bwd(int dtype, const void* x, const void* w, const void* dy, void* dx, void* dw, void* workspace,
@@ -627,7 +651,7 @@ int q3_norm_rope_fwd(int dtype, const void* x, const void* w, const void* cos, c
 
 size_t q3_norm_rope_bwd_workspace_bytes(int64_t tokens, int64_t heads, int64_t d) {
   const int64_t nb = bwd_blocks(tokens * heads, d);
-  return (size_t)(nb + (nb + 63) / 64) * (size_t)d * sizeof(float);
+  return (size_t)nb * (size_t)d * sizeof(float);
 }
 
 int q3_norm_rope_bwd(int dtype, const void* x, const void* w, const void* cos, const void* sin, const void* dy,
