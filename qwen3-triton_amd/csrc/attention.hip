@@ -1605,6 +1605,16 @@ int fwd_mfma(const void* q, Lay ql, const void* k, Lay kl, const void* vt, void*
   }
 }
 
+}  // namespace
+
+// dK/dV with one query head per wave (attention_bwd.hip); Hq / Hkv must be a multiple of 4.
+int q3i_attn_bwd_dkdv_v4(int dtype, const void* q, int64_t qsb, int64_t qsh, int64_t qss, const void* k,
+                         const void* v, int64_t ksb, int64_t ksh, int64_t kss, const void* dout, const float* lse,
+                         const float* delta, void* dk, void* dv, int B, int Hq, int Hkv, int Lq, int Lk, float scale,
+                         hipStream_t s);
+
+namespace {
+
 template <typename T, int GH>
 int bwd_dq_v3(const void* q, Lay ql, const void* k, const void* v, Lay kl, const void* kt, const void* dout,
               const float* lse, const float* delta, void* dq, int B, int Hq, int Hkv, int Lq, int Lk, int ldkt,
@@ -1630,6 +1640,9 @@ int bwd_mfma(const void* q, Lay ql, const void* k, const void* v, Lay kl, const 
       rc = bwd_dq_v3<T, 2>(q, ql, k, v, kl, kt, dout, lse, delta, dq, B, Hq, Hkv, Lq, Lk, ldkt, scale, s);
     else rc = bwd_dq_v3<T, 1>(q, ql, k, v, kl, kt, dout, lse, delta, dq, B, Hq, Hkv, Lq, Lk, ldkt, scale, s);
     if (rc) return rc;
+    if (grp % 4 == 0)  // one query head per wave, 48-key wave tiles (attention_bwd.hip)
+      return q3i_attn_bwd_dkdv_v4(T::code, q, ql.b, ql.h, ql.s, k, v, kl.b, kl.h, kl.s, dout, lse, delta, dk, dv, B,
+                                  Hq, Hkv, Lq, Lk, scale, s);
     dim3 g2((unsigned)(B * Hkv), (unsigned)((Lk + 127) / 128));
     attn_bwd_dkdv_v3<T><<<g2, 256, 0, s>>>((const u16*)q, ql, (const u16*)k, (const u16*)v, kl, (const u16*)dout, lse,
                                            delta, (u16*)dk, (u16*)dv, Hq, Hkv, Lq, Lk, scale, scale * kLog2e);
