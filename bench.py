@@ -56,6 +56,9 @@ class GemmTimer:
         # the gate/up GEMM with the SwiGLU epilogue (two weights, one launch)
         self.gu_mods = [m for m in modules if hasattr(m, "gate_up_swiglu_into")]
         self.gu_orig = self.gu_mods[0].gate_up_swiglu_into if self.gu_mods else None
+        # the shared-input projections (q/k/v: up to three weights, one launch)
+        self.mu_mods = [m for m in modules if hasattr(m, "gemm_nt_multi_into")]
+        self.mu_orig = self.mu_mods[0].gemm_nt_multi_into if self.mu_mods else None
         self.records = []
         self.active = False
 
@@ -81,10 +84,21 @@ class GemmTimer:
             e.record()
             self.records.append((s, e, 2.0 * 2 * m * n * k))
 
+        def timed_mu(a, weights, outs, m, k):
+            if not self.active:
+                return self.mu_orig(a, weights, outs, m, k)
+            s, e = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            s.record()
+            self.mu_orig(a, weights, outs, m, k)
+            e.record()
+            self.records.append((s, e, 2.0 * m * k * sum(w.shape[0] for w in weights)))
+
         for m in self.mods:
             m.gemm_nt_into = timed
         for m in self.gu_mods:
             m.gate_up_swiglu_into = timed_gu
+        for m in self.mu_mods:
+            m.gemm_nt_multi_into = timed_mu
         return self
 
     def __exit__(self, *exc):
@@ -92,6 +106,8 @@ class GemmTimer:
             m.gemm_nt_into = self.orig
         for m in self.gu_mods:
             m.gate_up_swiglu_into = self.gu_orig
+        for m in self.mu_mods:
+            m.gemm_nt_multi_into = self.mu_orig
 
     def summary(self):
         ms = sum(s.elapsed_time(e) for s, e, _ in self.records)

@@ -151,6 +151,17 @@ int q3_gemm_nt(int in_dtype, int out_dtype, const void* A, int64_t lda, const vo
 int q3_gemm_gate_up_swiglu(int dtype, const void* x, int64_t ldx, const void* wg, const void* wu, int64_t ldw,
                            void* g, void* u, void* y, int64_t ldo, int64_t M, int64_t N, int64_t K,
                            hipStream_t stream);
+/* Several projections of one input in one matrix-core launch: for A [M, K] and nseg (1..3) weights
+ * Bs[s] [Ns[s], K] (common row stride ldb), writes Cs[s] = A Bs[s]^T ([M, Ns[s]] at row stride
+ * ldcs[s]), fp32 accumulation, one rounding, bit-identical to nseg separate q3_gemm_nt calls with
+ * the same tile plan.  M % 256 == 0, every Ns[s] % 256 == 0, K % 64 == 0, ldcs[s] % 8 == 0,
+ * pointers 16-byte aligned.  The K and V projections of Qwen3-8B (N = 1024) alone fill only half
+ * of the 256 CUs with 256 x 256 tiles; side by side with Q they share one well-filled grid.
+ * Replaces: components.py:19-21 / _model.py (q_proj, k_proj, v_proj: three kernels/linear.py
+ * launches on the same input). */
+int q3_gemm_nt_multi(int dtype, const void* A, int64_t lda, int nseg, const void* const* Bs, int64_t ldb,
+                     void* const* Cs, const int64_t* Ns, const int64_t* ldcs, int64_t M, int64_t K,
+                     hipStream_t stream);
 /* Same product for arbitrary element strides: A(m,k) = A[m*sam + k*sak], B(k,n) = B[k*sbk + n*sbn];
  * any dtype (fp32 included).  SIMT path for shapes the matrix-core kernel does not take.
  * Replaces: kernels/linear.py:13-42 (_gemm with arbitrary strides). */

@@ -11,6 +11,6 @@ const char* q3_error_string(int code) {
   return hipGetErrorString((hipError_t)code);
 }
 
-int q3_abi_version(void) { return 4; }
+int q3_abi_version(void) { return 5; }
 
 }  // extern "C"

@@ -185,6 +185,10 @@ template <int CPR> Q3_DEV int gemm_swz(int r) {
 // (block / 2) * 16 + r % 16), so each lane holds the gate and up accumulators of the same output
 // element in neighbouring 16 x 16 fragments.  It stores G = bf16(x Wg^T), U = bf16(x Wu^T) and
 // Y = silu(G) * U computed from the rounded G and U (row stride ldc, C = Y).
+// Segmented operand (EPI = 4): the B rows are the concatenation of up to 3 weights (the Q, K and V
+// projections of one input) and each output column segment goes to its own matrix; every segment
+// boundary is a multiple of BN, so a tile reads one weight and writes one output (plain EPI 0
+// epilogue with that segment's pointers).
 struct CeEpi {
   const int64_t* tgt;
   const float* lse;
@@ -200,6 +204,12 @@ struct CeEpi {
   u16* u_out;
   u16* zt;       // EPI 1: optional transposed copy of dz ([N][M] at row stride ldzt)
   int64_t ldzt;
+  // EPI 4: up to 3 column segments [seg_n0[s], seg_n0[s + 1]) of B / C, each its own weight and output
+  const u16* seg_b[3];
+  u16* seg_c[3];
+  int64_t seg_ldc[3];
+  int64_t seg_n0[3];
+  int nseg;
 };
 
 Q3_DEV void lse_merge(float& m, float& s, float m2, float s2) {
@@ -229,6 +239,13 @@ __global__ __launch_bounds__(WM * WN * 64) void gemm_nt_v4_kernel(const u16* __r
   int tm, tn;
   tile_coords(blockIdx.x, (M + BM - 1) / BM, (N + BN - 1) / BN, tm, tn);
   const int m0 = tm * BM, n0 = tn * BN;
+  if constexpr (EPI == 4) {  // this tile's weight and output, shifted so column n0 addresses them
+    int sg = 0;
+    while (sg + 1 < ce.nseg && n0 >= ce.seg_n0[sg + 1]) ++sg;
+    B = ce.seg_b[sg] - ce.seg_n0[sg] * ldb;
+    C = reinterpret_cast<typename O::storage*>(ce.seg_c[sg]) - ce.seg_n0[sg];
+    ldc = ce.seg_ldc[sg];
+  }
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int wm = wave / WN, wn = wave % WN;
   const int wave_u = __builtin_amdgcn_readfirstlane(wave);
@@ -431,7 +448,7 @@ __global__ __launch_bounds__(WM * WN * 64) void gemm_nt_v4_kernel(const u16* __r
     }
     return;
   }
-  if constexpr (EPI == 0 && EVEN && O::vec == 8) {
+  if constexpr ((EPI == 0 || EPI == 4) && EVEN && O::vec == 8) {
     if (!accumulate && vec_store == 2) {
       constexpr auto NC = std::integral_constant<int, TNW>{};
       __syncthreads();  // every wave is done with the operand ring
@@ -630,6 +647,24 @@ int launch_gate_up(const void* X, int64_t ldx, const void* Wg, const void* Wu, i
   return launch_v4<T, T, 256, 256, 4, 2, 2, true, 64, 3>(X, ldx, Wg, ldw, Y, ldo, M, 2 * N, K, 1.f, 0, s, e);
 }
 
+// Q/K/V-style GEMM: one A, up to 3 weights side by side as the B rows, one output per weight
+// (256 x 256 tiles of full tiles only).
+template <typename T>
+int launch_multi(const void* A, int64_t lda, int nseg, const void* const* Bs, int64_t ldb, void* const* Cs,
+                 const int64_t* Ns, const int64_t* ldcs, int64_t M, int64_t K, hipStream_t s) {
+  CeEpi e{};
+  int64_t n = 0;
+  for (int i = 0; i < nseg; ++i) {
+    e.seg_b[i] = (const u16*)Bs[i];
+    e.seg_c[i] = (u16*)Cs[i];
+    e.seg_ldc[i] = ldcs[i];
+    e.seg_n0[i] = n;
+    n += Ns[i];
+  }
+  e.nseg = nseg;
+  return launch_v4<T, T, 256, 256, 4, 2, 2, true, 64, 4>(A, lda, Bs[0], ldb, Cs[0], ldcs[0], M, n, K, 1.f, 0, s, e);
+}
+
 // ---------------------------------------------------------------- strided SIMT fallback
 // C[m,n] = alpha * sum_k A[m*sam + k*sak] * B[k*sbk + n*sbn] (+ C).  64x64 tile, 4x4 per thread.
 template <typename T, typename O>
@@ -804,6 +839,23 @@ int q3_gemm_gate_up_swiglu(int dtype, const void* x, int64_t ldx, const void* wg
              al16(wg) && al16(wu) && al16(g) && al16(u) && al16(y));
   if (dtype == Q3_BF16) return launch_gate_up<BF16>(x, ldx, wg, wu, ldw, g, u, y, ldo, M, N, K, stream);
   return launch_gate_up<F16>(x, ldx, wg, wu, ldw, g, u, y, ldo, M, N, K, stream);
+}
+
+int q3_gemm_nt_multi(int dtype, const void* A, int64_t lda, int nseg, const void* const* Bs, int64_t ldb,
+                     void* const* Cs, const int64_t* Ns, const int64_t* ldcs, int64_t M, int64_t K,
+                     hipStream_t stream) {
+  Q3_REQUIRE((dtype == Q3_BF16 || dtype == Q3_F16) && A && Bs && Cs && Ns && ldcs && nseg >= 1 && nseg <= 3);
+  Q3_REQUIRE(M > 0 && K > 0 && M % 256 == 0 && K % 64 == 0 && M < (1ll << 31) && K < (1ll << 31));
+  Q3_REQUIRE(lda % 8 == 0 && ldb % 8 == 0 && lda >= K && ldb >= K && al16(A));
+  int64_t n = 0;
+  for (int i = 0; i < nseg; ++i) {
+    Q3_REQUIRE(Bs[i] && Cs[i] && Ns[i] > 0 && Ns[i] % 256 == 0 && ldcs[i] >= Ns[i] && ldcs[i] % 8 == 0 &&
+               al16(Bs[i]) && al16(Cs[i]));
+    n += Ns[i];
+  }
+  Q3_REQUIRE(n < (1ll << 31) && (M / 256) * (n / 256) < (1ll << 31));
+  if (dtype == Q3_BF16) return launch_multi<BF16>(A, lda, nseg, Bs, ldb, Cs, Ns, ldcs, M, K, stream);
+  return launch_multi<F16>(A, lda, nseg, Bs, ldb, Cs, Ns, ldcs, M, K, stream);
 }
 
 int q3_gemm_strided(int in_dtype, int out_dtype, const void* A, int64_t sam, int64_t sak, const void* B, int64_t sbk,

@@ -10,6 +10,8 @@ contiguous; an operand that is K-major only as a transposed view is first re-lai
 ``q3_gemm_strided`` kernel.  ``optimized`` is accepted for signature compatibility; the tile
 plan is fixed for gfx950.
 """
+import ctypes
+
 import torch
 
 from .. import _hip as H
@@ -45,6 +47,24 @@ def gate_up_swiglu_into(x, wg, wu, g, u, y, m, n, k):
     K % 64 == 0; contiguous [M, K] x and [N, K] weights, contiguous [M, N] outputs)."""
     H.call("q3_gemm_gate_up_swiglu", H.code(x.dtype), x.data_ptr(), k, wg.data_ptr(), wu.data_ptr(), k,
            g.data_ptr(), u.data_ptr(), y.data_ptr(), n, m, n, k, H.stream())
+
+
+def gemm_nt_multi_into(a, weights, outs, m, k):
+    """outs[i][m, n_i] = a[m, k] . weights[i][n_i, k]^T for up to 3 weights in one matrix-core launch
+    (contiguous a / weights / outs; M % 256 == 0, each n_i % 256 == 0, K % 64 == 0)."""
+    n = len(weights)
+    bs = (ctypes.c_void_p * n)(*[w.data_ptr() for w in weights])
+    cs = (ctypes.c_void_p * n)(*[o.data_ptr() for o in outs])
+    ns = (ctypes.c_int64 * n)(*[w.shape[0] for w in weights])
+    lds = (ctypes.c_int64 * n)(*[o.stride(0) for o in outs])
+    H.call("q3_gemm_nt_multi", H.code(a.dtype), a.data_ptr(), k, n, bs, k, cs, ns, lds, m, k, H.stream())
+
+
+def gemm_multi_ok(x, m, k, weights):
+    """The one-launch path needs 16-bit data, full 256 x 256 tiles and a grid of at least 256 tiles."""
+    ntot = sum(w.shape[0] for w in weights)
+    return x.dtype in (torch.bfloat16, torch.float16) and len(weights) <= 3 and m % 256 == 0 and k % 64 == 0 and \
+        all(w.shape[0] % 256 == 0 for w in weights) and (m // 256) * (ntot // 256) >= 256
 
 
 def gate_up_fused_ok(x, m, n, k):
@@ -120,7 +140,15 @@ class _SharedInputProjections(torch.autograd.Function):
     @staticmethod
     def forward(ctx, x, *weights):
         flat = x.view(-1, x.shape[-1])
-        outs = [matmul(flat, w.t()).view(*x.shape[:-1], w.shape[0]) for w in weights]
+        m, k = flat.shape
+        if gemm_multi_ok(x, m, k, weights):
+            # one launch over the weights side by side (the narrow K / V projections alone would leave
+            # half of the CUs idle)
+            outs = [torch.empty((m, w.shape[0]), device=x.device, dtype=x.dtype) for w in weights]
+            gemm_nt_multi_into(flat, weights, outs, m, k)
+            outs = [o.view(*x.shape[:-1], o.shape[1]) for o in outs]
+        else:
+            outs = [matmul(flat, w.t()).view(*x.shape[:-1], w.shape[0]) for w in weights]
         ctx.save_for_backward(flat, *weights)
         ctx.shape = x.shape
         return tuple(outs)

@@ -150,3 +150,23 @@ def test_gate_up_swiglu_gemm(m, n, k, dtype):
     tol = 8e-3 if dtype == torch.bfloat16 else 1e-3
     assert max_rel(g[rows], eg) <= tol and max_rel(u[rows], eu) <= tol
     assert max_rel(y[rows], O.swiglu_reference(eg, eu, dtype=torch.float64)) <= 2 * tol
+
+
+@pytest.mark.parametrize("m,ns,k", [(256, (256,), 64), (512, (512, 256, 256), 128), (8192, (4096, 1024, 1024), 4096)])
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+def test_gemm_nt_multi(m, ns, k, dtype):
+    """One launch over up to 3 weights (the q/k/v projections): every output equals its own q3_gemm_nt
+    product bit for bit, and matches fp64 within one rounding."""
+    from qwen3_triton.kernels.linear import gemm_nt_multi_into
+    print(f"gemm_nt_multi {m}x{ns}x{k} {dtype}", flush=True)
+    gen = seeded(m + sum(ns) + k)
+    a = randn(m, k, gen=gen, dtype=dtype).cuda()
+    ws = [randn(n, k, gen=gen, dtype=dtype).cuda() for n in ns]
+    outs = [torch.empty(m, n, device="cuda", dtype=dtype) for n in ns]
+    gemm_nt_multi_into(a, ws, outs, m, k)
+    for w, o in zip(ws, outs):
+        single = torch.empty_like(o)
+        gemm_nt_into(a, k, w, k, single, m, w.shape[0], k)
+        assert torch.equal(o, single)
+        if m <= 512:
+            assert max_rel(o, ref(a.cpu(), w.cpu().t())) < 8e-3
