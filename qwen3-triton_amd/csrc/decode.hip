@@ -168,6 +168,170 @@ __global__ __launch_bounds__(NW * 64) void dlinear_kernel(DecArgs a) {
   }
 }
 
+// Persistent variant for K = NW * KB * 128 (Qwen3-8B: K = 4096) and modes 0 / 2: the input rows (the
+// RMSNorm-weighted rows when NORM) are read once per workgroup and stay in registers, and "units" of
+// 16 weight rows (mode 2: a gate unit, then the up unit of the same rows) stream through a two-deep
+// register pipeline -- the loads of the next unit are in flight while the current unit's MFMAs and
+// its cross-wave fold run.  The sum of squares of the input rows is formed once per workgroup, while
+// the first unit's weights are already in flight.  Lane (r, kq) of wave w holds k = (w + NW i) * 128
+// + 32 c + 8 kq, i < KB, c < 4, of token row r (A operand) and weight row n0 + r (B operand); the
+// waves' partial 16 x 16 tiles fold in LDS in wave order (fixed order: deterministic).
+template <typename T, int MODE, bool NORM, int NW, int KB>
+__global__ __launch_bounds__(NW * 64) void dlinear_stream_kernel(DecArgs a, int units) {
+  static_assert(MODE == 0 || MODE == 2, "projection or SwiGLU");
+  __shared__ f32x4 red[2][NW][64];
+  __shared__ float red_ss[NW][64];
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int r = lane & 15, kq = lane >> 4;
+  const int M = a.M, K = a.K;
+  const bool xrow = r < M;
+  auto unit_src = [&](int u, const u16*& w, int& n0, int& nrows) {
+    if constexpr (MODE == 2) {
+      w = a.seg[u & 1].w;
+      n0 = (u >> 1) * 16;
+      nrows = a.seg[0].n;
+    } else {
+      int s = 0, t = u;
+      while (s + 1 < a.nseg && t >= a.seg[s].tiles) t -= a.seg[s++].tiles;
+      w = a.seg[s].w;
+      n0 = t * 16;
+      nrows = a.seg[s].n;
+    }
+  };
+  constexpr int LPU = KB * 4;  // weight loads per unit and lane
+  i32x4 xv[KB][4];
+  float inv_m[4] = {1.f, 1.f, 1.f, 1.f};
+  i32x4 wb[2][KB][4];
+  auto issue = [&](int u, auto buf_c) {
+    constexpr int B = decltype(buf_c)::value;
+    const u16* w;
+    int n0, nrows;
+    unit_src(u, w, n0, nrows);
+    const u16* row = w + (int64_t)min(n0 + r, nrows - 1) * K + 8 * kq;
+#pragma unroll
+    for (int i = 0; i < KB; ++i)
+#pragma unroll
+      for (int c = 0; c < 4; ++c) wb[B][i][c] = *reinterpret_cast<const i32x4*>(row + (wave + NW * i) * 128 + 32 * c);
+  };
+  float gate[4] = {0.f, 0.f, 0.f, 0.f};
+  // wave 0: fold the waves' partial tiles in order, then the epilogue (lane holds D[m = 4 kq + e][n = r])
+  auto finish = [&](int u, int par) {
+    f32x4 t = red[par][0][lane];
+#pragma unroll
+    for (int w = 1; w < NW; ++w) t += red[par][w][lane];
+    float v[4];
+#pragma unroll
+    for (int e = 0; e < 4; ++e) v[e] = t[e] * inv_m[e];
+    if constexpr (MODE == 2) {
+      if ((u & 1) == 0) {  // gate unit: kept for the up unit that follows
+#pragma unroll
+        for (int e = 0; e < 4; ++e) gate[e] = v[e];
+        return;
+      }
+    }
+    int s = 0, tt = u;
+    if constexpr (MODE == 2) {
+      tt = u >> 1;
+    } else {
+      while (s + 1 < a.nseg && tt >= a.seg[s].tiles) tt -= a.seg[s++].tiles;
+    }
+    const DecSeg sg = a.seg[s];
+    const int n = tt * 16 + r;
+    if (n >= sg.n) return;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      const int m = 4 * kq + e;
+      if (m >= M) continue;
+      float o = to_f32<T>(from_f32<T>(v[e]));
+      if constexpr (MODE == 2) {
+        const float g = to_f32<T>(from_f32<T>(gate[e]));
+        o = g * q3_sigmoid(g) * o;
+      }
+      sg.y[m * sg.ldy + n] = from_f32<T>(o);
+    }
+  };
+  auto compute = [&](auto buf_c) {
+    constexpr int B = decltype(buf_c)::value;
+    f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int i = 0; i < KB; ++i)
+#pragma unroll
+      for (int c = 0; c < 4; ++c)
+        acc = mfma_16x16x32<T>(__builtin_bit_cast(bf16x8_t, xv[i][c]), __builtin_bit_cast(bf16x8_t, wb[B][i][c]), acc);
+    return acc;
+  };
+  // this workgroup's units: blockIdx.x, + gridDim.x, ... (mode 2: the (gate, up) unit pairs of those tiles)
+  const int step = MODE == 2 ? 2 * gridDim.x : gridDim.x;
+  int u = MODE == 2 ? 2 * blockIdx.x : blockIdx.x;
+  auto next_u = [&](int v) { return MODE == 2 ? ((v & 1) ? v - 1 + step : v + 1) : v + step; };
+  if (u >= units) return;  // uniform over the workgroup
+  i32x4 nvv[NORM ? KB : 1][4];
+#pragma unroll
+  for (int i = 0; i < KB; ++i)
+#pragma unroll
+    for (int c = 0; c < 4; ++c) {
+      const int k = (wave + NW * i) * 128 + 32 * c + 8 * kq;
+      xv[i][c] = *reinterpret_cast<const i32x4*>(a.x + (int64_t)(xrow ? r : 0) * a.ldx + k);
+      if constexpr (NORM) nvv[i][c] = *reinterpret_cast<const i32x4*>(a.nw + k);
+    }
+  issue(u, std::integral_constant<int, 0>{});
+#pragma unroll
+  for (int i = 0; i < KB; ++i)
+#pragma unroll
+    for (int c = 0; c < 4; ++c)
+      if (!xrow) xv[i][c] = i32x4{0, 0, 0, 0};
+  if constexpr (NORM) {
+    // the input rows and norm weight landed (older than the first unit's weight loads)
+    __builtin_amdgcn_s_waitcnt((LPU & 15) | ((LPU >> 4) << 14) | (7 << 4) | (0xF << 8));
+    float ssq = 0.f;
+#pragma unroll
+    for (int i = 0; i < KB; ++i)
+#pragma unroll
+      for (int c = 0; c < 4; ++c)
+#pragma unroll
+        for (int w = 0; w < 4; ++w) {
+          const uint32_t xx = (uint32_t)xv[i][c][w], ww = (uint32_t)nvv[i][c][w];
+          const float x0 = to_f32<T>((u16)(xx & 0xffffu)), x1 = to_f32<T>((u16)(xx >> 16));
+          ssq += x0 * x0 + x1 * x1;
+          xv[i][c][w] = (int)pack2<T>(x0 * to_f32<T>((u16)(ww & 0xffffu)), x1 * to_f32<T>((u16)(ww >> 16)));
+        }
+    ssq += __shfl_xor(ssq, 16, 64);  // row r over the 4 quarters, then over the waves
+    ssq += __shfl_xor(ssq, 32, 64);
+    red_ss[wave][lane] = ssq;
+    __syncthreads();
+    float t = 0.f;
+#pragma unroll
+    for (int w = 0; w < NW; ++w) t += red_ss[w][lane];
+    const float inv_r = rsqrtf(t * (1.f / (float)K) + a.eps);
+#pragma unroll
+    for (int e = 0; e < 4; ++e) inv_m[e] = __shfl(inv_r, 4 * kq + e, 64);
+  }
+  // Two units per trip (register buffers 0 and 1); the LDS fold buffer alternates with the unit, so one
+  // barrier per unit suffices (wave 0 has read a buffer before any wave passes the next barrier).
+  int it = 0;
+  auto one = [&](auto cur_c, int cu, bool more) {
+    constexpr int CUR = decltype(cur_c)::value;
+    __builtin_amdgcn_sched_barrier(0);
+    if (more) issue(next_u(cu), std::integral_constant<int, CUR ^ 1>{});
+    __builtin_amdgcn_sched_barrier(0);
+    if (more) __builtin_amdgcn_s_waitcnt((LPU & 15) | ((LPU >> 4) << 14) | (7 << 4) | (0xF << 8));
+    else __builtin_amdgcn_s_waitcnt((7 << 4) | (0xF << 8));
+    red[it & 1][wave][lane] = compute(cur_c);
+    __syncthreads();
+    if (wave == 0) finish(cu, it & 1);
+    ++it;
+  };
+  while (true) {
+    const int u1 = next_u(u);
+    one(std::integral_constant<int, 0>{}, u, u1 < units);
+    if (u1 >= units) break;
+    const int u2 = next_u(u1);
+    one(std::integral_constant<int, 1>{}, u1, u2 < units);
+    if (u2 >= units) break;
+    u = u2;
+  }
+}
+
 // Waves per workgroup x k blocks in flight per wave, per mode: measured on MI355X inside the captured
 // Qwen3-8B decode step (B1 and B8) over {2, 4, 8, 16} waves x {1, 2, 4} blocks, each projection
 // kind separately: the normed Q/K/V (and LM head) 8 x 2; O and down (+ residual) 8 x 1; gate/up +
@@ -179,8 +343,32 @@ int dlinear_launch(const DecArgs& a, int tiles, hipStream_t s) {
   return (int)hipGetLastError();
 }
 
+// Units per workgroup of the streaming kernel, by the number of 16-row tiles (pairs in mode 2); measured
+// inside a captured 36-layer step on MI355X: 2 for Q/K/V (384 tiles), 3 for gate/up (768 pairs), 8 for
+// the LM head (9496 tiles); one unit per workgroup up to 256 tiles.
+inline int stream_units_per_wg(int tiles) { return tiles <= 256 ? 1 : tiles <= 512 ? 2 : tiles <= 1024 ? 3 : 8; }
+
+template <typename T, int MODE, bool NORM, int KB>
+int dlinear_stream_launch(const DecArgs& a, int tiles, hipStream_t s) {
+  const int upw = stream_units_per_wg(tiles);
+  const int units = MODE == 2 ? 2 * tiles : tiles;
+  dlinear_stream_kernel<T, MODE, NORM, 8, KB><<<(unsigned)((tiles + upw - 1) / upw), 512, 0, s>>>(a, units);
+  return (int)hipGetLastError();
+}
+
+template <typename T, int MODE, bool NORM>
+int dlinear_stream_k(const DecArgs& a, int tiles, hipStream_t s) {
+  if (a.K == 1024) return dlinear_stream_launch<T, MODE, NORM, 1>(a, tiles, s);
+  if (a.K == 2048) return dlinear_stream_launch<T, MODE, NORM, 2>(a, tiles, s);
+  return dlinear_stream_launch<T, MODE, NORM, 4>(a, tiles, s);
+}
+
 template <typename T>
 int dlinear_t(const DecArgs& a, int tiles, int mode, bool norm, hipStream_t s) {
+  if ((a.K == 1024 || a.K == 2048 || a.K == 4096) && mode != 1 && a.ldx % 8 == 0) {
+    if (mode == 0) return norm ? dlinear_stream_k<T, 0, true>(a, tiles, s) : dlinear_stream_k<T, 0, false>(a, tiles, s);
+    return norm ? dlinear_stream_k<T, 2, true>(a, tiles, s) : dlinear_stream_k<T, 2, false>(a, tiles, s);
+  }
   if (mode == 0) return norm ? dlinear_launch<T, 0, true>(a, tiles, s) : dlinear_launch<T, 0, false>(a, tiles, s);
   if (mode == 1) return norm ? dlinear_launch<T, 1, true>(a, tiles, s) : dlinear_launch<T, 1, false>(a, tiles, s);
   return norm ? dlinear_launch<T, 2, true>(a, tiles, s) : dlinear_launch<T, 2, false>(a, tiles, s);
