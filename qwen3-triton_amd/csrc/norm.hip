@@ -188,13 +188,14 @@ __global__ __launch_bounds__(kBlock) void rmsnorm_bwd_kernel(const typename T::s
 
 // Column sums of an fp32 [R][h] partial matrix in one launch: a workgroup owns L * V columns
 // (L lanes of V consecutive columns) and 256 / L row groups; row group g sums rows g, g + 256 / L,
-// ... in order, then the groups fold through LDS as a fixed binary tree.  Same (R, h) -> same
-// summation order -> bitwise reproducible results.
+// ... in order, then the groups fold by a lane butterfly inside each wave and through LDS across the
+// waves.  Same (R, h) -> same summation order -> bitwise reproducible results.
 template <typename O, int L, int V>
 __global__ __launch_bounds__(kBlock) void colsum_kernel(const float* __restrict__ in,
                                                         typename O::storage* __restrict__ out, int rows, int h) {
   constexpr int RG = kBlock / L, W = L * V;
-  __shared__ float red[RG][W];
+  static_assert(L <= 64 && 64 % L == 0, "row groups of one column set spread over every wave");
+  __shared__ float red[kBlock / 64][W];
   const int lc = threadIdx.x % L, g = threadIdx.x / L;
   const int c0 = (blockIdx.x * L + lc) * V;
   const int cc = c0 < h ? c0 : 0;
@@ -222,20 +223,25 @@ __global__ __launch_bounds__(kBlock) void colsum_kernel(const float* __restrict_
         for (int e = 0; e < V; ++e) s[e] += v[i][e];
       }
   }
+  // the row groups of a wave (lanes L apart) by a lane butterfly, then the 4 waves in order
 #pragma unroll
-  for (int e = 0; e < V; ++e) red[g][lc * V + e] = s[e];
-  __syncthreads();
+  for (int o = L; o < 64; o <<= 1)
 #pragma unroll
-  for (int half = RG / 2; half >= 1; half >>= 1) {
-    if (g < half) {
+    for (int e = 0; e < V; ++e) s[e] += __shfl_xor(s[e], o, 64);
+  const int wi = threadIdx.x >> 6;
+  if ((threadIdx.x & 63) < L) {
 #pragma unroll
-      for (int e = 0; e < V; ++e) red[g][lc * V + e] += red[g + half][lc * V + e];
-    }
-    __syncthreads();
+    for (int e = 0; e < V; ++e) red[wi][lc * V + e] = s[e];
   }
-  if (g == 0 && c0 < h) {
+  __syncthreads();
+  if (threadIdx.x < L && c0 < h) {
 #pragma unroll
-    for (int e = 0; e < V; ++e) out[c0 + e] = from_f32<O>(red[0][lc * V + e]);
+    for (int e = 0; e < V; ++e) {
+      float sum = red[0][lc * V + e];
+#pragma unroll
+      for (int w = 1; w < kBlock / 64; ++w) sum += red[w][lc * V + e];
+      out[c0 + e] = from_f32<O>(sum);
+    }
   }
 }
 
@@ -395,7 +401,7 @@ __global__ __launch_bounds__(kBlock) void norm_rope_bwd_kernel(const typename T:
                                                                float* __restrict__ partial, int64_t rows, int heads,
                                                                float eps) {
   constexpr int V = T::vec, D = TPR * V, RPB = kBlock / TPR;
-  __shared__ float fold[D];
+  __shared__ float fold[kBlock / 64][D];
   const int t = threadIdx.x % TPR, g = threadIdx.x / TPR;
   const float sign = (t < TPR / 2) ? 1.f : -1.f;
   const Vec<T> wv = load_vec<T>(w + t * V);
@@ -443,14 +449,24 @@ __global__ __launch_bounds__(kBlock) void norm_rope_bwd_kernel(const typename T:
       if (valid) store_vec<T>(dx + row * D + t * V, o);
     }
   }
-  for (int gi = 0; gi < RPB; ++gi) {
-    if (g == gi) {
+  // Fold the RPB row groups: the 64 / TPR groups of a wave by a lane butterfly, then the waves through
+  // LDS in wave order (one barrier; fixed order, so the partial rows are reproducible).
 #pragma unroll
-      for (int e = 0; e < V; ++e) fold[t * V + e] = (gi == 0) ? acc[e] : fold[t * V + e] + acc[e];
-    }
-    __syncthreads();
+  for (int o = TPR; o < 64; o <<= 1)
+#pragma unroll
+    for (int e = 0; e < V; ++e) acc[e] += __shfl_xor(acc[e], o, 64);
+  const int wi = threadIdx.x >> 6;
+  if ((threadIdx.x & 63) < TPR) {
+#pragma unroll
+    for (int e = 0; e < V; ++e) fold[wi][t * V + e] = acc[e];
   }
-  for (int c = threadIdx.x; c < D; c += kBlock) partial[(int64_t)blockIdx.x * D + c] = fold[c];
+  __syncthreads();
+  for (int c = threadIdx.x; c < D; c += kBlock) {
+    float sum = fold[0][c];
+#pragma unroll
+    for (int w = 1; w < kBlock / 64; ++w) sum += fold[w][c];
+    partial[(int64_t)blockIdx.x * D + c] = sum;
+  }
 }
 
 // ---------------------------------------------------------------- host-side planning
