@@ -151,6 +151,19 @@ int q3_gemm_nt(int in_dtype, int out_dtype, const void* A, int64_t lda, const vo
 int q3_gemm_gate_up_swiglu(int dtype, const void* x, int64_t ldx, const void* wg, const void* wu, int64_t ldw,
                            void* g, void* u, void* y, int64_t ldo, int64_t M, int64_t N, int64_t K,
                            hipStream_t stream);
+/* Down-projection input gradient with the SwiGLU backward in its epilogue: dY = dy wt^T for
+ * dy [M, K] and wt [N, K] (the transposed down weight: K-contiguous rows), rounded to dtype as a
+ * standalone GEMM output, then dg = dY u s (1 + g (1 - s)), du = dY g s with s = sigmoid(g) for
+ * the saved SwiGLU inputs g, u [M, N] (row stride ldgu) -- the q3_swiglu_bwd formula, so the result
+ * is bit-identical to q3_gemm_nt + q3_swiglu_bwd.  Stores dg, du [M, N] at row stride ldd and, when
+ * dgt / dut are non-null, their transposes [N, M] at row stride lddt (the operands of the gate/up
+ * weight-gradient GEMM), so dY never reaches memory and no separate transpose pass runs.
+ * M % 256 == 0, N % 256 == 0, K % 64 == 0, strides % 8 == 0, pointers 16-byte aligned.
+ * Replaces: kernels/mlp_precision.py:36-63 (_GateUp.backward: the down-projection dX GEMM of
+ * kernels/linear.py:92-100 followed by the SwiGLU backward of kernels/activation.py:22-36). */
+int q3_gemm_swiglu_bwd(int dtype, const void* dy, int64_t lddy, const void* wt, int64_t ldw, const void* g,
+                       const void* u, int64_t ldgu, void* dg, void* du, int64_t ldd, void* dgt, void* dut,
+                       int64_t lddt, int64_t M, int64_t N, int64_t K, hipStream_t stream);
 /* Several projections of one input in one matrix-core launch: for A [M, K] and nseg (1..3) weights
  * Bs[s] [Ns[s], K] (common row stride ldb), writes Cs[s] = A Bs[s]^T ([M, Ns[s]] at row stride
  * ldcs[s]), fp32 accumulation, one rounding, bit-identical to nseg separate q3_gemm_nt calls with

@@ -189,6 +189,11 @@ template <int CPR> Q3_DEV int gemm_swz(int r) {
 // projections of one input) and each output column segment goes to its own matrix; every segment
 // boundary is a multiple of BN, so a tile reads one weight and writes one output (plain EPI 0
 // epilogue with that segment's pointers).
+// SwiGLU-backward epilogue (EPI 5): the tile is dY = A B^T, the gradient of the SwiGLU output
+// y = silu(g) * u (dOut W_down with B = W_down^T); it is rounded to the storage type as a standalone
+// GEMM output would be, and the kernel stores dg = dY u s (1 + g (1 - s)) and du = dY g s (s = sigmoid(g),
+// the formula of the SwiGLU backward kernel, so results are bit-identical to GEMM + that kernel),
+// plus, when dgt is set, the transposes of dg and du -- the operands the weight-gradient GEMM needs.
 struct CeEpi {
   const int64_t* tgt;
   const float* lse;
@@ -210,6 +215,17 @@ struct CeEpi {
   int64_t seg_ldc[3];
   int64_t seg_n0[3];
   int nseg;
+  // EPI 5: SwiGLU inputs g / u [M, N] (row stride ldgu), gradients dg / du [M, N] (row stride lddgu) and
+  // optionally their transposes dgt / dut [N, M] (row stride lddt)
+  const u16* gin;
+  const u16* uin;
+  int64_t ldgu;
+  u16* dgo;
+  u16* duo;
+  int64_t lddgu;
+  u16* dgt;
+  u16* dut;
+  int64_t lddt;
 };
 
 Q3_DEV void lse_merge(float& m, float& s, float m2, float s2) {
@@ -448,6 +464,97 @@ __global__ __launch_bounds__(WM * WN * 64) void gemm_nt_v4_kernel(const u16* __r
     }
     return;
   }
+  if constexpr (EPI == 5) {
+    static_assert(EVEN && O::vec == 8 && TMW == 64 && TNW == 128, "full 256 x 256 tiles, 64 x 128 per wave");
+    constexpr int CH = TNW / 8, RPI = 64 / CH, NQ = TMW / RPI;  // 16 chunks per row, 4 rows per pass, 16 passes
+    __syncthreads();  // every wave is done with the operand ring
+    // dY rounded to the storage type, staged row-major in the wave's block
+#pragma unroll
+    for (int i = 0; i < FM; ++i)
+#pragma unroll
+      for (int j = 0; j < FN; ++j)
+        stage(std::integral_constant<int, TNW>{}, i, j, pack2<O>(acc[i][j][0], acc[i][j][1]),
+              pack2<O>(acc[i][j][2], acc[i][j][3]));
+    __builtin_amdgcn_s_waitcnt((15) | (7 << 4) | (0 << 8) | (3 << 14));
+    __builtin_amdgcn_wave_barrier();
+    const int64_t row0 = m0 + wm * TMW, col0 = n0 + wn * TNW;
+    const int c = lane % CH;
+    i32x4 dgp[NQ], dup[NQ];
+    // two halves of the rows: g / u loads of a half all in flight before the first use
+#pragma unroll
+    for (int hh = 0; hh < 2; ++hh) {
+      i32x4 gv[NQ / 2], uv[NQ / 2], dv[NQ / 2];
+#pragma unroll
+      for (int q = 0; q < NQ / 2; ++q) {
+        const int r = (hh * (NQ / 2) + q) * RPI + lane / CH;
+        gv[q] = *reinterpret_cast<const i32x4*>(ce.gin + (row0 + r) * ce.ldgu + col0 + c * 8);
+        uv[q] = *reinterpret_cast<const i32x4*>(ce.uin + (row0 + r) * ce.ldgu + col0 + c * 8);
+        dv[q] = *reinterpret_cast<const i32x4*>(wl + r * (TNW * 2) + ((c ^ (r & 15)) << 4));
+      }
+#pragma unroll
+      for (int q = 0; q < NQ / 2; ++q) {
+        const int r = (hh * (NQ / 2) + q) * RPI + lane / CH;
+        const Vec<O> gf = unpack_vec<O>(gv[q]), uf = unpack_vec<O>(uv[q]), df = unpack_vec<O>(dv[q]);
+        Vec<O> og, ou;
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+          const float sg = q3_sigmoid(gf.v[e]);
+          og.v[e] = df.v[e] * uf.v[e] * sg * (1.f + gf.v[e] * (1.f - sg));
+          ou.v[e] = df.v[e] * gf.v[e] * sg;
+        }
+        i32x4 pg, pu;
+#pragma unroll
+        for (int w = 0; w < 4; ++w) {
+          pg[w] = (int)pack2<O>(og.v[2 * w], og.v[2 * w + 1]);
+          pu[w] = (int)pack2<O>(ou.v[2 * w], ou.v[2 * w + 1]);
+        }
+        *reinterpret_cast<i32x4*>(ce.dgo + (row0 + r) * ce.lddgu + col0 + c * 8) = pg;
+        *reinterpret_cast<i32x4*>(ce.duo + (row0 + r) * ce.lddgu + col0 + c * 8) = pu;
+        dgp[hh * (NQ / 2) + q] = pg;
+        dup[hh * (NQ / 2) + q] = pu;
+      }
+    }
+    if (ce.dgt) {
+      // Transposed copies through the wave's block: the [64 rows][128 columns] gradient tile is written
+      // row-major (16-byte stores, chunks XOR-swizzled by row), then read back transposed with the gfx950
+      // LDS transpose read: in each 16-lane group, lane a addresses 4 columns of row R0 + a / 4, so lane j
+      // receives column T0 + j of rows R0 .. R0 + 3 (a second read gives R0 + 4 .. R0 + 7), i.e. 16 bytes
+      // of one row of the transposed output.  Four groups take consecutive 8-row blocks of one column
+      // block, so every column's 64 transposed bytes are written by four lanes of one store.
+      auto tstore = [&](const i32x4 (&p)[NQ], u16* dst) {
+        __builtin_amdgcn_s_waitcnt((15) | (7 << 4) | (0 << 8) | (3 << 14));  // earlier reads of the block done
+        __builtin_amdgcn_wave_barrier();
+#pragma unroll
+        for (int q = 0; q < NQ; ++q) {
+          const int r = q * RPI + lane / CH;
+          *reinterpret_cast<i32x4*>(wl + r * (TNW * 2) + ((c ^ (r & 15)) << 4)) = p[q];
+        }
+        __builtin_amdgcn_s_waitcnt((15) | (7 << 4) | (0 << 8) | (3 << 14));
+        __builtin_amdgcn_wave_barrier();
+        const int j = lane & 15, grp = lane >> 4;
+#pragma unroll
+        for (int pi = 0; pi < (TNW / 16) * (TMW / 32); ++pi) {
+          const int t0 = 16 * (pi % (TNW / 16)), r0 = 32 * (pi / (TNW / 16)) + 8 * grp;
+          i32x4 v;
+#pragma unroll
+          for (int hh = 0; hh < 2; ++hh) {
+            const int row = r0 + 4 * hh + (j >> 2);
+            const int cb = 2 * t0 + 8 * (j & 3);  // byte offset of the 4 columns in the row
+            const char* pa = wl + row * (TNW * 2) + ((((cb >> 4) ^ (row & 15))) << 4) + (cb & 15);
+            typedef short v4s_t __attribute__((ext_vector_type(4)));
+            const i32x2 t = __builtin_bit_cast(
+                i32x2, __builtin_amdgcn_ds_read_tr16_b64_v4i16((__attribute__((address_space(3))) v4s_t*)pa));
+            v[2 * hh] = t[0];
+            v[2 * hh + 1] = t[1];
+          }
+          *reinterpret_cast<i32x4*>(dst + (col0 + t0 + j) * ce.lddt + row0 + r0) = v;
+        }
+      };
+      tstore(dgp, ce.dgt);
+      tstore(dup, ce.dut);
+    }
+    return;
+  }
   if constexpr ((EPI == 0 || EPI == 4) && EVEN && O::vec == 8) {
     if (!accumulate && vec_store == 2) {
       constexpr auto NC = std::integral_constant<int, TNW>{};
@@ -647,6 +754,13 @@ int launch_gate_up(const void* X, int64_t ldx, const void* Wg, const void* Wu, i
   return launch_v4<T, T, 256, 256, 4, 2, 2, true, 64, 3>(X, ldx, Wg, ldw, Y, ldo, M, 2 * N, K, 1.f, 0, s, e);
 }
 
+// dY = A B^T with the SwiGLU-backward epilogue (full 256 x 256 tiles only).
+template <typename T>
+int launch_swiglu_bwd(const void* A, int64_t lda, const void* B, int64_t ldb, int64_t M, int64_t N, int64_t K,
+                      const CeEpi& e, hipStream_t s) {
+  return launch_v4<T, T, 256, 256, 4, 2, 2, true, 64, 5>(A, lda, B, ldb, e.dgo, e.lddgu, M, N, K, 1.f, 0, s, e);
+}
+
 // Q/K/V-style GEMM: one A, up to 3 weights side by side as the B rows, one output per weight
 // (256 x 256 tiles of full tiles only).
 template <typename T>
@@ -839,6 +953,29 @@ int q3_gemm_gate_up_swiglu(int dtype, const void* x, int64_t ldx, const void* wg
              al16(wg) && al16(wu) && al16(g) && al16(u) && al16(y));
   if (dtype == Q3_BF16) return launch_gate_up<BF16>(x, ldx, wg, wu, ldw, g, u, y, ldo, M, N, K, stream);
   return launch_gate_up<F16>(x, ldx, wg, wu, ldw, g, u, y, ldo, M, N, K, stream);
+}
+
+int q3_gemm_swiglu_bwd(int dtype, const void* dy, int64_t lddy, const void* wt, int64_t ldw, const void* g,
+                       const void* u, int64_t ldgu, void* dg, void* du, int64_t ldd, void* dgt, void* dut,
+                       int64_t lddt, int64_t M, int64_t N, int64_t K, hipStream_t stream) {
+  Q3_REQUIRE((dtype == Q3_BF16 || dtype == Q3_F16) && dy && wt && g && u && dg && du && (!dgt == !dut));
+  Q3_REQUIRE(M > 0 && N > 0 && K > 0 && M % 256 == 0 && N % 256 == 0 && K % 64 == 0 && M < (1ll << 31) &&
+             N < (1ll << 31) && K < (1ll << 31) && (M / 256) * (N / 256) < (1ll << 31));
+  Q3_REQUIRE(lddy % 8 == 0 && ldw % 8 == 0 && ldgu % 8 == 0 && ldd % 8 == 0 && lddy >= K && ldw >= K &&
+             ldgu >= N && ldd >= N && al16(dy) && al16(wt) && al16(g) && al16(u) && al16(dg) && al16(du));
+  Q3_REQUIRE(!dgt || (lddt % 8 == 0 && lddt >= M && al16(dgt) && al16(dut)));
+  CeEpi e{};
+  e.gin = (const u16*)g;
+  e.uin = (const u16*)u;
+  e.ldgu = ldgu;
+  e.dgo = (u16*)dg;
+  e.duo = (u16*)du;
+  e.lddgu = ldd;
+  e.dgt = (u16*)dgt;
+  e.dut = (u16*)dut;
+  e.lddt = lddt;
+  if (dtype == Q3_BF16) return launch_swiglu_bwd<BF16>(dy, lddy, wt, ldw, M, N, K, e, stream);
+  return launch_swiglu_bwd<F16>(dy, lddy, wt, ldw, M, N, K, e, stream);
 }
 
 int q3_gemm_nt_multi(int dtype, const void* A, int64_t lda, int nseg, const void* const* Bs, int64_t ldb,

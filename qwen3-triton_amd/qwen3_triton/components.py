@@ -3,7 +3,8 @@
 ``HFOrderNorm`` / ``Attention`` / ``MLP`` / ``DecoderLayer`` / ``Backbone`` keep the reference's
 module structure and option switches (the q/k/v projections keep their own parameters and run
 through one shared-input projection op whose backward is a single dX GEMM): ``norm_rope_fusion`` selects the fused per-head RMSNorm +
-RoPE kernel, ``mlp_fusion`` the gate/up + SwiGLU op.  The reference's SM86 rounding-order options
+RoPE kernel, ``mlp_fusion`` the fused gate/up + SwiGLU + down block (``mlp_block``: SwiGLU backward in
+the down projection's input-gradient GEMM epilogue).  The reference's SM86 rounding-order options
 (``precision_options``) are accepted and select nothing on gfx950.
 """
 import torch
@@ -13,7 +14,7 @@ from .kernels.activation import swiglu
 from .kernels.attention import causal_attention_bshd
 from .kernels.linear import shared_input_projections
 from .kernels.math_precision import norm_rope, rms_norm
-from .kernels.mlp_precision import gate_up_swiglu
+from .kernels.mlp_precision import mlp_block
 from .kernels.rotary import apply_rotary
 
 
@@ -52,7 +53,8 @@ class MLP(TritonMLP):
     def forward(self, x):
         opts = self.gate_proj.options
         if getattr(opts, 'mlp_fusion', False):
-            y = gate_up_swiglu(x, self.gate_proj.weight, self.up_proj.weight, optimized=opts.linear_optimized)
+            return mlp_block(x, self.gate_proj.weight, self.up_proj.weight, self.down_proj.weight,
+                             optimized=opts.linear_optimized)
         else:
             y = swiglu(self.gate_proj(x), self.up_proj(x))
         return self.down_proj(y)

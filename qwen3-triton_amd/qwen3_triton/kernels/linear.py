@@ -49,6 +49,21 @@ def gate_up_swiglu_into(x, wg, wu, g, u, y, m, n, k):
            g.data_ptr(), u.data_ptr(), y.data_ptr(), n, m, n, k, H.stream())
 
 
+def swiglu_bwd_gemm_into(dy, wt, g, u, dg, du, dgt, dut, m, n, k):
+    """dg, du (and their transposes dgt, dut when given) of y = silu(g) * u for the upstream gradient
+    dY = dy wt^T, computed in one matrix-core GEMM whose epilogue runs the SwiGLU backward
+    (dy [m, k], wt [n, k]; g, u, dg, du [m, n] views at a common row stride; M % 256 == 0,
+    N % 256 == 0, K % 64 == 0)."""
+    H.call("q3_gemm_swiglu_bwd", H.code(dy.dtype), dy.data_ptr(), dy.stride(0), wt.data_ptr(), wt.stride(0),
+           g.data_ptr(), u.data_ptr(), g.stride(0), dg.data_ptr(), du.data_ptr(), dg.stride(0),
+           0 if dgt is None else dgt.data_ptr(), 0 if dut is None else dut.data_ptr(),
+           0 if dgt is None else dgt.stride(0), m, n, k, H.stream())
+
+
+def swiglu_bwd_gemm_ok(dtype, m, n, k):
+    return dtype in (torch.bfloat16, torch.float16) and m % 256 == 0 and n % 256 == 0 and k % 64 == 0
+
+
 def gemm_nt_multi_into(a, weights, outs, m, k):
     """outs[i][m, n_i] = a[m, k] . weights[i][n_i, k]^T for up to 3 weights in one matrix-core launch
     (contiguous a / weights / outs; M % 256 == 0, each n_i % 256 == 0, K % 64 == 0)."""

@@ -11,7 +11,8 @@ buffer, so dX is a single GEMM over K = 2N and both weight gradients come from o
 import torch
 
 from . import _ops
-from .linear import gate_up_fused_ok, gate_up_swiglu_into, gemm_nt_into, matmul, matmul_into
+from .linear import (gate_up_fused_ok, gate_up_swiglu_into, gemm_nt_into, linear, matmul, matmul_into,
+                     swiglu_bwd_gemm_into, swiglu_bwd_gemm_ok)
 
 
 class _GateUp(torch.autograd.Function):
@@ -72,3 +73,70 @@ class _GateUp(torch.autograd.Function):
 def gate_up_swiglu(x, gate_weight, up_weight, *, optimized=False):
     """``kernels/mlp_precision.py:65``."""
     return _GateUp.apply(x, gate_weight, up_weight, optimized)
+
+
+def _gate_up_forward(flat, wg, wu, m, n, k):
+    if gate_up_fused_ok(flat, m, n, k):
+        g, u, y = (torch.empty((m, n), device=flat.device, dtype=flat.dtype) for _ in range(3))
+        gate_up_swiglu_into(flat, wg, wu, g, u, y, m, n, k)
+        return g, u, y
+    g = matmul(flat, wg.t())
+    u = matmul(flat, wu.t())
+    return g, u, _ops.swiglu_fwd(g, u)
+
+
+class _MLPBlock(torch.autograd.Function):
+    """out = (silu(X Wg^T) * (X Wu^T)) Wd^T as one op, so the backward can run the SwiGLU backward in
+    the epilogue of the down projection's input-gradient GEMM: dY never reaches memory, and the same
+    epilogue writes [dG | dU] row-major (the gate/up dX GEMM operand) and transposed (the gate/up
+    weight-gradient GEMM operand), replacing the SwiGLU backward kernel and one transpose pass.
+    Every GEMM and rounding point is the one of ``gate_up_swiglu`` followed by ``linear``."""
+
+    @staticmethod
+    def forward(ctx, x, wg, wu, wd):
+        m, k, n = x.numel() // x.shape[-1], x.shape[-1], wg.shape[0]
+        flat = x.view(m, k)
+        g, u, y = _gate_up_forward(flat, wg, wu, m, n, k)
+        out = torch.empty((m, wd.shape[0]), device=x.device, dtype=x.dtype)
+        gemm_nt_into(y, n, wd, n, out, m, wd.shape[0], n)
+        ctx.save_for_backward(x, wg, wu, wd, g, u, y)
+        return out.view(*x.shape[:-1], wd.shape[0])
+
+    @staticmethod
+    def backward(ctx, dout):
+        x, wg, wu, wd, g, u, y = ctx.saved_tensors
+        m, k, n = x.numel() // x.shape[-1], x.shape[-1], wg.shape[0]
+        h = wd.shape[0]
+        dev, dt = x.device, x.dtype
+        dof = dout.contiguous().view(m, h)
+        dwd = matmul(dof.t(), y)
+        wdt = _ops.transpose_into(wd, torch.empty((n, h), device=dev, dtype=dt))
+        dgu = torch.empty((m, 2 * n), device=dev, dtype=dt)
+        dgut = torch.empty((2 * n, m), device=dev, dtype=dt)
+        swiglu_bwd_gemm_into(dof, wdt, g, u, dgu[:, :n], dgu[:, n:], dgut[:n], dgut[n:], m, n, h)
+        wt = torch.empty((k, 2 * n), device=dev, dtype=dt)
+        _ops.transpose_into(wg, wt[:, :n])
+        _ops.transpose_into(wu, wt[:, n:])
+        dx = torch.empty((m, k), device=dev, dtype=dt)
+        gemm_nt_into(dgu, 2 * n, wt, 2 * n, dx, m, k, 2 * n)
+        xt = _ops.transpose_into(x.view(m, k), torch.empty((k, m), device=dev, dtype=dt))
+        dw = torch.empty((2 * n, k), device=dev, dtype=dt)
+        gemm_nt_into(dgut, m, xt, m, dw, 2 * n, k, m)
+        return dx.view(x.shape), dw[:n], dw[n:], dwd
+
+
+def mlp_block(x, gate_weight, up_weight, down_weight, *, optimized=False):
+    """down(silu(gate(x)) * up(x)) -- ``components.py`` MLP: ``gate_up_swiglu`` then the down
+    ``linear`` -- with the fused backward above when every operand suits the matrix-core epilogue
+    (16-bit contiguous operands, tokens and intermediate size multiples of 256, hidden a multiple
+    of 64); otherwise exactly that composition."""
+    m, k, n = x.numel() // x.shape[-1], x.shape[-1], gate_weight.shape[0]
+    ok = x.is_cuda and x.is_contiguous() and down_weight.ndim == 2 and down_weight.shape[1] == n and \
+        gate_weight.shape == up_weight.shape and gate_weight.shape[1] == k and \
+        all(t.dtype == x.dtype and t.device == x.device and t.is_contiguous()
+            for t in (gate_weight, up_weight, down_weight)) and \
+        swiglu_bwd_gemm_ok(x.dtype, m, n, down_weight.shape[0]) and k % 8 == 0 and down_weight.shape[0] % 8 == 0
+    if not ok:
+        return linear(gate_up_swiglu(x, gate_weight, up_weight, optimized=optimized), down_weight,
+                      optimized=optimized)
+    return _MLPBlock.apply(x, gate_weight, up_weight, down_weight)

@@ -170,3 +170,75 @@ def test_gemm_nt_multi(m, ns, k, dtype):
         assert torch.equal(o, single)
         if m <= 512:
             assert max_rel(o, ref(a.cpu(), w.cpu().t())) < 8e-3
+
+
+@pytest.mark.parametrize("m,n,k", [(256, 256, 64), (512, 768, 256), (8192, 12288, 4096)])
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("transposed", [True, False])
+def test_swiglu_bwd_gemm(m, n, k, dtype, transposed):
+    """q3_gemm_swiglu_bwd: dg / du bit-equal to q3_gemm_nt (same 256 x 256 tile where the plain GEMM
+    picks it) followed by q3_swiglu_bwd, the transposed copies bit-equal to dg^T / du^T, and sampled
+    rows against the fp64 SwiGLU backward of the fp64 product."""
+    from qwen3_triton.kernels import _ops
+    from qwen3_triton.kernels.linear import swiglu_bwd_gemm_into
+    import oracle as O
+    print(f"swiglu_bwd_gemm {m}x{n}x{k} {dtype} transposed={transposed}", flush=True)
+    gen = seeded(m + 3 * n + k)
+    dy = randn(m, k, gen=gen, dtype=dtype).cuda()
+    wt = randn(n, k, gen=gen, dtype=dtype, scale=0.05).cuda()
+    g = randn(m, n, gen=gen, dtype=dtype).cuda()
+    u = randn(m, n, gen=gen, dtype=dtype).cuda()
+    dgu = torch.full((m, 2 * n), 7.0, device="cuda", dtype=dtype)
+    dgut = torch.full((2 * n, m), 7.0, device="cuda", dtype=dtype) if transposed else None
+    swiglu_bwd_gemm_into(dy, wt, g, u, dgu[:, :n], dgu[:, n:], None if dgut is None else dgut[:n],
+                         None if dgut is None else dgut[n:], m, n, k)
+    dY = torch.empty(m, n, device="cuda", dtype=dtype)
+    gemm_nt_into(dy, k, wt, k, dY, m, n, k)
+    eg, eu = _ops.swiglu_bwd(g, u, dY)
+    if m * n >= 256 * 256 * 256:   # the plain GEMM picks the same 256 x 256 tile there
+        assert torch.equal(dgu[:, :n], eg) and torch.equal(dgu[:, n:], eu)
+    else:
+        assert max_rel(dgu[:, :n], eg) <= 2e-2 and max_rel(dgu[:, n:], eu) <= 2e-2
+    if transposed:
+        assert torch.equal(dgut[:n], dgu[:, :n].t()) and torch.equal(dgut[n:], dgu[:, n:].t())
+    rows = torch.arange(0, m, max(1, m // 64))
+    e_dy = dy[rows].cpu().double() @ wt.cpu().double().t()
+    rg, ru = O.swiglu_backward_reference(g[rows].cpu().double(), u[rows].cpu().double(), e_dy, dtype=torch.float64)
+    tol = 3e-2 if dtype == torch.bfloat16 else 3e-3
+    assert max_rel(dgu[rows, :n], rg) <= tol and max_rel(dgu[rows, n:], ru) <= tol
+
+
+@pytest.mark.parametrize("b,s,h,i", [(2, 256, 256, 768), (1, 512, 512, 1024)])
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+def test_mlp_block_matches_composition(b, s, h, i, dtype):
+    """mlp_block (fused SwiGLU backward in the down projection's dX GEMM) gives the outputs and every
+    gradient of gate_up_swiglu + linear bit for bit, and matches the fp64 oracle MLP."""
+    from qwen3_triton.kernels.mlp_precision import gate_up_swiglu, mlp_block
+    import oracle as O
+    print(f"mlp_block b{b} s{s} h{h} i{i} {dtype}", flush=True)
+    gen = seeded(b * s + h + i)
+    x0 = randn(b, s, h, gen=gen, dtype=dtype)
+    ws = [randn(i, h, gen=gen, dtype=dtype, scale=0.05), randn(i, h, gen=gen, dtype=dtype, scale=0.05),
+          randn(h, i, gen=gen, dtype=dtype, scale=0.05)]
+    dout = randn(b, s, h, gen=gen, dtype=dtype)
+    res = []
+    for fused in (True, False):
+        x = x0.cuda().requires_grad_()
+        wg, wu, wd = (w.cuda().requires_grad_() for w in ws)
+        if fused:
+            y = mlp_block(x, wg, wu, wd)
+        else:
+            from qwen3_triton.kernels.linear import linear
+            y = linear(gate_up_swiglu(x, wg, wu), wd)
+        y.backward(dout.cuda())
+        res.append([y.detach(), x.grad, wg.grad, wu.grad, wd.grad])
+    for a, e in zip(*res):
+        assert torch.equal(a, e)
+    xr = x0.double().requires_grad_()
+    wr = [w.double().requires_grad_() for w in ws]
+    er = O.swiglu_reference(xr @ wr[0].t(), xr @ wr[1].t(), dtype=torch.float64) @ wr[2].t()
+    eg = torch.autograd.grad(er, [xr, *wr], dout.double())
+    tol = 2e-2 if dtype == torch.bfloat16 else 3e-3
+    assert max_rel(res[0][0], er) <= tol
+    for a, e in zip(res[0][1:], eg):
+        assert cosine(a, e) >= 0.999
