@@ -72,6 +72,14 @@ __global__ __launch_bounds__(NW * 64) void dlinear_kernel(DecArgs a) {
   f32x4 acc[NB];
 #pragma unroll
   for (int j = 0; j < NB; ++j) acc[j] = f32x4{0.f, 0.f, 0.f, 0.f};
+  // MODE 1: the residual values of this lane's outputs (rows m = 4 kq + e, column n0 + r), loaded at
+  // entry so their latency overlaps the weight stream instead of following the fold
+  [[maybe_unused]] u16 resv[4];
+  if constexpr (MODE == 1) {
+    const int nr = min(n0 + r, sg.n - 1);
+#pragma unroll
+    for (int e = 0; e < 4; ++e) resv[e] = a.res[(int64_t)min(4 * kq + e, M - 1) * a.ldres + nr];
+  }
 
   // Q blocks of 128 k at kb[0..Q): all loads first, then the MFMAs.  `guard` bounds each 16-byte
   // chunk by K (the ragged last block).
@@ -159,7 +167,7 @@ __global__ __launch_bounds__(NW * 64) void dlinear_kernel(DecArgs a) {
     const int m = 4 * kq + e;
     if (m >= M) continue;
     float o = to_f32<T>(from_f32<T>(v[0][e]));
-    if constexpr (MODE == 1) o = to_f32<T>(a.res[m * a.ldres + n]) + o;
+    if constexpr (MODE == 1) o = to_f32<T>(resv[e]) + o;
     if constexpr (MODE == 2) {
       const float u = to_f32<T>(from_f32<T>(v[1][e]));
       o = o * q3_sigmoid(o) * u;
@@ -332,14 +340,21 @@ __global__ __launch_bounds__(NW * 64) void dlinear_stream_kernel(DecArgs a, int 
   }
 }
 
-// Waves per workgroup x k blocks in flight per wave, per mode: measured on MI355X inside the captured
-// Qwen3-8B decode step (B1 and B8) over {2, 4, 8, 16} waves x {1, 2, 4} blocks, each projection
-// kind separately: the normed Q/K/V (and LM head) 8 x 2; O and down (+ residual) 8 x 1; gate/up +
-// SwiGLU 8 x 1.
+// Waves per workgroup x k blocks in flight per wave, per mode: measured on MI355X over {4, 8, 16} waves
+// x {1, 2, 4} blocks, each projection kind separately (36 distinct weights per captured graph): modes
+// 0 / 2 (shapes the streaming kernel does not take) 8 x 2 and 8 x 1; mode 1 (O and down + residual)
+// 8 x 4 up to K = 4096 (every block of a wave in flight: O 9.0 -> 8.2 us at B1), 8 x 1 above (down,
+// K = 12288: more blocks in flight measured slower at B8).
 template <typename T, int MODE, bool NORM>
 int dlinear_launch(const DecArgs& a, int tiles, hipStream_t s) {
-  constexpr int NW = 8, P = MODE == 0 ? 2 : 1;
-  dlinear_kernel<T, MODE, NORM, NW, P><<<(unsigned)tiles, NW * 64, 0, s>>>(a);
+  constexpr int NW = 8;
+  if constexpr (MODE == 1) {
+    if (a.K <= 4096) {
+      dlinear_kernel<T, MODE, NORM, NW, 4><<<(unsigned)tiles, NW * 64, 0, s>>>(a);
+      return (int)hipGetLastError();
+    }
+  }
+  dlinear_kernel<T, MODE, NORM, NW, MODE == 0 ? 2 : 1><<<(unsigned)tiles, NW * 64, 0, s>>>(a);
   return (int)hipGetLastError();
 }
 
