@@ -30,10 +30,10 @@ PEAK_BF16_TFLOPS = 2500.0   # MI355X dense bf16 matrix-core peak
 PEAK_HBM_GBS = 8000.0       # MI355X HBM3E
 # HBM bytes per GEMM launch of the layer step, from two rocprofv3 counter passes over
 # `bench.py --pmc-probe` (FETCH_SIZE x 2.000 and WRITE_SIZE x 1.000: the factors that make a 1 GiB
-# device copy read 1 GiB), averaged over the step's 15 GEMM launches.  Re-measure with those two
+# device copy read 1 GiB), averaged over the step's 12 GEMM launches.  Re-measure with those two
 # passes (rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE -- python bench.py --pmc-probe) when the GEMM
 # kernels change.
-GEMM_TRAFFIC_BYTES_PER_LAUNCH = 948.1e6 + 118.5e6
+GEMM_TRAFFIC_BYTES_PER_LAUNCH = 1207.8e6 + 187.7e6
 
 
 def qwen3_8b_config(layers):
@@ -59,6 +59,9 @@ class GemmTimer:
         # the shared-input projections (q/k/v: up to three weights, one launch)
         self.mu_mods = [m for m in modules if hasattr(m, "gemm_nt_multi_into")]
         self.mu_orig = self.mu_mods[0].gemm_nt_multi_into if self.mu_mods else None
+        # the down projection's input-gradient GEMM with the SwiGLU backward epilogue
+        self.sb_mods = [m for m in modules if hasattr(m, "swiglu_bwd_gemm_into")]
+        self.sb_orig = self.sb_mods[0].swiglu_bwd_gemm_into if self.sb_mods else None
         self.records = []
         self.active = False
 
@@ -93,8 +96,19 @@ class GemmTimer:
             e.record()
             self.records.append((s, e, 2.0 * m * k * sum(w.shape[0] for w in weights)))
 
+        def timed_sb(dy, wt, g, u, dg, du, dgt, dut, m, n, k):
+            if not self.active:
+                return self.sb_orig(dy, wt, g, u, dg, du, dgt, dut, m, n, k)
+            s, e = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            s.record()
+            self.sb_orig(dy, wt, g, u, dg, du, dgt, dut, m, n, k)
+            e.record()
+            self.records.append((s, e, 2.0 * m * n * k))
+
         for m in self.mods:
             m.gemm_nt_into = timed
+        for m in self.sb_mods:
+            m.swiglu_bwd_gemm_into = timed_sb
         for m in self.gu_mods:
             m.gate_up_swiglu_into = timed_gu
         for m in self.mu_mods:
@@ -108,6 +122,8 @@ class GemmTimer:
             m.gate_up_swiglu_into = self.gu_orig
         for m in self.mu_mods:
             m.gemm_nt_multi_into = self.mu_orig
+        for m in self.sb_mods:
+            m.swiglu_bwd_gemm_into = self.sb_orig
 
     def summary(self):
         ms = sum(s.elapsed_time(e) for s, e, _ in self.records)
