@@ -59,6 +59,9 @@ class GemmTimer:
         # the shared-input projections (q/k/v: up to three weights, one launch)
         self.mu_mods = [m for m in modules if hasattr(m, "gemm_nt_multi_into")]
         self.mu_orig = self.mu_mods[0].gemm_nt_multi_into if self.mu_mods else None
+        # the projection GEMM with the residual sum in its epilogue
+        self.rs_mods = [m for m in modules if hasattr(m, "gemm_nt_residual_into")]
+        self.rs_orig = self.rs_mods[0].gemm_nt_residual_into if self.rs_mods else None
         # the down projection's input-gradient GEMM with the SwiGLU backward epilogue
         self.sb_mods = [m for m in modules if hasattr(m, "swiglu_bwd_gemm_into")]
         self.sb_orig = self.sb_mods[0].swiglu_bwd_gemm_into if self.sb_mods else None
@@ -105,8 +108,19 @@ class GemmTimer:
             e.record()
             self.records.append((s, e, 2.0 * m * n * k))
 
+        def timed_rs(a, lda, bnk, ldb, res, out, m, n, k):
+            if not self.active:
+                return self.rs_orig(a, lda, bnk, ldb, res, out, m, n, k)
+            s, e = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            s.record()
+            self.rs_orig(a, lda, bnk, ldb, res, out, m, n, k)
+            e.record()
+            self.records.append((s, e, 2.0 * m * n * k))
+
         for m in self.mods:
             m.gemm_nt_into = timed
+        for m in self.rs_mods:
+            m.gemm_nt_residual_into = timed_rs
         for m in self.sb_mods:
             m.swiglu_bwd_gemm_into = timed_sb
         for m in self.gu_mods:
@@ -124,6 +138,8 @@ class GemmTimer:
             m.gemm_nt_multi_into = self.mu_orig
         for m in self.sb_mods:
             m.swiglu_bwd_gemm_into = self.sb_orig
+        for m in self.rs_mods:
+            m.gemm_nt_residual_into = self.rs_orig
 
     def summary(self):
         ms = sum(s.elapsed_time(e) for s, e, _ in self.records)

@@ -140,6 +140,15 @@ int q3_embedding_bwd(int dtype, const void* ids, int ids_is_int64, const void* d
  *           ops/triton/gate_up_swiglu.py:151-176 (_matmul_kernel). */
 int q3_gemm_nt(int in_dtype, int out_dtype, const void* A, int64_t lda, const void* B, int64_t ldb, void* C,
                int64_t ldc, int64_t M, int64_t N, int64_t K, float alpha, int accumulate, hipStream_t stream);
+/* Projection plus residual in one matrix-core GEMM: C = R + A B^T for A [M, K], B [N, K] (K-contiguous
+ * rows) and the residual R [M, N] (row stride ldr); the GEMM output is rounded to dtype and then
+ * added to R in fp32 and rounded again, so C is bit-identical to q3_gemm_nt followed by q3_add.
+ * C may alias R.  M % 256 == 0, N % 256 == 0, K % 64 == 0, (M / 256) (N / 256) >= 256 (the full-tile
+ * grid), strides % 8 == 0, pointers 16-byte aligned.
+ * Replaces: _model.py:60-108 / components.py (x = x + self_attn(...), x = x + mlp(...): the o_proj /
+ * down_proj kernels/linear.py launch followed by kernels/residual.py:13-30). */
+int q3_gemm_nt_residual(int dtype, const void* A, int64_t lda, const void* B, int64_t ldb, const void* R,
+                        int64_t ldr, void* C, int64_t ldc, int64_t M, int64_t N, int64_t K, hipStream_t stream);
 /* Gate/up projections with the SwiGLU epilogue in one matrix-core GEMM: for x [M, K] and weights
  * wg, wu [N, K] (K-contiguous rows, row stride ldw), stores G = x wg^T, U = x wu^T (each rounded to
  * dtype) and Y = silu(G) * U computed from the rounded G and U (the same expression as

@@ -226,6 +226,9 @@ struct CeEpi {
   u16* dgt;
   u16* dut;
   int64_t lddt;
+  // EPI 0 (16-bit output, full 256 x 256 tiles): when set, C = res + the GEMM output (row stride ldres)
+  const u16* res;
+  int64_t ldres;
 };
 
 Q3_DEV void lse_merge(float& m, float& s, float m2, float s2) {
@@ -565,6 +568,32 @@ __global__ __launch_bounds__(WM * WN * 64) void gemm_nt_v4_kernel(const u16* __r
         for (int j = 0; j < FN; ++j)
           stage(NC, i, j, pack2<O>(alpha * acc[i][j][0], alpha * acc[i][j][1]),
                 pack2<O>(alpha * acc[i][j][2], alpha * acc[i][j][3]));
+      if (ce.res) {
+        // C = res + round(acc): the residual rows of this wave's block are loaded (all 16 row passes in
+        // flight) while the staging writes land, then added in fp32 to the rounded GEMM output and
+        // rounded again -- exactly a GEMM output followed by q3_add.
+        constexpr int CH = TNW / 8, RPI = 64 / CH;
+        const int c = lane % CH;
+        const u16* rsrc = ce.res + (int64_t)(m0 + wm * TMW) * ce.ldres + n0 + wn * TNW + c * 8;
+        i32x4 rv[TMW / RPI];
+#pragma unroll
+        for (int q = 0; q < TMW / RPI; ++q)
+          rv[q] = *reinterpret_cast<const i32x4*>(rsrc + (int64_t)(q * RPI + lane / CH) * ce.ldres);
+        __builtin_amdgcn_s_waitcnt((15) | (7 << 4) | (0 << 8) | (3 << 14));  // this wave's staging writes
+        __builtin_amdgcn_wave_barrier();
+        typename O::storage* dst = C + (int64_t)(m0 + wm * TMW) * ldc + n0 + wn * TNW + c * 8;
+#pragma unroll
+        for (int q = 0; q < TMW / RPI; ++q) {
+          const int r = q * RPI + lane / CH;
+          const Vec<O> a = unpack_vec<O>(*reinterpret_cast<const i32x4*>(wl + r * (TNW * 2) + ((c ^ (r & 15)) << 4)));
+          const Vec<O> b = unpack_vec<O>(rv[q]);
+          i32x4 o;
+#pragma unroll
+          for (int w = 0; w < 4; ++w) o[w] = (int)pack2<O>(a.v[2 * w] + b.v[2 * w], a.v[2 * w + 1] + b.v[2 * w + 1]);
+          *reinterpret_cast<i32x4*>(dst + (int64_t)r * ldc) = o;
+        }
+        return;
+      }
       flush(NC, C + (int64_t)(m0 + wm * TMW) * ldc + n0 + wn * TNW, ldc, std::integral_constant<int, TMW>{});
       return;
     }
@@ -953,6 +982,21 @@ int q3_gemm_gate_up_swiglu(int dtype, const void* x, int64_t ldx, const void* wg
              al16(wg) && al16(wu) && al16(g) && al16(u) && al16(y));
   if (dtype == Q3_BF16) return launch_gate_up<BF16>(x, ldx, wg, wu, ldw, g, u, y, ldo, M, N, K, stream);
   return launch_gate_up<F16>(x, ldx, wg, wu, ldw, g, u, y, ldo, M, N, K, stream);
+}
+
+int q3_gemm_nt_residual(int dtype, const void* A, int64_t lda, const void* B, int64_t ldb, const void* R,
+                        int64_t ldr, void* C, int64_t ldc, int64_t M, int64_t N, int64_t K, hipStream_t stream) {
+  Q3_REQUIRE((dtype == Q3_BF16 || dtype == Q3_F16) && A && B && R && C);
+  Q3_REQUIRE(M > 0 && N > 0 && K > 0 && M % 256 == 0 && N % 256 == 0 && K % 64 == 0 && M < (1ll << 31) &&
+             N < (1ll << 31) && K < (1ll << 31) && (M / 256) * (N / 256) >= 256 && (M / 256) * (N / 256) < (1ll << 31));
+  Q3_REQUIRE(lda % 8 == 0 && ldb % 8 == 0 && ldr % 8 == 0 && ldc % 8 == 0 && lda >= K && ldb >= K && ldr >= N &&
+             ldc >= N && al16(A) && al16(B) && al16(R) && al16(C));
+  CeEpi e{};
+  e.res = (const u16*)R;
+  e.ldres = ldr;
+  if (dtype == Q3_BF16)
+    return launch_v4<BF16, BF16, 256, 256, 4, 2, 2, true>(A, lda, B, ldb, C, ldc, M, N, K, 1.f, 0, stream, e);
+  return launch_v4<F16, F16, 256, 256, 4, 2, 2, true>(A, lda, B, ldb, C, ldc, M, N, K, 1.f, 0, stream, e);
 }
 
 int q3_gemm_swiglu_bwd(int dtype, const void* dy, int64_t lddy, const void* wt, int64_t ldw, const void* g,

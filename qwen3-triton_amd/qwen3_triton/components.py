@@ -4,17 +4,20 @@
 module structure and option switches (the q/k/v projections keep their own parameters and run
 through one shared-input projection op whose backward is a single dX GEMM): ``norm_rope_fusion`` selects the fused per-head RMSNorm +
 RoPE kernel, ``mlp_fusion`` the fused gate/up + SwiGLU + down block (``mlp_block``: SwiGLU backward in
-the down projection's input-gradient GEMM epilogue).  The reference's SM86 rounding-order options
-(``precision_options``) are accepted and select nothing on gfx950.
+the down projection's input-gradient GEMM epilogue).  The decoder layer hands each block its
+residual input, so the residual sums ride in the epilogues of the o_proj and down_proj GEMMs.  The
+reference's SM86 rounding-order options (``precision_options``) are accepted and select nothing on
+gfx950.
 """
 import torch
 
 from ._model import TritonAttention, TritonDecoderLayer, TritonMLP, TritonNorm, TritonQwen3Model
 from .kernels.activation import swiglu
 from .kernels.attention import causal_attention_bshd
-from .kernels.linear import shared_input_projections
+from .kernels.linear import linear_residual, shared_input_projections
 from .kernels.math_precision import norm_rope, rms_norm
 from .kernels.mlp_precision import mlp_block
+from .kernels.norm import rms_norm_fork
 from .kernels.rotary import apply_rotary
 
 
@@ -30,7 +33,7 @@ class Attention(TritonAttention):
         self.q_norm = HFOrderNorm(self.head_dim, config.rms_norm_eps)
         self.k_norm = HFOrderNorm(self.head_dim, config.rms_norm_eps)
 
-    def forward(self, x, positions):
+    def forward(self, x, positions, residual=None):
         b, s, _ = x.shape
         d = self.head_dim
         cos, sin = positions
@@ -45,19 +48,22 @@ class Attention(TritonAttention):
         else:
             q = apply_rotary(self.q_norm(q), cos, sin)
             k = apply_rotary(self.k_norm(k), cos, sin)
-        y = causal_attention_bshd(q, k, v, scale=d ** -0.5)
-        return self.o_proj(y.reshape(b, s, self.num_heads * d))
+        y = causal_attention_bshd(q, k, v, scale=d ** -0.5).reshape(b, s, self.num_heads * d)
+        if residual is None:
+            return self.o_proj(y)
+        return linear_residual(y, self.o_proj.weight, residual, optimized=self.o_proj.options.linear_optimized)
 
 
 class MLP(TritonMLP):
-    def forward(self, x):
+    def forward(self, x, residual=None):
         opts = self.gate_proj.options
         if getattr(opts, 'mlp_fusion', False):
             return mlp_block(x, self.gate_proj.weight, self.up_proj.weight, self.down_proj.weight,
-                             optimized=opts.linear_optimized)
-        else:
-            y = swiglu(self.gate_proj(x), self.up_proj(x))
-        return self.down_proj(y)
+                             optimized=opts.linear_optimized, residual=residual)
+        y = swiglu(self.gate_proj(x), self.up_proj(x))
+        if residual is None:
+            return self.down_proj(y)
+        return linear_residual(y, self.down_proj.weight, residual, optimized=opts.linear_optimized)
 
 
 class DecoderLayer(TritonDecoderLayer):
@@ -67,6 +73,14 @@ class DecoderLayer(TritonDecoderLayer):
         self.mlp = MLP(c, options)
         self.input_layernorm = HFOrderNorm(c.hidden_size, c.rms_norm_eps)
         self.post_attention_layernorm = HFOrderNorm(c.hidden_size, c.rms_norm_eps)
+
+    def forward(self, x, position_embeddings):
+        # ``_model.py:60-108`` layer order; x forks into the norm and the residual sum (one autograd node
+        # whose backward adds both gradients), and each block adds its residual in its last GEMM.
+        x, h = rms_norm_fork(x, self.input_layernorm.weight, self.input_layernorm.eps)
+        x = self.self_attn(h, position_embeddings, residual=x)
+        x, h = rms_norm_fork(x, self.post_attention_layernorm.weight, self.post_attention_layernorm.eps)
+        return self.mlp(h, residual=x)
 
 
 class Backbone(TritonQwen3Model):

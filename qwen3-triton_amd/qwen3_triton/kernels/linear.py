@@ -49,6 +49,19 @@ def gate_up_swiglu_into(x, wg, wu, g, u, y, m, n, k):
            g.data_ptr(), u.data_ptr(), y.data_ptr(), n, m, n, k, H.stream())
 
 
+def gemm_nt_residual_into(a, lda, bnk, ldb, res, out, m, n, k):
+    """out[m, n] = res + a[m, k] . bnk[n, k]^T in one matrix-core launch (the GEMM output rounded, then
+    the residual added and rounded again: bit-identical to the GEMM followed by the add kernel)."""
+    H.call("q3_gemm_nt_residual", H.code(a.dtype), a.data_ptr(), lda, bnk.data_ptr(), ldb, res.data_ptr(),
+           res.stride(0), out.data_ptr(), out.stride(0), m, n, k, H.stream())
+
+
+def gemm_residual_ok(dtype, m, n, k):
+    """The fused residual epilogue serves 16-bit full-tile grids that cover the 256 CUs."""
+    return dtype in (torch.bfloat16, torch.float16) and m % 256 == 0 and n % 256 == 0 and k % 64 == 0 and \
+        (m // 256) * (n // 256) >= 256
+
+
 def swiglu_bwd_gemm_into(dy, wt, g, u, dg, du, dgt, dut, m, n, k):
     """dg, du (and their transposes dgt, dut when given) of y = silu(g) * u for the upstream gradient
     dY = dy wt^T, computed in one matrix-core GEMM whose epilogue runs the SwiGLU backward
@@ -144,6 +157,46 @@ class _Linear(torch.autograd.Function):
 def linear(x, weight, *, optimized=False):
     """``kernels/linear.py:104``."""
     return _Linear.apply(x, weight, optimized)
+
+
+class _LinearResidual(torch.autograd.Function):
+    """res + X W^T (an output projection and the residual sum after it) as one op: one matrix-core
+    launch with the residual in the epilogue where the shape allows it; backward dX = dY W,
+    dW = dY^T X, dRes = dY."""
+
+    @staticmethod
+    def forward(ctx, x, weight, res, optimized):
+        if x.ndim < 2 or weight.ndim != 2 or x.shape[-1] != weight.shape[1]:
+            raise ValueError('Expected X[...,K] and weight[N,K]')
+        if not x.is_contiguous() or not res.is_contiguous():
+            raise ValueError('Linear input and residual must be contiguous; no hidden layout copy')
+        if res.shape != (*x.shape[:-1], weight.shape[0]) or res.dtype != x.dtype or res.device != x.device:
+            raise ValueError('residual must match the projection output')
+        flat = x.view(-1, x.shape[-1])
+        m, k = flat.shape
+        n = weight.shape[0]
+        if gemm_residual_ok(x.dtype, m, n, k) and weight.dtype == x.dtype and weight.is_contiguous():
+            out = torch.empty((m, n), device=x.device, dtype=x.dtype)
+            gemm_nt_residual_into(flat, k, weight, k, res.view(m, n), out, m, n, k)
+        else:
+            out = _ops.add(res.view(m, n), matmul(flat, weight.t(), optimized=optimized))
+        ctx.save_for_backward(flat, weight)
+        ctx.shape = x.shape
+        ctx.optimized = optimized
+        return out.view(res.shape)
+
+    @staticmethod
+    def backward(ctx, dy):
+        x, w = ctx.saved_tensors
+        dyf = dy.contiguous().view(-1, w.shape[0])
+        dx = matmul(dyf, w, optimized=ctx.optimized).view(ctx.shape) if ctx.needs_input_grad[0] else None
+        dw = matmul(dyf.t(), x, optimized=ctx.optimized) if ctx.needs_input_grad[1] else None
+        return dx, dw, dy, None
+
+
+def linear_residual(x, weight, res, *, optimized=False):
+    """``res + linear(x, weight)`` (``kernels/residual.py:30`` after ``kernels/linear.py:104``)."""
+    return _LinearResidual.apply(x, weight, res, optimized)
 
 
 class _SharedInputProjections(torch.autograd.Function):

@@ -11,8 +11,8 @@ buffer, so dX is a single GEMM over K = 2N and both weight gradients come from o
 import torch
 
 from . import _ops
-from .linear import (gate_up_fused_ok, gate_up_swiglu_into, gemm_nt_into, linear, matmul, matmul_into,
-                     swiglu_bwd_gemm_into, swiglu_bwd_gemm_ok)
+from .linear import (gate_up_fused_ok, gate_up_swiglu_into, gemm_nt_into, gemm_nt_residual_into, gemm_residual_ok,
+                     linear, linear_residual, matmul, matmul_into, swiglu_bwd_gemm_into, swiglu_bwd_gemm_ok)
 
 
 class _GateUp(torch.autograd.Function):
@@ -93,14 +93,22 @@ class _MLPBlock(torch.autograd.Function):
     Every GEMM and rounding point is the one of ``gate_up_swiglu`` followed by ``linear``."""
 
     @staticmethod
-    def forward(ctx, x, wg, wu, wd):
+    def forward(ctx, x, wg, wu, wd, res):
         m, k, n = x.numel() // x.shape[-1], x.shape[-1], wg.shape[0]
+        h = wd.shape[0]
         flat = x.view(m, k)
         g, u, y = _gate_up_forward(flat, wg, wu, m, n, k)
-        out = torch.empty((m, wd.shape[0]), device=x.device, dtype=x.dtype)
-        gemm_nt_into(y, n, wd, n, out, m, wd.shape[0], n)
+        out = torch.empty((m, h), device=x.device, dtype=x.dtype)
+        if res is None:
+            gemm_nt_into(y, n, wd, n, out, m, h, n)
+        elif gemm_residual_ok(x.dtype, m, h, n):  # the residual sum rides in the down GEMM's epilogue
+            gemm_nt_residual_into(y, n, wd, n, res.view(m, h), out, m, h, n)
+        else:
+            gemm_nt_into(y, n, wd, n, out, m, h, n)
+            out = _ops.add(res.view(m, h), out)
         ctx.save_for_backward(x, wg, wu, wd, g, u, y)
-        return out.view(*x.shape[:-1], wd.shape[0])
+        ctx.has_res = res is not None
+        return out.view(*x.shape[:-1], h)
 
     @staticmethod
     def backward(ctx, dout):
@@ -122,21 +130,26 @@ class _MLPBlock(torch.autograd.Function):
         xt = _ops.transpose_into(x.view(m, k), torch.empty((k, m), device=dev, dtype=dt))
         dw = torch.empty((2 * n, k), device=dev, dtype=dt)
         gemm_nt_into(dgut, m, xt, m, dw, 2 * n, k, m)
-        return dx.view(x.shape), dw[:n], dw[n:], dwd
+        return dx.view(x.shape), dw[:n], dw[n:], dwd, (dout if ctx.has_res else None)
 
 
-def mlp_block(x, gate_weight, up_weight, down_weight, *, optimized=False):
-    """down(silu(gate(x)) * up(x)) -- ``components.py`` MLP: ``gate_up_swiglu`` then the down
-    ``linear`` -- with the fused backward above when every operand suits the matrix-core epilogue
-    (16-bit contiguous operands, tokens and intermediate size multiples of 256, hidden a multiple
-    of 64); otherwise exactly that composition."""
+def mlp_block(x, gate_weight, up_weight, down_weight, *, optimized=False, residual=None):
+    """down(silu(gate(x)) * up(x)) (+ ``residual``) -- ``components.py`` MLP: ``gate_up_swiglu`` then the
+    down ``linear`` (then the residual sum) -- with the fused backward above when every operand suits
+    the matrix-core epilogue (16-bit contiguous operands, tokens and intermediate size multiples of
+    256, hidden a multiple of 64); otherwise exactly that composition."""
     m, k, n = x.numel() // x.shape[-1], x.shape[-1], gate_weight.shape[0]
     ok = x.is_cuda and x.is_contiguous() and down_weight.ndim == 2 and down_weight.shape[1] == n and \
         gate_weight.shape == up_weight.shape and gate_weight.shape[1] == k and \
         all(t.dtype == x.dtype and t.device == x.device and t.is_contiguous()
             for t in (gate_weight, up_weight, down_weight)) and \
         swiglu_bwd_gemm_ok(x.dtype, m, n, down_weight.shape[0]) and k % 8 == 0 and down_weight.shape[0] % 8 == 0
+    if residual is not None:
+        ok = ok and residual.is_contiguous() and residual.dtype == x.dtype and residual.device == x.device and \
+            residual.shape == (*x.shape[:-1], down_weight.shape[0])
     if not ok:
-        return linear(gate_up_swiglu(x, gate_weight, up_weight, optimized=optimized), down_weight,
-                      optimized=optimized)
-    return _MLPBlock.apply(x, gate_weight, up_weight, down_weight)
+        y = gate_up_swiglu(x, gate_weight, up_weight, optimized=optimized)
+        if residual is None:
+            return linear(y, down_weight, optimized=optimized)
+        return linear_residual(y, down_weight, residual, optimized=optimized)
+    return _MLPBlock.apply(x, gate_weight, up_weight, down_weight, residual)

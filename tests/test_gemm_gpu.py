@@ -242,3 +242,29 @@ def test_mlp_block_matches_composition(b, s, h, i, dtype):
     assert max_rel(res[0][0], er) <= tol
     for a, e in zip(res[0][1:], eg):
         assert cosine(a, e) >= 0.999
+
+
+@pytest.mark.parametrize("m,n,k", [(4096, 4096, 256), (8192, 4096, 4096)])
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+def test_gemm_nt_residual(m, n, k, dtype):
+    """q3_gemm_nt_residual: bit-equal to q3_gemm_nt followed by q3_add (in place on the residual too),
+    and within one rounding of the fp64 sum."""
+    from qwen3_triton.kernels import _ops
+    from qwen3_triton.kernels.linear import gemm_nt_residual_into
+    print(f"gemm_nt_residual {m}x{n}x{k} {dtype}", flush=True)
+    gen = seeded(m + 5 * n + k)
+    a = randn(m, k, gen=gen, dtype=dtype).cuda()
+    w = randn(n, k, gen=gen, dtype=dtype, scale=0.05).cuda()
+    r = randn(m, n, gen=gen, dtype=dtype).cuda()
+    out = torch.empty(m, n, device="cuda", dtype=dtype)
+    gemm_nt_residual_into(a, k, w, k, r, out, m, n, k)
+    y = torch.empty_like(out)
+    gemm_nt_into(a, k, w, k, y, m, n, k)
+    e = _ops.add(r, y)
+    assert torch.equal(out, e)
+    r2 = r.clone()
+    gemm_nt_residual_into(a, k, w, k, r2, r2, m, n, k)   # C aliasing R
+    assert torch.equal(r2, e)
+    rows = torch.arange(0, m, max(1, m // 64))
+    ref64 = r[rows].cpu().double() + a[rows].cpu().double() @ w.cpu().double().t()
+    assert max_rel(out[rows], ref64) <= (1.6e-2 if dtype == torch.bfloat16 else 2e-3)

@@ -110,6 +110,43 @@ def test_decoder_layer_8b_shape():
         assert c >= 0.999, f"{name}: {c}"
 
 
+def test_decoder_layer_fused_residuals_match_composition():
+    """The Qwen3-8B decoder layer at 4096 tokens (the full-tile grid, so the o_proj / down_proj GEMMs
+    take the residual epilogue and the MLP block its SwiGLU-backward epilogue): output and every
+    gradient bit-equal to the same modules composed with separate residual adds."""
+    from qwen3_triton.kernels.norm import rms_norm_fork
+    from qwen3_triton.kernels.residual import residual_add
+    from qwen3_triton.kernels.mlp_precision import gate_up_swiglu
+    from qwen3_triton.kernels.linear import linear
+    oc = O.OracleConfig(vocab_size=16, hidden_size=4096, intermediate_size=12288, num_hidden_layers=1,
+                        num_attention_heads=32, num_key_value_heads=8, head_dim=128)
+    torch.manual_seed(5)
+    layer = DecoderLayer(hf_config(oc), OptimizationOptions()).cuda().to(torch.bfloat16)
+    gen = seeded(5)
+    x = torch.randn(2, 2048, 4096, generator=gen).to(torch.bfloat16).cuda()
+    dy = torch.randn(2, 2048, 4096, generator=gen).to(torch.bfloat16).cuda()
+    pos = torch.arange(2048)[None].expand(2, 2048).contiguous()
+    cos, sin = O.rotary_tables_reference(pos, O.rope_inv_freq(1e6, 128), dtype=torch.bfloat16)
+    pe = (cos.cuda(), sin.cuda())
+
+    def composed(xi):
+        a, m = layer.self_attn, layer.mlp
+        xa, h = rms_norm_fork(xi, layer.input_layernorm.weight, layer.input_layernorm.eps)
+        xa = residual_add(xa, a(h, pe))
+        xb, h = rms_norm_fork(xa, layer.post_attention_layernorm.weight, layer.post_attention_layernorm.eps)
+        return residual_add(xb, linear(gate_up_swiglu(h, m.gate_proj.weight, m.up_proj.weight), m.down_proj.weight))
+
+    runs = []
+    for fn in (lambda xi: layer(xi, pe), composed):
+        layer.zero_grad(set_to_none=True)
+        xi = x.clone().requires_grad_()
+        y = fn(xi)
+        y.backward(dy)
+        runs.append([y.detach(), xi.grad] + [p.grad.clone() for p in layer.parameters()])
+    for i, (a, b) in enumerate(zip(*runs)):
+        assert torch.equal(a, b), i
+
+
 SMALL = O.OracleConfig(vocab_size=1000, hidden_size=512, intermediate_size=1024, num_hidden_layers=2,
                        num_attention_heads=4, num_key_value_heads=2, head_dim=128)
 
