@@ -14,9 +14,31 @@ from ..configuration import OptimizationOptions
 from ..kernels import _ops
 from ..kernels.activation import swiglu
 from ..kernels.embedding import embedding
+from ..kernels.linear import gemm_multi_ok, gemm_nt_multi_into, gemm_nt_residual_into, gemm_residual_ok
 from ..kernels.mlp_precision import gate_up_swiglu
 from ..kernels.residual import residual_add
 from . import kernels
+
+
+def _projections(h, weights, gemv):
+    """[h W^T for W in weights] for a prefill chunk: one matrix-core launch over the weights side by
+    side (``q3_gemm_nt_multi``) where the shapes allow it, else one projection each."""
+    m, k = h.numel() // h.shape[-1], h.shape[-1]
+    if gemm_multi_ok(h, m, k, weights) and h.is_contiguous() and all(w.is_contiguous() for w in weights):
+        outs = [torch.empty((*h.shape[:-1], w.shape[0]), device=h.device, dtype=h.dtype) for w in weights]
+        gemm_nt_multi_into(h.view(m, k), weights, [o.view(m, w.shape[0]) for o, w in zip(outs, weights)], m, k)
+        return outs
+    return [kernels.linear(h, w, gemv=gemv) for w in weights]
+
+
+def _residual_projection(x, y, weight, gemv):
+    """x + y W^T, the residual sum in the projection GEMM's epilogue where the shapes allow it."""
+    m, k, n = y.numel() // y.shape[-1], y.shape[-1], weight.shape[0]
+    if gemm_residual_ok(y.dtype, m, n, k) and y.is_contiguous() and x.is_contiguous() and weight.is_contiguous():
+        out = torch.empty_like(x)
+        gemm_nt_residual_into(y.view(m, k), k, weight, k, x.view(m, n), out.view(m, n), m, n, k)
+        return out
+    return residual_add(x, kernels.linear(y, weight, gemv=gemv))
 
 
 @dataclass
@@ -186,15 +208,16 @@ class TritonQwen3Inference(nn.Module):
                     x = kernels.decode_linear(y, [m.down_proj.weight], mode=1, res=x)
                     continue
                 h = kernels.rms_norm(x, layer.input_layernorm.weight, layer.input_layernorm.eps)
-                q = kernels.linear(h, a.q_proj.weight, gemv=self.gemv).view(b, s, a.num_heads, d)
-                k = kernels.linear(h, a.k_proj.weight, gemv=self.gemv).view(b, s, a.num_kv_heads, d)
-                v = kernels.linear(h, a.v_proj.weight, gemv=self.gemv).view(b, s, a.num_kv_heads, d)
+                q, k, v = _projections(h, [a.q_proj.weight, a.k_proj.weight, a.v_proj.weight], self.gemv)
+                q = q.view(b, s, a.num_heads, d)
+                k = k.view(b, s, a.num_kv_heads, d)
+                v = v.view(b, s, a.num_kv_heads, d)
                 q = kernels.norm_rope(q, a.q_norm.weight, cos, sin, a.q_norm.eps)
                 k = kernels.norm_rope(k, a.k_norm.weight, cos, sin, a.k_norm.eps)
                 kernels.append(k, v, cache.keys[i], cache.values[i], start, start_dev)
                 y = kernels.attention(q, cache.keys[i], cache.values[i], start, split_decode=self.split_decode,
                                       start_dev=start_dev).reshape(b, s, -1)
-                x = residual_add(x, kernels.linear(y, a.o_proj.weight, gemv=self.gemv))
+                x = _residual_projection(x, y, a.o_proj.weight, self.gemv)
                 h = kernels.rms_norm(x, layer.post_attention_layernorm.weight, layer.post_attention_layernorm.eps)
                 m = layer.mlp
                 if b * s <= 8 and self.gemv:
@@ -202,7 +225,7 @@ class TritonQwen3Inference(nn.Module):
                                kernels.linear(h, m.up_proj.weight, gemv=True))
                 else:
                     y = gate_up_swiglu(h, m.gate_proj.weight, m.up_proj.weight, optimized=True)
-                x = residual_add(x, kernels.linear(y, m.down_proj.weight, gemv=self.gemv))
+                x = _residual_projection(x, y, m.down_proj.weight, self.gemv)
             if logits_to_keep:
                 x = x[:, -logits_to_keep:, :].contiguous()
             if fused:
@@ -301,6 +324,15 @@ class DecodeSession:
         self.length = torch.zeros((1,), device=dev, dtype=torch.int64)
         self.done = torch.zeros((batch,), device=dev, dtype=torch.bool)
         self.graph = None
+        self.prompt_len = 0
+
+    @torch.inference_mode()
+    def reset(self):
+        """Forget the request (cache contents, length, finished rows); memory and any captured step
+        graph stay valid for the next prompt."""
+        self.cache.reset()
+        self.length.zero_()
+        self.done.zero_()
         self.prompt_len = 0
 
     @torch.inference_mode()
