@@ -416,12 +416,8 @@ __global__ __launch_bounds__(kThreads) void kv_append_kernel(const u16* __restri
 // ============================================================================ decode attention
 // One workgroup (4 waves) per (b, kv head, split of kSplit = 64 cached keys) computes all G query
 // heads of the GQA group, so every K/V byte is read once; each wave owns 16 keys and issues all of
-// its K and V loads before using any.  Scores: 16 lanes per key (8 of its 128 dims each), 4 keys per
-// step, a 16-lane DPP reduction per query head; they go to LDS.  Softmax: every wave takes the
-// workgroup's 64 scores one per lane (wave max / sum by DPP, identical in all waves).  P V: each lane
-// owns 2 of the 128 output dims for the wave's 16 keys (V read as 256 contiguous bytes per key) and
-// takes each key's probability with a lane read, so no cross-lane output reduction is needed; the
-// 4 waves fold through LDS.  A second kernel merges the splits in fixed order (deterministic).
+// its K and V loads before using any.  A second kernel merges the splits in fixed order
+// (deterministic).
 constexpr int kSplit = 64;
 
 struct DecAttnArgs {
@@ -449,167 +445,178 @@ struct DecAttnArgs {
   int64_t csb;
 };
 
-// RMSNorm over the 128 dims held by a 16-lane row (8 per lane) times the norm weight, then the
-// rotate-half RoPE with the partner dims 64 away (lane t ^ 8: DPP row_ror:8), rounded to the storage
-// type exactly like the standalone QK-norm + RoPE kernel.
-// w, cs, sn: this lane's 8 elements (t * 8 ..) of the norm weight and the rotary tables, packed.
+// Per wave:
+// S^T = K q^T on v_mfma_f32_16x16x32 (K rows loaded straight into the A-operand layout, the group's
+// G query rows -- normalised once per workgroup, one wave per head -- as the B operand padded to 16
+// columns); the accumulator layout of S^T (lane: head l % 16, keys 4 (l / 16) .. + 3) is exactly the
+// A-operand layout of P for O = P V on v_mfma_f32_16x16x16, whose V operand (4 consecutive keys of
+// one dimension per lane) comes from the wave's V tile in LDS through the gfx950 transpose read.
+// The softmax max and sum are formed per head over the workgroup's 64 keys (lane butterflies, then
+// the 4 waves through LDS); P is rounded to the storage type for the P V product, as in the
+// prefill kernels.
+typedef short v4s_t __attribute__((ext_vector_type(4)));
+typedef _Float16 v4h_t __attribute__((ext_vector_type(4)));
+typedef __attribute__((__vector_size__(2 * sizeof(int)))) int i32x2;
+template <typename T> Q3_DEV f32x4 mfma_16x16x16(i32x2 a, i32x2 b, f32x4 c);
+template <> Q3_DEV f32x4 mfma_16x16x16<BF16>(i32x2 a, i32x2 b, f32x4 c) {
+  return __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(__builtin_bit_cast(v4s_t, a), __builtin_bit_cast(v4s_t, b), c, 0, 0,
+                                                   0);
+}
+template <> Q3_DEV f32x4 mfma_16x16x16<F16>(i32x2 a, i32x2 b, f32x4 c) {
+  return __builtin_amdgcn_mfma_f32_16x16x16f16(__builtin_bit_cast(v4h_t, a), __builtin_bit_cast(v4h_t, b), c, 0, 0, 0);
+}
+
+// RMSNorm + rotate-half RoPE of one 128-dim row held 2 dims per lane (lane l: dims 2 l, 2 l + 1; the
+// partner dims 64 away live in lane l ^ 32), rounded to the storage type exactly like the standalone
+// QK-norm + RoPE kernel.
 template <typename T>
-Q3_DEV void norm_rope8(float (&x)[8], i32x4 w, i32x4 cs, i32x4 sn, int t, float eps) {
-  float ss = 0.f;
-#pragma unroll
-  for (int e = 0; e < 8; ++e) ss += x[e] * x[e];
-  const float inv = rsqrtf(group_sum<16>(ss) * (1.f / 128.f) + eps);
-  const Vec<T> wv = unpack_vec<T>(w), cv = unpack_vec<T>(cs), sv = unpack_vec<T>(sn);
-  const float sign = t < 8 ? -1.f : 1.f;
-#pragma unroll
-  for (int e = 0; e < 8; ++e) {
-    const float n = x[e] * inv * wv.v[e];
-    const float np = __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, n), 0x128, 0xF, 0xF,
-                                                                        true));
-    x[e] = to_f32<T>(from_f32<T>(n * cv.v[e] + sign * np * sv.v[e]));
-  }
+Q3_DEV void norm_rope2(float& x0, float& x1, uint32_t w, uint32_t cs, uint32_t sn, int lane, float eps) {
+  const float inv = rsqrtf(group_sum<64>(x0 * x0 + x1 * x1) * (1.f / 128.f) + eps);
+  const float n0 = x0 * inv * to_f32<T>((u16)(w & 0xffffu)), n1 = x1 * inv * to_f32<T>((u16)(w >> 16));
+  const float p0 = __shfl_xor(n0, 32, 64), p1 = __shfl_xor(n1, 32, 64);
+  const float sign = lane < 32 ? -1.f : 1.f;
+  x0 = to_f32<T>(from_f32<T>(n0 * to_f32<T>((u16)(cs & 0xffffu)) + sign * p0 * to_f32<T>((u16)(sn & 0xffffu))));
+  x1 = to_f32<T>(from_f32<T>(n1 * to_f32<T>((u16)(cs >> 16)) + sign * p1 * to_f32<T>((u16)(sn >> 16))));
 }
 
 template <typename T, int G, bool FUSED>
-__global__ __launch_bounds__(256) void decode_attn_kernel(DecAttnArgs a) {
-  constexpr int D = 128, KPW = kSplit / 4;  // keys per wave
-  __shared__ float sc[G][kSplit];
+__global__ __launch_bounds__(256) void decode_attn_mfma_kernel(DecAttnArgs a) {
+  constexpr int D = 128, KPW = kSplit / 4, HPW = (G + 3) / 4;  // keys and query heads per wave
+  __shared__ __attribute__((aligned(16))) u16 vt[4][KPW * D];  // per-wave V tile, 16-byte chunks swizzled
+  __shared__ __attribute__((aligned(16))) u16 qs[G][D];
+  __shared__ __attribute__((aligned(16))) u16 knew[D];
+  __shared__ float wred[2][4][16];
   __shared__ float red_o[4][G][D];
   const int split = blockIdx.x, bk = blockIdx.y, b = bk / a.Hkv, hk = bk % a.Hkv;
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, t = lane & 15, kg = lane >> 4;
-  // Every global load is issued before any is used: the cache rows of this split are read
-  // unconditionally (rows up to the capacity exist; rows at or past the length, and the new token's
-  // own row, are replaced below), together with q, the new token's k/v and the norm/rotary tables.
+  const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int r = lane & 15, kq = lane >> 4;
   const int k0 = split * kSplit, kw = k0 + wave * KPW;
   u16* kb = a.ck + b * a.ksb + hk * a.ksh;
   u16* vb = a.cv + b * a.ksb + hk * a.ksh;
-  i32x4 kr[KPW / 4];
-  uint32_t vr[KPW];
+  // Every global load first (cache rows read unconditionally up to the capacity, masked below):
+  // K A-operand fragments (lane (r, kq): key kw + r, dims 32 s + 8 kq), V rows (lane: key kw + lane / 4,
+  // 16-byte chunks lane % 4 + 4 c), this wave's query rows and the new token's k / v with the tables.
+  i32x4 kf[4], vr[4];
+  const int64_t krow = (int64_t)min(kw + r, a.capacity - 1) * D;
 #pragma unroll
-  for (int it = 0; it < KPW / 4; ++it)
-    kr[it] = *reinterpret_cast<const i32x4*>(kb + (int64_t)min(kw + it * 4 + kg, a.capacity - 1) * D + t * 8);
+  for (int s = 0; s < 4; ++s) kf[s] = *reinterpret_cast<const i32x4*>(kb + krow + 32 * s + 8 * kq);
+  const int vkey = lane >> 2;
+  const int64_t vrow = (int64_t)min(kw + vkey, a.capacity - 1) * D;
 #pragma unroll
-  for (int k = 0; k < KPW; ++k)
-    vr[k] = *reinterpret_cast<const uint32_t*>(vb + (int64_t)min(kw + k, a.capacity - 1) * D + 2 * lane);
-  i32x4 qraw[G];
+  for (int c = 0; c < 4; ++c) vr[c] = *reinterpret_cast<const i32x4*>(vb + vrow + ((lane & 3) + 4 * c) * 8);
+  uint32_t qraw[HPW];
 #pragma unroll
-  for (int g = 0; g < G; ++g)
-    qraw[g] = *reinterpret_cast<const i32x4*>(a.q + b * a.qsb + (int64_t)(hk * G + g) * a.qsh + t * 8);
-  i32x4 kraw = {0, 0, 0, 0}, qwv = {0, 0, 0, 0}, kwv = {0, 0, 0, 0}, csv = {0, 0, 0, 0}, snv = {0, 0, 0, 0};
-  uint32_t vraw = 0u;
+  for (int i = 0; i < HPW; ++i) {
+    const int h = min(wave + 4 * i, G - 1);
+    qraw[i] = *reinterpret_cast<const uint32_t*>(a.q + b * a.qsb + (int64_t)(hk * G + h) * a.qsh + 2 * lane);
+  }
+  uint32_t kraw = 0u, vraw = 0u, qwv = 0u, kwv = 0u, csv = 0u, snv = 0u;
+  i32x4 vnew[4] = {};
   if constexpr (FUSED) {
-    kraw = *reinterpret_cast<const i32x4*>(a.k + b * a.kvsb + hk * a.kvsh + t * 8);
-    vraw = *reinterpret_cast<const uint32_t*>(a.v + b * a.kvsb + hk * a.kvsh + 2 * lane);
-    qwv = *reinterpret_cast<const i32x4*>(a.qw + t * 8);
-    kwv = *reinterpret_cast<const i32x4*>(a.kw + t * 8);
-    csv = *reinterpret_cast<const i32x4*>(a.cs + b * a.csb + t * 8);
-    snv = *reinterpret_cast<const i32x4*>(a.sn + b * a.csb + t * 8);
+    const u16* kn = a.k + b * a.kvsb + hk * a.kvsh;
+    const u16* vn = a.v + b * a.kvsb + hk * a.kvsh;
+    kraw = *reinterpret_cast<const uint32_t*>(kn + 2 * lane);
+    vraw = *reinterpret_cast<const uint32_t*>(vn + 2 * lane);
+#pragma unroll
+    for (int c = 0; c < 4; ++c) vnew[c] = *reinterpret_cast<const i32x4*>(vn + ((lane & 3) + 4 * c) * 8);
+    qwv = *reinterpret_cast<const uint32_t*>(a.qw + 2 * lane);
+    kwv = *reinterpret_cast<const uint32_t*>(a.kw + 2 * lane);
+    csv = *reinterpret_cast<const uint32_t*>(a.cs + b * a.csb + 2 * lane);
+    snv = *reinterpret_cast<const uint32_t*>(a.sn + b * a.csb + 2 * lane);
   }
   // len_dev holds the cache length before this token: the token itself is at that position.
   const int pos = a.len_dev ? (int)*a.len_dev : a.T_len - 1;
   const int T_len = a.len_dev ? min(pos + 1, a.capacity) : a.T_len;
   const bool own = FUSED && pos >= k0 && pos < k0 + kSplit && pos < a.capacity;  // this split holds the token
-#pragma unroll
-  for (int it = 0; it < KPW / 4; ++it)
-    if (kw + it * 4 + kg >= T_len || (own && kw + it * 4 + kg == pos)) kr[it] = i32x4{0, 0, 0, 0};
-#pragma unroll
-  for (int k = 0; k < KPW; ++k)
-    if (kw + k >= T_len || (own && kw + k == pos)) vr[k] = 0u;
 
+  // query rows of this wave's heads (normalised + rotated when fused) -> LDS
+#pragma unroll
+  for (int i = 0; i < HPW; ++i) {
+    const int h = wave + 4 * i;
+    if (h < G) {
+      float x0 = to_f32<T>((u16)(qraw[i] & 0xffffu)), x1 = to_f32<T>((u16)(qraw[i] >> 16));
+      if constexpr (FUSED) norm_rope2<T>(x0, x1, qwv, csv, snv, lane, a.eps);
+      *reinterpret_cast<uint32_t*>(&qs[h][2 * lane]) = pack2<T>(x0, x1);
+    }
+  }
   if constexpr (FUSED) {
-    if (own) {  // the new token: k = rope(norm(k_raw)), v raw; into the cache and into this step
-      const Vec<T> kv = unpack_vec<T>(kraw);
-      float kn[8];
-#pragma unroll
-      for (int e = 0; e < 8; ++e) kn[e] = kv.v[e];
-      norm_rope8<T>(kn, kwv, csv, snv, t, a.eps);
-      i32x4 kp;
-#pragma unroll
-      for (int w = 0; w < 4; ++w) kp[w] = (int)pack2<T>(kn[2 * w], kn[2 * w + 1]);
-#pragma unroll
-      for (int it = 0; it < KPW / 4; ++it)
-        if (kw + it * 4 + kg == pos) kr[it] = kp;
-#pragma unroll
-      for (int k = 0; k < KPW; ++k)
-        if (kw + k == pos) vr[k] = vraw;
-      if (wave == 0 && kg == 0) *reinterpret_cast<i32x4*>(kb + (int64_t)pos * D + t * 8) = kp;
-      if (wave == 0) *reinterpret_cast<uint32_t*>(vb + (int64_t)pos * D + 2 * lane) = vraw;
+    if (own && wave == 0) {  // the new token: k = rope(norm(k_raw)), v raw; into the cache and into LDS
+      float x0 = to_f32<T>((u16)(kraw & 0xffffu)), x1 = to_f32<T>((u16)(kraw >> 16));
+      norm_rope2<T>(x0, x1, kwv, csv, snv, lane, a.eps);
+      const uint32_t kp = pack2<T>(x0, x1);
+      *reinterpret_cast<uint32_t*>(&knew[2 * lane]) = kp;
+      *reinterpret_cast<uint32_t*>(kb + (int64_t)pos * D + 2 * lane) = kp;
+      *reinterpret_cast<uint32_t*>(vb + (int64_t)pos * D + 2 * lane) = vraw;
     }
   }
-  float qf[G][8];
+  // V tile: rows past the length zeroed (their probabilities are 0, but the cache may hold anything),
+  // the new token's row from its raw v
+  {
+    const bool live = kw + vkey < T_len;
+    const bool mine = own && kw + vkey == pos;
 #pragma unroll
-  for (int g = 0; g < G; ++g) {
-    const Vec<T> qv = unpack_vec<T>(qraw[g]);
-#pragma unroll
-    for (int e = 0; e < 8; ++e) qf[g][e] = qv.v[e];
-    if constexpr (FUSED) norm_rope8<T>(qf[g], qwv, csv, snv, t, a.eps);
-#pragma unroll
-    for (int e = 0; e < 8; ++e) qf[g][e] *= a.scale2;  // scores in log2 units
-  }
-#pragma unroll
-  for (int it = 0; it < KPW / 4; ++it) {
-    float kf[8];
-#pragma unroll
-    for (int w = 0; w < 4; ++w) {
-      const uint32_t x = (uint32_t)kr[it][w];
-      kf[2 * w] = to_f32<T>((u16)(x & 0xffffu));
-      kf[2 * w + 1] = to_f32<T>((u16)(x >> 16));
-    }
-    const int key = kw + it * 4 + kg;
-#pragma unroll
-    for (int g = 0; g < G; ++g) {
-      float sg = 0.f;
-#pragma unroll
-      for (int e = 0; e < 8; ++e) sg += qf[g][e] * kf[e];
-      sg = group_sum<16>(sg);
-      if (t == 0) sc[g][key - k0] = key < T_len ? sg : -INFINITY;
+    for (int c = 0; c < 4; ++c) {
+      i32x4 val = mine ? vnew[c] : live ? vr[c] : i32x4{0, 0, 0, 0};
+      const int ch = ((lane & 3) + 4 * c) ^ (2 * (vkey & 7));
+      *reinterpret_cast<i32x4*>(&vt[wave][vkey * D + ch * 8]) = val;
     }
   }
   __syncthreads();
-  // softmax over the workgroup's 64 keys (lane = key), the same in every wave
-  float p[G], m[G], l[G];
+  if (own && pos >= kw && pos < kw + KPW && r == pos - kw) {  // the new key's fragments
 #pragma unroll
-  for (int g = 0; g < G; ++g) {
-    const float x = sc[g][lane];
-    float mx = x;
-#pragma unroll
-    for (int o = 1; o < 64; o <<= 1) mx = fmaxf(mx, __shfl_xor(mx, o, 64));
-    m[g] = mx;
-    p[g] = mx == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(x - mx);
-    l[g] = group_sum<64>(p[g]);
+    for (int s = 0; s < 4; ++s) kf[s] = *reinterpret_cast<const i32x4*>(&knew[32 * s + 8 * kq]);
   }
-  // P V over this wave's keys: lane owns dims 2*lane, 2*lane+1
-  float o[G][2];
+  // S^T = K q^T (16 keys x 16 heads, heads >= G are zero columns)
+  f32x4 sacc = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-  for (int g = 0; g < G; ++g) o[g][0] = o[g][1] = 0.f;
-#pragma unroll
-  for (int k = 0; k < KPW; ++k) {
-    const float v0 = to_f32<T>((u16)(vr[k] & 0xffffu)), v1 = to_f32<T>((u16)(vr[k] >> 16));
-#pragma unroll
-    for (int g = 0; g < G; ++g) {
-      const float pk = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, p[g]),
-                                                                           wave * KPW + k));
-      o[g][0] += pk * v0;
-      o[g][1] += pk * v1;
-    }
+  for (int s = 0; s < 4; ++s) {
+    const i32x4 qf = r < G ? *reinterpret_cast<const i32x4*>(&qs[min(r, G - 1)][32 * s + 8 * kq]) : i32x4{0, 0, 0, 0};
+    sacc = mfma_16x16x32<T>(__builtin_bit_cast(bf16x8_t, kf[s]), __builtin_bit_cast(bf16x8_t, qf), sacc);
   }
+  float sv[4];
 #pragma unroll
-  for (int g = 0; g < G; ++g) {
-    red_o[wave][g][2 * lane] = o[g][0];
-    red_o[wave][g][2 * lane + 1] = o[g][1];
+  for (int e = 0; e < 4; ++e) sv[e] = (kw + 4 * kq + e < T_len && r < G) ? sacc[e] * a.scale2 : -INFINITY;
+  float mx = fmaxf(fmaxf(sv[0], sv[1]), fmaxf(sv[2], sv[3]));
+  mx = fmaxf(mx, __shfl_xor(mx, 16, 64));
+  mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
+  if (kq == 0) wred[0][wave][r] = mx;
+  __syncthreads();
+  const float m = fmaxf(fmaxf(wred[0][0][r], wred[0][1][r]), fmaxf(wred[0][2][r], wred[0][3][r]));
+  float p[4];
+#pragma unroll
+  for (int e = 0; e < 4; ++e) p[e] = m == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(sv[e] - m);
+  float sum = (p[0] + p[1]) + (p[2] + p[3]);
+  sum += __shfl_xor(sum, 16, 64);
+  sum += __shfl_xor(sum, 32, 64);
+  if (kq == 0) wred[1][wave][r] = sum;
+  // O = P V over this wave's 16 keys, 8 blocks of 16 dims
+  const i32x2 pa = i32x2{(int)pack2<T>(p[0], p[1]), (int)pack2<T>(p[2], p[3])};
+  const int trow = 4 * kq + (r >> 2);
+  const char* vbase = reinterpret_cast<const char*>(&vt[wave][trow * D]);
+  f32x4 o[D / 16];
+#pragma unroll
+  for (int db = 0; db < D / 16; ++db) {
+    const int cb = 32 * db + 8 * (r & 3);  // byte offset of the 4 dims this lane addresses
+    const char* pv = vbase + ((((cb >> 4) ^ (2 * (trow & 7)))) << 4) + (cb & 15);
+    const i32x2 vf = __builtin_bit_cast(
+        i32x2, __builtin_amdgcn_ds_read_tr16_b64_v4i16((__attribute__((address_space(3))) v4s_t*)pv));
+    o[db] = mfma_16x16x16<T>(pa, vf, f32x4{0.f, 0.f, 0.f, 0.f});
   }
+  // o[db][e] = O[head 4 kq + e][dim 16 db + r]
+#pragma unroll
+  for (int db = 0; db < D / 16; ++db)
+#pragma unroll
+    for (int e = 0; e < 4; ++e)
+      if (4 * kq + e < G) red_o[wave][4 * kq + e][16 * db + r] = o[db][e];
   __syncthreads();
   const int64_t pbase = ((int64_t)bk * a.splits + split) * G;
   for (int i = tid; i < G * D; i += 256) {
     const int g = i / D, d = i % D;
     a.opart[(pbase + g) * D + d] = red_o[0][g][d] + red_o[1][g][d] + red_o[2][g][d] + red_o[3][g][d];
   }
-  if (tid == 0) {  // m and l are wave-uniform
-#pragma unroll
-    for (int g = 0; g < G; ++g) {
-      a.mpart[pbase + g] = m[g];
-      a.lpart[pbase + g] = l[g];
-    }
+  if (tid < G) {
+    a.mpart[pbase + tid] = fmaxf(fmaxf(wred[0][0][tid], wred[0][1][tid]), fmaxf(wred[0][2][tid], wred[0][3][tid]));
+    a.lpart[pbase + tid] = (wred[1][0][tid] + wred[1][1][tid]) + (wred[1][2][tid] + wred[1][3][tid]);
   }
 }
 
@@ -759,7 +766,7 @@ int64_t decode_splits(int64_t span) { return (span + kSplit - 1) / kSplit; }
 
 template <typename T, int G, bool FUSED>
 int decode_g(const DecAttnArgs& a, dim3 grid, void* out, int64_t osb, int64_t osh, hipStream_t s) {
-  decode_attn_kernel<T, G, FUSED><<<grid, 256, 0, s>>>(a);
+  decode_attn_mfma_kernel<T, G, FUSED><<<grid, 256, 0, s>>>(a);
   decode_merge_kernel<T, G><<<grid.y * G, 512, 0, s>>>(a.opart, a.mpart, a.lpart, (u16*)out, osb, osh, a.Hkv * G,
                                                        a.splits);
   return (int)hipGetLastError();
