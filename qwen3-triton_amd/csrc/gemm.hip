@@ -6,7 +6,7 @@
 //
 // Main path (K % 64 == 0), gemm_nt_v4_kernel: v_mfma_f32_16x16x32 (on MI355X it sustains a higher
 // rate than the 32x32x16 form under the board power limit with random data), 8 waves per
-// 256 x 256 x 64 tile (each 64 x 128) or 4 waves for 256 x 128 / 128 x 128 tiles, picked so the grid
+// 256 x 256 x 64 tile (each 64 x 128) or 4 waves for 128 x 128 tiles, picked so the grid
 // still covers the 256 CUs.  Operand tiles go global -> LDS with wave-wide global_load_lds_dwordx4
 // into a ring of k-tiles (no register staging); LDS rows are unpadded and XOR-swizzled so the
 // fragment reads are bank-conflict free; fragment reads are software-pipelined one k-step ahead.
@@ -858,17 +858,13 @@ template <typename T, typename O>
 int launch_nt(const void* A, int64_t lda, const void* B, int64_t ldb, void* C, int64_t ldc, int64_t M, int64_t N,
               int64_t K, float alpha, int acc, hipStream_t s) {
   if (K % 64 == 0) {
-    // Largest tile that still gives every CU (256) a workgroup (tile choice measured on MI355X
-    // for the Qwen3-8B projection shapes).
+    // 256 x 256 tiles when they still give every CU (256) a workgroup, else 128 x 128 (measured on
+    // MI355X for the Qwen3-8B projection shapes: below 256 tiles of 256 x 256, 128 x 128 beats both
+    // 256 x 256 and 256 x 128, e.g. 2048 x 4096 x 12288 in 190 us against 250 / 203 us).
     if (tiles_of(M, N, 256, 256) >= 256) {
       if (M % 256 == 0 && N % 256 == 0)
         return launch_v4<T, O, 256, 256, 4, 2, 2, true>(A, lda, B, ldb, C, ldc, M, N, K, alpha, acc, s);
       return launch_v4<T, O, 256, 256, 4, 2, 2, false>(A, lda, B, ldb, C, ldc, M, N, K, alpha, acc, s);
-    }
-    if (tiles_of(M, N, 256, 128) >= 256) {
-      if (M % 256 == 0 && N % 128 == 0)
-        return launch_v4<T, O, 256, 128, 2, 2, 3, true>(A, lda, B, ldb, C, ldc, M, N, K, alpha, acc, s);
-      return launch_v4<T, O, 256, 128, 2, 2, 3, false>(A, lda, B, ldb, C, ldc, M, N, K, alpha, acc, s);
     }
     if (M % 128 == 0 && N % 128 == 0)
       return launch_v4<T, O, 128, 128, 2, 2, 4, true>(A, lda, B, ldb, C, ldc, M, N, K, alpha, acc, s);
