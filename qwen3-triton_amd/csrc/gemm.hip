@@ -861,7 +861,21 @@ int launch_nt(const void* A, int64_t lda, const void* B, int64_t ldb, void* C, i
     // 256 x 256 tiles when they still give every CU (256) a workgroup, else 128 x 128 (measured on
     // MI355X for the Qwen3-8B projection shapes: below 256 tiles of 256 x 256, 128 x 128 beats both
     // 256 x 256 and 256 x 128, e.g. 2048 x 4096 x 12288 in 190 us against 250 / 203 us).
-    if (tiles_of(M, N, 256, 256) >= 256) {
+    const int64_t t256 = tiles_of(M, N, 256, 256), nN = (N + 255) / 256;
+    // A last round of 256 x 256 tiles that would leave at least half of the CUs idle (e.g. the
+    // 6144 x 4096 Q/K/V weight gradient: 384 tiles) is split off along M: the rows that fill whole
+    // rounds run as 256 x 256 tiles, the remaining rows as 128 x 128 tiles in a second launch
+    // (same per-element k order, so the result is bit-identical to one launch).
+    if (t256 > 256 && t256 % 256 != 0 && t256 % 256 <= 128 && 256 % nN == 0) {
+      const int64_t m1 = (t256 / 256) * 256 / nN * 256;
+      if (m1 > 0 && m1 < M) {
+        const int rc = launch_nt<T, O>(A, lda, B, ldb, C, ldc, m1, N, K, alpha, acc, s);
+        if (rc != 0) return rc;
+        return launch_nt<T, O>(static_cast<const u16*>(A) + m1 * lda, lda, B, ldb,
+                               static_cast<typename O::storage*>(C) + m1 * ldc, ldc, M - m1, N, K, alpha, acc, s);
+      }
+    }
+    if (t256 >= 256) {
       if (M % 256 == 0 && N % 256 == 0)
         return launch_v4<T, O, 256, 256, 4, 2, 2, true>(A, lda, B, ldb, C, ldc, M, N, K, alpha, acc, s);
       return launch_v4<T, O, 256, 256, 4, 2, 2, false>(A, lda, B, ldb, C, ldc, M, N, K, alpha, acc, s);

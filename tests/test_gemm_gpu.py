@@ -16,7 +16,8 @@ def ref(a, b):
 @pytest.mark.parametrize("m,n,k", [(32, 32, 16), (256, 128, 64), (300, 200, 8), (1, 4096, 4096), (8, 1024, 4096),
                                    (513, 687, 688), (2048, 1024, 4096), (64, 151936 // 16, 256), (1000, 3000, 128),
                                    (8192, 4096, 4096), (4096, 12288, 640), (8192, 1024, 192), (333, 4100, 4160),
-                                   (4353, 4100, 1024), (2050, 4000, 512)])
+                                   (4353, 4100, 1024), (2050, 4000, 512), (6144, 4096, 256),
+                                   (5000, 4096, 128)])
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
 def test_gemm_nt_shapes(m, n, k, dtype):
     print(f"gemm_nt {m}x{n}x{k} {dtype}", flush=True)
