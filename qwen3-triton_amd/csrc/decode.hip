@@ -184,15 +184,27 @@ __global__ __launch_bounds__(NW * 64) void dlinear_kernel(DecArgs a) {
 // the first unit's weights are already in flight.  Lane (r, kq) of wave w holds k = (w + NW i) * 128
 // + 32 c + 8 kq, i < KB, c < 4, of token row r (A operand) and weight row n0 + r (B operand); the
 // waves' partial 16 x 16 tiles fold in LDS in wave order (fixed order: deterministic).
-template <typename T, int MODE, bool NORM, int NW, int KB>
+// RU = 8 (mode 0, at most 8 token rows): units of 8 weight rows, so that a launch whose 16-row units
+// would leave CUs idle (Q/K/V: 384 units of 16 rows on 256 CUs) divides evenly (768 units of 8).  Each
+// 64-wide k step is split in two 32-wide halves h that sit on different MFMA rows and columns: lane
+// (r, kq) takes weight row r % 8 and token row r % 8 at k = 64 c + 32 h + 8 kq with h = r / 8, so
+// D[m + 8 h][n + 8 h] is half h of the dot product of token row m and weight row n (the cross-half
+// blocks are unused), and every load instruction reads 128 contiguous bytes of 8 rows.
+template <typename T, int MODE, bool NORM, int NW, int KB, int RU = 16>
 __global__ __launch_bounds__(NW * 64) void dlinear_stream_kernel(DecArgs a, int units) {
   static_assert(MODE == 0 || MODE == 2, "projection or SwiGLU");
+  static_assert(RU == 16 || (RU == 8 && MODE == 0), "8-row units: projections only");
+  constexpr int CPB = RU == 16 ? 4 : 2;  // 16-byte chunks per lane and 128-wide k block
   __shared__ f32x4 red[2][NW][64];
   __shared__ float red_ss[NW][64];
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int r = lane & 15, kq = lane >> 4;
+  const int rr = RU == 16 ? r : (r & 7), hh = RU == 16 ? 0 : (r >> 3);  // unit row, k half (RU 8)
   const int M = a.M, K = a.K;
-  const bool xrow = r < M;
+  const bool xrow = rr < M;
+  auto koff = [&](int i, int c) {
+    return (wave + NW * i) * 128 + (RU == 16 ? 32 * c + 8 * kq : 64 * c + 32 * hh + 8 * kq);
+  };
   auto unit_src = [&](int u, const u16*& w, int& n0, int& nrows) {
     if constexpr (MODE == 2) {
       w = a.seg[u & 1].w;
@@ -202,24 +214,24 @@ __global__ __launch_bounds__(NW * 64) void dlinear_stream_kernel(DecArgs a, int 
       int s = 0, t = u;
       while (s + 1 < a.nseg && t >= a.seg[s].tiles) t -= a.seg[s++].tiles;
       w = a.seg[s].w;
-      n0 = t * 16;
+      n0 = t * RU;
       nrows = a.seg[s].n;
     }
   };
-  constexpr int LPU = KB * 4;  // weight loads per unit and lane
-  i32x4 xv[KB][4];
+  constexpr int LPU = KB * CPB;  // weight loads per unit and lane
+  i32x4 xv[KB][CPB];
   float inv_m[4] = {1.f, 1.f, 1.f, 1.f};
-  i32x4 wb[2][KB][4];
+  i32x4 wb[2][KB][CPB];
   auto issue = [&](int u, auto buf_c) {
     constexpr int B = decltype(buf_c)::value;
     const u16* w;
     int n0, nrows;
     unit_src(u, w, n0, nrows);
-    const u16* row = w + (int64_t)min(n0 + r, nrows - 1) * K + 8 * kq;
+    const u16* row = w + (int64_t)min(n0 + rr, nrows - 1) * K;
 #pragma unroll
     for (int i = 0; i < KB; ++i)
 #pragma unroll
-      for (int c = 0; c < 4; ++c) wb[B][i][c] = *reinterpret_cast<const i32x4*>(row + (wave + NW * i) * 128 + 32 * c);
+      for (int c = 0; c < CPB; ++c) wb[B][i][c] = *reinterpret_cast<const i32x4*>(row + koff(i, c));
   };
   float gate[4] = {0.f, 0.f, 0.f, 0.f};
   // wave 0: fold the waves' partial tiles in order, then the epilogue (lane holds D[m = 4 kq + e][n = r])
@@ -227,6 +239,11 @@ __global__ __launch_bounds__(NW * 64) void dlinear_stream_kernel(DecArgs a, int 
     f32x4 t = red[par][0][lane];
 #pragma unroll
     for (int w = 1; w < NW; ++w) t += red[par][w][lane];
+    if constexpr (RU == 8) {
+      // D[m][n] (lane n + 16 (m / 4), n < 8, m < 8) + D[m + 8][n + 8] (that lane + 40)
+#pragma unroll
+      for (int e = 0; e < 4; ++e) t[e] += __shfl(t[e], (lane + 40) & 63, 64);
+    }
     float v[4];
 #pragma unroll
     for (int e = 0; e < 4; ++e) v[e] = t[e] * inv_m[e];
@@ -244,7 +261,8 @@ __global__ __launch_bounds__(NW * 64) void dlinear_stream_kernel(DecArgs a, int 
       while (s + 1 < a.nseg && tt >= a.seg[s].tiles) tt -= a.seg[s++].tiles;
     }
     const DecSeg sg = a.seg[s];
-    const int n = tt * 16 + r;
+    if (RU == 8 && (r >= 8 || kq >= 2)) return;
+    const int n = tt * RU + r;
     if (n >= sg.n) return;
 #pragma unroll
     for (int e = 0; e < 4; ++e) {
@@ -264,7 +282,7 @@ __global__ __launch_bounds__(NW * 64) void dlinear_stream_kernel(DecArgs a, int 
 #pragma unroll
     for (int i = 0; i < KB; ++i)
 #pragma unroll
-      for (int c = 0; c < 4; ++c)
+      for (int c = 0; c < CPB; ++c)
         acc = mfma_16x16x32<T>(__builtin_bit_cast(bf16x8_t, xv[i][c]), __builtin_bit_cast(bf16x8_t, wb[B][i][c]), acc);
     return acc;
   };
@@ -273,20 +291,20 @@ __global__ __launch_bounds__(NW * 64) void dlinear_stream_kernel(DecArgs a, int 
   int u = MODE == 2 ? 2 * blockIdx.x : blockIdx.x;
   auto next_u = [&](int v) { return MODE == 2 ? ((v & 1) ? v - 1 + step : v + 1) : v + step; };
   if (u >= units) return;  // uniform over the workgroup
-  i32x4 nvv[NORM ? KB : 1][4];
+  i32x4 nvv[NORM ? KB : 1][CPB];
 #pragma unroll
   for (int i = 0; i < KB; ++i)
 #pragma unroll
-    for (int c = 0; c < 4; ++c) {
-      const int k = (wave + NW * i) * 128 + 32 * c + 8 * kq;
-      xv[i][c] = *reinterpret_cast<const i32x4*>(a.x + (int64_t)(xrow ? r : 0) * a.ldx + k);
+    for (int c = 0; c < CPB; ++c) {
+      const int k = koff(i, c);
+      xv[i][c] = *reinterpret_cast<const i32x4*>(a.x + (int64_t)(xrow ? rr : 0) * a.ldx + k);
       if constexpr (NORM) nvv[i][c] = *reinterpret_cast<const i32x4*>(a.nw + k);
     }
   issue(u, std::integral_constant<int, 0>{});
 #pragma unroll
   for (int i = 0; i < KB; ++i)
 #pragma unroll
-    for (int c = 0; c < 4; ++c)
+    for (int c = 0; c < CPB; ++c)
       if (!xrow) xv[i][c] = i32x4{0, 0, 0, 0};
   if constexpr (NORM) {
     // the input rows and norm weight landed (older than the first unit's weight loads)
@@ -295,7 +313,7 @@ __global__ __launch_bounds__(NW * 64) void dlinear_stream_kernel(DecArgs a, int 
 #pragma unroll
     for (int i = 0; i < KB; ++i)
 #pragma unroll
-      for (int c = 0; c < 4; ++c)
+      for (int c = 0; c < CPB; ++c)
 #pragma unroll
         for (int w = 0; w < 4; ++w) {
           const uint32_t xx = (uint32_t)xv[i][c][w], ww = (uint32_t)nvv[i][c][w];
@@ -303,8 +321,9 @@ __global__ __launch_bounds__(NW * 64) void dlinear_stream_kernel(DecArgs a, int 
           ssq += x0 * x0 + x1 * x1;
           xv[i][c][w] = (int)pack2<T>(x0 * to_f32<T>((u16)(ww & 0xffffu)), x1 * to_f32<T>((u16)(ww >> 16)));
         }
-    ssq += __shfl_xor(ssq, 16, 64);  // row r over the 4 quarters, then over the waves
+    ssq += __shfl_xor(ssq, 16, 64);  // row r over the 4 quarters (RU 8: and both k halves), then over the waves
     ssq += __shfl_xor(ssq, 32, 64);
+    if constexpr (RU == 8) ssq += __shfl_xor(ssq, 8, 64);
     red_ss[wave][lane] = ssq;
     __syncthreads();
     float t = 0.f;
@@ -371,8 +390,27 @@ int dlinear_stream_launch(const DecArgs& a, int tiles, hipStream_t s) {
   return (int)hipGetLastError();
 }
 
+// 8-row units for a projection of at most 8 token rows whose 16-row units would need two per
+// workgroup on fewer workgroups than CUs (256 < tiles <= 512).
+template <typename T, bool NORM, int KB>
+int dlinear_stream_r8(const DecArgs& a0, hipStream_t s) {
+  DecArgs a = a0;
+  int units = 0;
+  for (int i = 0; i < a.nseg; ++i) units += (a.seg[i].tiles = (a.seg[i].n + 7) / 8);
+  const int upw = stream_units_per_wg(units);
+  dlinear_stream_kernel<T, 0, NORM, 8, KB, 8><<<(unsigned)((units + upw - 1) / upw), 512, 0, s>>>(a, units);
+  return (int)hipGetLastError();
+}
+
 template <typename T, int MODE, bool NORM>
 int dlinear_stream_k(const DecArgs& a, int tiles, hipStream_t s) {
+  if constexpr (MODE == 0) {
+    if (a.M <= 8 && tiles > 256 && tiles <= 512) {
+      if (a.K == 1024) return dlinear_stream_r8<T, NORM, 1>(a, s);
+      if (a.K == 2048) return dlinear_stream_r8<T, NORM, 2>(a, s);
+      return dlinear_stream_r8<T, NORM, 4>(a, s);
+    }
+  }
   if (a.K == 1024) return dlinear_stream_launch<T, MODE, NORM, 1>(a, tiles, s);
   if (a.K == 2048) return dlinear_stream_launch<T, MODE, NORM, 2>(a, tiles, s);
   return dlinear_stream_launch<T, MODE, NORM, 4>(a, tiles, s);

@@ -55,6 +55,29 @@ def test_decode_linear_modes(m, k, norm):
     assert torch.equal(y2, K.decode_linear(x.cuda(), [g.cuda(), u.cuda()], mode=2, **kw))  # deterministic
 
 
+@pytest.mark.parametrize("m", [1, 5, 8, 9])
+@pytest.mark.parametrize("k", [4096, 2048, 1024])
+@pytest.mark.parametrize("norm", [False, True])
+def test_decode_linear_eight_row_units(m, k, norm):
+    """Projections with 256 < 16-row tiles <= 512 (the Q/K/V launch) run on 8-row units for at most 8
+    token rows: ragged segment ends, every row of every segment checked against fp64 math."""
+    print(f"decode_linear 8-row units m={m} k={k} norm={norm}", flush=True)
+    gen = seeded(m * 11 + k + int(norm))
+    dt = torch.bfloat16
+    x = randn(m, k, gen=gen, dtype=dt)
+    nw = (1.0 + 0.1 * randn(k, gen=gen)).to(dt)
+    ws = [randn(n, k, gen=gen, dtype=dt, scale=0.02) for n in (4096, 1024, 1028)]
+    xn = O.rms_norm_reference(x, nw, 1e-6, dtype=torch.float64).to(dt) if norm else x
+    ys = K.decode_linear(x.cuda(), [w.cuda() for w in ws], norm_weight=nw.cuda() if norm else None, eps=1e-6)
+    for y, w in zip(ys, ws):
+        e = xn.double() @ w.double().t()
+        assert y.shape == e.shape
+        assert max_rel(y, e) <= 1e-2
+        # row-wise too: a wrong unit or k-half mapping would corrupt whole rows of a segment
+        err = (y.double().cpu() - e).abs().amax(dim=0) / e.abs().amax()
+        assert float(err.max()) <= 2e-2
+
+
 def test_kv_append():
     gen = seeded(1)
     k = randn(2, 5, 3, 128, gen=gen, dtype=torch.bfloat16)
