@@ -294,7 +294,7 @@ int q3_kv_append(int dtype, const void* k, const void* v, void* cache_k, void* c
                  int64_t H, int64_t D, int64_t capacity, int64_t start, const int64_t* start_dev,
                  hipStream_t stream);
 /* One query per (b, head) against the first T_len cached positions (D = 128, Hq/Hkv <= 8): one
- * workgroup per (b, kv head, 64-key split) serves the whole GQA group,
+ * workgroup per (b, kv head, 128-key split) serves the whole GQA group,
  * then a fixed-order merge of the split partials.  q/out element strides (batch, head);
  * cache strides (ksb, ksh) with position stride D.  With len_dev non-NULL, T_len = *len_dev + 1 is
  * read at run time and the launch covers the whole capacity (workspace sized for T_len = capacity).
@@ -324,7 +324,7 @@ int q3_decode_step_attention(int dtype, const void* q, int64_t qsb, int64_t qsh,
  * process ends), so the call allocates nothing.  No counterpart in the reference: it is for callers that cannot allocate
  * device memory (code under HIP graph capture, serving loops that forbid allocation).  The
  * limit is q3_decode_attention_workspace_bytes(B, Hq, Hkv, span) <= Q3_NOALLOC_SCRATCH_BYTES, span =
- * capacity when len_dev is given, else T_len (B 8 x Hq 32 fits a span of 8064 positions);
+ * capacity when len_dev is given, else T_len (B 8 x Hq 32 fits a span of 16128 positions);
  * larger requests return Q3_ERR_SCRATCH before any launch.  Every call on one GPU shares that
  * GPU's array, so calls that overlap on one GPU (concurrent streams or threads) race; calls in
  * one stream are ordered and safe.  Arguments and results otherwise as q3_decode_step_attention

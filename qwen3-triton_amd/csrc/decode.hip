@@ -452,11 +452,10 @@ __global__ __launch_bounds__(kThreads) void kv_append_kernel(const u16* __restri
 }
 
 // ============================================================================ decode attention
-// One workgroup (4 waves) per (b, kv head, split of kSplit = 64 cached keys) computes all G query
-// heads of the GQA group, so every K/V byte is read once; each wave owns 16 keys and issues all of
-// its K and V loads before using any.  A second kernel merges the splits in fixed order
+// One workgroup (NWV waves) per (b, kv head, split of 16 NWV cached keys) computes all G
+// query heads of the GQA group, so every K/V byte is read once; each wave owns 16 keys and issues all
+// of its K and V loads before using any.  A second kernel merges the splits in fixed order
 // (deterministic).
-constexpr int kSplit = 64;
 
 struct DecAttnArgs {
   const u16* q;  // [B, Hq, D] at strides (qsb, qsh)
@@ -489,8 +488,8 @@ struct DecAttnArgs {
 // columns); the accumulator layout of S^T (lane: head l % 16, keys 4 (l / 16) .. + 3) is exactly the
 // A-operand layout of P for O = P V on v_mfma_f32_16x16x16, whose V operand (4 consecutive keys of
 // one dimension per lane) comes from the wave's V tile in LDS through the gfx950 transpose read.
-// The softmax max and sum are formed per head over the workgroup's 64 keys (lane butterflies, then
-// the 4 waves through LDS); P is rounded to the storage type for the P V product, as in the
+// The softmax max and sum are formed per head over the workgroup's 16 NWV keys (lane butterflies,
+// then the waves through LDS); P is rounded to the storage type for the P V product, as in the
 // prefill kernels.
 typedef short v4s_t __attribute__((ext_vector_type(4)));
 typedef _Float16 v4h_t __attribute__((ext_vector_type(4)));
@@ -517,14 +516,15 @@ Q3_DEV void norm_rope2(float& x0, float& x1, uint32_t w, uint32_t cs, uint32_t s
   x1 = to_f32<T>(from_f32<T>(n1 * to_f32<T>((u16)(cs >> 16)) + sign * p1 * to_f32<T>((u16)(sn >> 16))));
 }
 
-template <typename T, int G, bool FUSED>
-__global__ __launch_bounds__(256) void decode_attn_mfma_kernel(DecAttnArgs a) {
-  constexpr int D = 128, KPW = kSplit / 4, HPW = (G + 3) / 4;  // keys and query heads per wave
-  __shared__ __attribute__((aligned(16))) u16 vt[4][KPW * D];  // per-wave V tile, 16-byte chunks swizzled
+template <typename T, int G, bool FUSED, int NWV>
+__global__ __launch_bounds__(NWV * 64) void decode_attn_mfma_kernel(DecAttnArgs a) {
+  constexpr int D = 128, KPW = 16, HPW = (G + NWV - 1) / NWV;  // keys and query heads per wave
+  constexpr int kSplit = KPW * NWV;
+  __shared__ __attribute__((aligned(16))) u16 vt[NWV][KPW * D];  // per-wave V tile, 16-byte chunks swizzled
   __shared__ __attribute__((aligned(16))) u16 qs[G][D];
   __shared__ __attribute__((aligned(16))) u16 knew[D];
-  __shared__ float wred[2][4][16];
-  __shared__ float red_o[4][G][D];
+  __shared__ float wred[2][NWV][16];
+  __shared__ float red_o[NWV][G][D];
   const int split = blockIdx.x, bk = blockIdx.y, b = bk / a.Hkv, hk = bk % a.Hkv;
   const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int r = lane & 15, kq = lane >> 4;
@@ -545,7 +545,7 @@ __global__ __launch_bounds__(256) void decode_attn_mfma_kernel(DecAttnArgs a) {
   uint32_t qraw[HPW];
 #pragma unroll
   for (int i = 0; i < HPW; ++i) {
-    const int h = min(wave + 4 * i, G - 1);
+    const int h = min(wave + NWV * i, G - 1);
     qraw[i] = *reinterpret_cast<const uint32_t*>(a.q + b * a.qsb + (int64_t)(hk * G + h) * a.qsh + 2 * lane);
   }
   uint32_t kraw = 0u, vraw = 0u, qwv = 0u, kwv = 0u, csv = 0u, snv = 0u;
@@ -570,7 +570,7 @@ __global__ __launch_bounds__(256) void decode_attn_mfma_kernel(DecAttnArgs a) {
   // query rows of this wave's heads (normalised + rotated when fused) -> LDS
 #pragma unroll
   for (int i = 0; i < HPW; ++i) {
-    const int h = wave + 4 * i;
+    const int h = wave + NWV * i;
     if (h < G) {
       float x0 = to_f32<T>((u16)(qraw[i] & 0xffffu)), x1 = to_f32<T>((u16)(qraw[i] >> 16));
       if constexpr (FUSED) norm_rope2<T>(x0, x1, qwv, csv, snv, lane, a.eps);
@@ -619,7 +619,9 @@ __global__ __launch_bounds__(256) void decode_attn_mfma_kernel(DecAttnArgs a) {
   mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
   if (kq == 0) wred[0][wave][r] = mx;
   __syncthreads();
-  const float m = fmaxf(fmaxf(wred[0][0][r], wred[0][1][r]), fmaxf(wred[0][2][r], wred[0][3][r]));
+  float m = wred[0][0][r];
+#pragma unroll
+  for (int w = 1; w < NWV; ++w) m = fmaxf(m, wred[0][w][r]);
   float p[4];
 #pragma unroll
   for (int e = 0; e < 4; ++e) p[e] = m == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(sv[e] - m);
@@ -648,13 +650,22 @@ __global__ __launch_bounds__(256) void decode_attn_mfma_kernel(DecAttnArgs a) {
       if (4 * kq + e < G) red_o[wave][4 * kq + e][16 * db + r] = o[db][e];
   __syncthreads();
   const int64_t pbase = ((int64_t)bk * a.splits + split) * G;
-  for (int i = tid; i < G * D; i += 256) {
+  for (int i = tid; i < G * D; i += NWV * 64) {
     const int g = i / D, d = i % D;
-    a.opart[(pbase + g) * D + d] = red_o[0][g][d] + red_o[1][g][d] + red_o[2][g][d] + red_o[3][g][d];
+    float o = red_o[0][g][d];
+#pragma unroll
+    for (int w = 1; w < NWV; ++w) o += red_o[w][g][d];
+    a.opart[(pbase + g) * D + d] = o;
   }
   if (tid < G) {
-    a.mpart[pbase + tid] = fmaxf(fmaxf(wred[0][0][tid], wred[0][1][tid]), fmaxf(wred[0][2][tid], wred[0][3][tid]));
-    a.lpart[pbase + tid] = (wred[1][0][tid] + wred[1][1][tid]) + (wred[1][2][tid] + wred[1][3][tid]);
+    float mx2 = wred[0][0][tid], l = wred[1][0][tid];
+#pragma unroll
+    for (int w = 1; w < NWV; ++w) {
+      mx2 = fmaxf(mx2, wred[0][w][tid]);
+      l += wred[1][w][tid];
+    }
+    a.mpart[pbase + tid] = mx2;
+    a.lpart[pbase + tid] = l;
   }
 }
 
@@ -798,13 +809,16 @@ __global__ void advance_kernel(int64_t* counter, int64_t by) { *counter += by; }
 
 bool al16(const void* p) { return ((uintptr_t)p & 15) == 0; }
 
+// Keys per split: 128 (8 waves of 16 keys).  Measured in the captured 36-layer step (2048 + 128-token
+// B1, 1024 + 128-token B8): 64-key splits 3.376 / 3.851 ms, 128: 3.346 / 3.836, 256: 3.444 / 4.049.
+constexpr int kSplitWaves = 8, kSplitKeys = 16 * kSplitWaves;
 // Workspace: per (b, kv head, split, head of the group) 128 partial outputs, then the maxima, then
 // the sums.
-int64_t decode_splits(int64_t span) { return (span + kSplit - 1) / kSplit; }
+int64_t decode_splits(int64_t span) { return (span + kSplitKeys - 1) / kSplitKeys; }
 
 template <typename T, int G, bool FUSED>
 int decode_g(const DecAttnArgs& a, dim3 grid, void* out, int64_t osb, int64_t osh, hipStream_t s) {
-  decode_attn_mfma_kernel<T, G, FUSED><<<grid, 256, 0, s>>>(a);
+  decode_attn_mfma_kernel<T, G, FUSED, kSplitWaves><<<grid, kSplitWaves * 64, 0, s>>>(a);
   decode_merge_kernel<T, G><<<grid.y * G, 512, 0, s>>>(a.opart, a.mpart, a.lpart, (u16*)out, osb, osh, a.Hkv * G,
                                                        a.splits);
   return (int)hipGetLastError();
@@ -832,7 +846,7 @@ int decode_attn_setup(DecAttnArgs& a, dim3& grid, int dtype, const void* q, int6
                       int64_t capacity, int64_t D, float scale) {
   Q3_REQUIRE((dtype == Q3_BF16 || dtype == Q3_F16) && q && cache_k && cache_v && out && workspace && B > 0 &&
              Hq > 0 && Hkv > 0 && Hq % Hkv == 0 && Hq / Hkv <= 8 && T_len > 0 && T_len <= capacity && D == 128 &&
-             B * Hkv < 65536 && (len_dev ? capacity : T_len) <= 1024 * kSplit);
+             B * Hkv < 65536 && decode_splits(len_dev ? capacity : T_len) <= 1024);
   Q3_REQUIRE(al16(q) && al16(cache_k) && al16(cache_v) && qsh % 8 == 0 && qsb % 8 == 0 && ksb % 8 == 0 && ksh % 8 == 0);
   // A device-resident length launches the fixed split count of the whole capacity (graph replay).
   const int64_t splits = decode_splits(len_dev ? capacity : T_len);

@@ -54,8 +54,9 @@ def test_noalloc_decode_attention_rejects_oversize_before_any_gpu_call():
     lib = H.load()
     assert b"scratch" in lib.q3_error_string(100001)
     limit = 16 << 20
-    assert H.query("q3_decode_attention_workspace_bytes", 8, 32, 8, 8064) <= limit
-    assert H.query("q3_decode_attention_workspace_bytes", 8, 32, 8, 8128) > limit
+    # 128-key splits: B 8 x Hq 32 fits 126 splits
+    assert H.query("q3_decode_attention_workspace_bytes", 8, 32, 8, 16128) <= limit
+    assert H.query("q3_decode_attention_workspace_bytes", 8, 32, 8, 16129) > limit
     args = [2, None, 0, 0, None, None, 0, 0, None, None, 1e-6, None, None, 0, None, None, 0, 0, None, 0, 0,
-            8, 32, 8, 8128, None, 8128, 128, 0.088, None]
+            8, 32, 8, 16256, None, 16256, 128, 0.088, None]
     assert lib.q3_decode_step_attention_noalloc(*args) == 100001
