@@ -374,7 +374,8 @@ def attention_bench(reps=10):
 
 def bandwidth_bench(reps=20):
     """Config #2: the bandwidth-bound ops at Qwen3-8B shape, bf16 (seed 1): RMSNorm on [8192, 4096],
-    fused per-head QK-norm + RoPE on Q [8192, 32, 128] and K [8192, 8, 128], RoPE on Q, SwiGLU on
+    fused per-head QK-norm + RoPE on Q [8192, 32, 128] and K [8192, 8, 128] (each alone, and both in
+    one launch as the layer runs them), RoPE on Q, SwiGLU on
     [8192, 12288].  Kernel launches on preallocated buffers; achieved = algorithmic HBM bytes (each
     operand read or written once: x/y 2 B per element, plus weights and rotary tables) / time."""
     import torch
@@ -406,6 +407,7 @@ def bandwidth_bench(reps=20):
     inv = (1.0 / (1e6 ** (torch.arange(0, 128, 2, dtype=torch.float32) / 128))).cuda()
     cos, sin = _ops.rope_tables(pos, inv, bf)
     tab = 2 * 2 * t * 128
+    keep = {}
     for name, heads in (("q", 32), ("k", 8)):
         xq = torch.randn(4, 2048, heads, 128, device="cuda", dtype=bf, generator=gen)
         wq = (1 + 0.1 * torch.randn(128, device="cuda", generator=gen)).to(bf)
@@ -422,7 +424,20 @@ def bandwidth_bench(reps=20):
             rec("rope_fwd_q", _event_ms(lambda: H.call("q3_rope_apply", H.BF16, xq.data_ptr(), cos.data_ptr(),
                                                        sin.data_ptr(), yq.data_ptr(), 4, 2048, heads, 128, 0, 0, st),
                                         reps), 2 * 2 * n + tab)
-        del xq, yq, dyq, dxq
+        keep[name] = (xq, wq, yq, dyq, dxq)
+    # the layer's Q and K heads in one launch per direction (q3_norm_rope_qk_*)
+    (xq, wq, yq, dyq, dxq), (xk, wk, yk, dyk, dxk) = keep["q"], keep["k"]
+    dwqk = torch.empty(2, 128, device="cuda", dtype=bf)
+    wsqk = H.workspace(H.query("q3_norm_rope_qk_bwd_workspace_bytes", t, 32, 8, 128), xq.device)
+    n = xq.numel() + xk.numel()
+    rec("qk_norm_rope_fwd_qk", _event_ms(lambda: H.call(
+        "q3_norm_rope_qk_fwd", H.BF16, xq.data_ptr(), xk.data_ptr(), wq.data_ptr(), wk.data_ptr(), cos.data_ptr(),
+        sin.data_ptr(), yq.data_ptr(), yk.data_ptr(), t, 32, 8, 128, 1e-6, st), reps), 2 * 2 * n + tab)
+    rec("qk_norm_rope_bwd_qk", _event_ms(lambda: H.call(
+        "q3_norm_rope_qk_bwd", H.BF16, xq.data_ptr(), xk.data_ptr(), wq.data_ptr(), wk.data_ptr(), cos.data_ptr(),
+        sin.data_ptr(), dyq.data_ptr(), dyk.data_ptr(), dxq.data_ptr(), dxk.data_ptr(), dwqk.data_ptr(),
+        wsqk.data_ptr(), t, 32, 8, 128, 1e-6, st), reps), 3 * 2 * n + tab)
+    del keep, xq, yq, dyq, dxq, xk, yk, dyk, dxk
     g = torch.randn(t, 12288, device="cuda", dtype=bf, generator=gen)
     u = torch.randn(t, 12288, device="cuda", dtype=bf, generator=gen)
     dyg, yg, dg, du = torch.randn_like(g), torch.empty_like(g), torch.empty_like(g), torch.empty_like(g)

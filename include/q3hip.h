@@ -71,6 +71,23 @@ size_t q3_norm_rope_bwd_workspace_bytes(int64_t tokens, int64_t heads, int64_t d
 int q3_norm_rope_bwd(int dtype, const void* x, const void* w, const void* cos, const void* sin, const void* dy,
                      void* dx, void* dw, void* workspace, int64_t tokens, int64_t heads, int64_t d, float eps,
                      hipStream_t stream);
+/* The query and key tensors of one layer in one launch per direction (same per-row arithmetic, so
+ * yq / yk and dxq / dxk are bit-identical to two q3_norm_rope_fwd / _bwd calls): q [tokens, hq, d]
+ * with weight wq, k [tokens, hk, d] with wk, shared cos/sin [tokens, d].  dw is [2, d]: dW_q, then
+ * dW_k (deterministic; the fp32 summation order differs from the single-tensor call).  Vector path
+ * only (d / 2 a multiple of 8 for 16-bit types, 4 for fp32, d / vector width in {8, 16, 32}); other
+ * shapes return Q3_ERR_INVALID.
+ * Replaces: ops/triton/fused_qk_norm_rope.py:237-273 (_FusedQKNormRoPEFunction, one launch per
+ *           tensor there), its forward _fused_one (:68-109) and backward _fused_backward_one
+ *           (:191-235) for the pair. */
+int q3_norm_rope_qk_fwd(int dtype, const void* q, const void* k, const void* wq, const void* wk, const void* cos,
+                        const void* sin, void* yq, void* yk, int64_t tokens, int64_t hq, int64_t hk, int64_t d,
+                        float eps, hipStream_t stream);
+size_t q3_norm_rope_qk_bwd_workspace_bytes(int64_t tokens, int64_t hq, int64_t hk, int64_t d);
+int q3_norm_rope_qk_bwd(int dtype, const void* q, const void* k, const void* wq, const void* wk, const void* cos,
+                        const void* sin, const void* dyq, const void* dyk, void* dxq, void* dxk, void* dw,
+                        void* workspace, int64_t tokens, int64_t hq, int64_t hk, int64_t d, float eps,
+                        hipStream_t stream);
 
 /* ------------------------------------------------------------------ RoPE
  * cos/sin[t, j] = cos/sin(fp32(pos[t]) * inv_freq[j mod d/2]) for j < d, stored in `dtype`.

@@ -469,10 +469,160 @@ __global__ __launch_bounds__(kBlock) void norm_rope_bwd_kernel(const typename T:
   }
 }
 
+// ---------------------------------------------------------------- Q and K heads in one launch
+// The query- and key-head halves of a layer's QK-norm + RoPE share the rotary tables and the row
+// shape, so one launch covers both: workgroups [0, blocks[0]) take the query-head rows, the others
+// the key-head rows (the split proportional to the row counts), each segment with its own input,
+// weight, gradient and output.  Per row the arithmetic is that of norm_rope_fwd_kernel /
+// norm_rope_bwd_kernel (bit-identical y and dx); each backward workgroup writes one partial row of
+// 2 D floats ([dW_q | dW_k], zeros in the other segment's half), reduced by one column sum.
+template <typename S> struct NrPair {
+  const S* x[2];
+  const S* w[2];
+  const S* dy[2];
+  S* y[2];  // forward output or input gradient
+  int64_t rows[2];
+  int heads[2];
+  int blocks[2];  // workgroups per segment
+};
+
+template <typename T, int TPR>
+__global__ __launch_bounds__(kBlock) void norm_rope_qk_fwd_kernel(NrPair<typename T::storage> p,
+                                                                  const typename T::storage* __restrict__ cs,
+                                                                  const typename T::storage* __restrict__ sn,
+                                                                  float eps) {
+  constexpr int V = T::vec, D = TPR * V, RPB = kBlock / TPR;
+  const int seg = (int)blockIdx.x >= p.blocks[0] ? 1 : 0;
+  const int blk = (int)blockIdx.x - (seg ? p.blocks[0] : 0), nblk = p.blocks[seg];
+  const typename T::storage* __restrict__ x = p.x[seg];
+  typename T::storage* __restrict__ y = p.y[seg];
+  const int64_t rows = p.rows[seg];
+  const int heads = p.heads[seg];
+  const int t = threadIdx.x % TPR, g = threadIdx.x / TPR;
+  const float sign = (t < TPR / 2) ? -1.f : 1.f;
+  const Vec<T> wv = load_vec<T>(p.w[seg] + t * V);
+  for (int64_t base = (int64_t)blk * RPB; base < rows; base += (int64_t)nblk * RPB) {
+    const int64_t row = base + g;
+    const bool valid = row < rows;
+    const int64_t tok = row / heads;
+    Vec<T> xv, cv, sv;
+    float ss = 0.f;
+    if (valid) {
+      xv = load_vec<T>(x + row * D + t * V);
+      cv = load_vec<T>(cs + tok * D + t * V);
+      sv = load_vec<T>(sn + tok * D + t * V);
+#pragma unroll
+      for (int e = 0; e < V; ++e) ss += xv.v[e] * xv.v[e];
+    }
+    const float inv = rsqrtf(group_sum<TPR>(ss) * (1.f / D) + eps);
+    Vec<T> o;
+#pragma unroll
+    for (int e = 0; e < V; ++e) {
+      const float n = xv.v[e] * inv * wv.v[e];
+      const float np = partner<TPR>(n);
+      o.v[e] = n * cv.v[e] + sign * np * sv.v[e];
+    }
+    if (valid) store_vec<T>(y + row * D + t * V, o);
+  }
+}
+
+template <typename T, int TPR>
+__global__ __launch_bounds__(kBlock) void norm_rope_qk_bwd_kernel(NrPair<typename T::storage> p,
+                                                                  const typename T::storage* __restrict__ cs,
+                                                                  const typename T::storage* __restrict__ sn,
+                                                                  float* __restrict__ partial, float eps) {
+  constexpr int V = T::vec, D = TPR * V, RPB = kBlock / TPR;
+  __shared__ float fold[kBlock / 64][D];
+  const int seg = (int)blockIdx.x >= p.blocks[0] ? 1 : 0;
+  const int blk = (int)blockIdx.x - (seg ? p.blocks[0] : 0), nblk = p.blocks[seg];
+  const typename T::storage* __restrict__ x = p.x[seg];
+  const typename T::storage* __restrict__ dy = p.dy[seg];
+  typename T::storage* __restrict__ dx = p.y[seg];
+  const int64_t rows = p.rows[seg];
+  const int heads = p.heads[seg];
+  const int t = threadIdx.x % TPR, g = threadIdx.x / TPR;
+  const float sign = (t < TPR / 2) ? 1.f : -1.f;
+  const Vec<T> wv = load_vec<T>(p.w[seg] + t * V);
+  float acc[V];
+#pragma unroll
+  for (int e = 0; e < V; ++e) acc[e] = 0.f;
+  // U rows per thread and iteration (RPB apart), every load issued before the first use at clamped
+  // row indices (rows past the end are masked at the store and in the dw sum).
+  constexpr int U = 4;
+  for (int64_t base = (int64_t)blk * RPB * U; base < rows; base += (int64_t)nblk * RPB * U) {
+    i32x4 xr[U], gr[U], cr[U], sr[U];
+#pragma unroll
+    for (int j = 0; j < U; ++j) {
+      const int64_t rc = min(base + j * RPB + g, rows - 1), tok = rc / heads;
+      xr[j] = *reinterpret_cast<const i32x4*>(x + rc * D + t * V);
+      gr[j] = *reinterpret_cast<const i32x4*>(dy + rc * D + t * V);
+      cr[j] = *reinterpret_cast<const i32x4*>(cs + tok * D + t * V);
+      sr[j] = *reinterpret_cast<const i32x4*>(sn + tok * D + t * V);
+    }
+#pragma unroll
+    for (int j = 0; j < U; ++j) {
+      const int64_t row = base + j * RPB + g;
+      const bool valid = row < rows;
+      const Vec<T> xv = unpack_vec<T>(xr[j]), gv = unpack_vec<T>(gr[j]), cv = unpack_vec<T>(cr[j]),
+                   sv = unpack_vec<T>(sr[j]);
+      float ss = 0.f, dot = 0.f;
+      float ng[V];
+#pragma unroll
+      for (int e = 0; e < V; ++e) {
+        const float gs_p = partner<TPR>(gv.v[e] * sv.v[e]);  // dy[p] * sin[p]
+        ng[e] = gv.v[e] * cv.v[e] + sign * gs_p;
+        ss += xv.v[e] * xv.v[e];
+        dot += ng[e] * wv.v[e] * xv.v[e];
+      }
+      ss = group_sum<TPR>(ss);
+      dot = group_sum<TPR>(dot);
+      const float inv = rsqrtf(ss * (1.f / D) + eps);
+      const float c = inv * inv * inv * dot * (1.f / D);
+      Vec<T> o;
+#pragma unroll
+      for (int e = 0; e < V; ++e) {
+        o.v[e] = ng[e] * wv.v[e] * inv - xv.v[e] * c;
+        if (valid) acc[e] += ng[e] * xv.v[e] * inv;
+      }
+      if (valid) store_vec<T>(dx + row * D + t * V, o);
+    }
+  }
+  // Fold the RPB row groups (lane butterfly inside a wave, then the waves through LDS in wave order).
+#pragma unroll
+  for (int o = TPR; o < 64; o <<= 1)
+#pragma unroll
+    for (int e = 0; e < V; ++e) acc[e] += __shfl_xor(acc[e], o, 64);
+  const int wi = threadIdx.x >> 6;
+  if ((threadIdx.x & 63) < TPR) {
+#pragma unroll
+    for (int e = 0; e < V; ++e) fold[wi][t * V + e] = acc[e];
+  }
+  __syncthreads();
+  float* prow = partial + (int64_t)blockIdx.x * 2 * D;
+  for (int c = threadIdx.x; c < D; c += kBlock) {
+    float sum = fold[0][c];
+#pragma unroll
+    for (int w = 1; w < kBlock / 64; ++w) sum += fold[w][c];
+    prow[seg * D + c] = sum;
+    prow[(1 - seg) * D + c] = 0.f;
+  }
+}
+
 // ---------------------------------------------------------------- host-side planning
 int64_t bwd_blocks(int64_t rows, int64_t h) {
   const int64_t cap = h <= 256 ? 1024 : 512;
   return rows < cap ? (rows < 4 ? 4 : rows) : cap;  // >= 4: the scalar path writes 4 rows per workgroup
+}
+
+// Q/K pair backward: the workgroups of both segments together, split in proportion to the rows (at
+// least one per segment).
+int64_t qk_bwd_blocks(int64_t rq, int64_t rk, int64_t d) {
+  const int64_t nb = bwd_blocks(rq + rk, d);
+  return nb < 2 ? 2 : nb;
+}
+int64_t qk_bwd_blocks_q(int64_t rq, int64_t rk, int64_t d) {
+  const int64_t nb = qk_bwd_blocks(rq, rk, d), bq = (nb * rq + (rq + rk) / 2) / (rq + rk);
+  return bq < 1 ? 1 : bq > nb - 1 ? nb - 1 : bq;
 }
 
 // The scalar backward writes 4 partial rows per workgroup: a quarter of the workgroups keeps the
@@ -623,6 +773,85 @@ int nr_bwd_dispatch(const void* x, const void* w, const void* cs, const void* sn
   return (int)hipGetLastError();
 }
 
+// Both Q/K launches need the vector path (d / 2 a multiple of the vector width, 8 / 16 / 32 lanes
+// per row); other shapes return Q3_ERR_INVALID and the caller runs the two single-tensor launches.
+template <typename T>
+int nr_qk_fwd_dispatch(const NrPair<typename T::storage>& p, const void* cs, const void* sn, int64_t d, float eps,
+                       hipStream_t s) {
+  constexpr int V = T::vec;
+  typedef typename T::storage S;
+  const int64_t tpr = d / V;
+  if (d % V != 0 || (d / 2) % V != 0 || (tpr != 8 && tpr != 16 && tpr != 32)) return Q3_ERR_INVALID;
+  // each segment's grid as its single-tensor launch sizes it
+  NrPair<S> q = p;
+  for (int i = 0; i < 2; ++i) {
+    const int64_t g = (p.rows[i] + kBlock / tpr - 1) / (kBlock / tpr);
+    q.blocks[i] = (int)(g > 256 * 16 ? 256 * 16 : g);
+  }
+  const unsigned grid = (unsigned)(q.blocks[0] + q.blocks[1]);
+  if (tpr == 8) norm_rope_qk_fwd_kernel<T, 8><<<grid, kBlock, 0, s>>>(q, (const S*)cs, (const S*)sn, eps);
+  else if (tpr == 16) norm_rope_qk_fwd_kernel<T, 16><<<grid, kBlock, 0, s>>>(q, (const S*)cs, (const S*)sn, eps);
+  else norm_rope_qk_fwd_kernel<T, 32><<<grid, kBlock, 0, s>>>(q, (const S*)cs, (const S*)sn, eps);
+  return (int)hipGetLastError();
+}
+
+template <typename T>
+int nr_qk_bwd_dispatch(const NrPair<typename T::storage>& p, const void* cs, const void* sn, void* dw, float* part,
+                       int64_t d, float eps, hipStream_t s) {
+  constexpr int V = T::vec;
+  typedef typename T::storage S;
+  const int64_t tpr = d / V, nb = qk_bwd_blocks(p.rows[0], p.rows[1], d);
+  if (d % V != 0 || (d / 2) % V != 0 || (tpr != 8 && tpr != 16 && tpr != 32)) return Q3_ERR_INVALID;
+  NrPair<S> q = p;
+  q.blocks[0] = (int)qk_bwd_blocks_q(p.rows[0], p.rows[1], d);
+  q.blocks[1] = (int)(nb - q.blocks[0]);
+  if (tpr == 8) norm_rope_qk_bwd_kernel<T, 8><<<(unsigned)nb, kBlock, 0, s>>>(q, (const S*)cs, (const S*)sn, part, eps);
+  else if (tpr == 16)
+    norm_rope_qk_bwd_kernel<T, 16><<<(unsigned)nb, kBlock, 0, s>>>(q, (const S*)cs, (const S*)sn, part, eps);
+  else norm_rope_qk_bwd_kernel<T, 32><<<(unsigned)nb, kBlock, 0, s>>>(q, (const S*)cs, (const S*)sn, part, eps);
+  colsum<T>(part, (S*)dw, (int)nb, (int)(2 * d), s);
+  return (int)hipGetLastError();
+}
+
+template <typename T>
+int nr_qk_fwd_t(const void* q, const void* k, const void* wq, const void* wk, const void* cs, const void* sn, void* yq,
+                void* yk, int64_t tokens, int64_t hq, int64_t hk, int64_t d, float eps, hipStream_t s) {
+  typedef typename T::storage S;
+  NrPair<S> p{};
+  p.x[0] = (const S*)q;
+  p.x[1] = (const S*)k;
+  p.w[0] = (const S*)wq;
+  p.w[1] = (const S*)wk;
+  p.y[0] = (S*)yq;
+  p.y[1] = (S*)yk;
+  p.rows[0] = tokens * hq;
+  p.rows[1] = tokens * hk;
+  p.heads[0] = (int)hq;
+  p.heads[1] = (int)hk;
+  return nr_qk_fwd_dispatch<T>(p, cs, sn, d, eps, s);
+}
+
+template <typename T>
+int nr_qk_bwd_t(const void* q, const void* k, const void* wq, const void* wk, const void* cs, const void* sn,
+                const void* dyq, const void* dyk, void* dxq, void* dxk, void* dw, float* part, int64_t tokens,
+                int64_t hq, int64_t hk, int64_t d, float eps, hipStream_t s) {
+  typedef typename T::storage S;
+  NrPair<S> p{};
+  p.x[0] = (const S*)q;
+  p.x[1] = (const S*)k;
+  p.w[0] = (const S*)wq;
+  p.w[1] = (const S*)wk;
+  p.dy[0] = (const S*)dyq;
+  p.dy[1] = (const S*)dyk;
+  p.y[0] = (S*)dxq;
+  p.y[1] = (S*)dxk;
+  p.rows[0] = tokens * hq;
+  p.rows[1] = tokens * hk;
+  p.heads[0] = (int)hq;
+  p.heads[1] = (int)hk;
+  return nr_qk_bwd_dispatch<T>(p, cs, sn, dw, part, d, eps, s);
+}
+
 bool dtype_ok(int dt) { return dt == Q3_F32 || dt == Q3_F16 || dt == Q3_BF16; }
 
 }  // namespace
@@ -677,6 +906,31 @@ int q3_norm_rope_bwd(int dtype, const void* x, const void* w, const void* cos, c
              d > 0 && d % 2 == 0 && d <= 4096 && eps > 0.f);
   return Q3_DISPATCH(dtype, nr_bwd_dispatch, x, w, cos, sin, dy, dx, dw, (float*)workspace, tokens * heads, heads, d,
                      eps, stream);
+}
+
+int q3_norm_rope_qk_fwd(int dtype, const void* q, const void* k, const void* wq, const void* wk, const void* cos,
+                        const void* sin, void* yq, void* yk, int64_t tokens, int64_t hq, int64_t hk, int64_t d,
+                        float eps, hipStream_t stream) {
+  Q3_REQUIRE(dtype_ok(dtype) && q && k && wq && wk && cos && sin && yq && yk && tokens > 0 && hq > 0 && hk > 0 &&
+             d > 0 && d % 2 == 0 && d <= 4096 && eps > 0.f && tokens * (hq + hk) < (1ll << 40));
+  return Q3_DISPATCH(dtype, nr_qk_fwd_t, q, k, wq, wk, cos, sin, yq, yk, tokens, hq, hk, d, eps, stream);
+}
+
+size_t q3_norm_rope_qk_bwd_workspace_bytes(int64_t tokens, int64_t hq, int64_t hk, int64_t d) {
+  if (tokens <= 0 || hq <= 0 || hk <= 0 || d <= 0) return 0;
+  const int64_t nb = qk_bwd_blocks(tokens * hq, tokens * hk, d);
+  return (size_t)nb * (size_t)(2 * d) * sizeof(float);
+}
+
+int q3_norm_rope_qk_bwd(int dtype, const void* q, const void* k, const void* wq, const void* wk, const void* cos,
+                        const void* sin, const void* dyq, const void* dyk, void* dxq, void* dxk, void* dw,
+                        void* workspace, int64_t tokens, int64_t hq, int64_t hk, int64_t d, float eps,
+                        hipStream_t stream) {
+  Q3_REQUIRE(dtype_ok(dtype) && q && k && wq && wk && cos && sin && dyq && dyk && dxq && dxk && dw && workspace &&
+             tokens > 0 && hq > 0 && hk > 0 && d > 0 && d % 2 == 0 && d <= 4096 && eps > 0.f &&
+             tokens * (hq + hk) < (1ll << 40));
+  return Q3_DISPATCH(dtype, nr_qk_bwd_t, q, k, wq, wk, cos, sin, dyq, dyk, dxq, dxk, dw, (float*)workspace, tokens,
+                     hq, hk, d, eps, stream);
 }
 
 }  // extern "C"

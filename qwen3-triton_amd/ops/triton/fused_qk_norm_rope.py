@@ -1,7 +1,6 @@
 """``ops/triton/fused_qk_norm_rope.py:237-273``: fused Q/K RMSNorm + RoPE, q/k [B,S,H,D]."""
-import torch
 
-from qwen3_triton.kernels import _ops
+from qwen3_triton.kernels.norm_rope import norm_rope_pair
 
 
 def _check(x, w, cos, sin):
@@ -14,32 +13,9 @@ def _check(x, w, cos, sin):
         raise TypeError("weight and cos/sin must have the dtype of x")
 
 
-class _FusedQKNormRoPEFunction(torch.autograd.Function):
-    @staticmethod
-    def forward(ctx, q, k, q_weight, k_weight, cos, sin, eps):
-        for x, w in ((q, q_weight), (k, k_weight)):
-            _check(x, w, cos, sin)
-        q, k = q.contiguous(), k.contiguous()
-        qw, kw = q_weight.contiguous().view(-1), k_weight.contiguous().view(-1)
-        cos, sin = cos.contiguous(), sin.contiguous()
-        ctx.save_for_backward(q, k, qw, kw, cos, sin)
-        ctx.eps = eps
-        ctx.shapes = (q_weight.shape, k_weight.shape)
-        return _ops.norm_rope_fwd(q, qw, cos, sin, eps), _ops.norm_rope_fwd(k, kw, cos, sin, eps)
-
-    @staticmethod
-    def backward(ctx, grad_q, grad_k):
-        q, k, qw, kw, cos, sin = ctx.saved_tensors
-        dq = dk = dqw = dkw = None
-        if grad_q is not None:
-            dq, dqw = _ops.norm_rope_bwd(q, qw, cos, sin, grad_q.contiguous(), ctx.eps)
-            dqw = dqw.view(ctx.shapes[0])
-        if grad_k is not None:
-            dk, dkw = _ops.norm_rope_bwd(k, kw, cos, sin, grad_k.contiguous(), ctx.eps)
-            dkw = dkw.view(ctx.shapes[1])
-        return dq, dk, dqw, dkw, None, None, None
-
-
 def fused_qk_norm_rope_triton(q, k, q_weight, k_weight, cos, sin, eps=1e-6):
-    """Fused Q/K RMSNorm + RoPE, one HIP launch per tensor."""
-    return _FusedQKNormRoPEFunction.apply(q, k, q_weight, k_weight, cos, sin, eps)
+    """Fused Q/K RMSNorm + RoPE: one HIP launch for both tensors per direction (one per tensor for
+    shapes outside the vector path)."""
+    for x, w in ((q, q_weight), (k, k_weight)):
+        _check(x, w, cos, sin)
+    return norm_rope_pair(q, k, q_weight, k_weight, cos, sin, eps)

@@ -18,6 +18,7 @@ from .kernels.linear import linear_residual, shared_input_projections
 from .kernels.math_precision import norm_rope, rms_norm
 from .kernels.mlp_precision import mlp_block
 from .kernels.norm import rms_norm_fork
+from .kernels.norm_rope import norm_rope_pair
 from .kernels.rotary import apply_rotary
 
 
@@ -42,7 +43,9 @@ class Attention(TritonAttention):
         q = q.view(b, s, self.num_heads, d)
         k = k.view(b, s, self.num_kv_heads, d)
         v = v.view(b, s, self.num_kv_heads, d)
-        if getattr(self.options, 'norm_rope_fusion', False):
+        if getattr(self.options, 'norm_rope_fusion', False) and self.q_norm.eps == self.k_norm.eps:
+            q, k = norm_rope_pair(q, k, self.q_norm.weight, self.k_norm.weight, cos, sin, self.q_norm.eps)
+        elif getattr(self.options, 'norm_rope_fusion', False):
             q = norm_rope(q, self.q_norm.weight, cos, sin, self.q_norm.eps)
             k = norm_rope(k, self.k_norm.weight, cos, sin, self.k_norm.eps)
         else:

@@ -71,6 +71,34 @@ def norm_rope_bwd(x, w, cos, sin, dy, eps):
     return dx, dw
 
 
+def norm_rope_qk_ok(q, k, d):
+    """Whether q3_norm_rope_qk_fwd / _bwd take this shape (the vector path of both tensors)."""
+    v = 4 if q.dtype == torch.float32 else 8
+    return d % 2 == 0 and (d // 2) % v == 0 and d // v in (8, 16, 32)
+
+
+def norm_rope_qk_fwd(q, k, wq, wk, cos, sin, eps):
+    """q [.., hq, d], k [.., hk, d] over the same tokens; one launch for both."""
+    d, hq, hk = q.shape[-1], q.shape[-2], k.shape[-2]
+    tokens = q.numel() // (d * hq)
+    yq, yk = torch.empty_like(q), torch.empty_like(k)
+    H.call("q3_norm_rope_qk_fwd", H.code(q.dtype), q.data_ptr(), k.data_ptr(), wq.data_ptr(), wk.data_ptr(),
+           cos.data_ptr(), sin.data_ptr(), yq.data_ptr(), yk.data_ptr(), tokens, hq, hk, d, float(eps), H.stream())
+    return yq, yk
+
+
+def norm_rope_qk_bwd(q, k, wq, wk, cos, sin, dyq, dyk, eps):
+    d, hq, hk = q.shape[-1], q.shape[-2], k.shape[-2]
+    tokens = q.numel() // (d * hq)
+    dxq, dxk = torch.empty_like(q), torch.empty_like(k)
+    dw = torch.empty((2, d), device=q.device, dtype=wq.dtype)
+    ws = H.workspace(H.query("q3_norm_rope_qk_bwd_workspace_bytes", tokens, hq, hk, d), q.device)
+    H.call("q3_norm_rope_qk_bwd", H.code(q.dtype), q.data_ptr(), k.data_ptr(), wq.data_ptr(), wk.data_ptr(),
+           cos.data_ptr(), sin.data_ptr(), dyq.data_ptr(), dyk.data_ptr(), dxq.data_ptr(), dxk.data_ptr(),
+           dw.data_ptr(), ws.data_ptr(), tokens, hq, hk, d, float(eps), H.stream())
+    return dxq, dxk, dw[0], dw[1]
+
+
 # ---------------------------------------------------------------- rope
 def rope_tables(position_ids, inv_freq, dtype):
     d = inv_freq.numel() * 2

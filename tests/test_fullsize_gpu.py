@@ -15,7 +15,7 @@ from _util import cosine, max_rel, randn, seeded
 
 from qwen3_triton.kernels.activation import swiglu
 from qwen3_triton.kernels.norm import rms_norm
-from qwen3_triton.kernels.norm_rope import norm_rope
+from qwen3_triton.kernels.norm_rope import norm_rope, norm_rope_pair
 from qwen3_triton.kernels.rotary import rotary_tables
 
 pytestmark = pytest.mark.gpu
@@ -69,6 +69,38 @@ def test_qk_norm_rope_full_size(heads):
     edx, _, edw, _ = O.fused_qk_norm_rope_backward_reference(x, x[:, :, :1], w, w, cf, sf, dy, dy[:, :, :1], 1e-6)
     check(dx, edx, f"norm_rope[{heads}] dx", T * heads)
     check(dw, edw, f"norm_rope[{heads}] dw", 1)
+
+
+def test_qk_norm_rope_pair_full_size():
+    """Q and K heads of the layer in one launch per direction: checked against the pair oracle row by
+    row, and y / dx bit-identical to the single-tensor launches (same per-row arithmetic)."""
+    gen = seeded(5)
+    q = randn(4, 2048, HQ, D, gen=gen, dtype=torch.bfloat16)
+    k = randn(4, 2048, HK, D, gen=gen, dtype=torch.bfloat16)
+    wq = randn(D, gen=gen, dtype=torch.bfloat16, scale=0.1, shift=1.0)
+    wk = randn(D, gen=gen, dtype=torch.bfloat16, scale=0.1, shift=1.0)
+    gq = randn(4, 2048, HQ, D, gen=gen, dtype=torch.bfloat16)
+    gk = randn(4, 2048, HK, D, gen=gen, dtype=torch.bfloat16)
+    pos = torch.arange(2048)[None].expand(4, 2048).contiguous()
+    cos, sin = rotary_tables(pos.cuda(), O.rope_inv_freq(1e6, D).cuda(), torch.bfloat16)
+    dev = [t.cuda().requires_grad_() for t in (q, k, wq, wk)]
+    yq, yk = norm_rope_pair(*dev, cos, sin, 1e-6)
+    dq, dk, dwq, dwk = torch.autograd.grad((yq, yk), dev, (gq.cuda(), gk.cuda()))
+    cf, sf = cos.float().cpu(), sin.float().cpu()
+    eq, ek = O.fused_qk_norm_rope_reference(q, k, wq, wk, cf, sf, 1e-6)
+    check(yq, eq, "pair yq", T * HQ)
+    check(yk, ek, "pair yk", T * HK)
+    edq, edk, edwq, edwk = O.fused_qk_norm_rope_backward_reference(q, k, wq, wk, cf, sf, gq, gk, 1e-6)
+    check(dq, edq, "pair dq", T * HQ)
+    check(dk, edk, "pair dk", T * HK)
+    check(dwq, edwq, "pair dwq", 1)
+    check(dwk, edwk, "pair dwk", 1)
+    for x, w, y, g, dx in ((dev[0], dev[2], yq, gq, dq), (dev[1], dev[3], yk, gk, dk)):
+        xs, ws = x.detach().clone().requires_grad_(), w.detach().clone().requires_grad_()
+        ys = norm_rope(xs, ws, cos, sin, 1e-6)
+        dxs, dws = torch.autograd.grad(ys, (xs, ws), g.cuda())
+        assert torch.equal(ys, y.detach()) and torch.equal(dxs, dx)
+        assert max_rel(dws, edwq if w is dev[2] else edwk) <= 2e-2
 
 
 def test_swiglu_8192x12288():
