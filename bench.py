@@ -30,10 +30,10 @@ PEAK_BF16_TFLOPS = 2500.0   # MI355X dense bf16 matrix-core peak
 PEAK_HBM_GBS = 8000.0       # MI355X HBM3E
 # HBM bytes per GEMM launch of the layer step, from two rocprofv3 counter passes over
 # `bench.py --pmc-probe` (FETCH_SIZE x 2.000 and WRITE_SIZE x 1.000: the factors that make a 1 GiB
-# device copy read 1 GiB), averaged over the step's 12 GEMM launches.  Re-measure with those two
-# passes (rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE -- python bench.py --pmc-probe) when the GEMM
-# kernels change.
-GEMM_TRAFFIC_BYTES_PER_LAUNCH = 1207.8e6 + 187.7e6
+# device copy read 1 GiB): every GEMM dispatch of one step (13: the Q/K/V weight gradient runs as two)
+# summed and divided by the step's 12 GEMM calls.  Re-measure with those two passes (rocprofv3 --pmc
+# FETCH_SIZE / WRITE_SIZE -- python bench.py --pmc-probe) when the GEMM kernels change.
+GEMM_TRAFFIC_BYTES_PER_LAUNCH = 1221.6e6 + 204.5e6
 
 
 def qwen3_8b_config(layers):
@@ -56,6 +56,9 @@ class GemmTimer:
         # the gate/up GEMM with the SwiGLU epilogue (two weights, one launch)
         self.gu_mods = [m for m in modules if hasattr(m, "gate_up_swiglu_into")]
         self.gu_orig = self.gu_mods[0].gate_up_swiglu_into if self.gu_mods else None
+        # the same with Y^T stored from the epilogue too (the MLP block's forward)
+        self.gt_mods = [m for m in modules if hasattr(m, "gate_up_swiglu_t_into")]
+        self.gt_orig = self.gt_mods[0].gate_up_swiglu_t_into if self.gt_mods else None
         # the shared-input projections (q/k/v: up to three weights, one launch)
         self.mu_mods = [m for m in modules if hasattr(m, "gemm_nt_multi_into")]
         self.mu_orig = self.mu_mods[0].gemm_nt_multi_into if self.mu_mods else None
@@ -87,6 +90,15 @@ class GemmTimer:
             s, e = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
             s.record()
             self.gu_orig(x, wg, wu, g, u, y, m, n, k)
+            e.record()
+            self.records.append((s, e, 2.0 * 2 * m * n * k))
+
+        def timed_gt(x, wg, wu, g, u, y, yt, m, n, k):
+            if not self.active:
+                return self.gt_orig(x, wg, wu, g, u, y, yt, m, n, k)
+            s, e = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            s.record()
+            self.gt_orig(x, wg, wu, g, u, y, yt, m, n, k)
             e.record()
             self.records.append((s, e, 2.0 * 2 * m * n * k))
 
@@ -125,6 +137,8 @@ class GemmTimer:
             m.swiglu_bwd_gemm_into = timed_sb
         for m in self.gu_mods:
             m.gate_up_swiglu_into = timed_gu
+        for m in self.gt_mods:
+            m.gate_up_swiglu_t_into = timed_gt
         for m in self.mu_mods:
             m.gemm_nt_multi_into = timed_mu
         return self
@@ -134,6 +148,8 @@ class GemmTimer:
             m.gemm_nt_into = self.orig
         for m in self.gu_mods:
             m.gate_up_swiglu_into = self.gu_orig
+        for m in self.gt_mods:
+            m.gate_up_swiglu_t_into = self.gt_orig
         for m in self.mu_mods:
             m.gemm_nt_multi_into = self.mu_orig
         for m in self.sb_mods:

@@ -177,6 +177,14 @@ int q3_gemm_nt_residual(int dtype, const void* A, int64_t lda, const void* B, in
 int q3_gemm_gate_up_swiglu(int dtype, const void* x, int64_t ldx, const void* wg, const void* wu, int64_t ldw,
                            void* g, void* u, void* y, int64_t ldo, int64_t M, int64_t N, int64_t K,
                            hipStream_t stream);
+/* q3_gemm_gate_up_swiglu that also stores Y^T [N, M] (row stride ldyt % 8 == 0, ldyt >= M) from the
+ * same epilogue: the operand the down projection's weight-gradient GEMM reads, so the backward needs no
+ * transpose pass over Y.  G, U, Y as q3_gemm_gate_up_swiglu (bit-identical); Y^T holds the same values.
+ * Replaces: kernels/mlp_precision.py:16-33 (the forward that feeds the block's backward; the
+ * reference's backward reads Y through a strided operand). */
+int q3_gemm_gate_up_swiglu_t(int dtype, const void* x, int64_t ldx, const void* wg, const void* wu, int64_t ldw,
+                             void* g, void* u, void* y, int64_t ldo, void* yt, int64_t ldyt, int64_t M, int64_t N,
+                             int64_t K, hipStream_t stream);
 /* Down-projection input gradient with the SwiGLU backward in its epilogue: dY = dy wt^T for
  * dy [M, K] and wt [N, K] (the transposed down weight: K-contiguous rows), rounded to dtype as a
  * standalone GEMM output, then dg = dY u s (1 + g (1 - s)), du = dY g s with s = sigmoid(g) for

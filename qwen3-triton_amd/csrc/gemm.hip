@@ -229,6 +229,9 @@ struct CeEpi {
   // EPI 0 (16-bit output, full 256 x 256 tiles): when set, C = res + the GEMM output (row stride ldres)
   const u16* res;
   int64_t ldres;
+  // EPI 3: when set, also Y^T [N, M] (row stride ldyt), the down projection's weight-gradient operand
+  u16* yt;
+  int64_t ldyt;
 };
 
 Q3_DEV void lse_merge(float& m, float& s, float m2, float s2) {
@@ -464,6 +467,32 @@ __global__ __launch_bounds__(WM * WN * 64) void gemm_nt_v4_kernel(const u16* __r
           stage(NC, i, p, pack2<T>(v[0], v[1]), pack2<T>(v[2], v[3]));
         }
       flush(NC, (out == 0 ? ce.g_out : out == 1 ? ce.u_out : C) + o0, ldc, std::integral_constant<int, TMW>{});
+    }
+    if (ce.yt) {
+      // Y^T from the Y block still staged in the wave's LDS ([TMW rows][NC columns], 16-byte chunks
+      // XOR-swizzled by row pair): the gfx950 transpose read gives lane j of a 16-lane group column
+      // t0 + j of 4 consecutive rows (lanes address row R0 + a / 4, columns t0 + 4 (a % 4)); two reads
+      // make 8 rows = one 16-byte store of a Y^T row.  Four groups take consecutive 8-row blocks.
+      typedef short v4s_t __attribute__((ext_vector_type(4)));
+      constexpr int NCV = decltype(NC)::value;
+      const int j = lane & 15, grp = lane >> 4;
+      const int64_t yrow0 = m0 + wm * TMW, ycol0 = (n0 + wn * TNW) / 2;
+#pragma unroll
+      for (int pi = 0; pi < (NCV / 16) * (TMW / 32); ++pi) {
+        const int t0 = 16 * (pi % (NCV / 16)), r0 = 32 * (pi / (NCV / 16)) + 8 * grp;
+        i32x4 v;
+#pragma unroll
+        for (int hh = 0; hh < 2; ++hh) {
+          const int row = r0 + 4 * hh + (j >> 2);
+          const int cb = 2 * t0 + 8 * (j & 3);  // byte offset of the 4 columns in the row
+          const char* pa = wl + row * (NCV * 2) + ((((cb >> 4) ^ ((row >> 1) & 7))) << 4) + (cb & 15);
+          const i32x2 t = __builtin_bit_cast(
+              i32x2, __builtin_amdgcn_ds_read_tr16_b64_v4i16((__attribute__((address_space(3))) v4s_t*)pa));
+          v[2 * hh] = t[0];
+          v[2 * hh + 1] = t[1];
+        }
+        *reinterpret_cast<i32x4*>(ce.yt + (ycol0 + t0 + j) * ce.ldyt + yrow0 + r0) = v;
+      }
     }
     return;
   }
@@ -775,11 +804,13 @@ int launch_ce_grad(const void* A, int64_t lda, const void* B, int64_t ldb, void*
 // tile covers 256 rows x 128 output columns (M % 256 == 0, N % 128 == 0).
 template <typename T>
 int launch_gate_up(const void* X, int64_t ldx, const void* Wg, const void* Wu, int64_t ldw, void* G, void* U, void* Y,
-                   int64_t ldo, int64_t M, int64_t N, int64_t K, hipStream_t s) {
+                   int64_t ldo, int64_t M, int64_t N, int64_t K, hipStream_t s, void* Yt = nullptr, int64_t ldyt = 0) {
   CeEpi e{};
   e.b2 = (const u16*)Wu;
   e.g_out = (u16*)G;
   e.u_out = (u16*)U;
+  e.yt = (u16*)Yt;
+  e.ldyt = ldyt;
   return launch_v4<T, T, 256, 256, 4, 2, 2, true, 64, 3>(X, ldx, Wg, ldw, Y, ldo, M, 2 * N, K, 1.f, 0, s, e);
 }
 
@@ -992,6 +1023,19 @@ int q3_gemm_gate_up_swiglu(int dtype, const void* x, int64_t ldx, const void* wg
              al16(wg) && al16(wu) && al16(g) && al16(u) && al16(y));
   if (dtype == Q3_BF16) return launch_gate_up<BF16>(x, ldx, wg, wu, ldw, g, u, y, ldo, M, N, K, stream);
   return launch_gate_up<F16>(x, ldx, wg, wu, ldw, g, u, y, ldo, M, N, K, stream);
+}
+
+int q3_gemm_gate_up_swiglu_t(int dtype, const void* x, int64_t ldx, const void* wg, const void* wu, int64_t ldw,
+                             void* g, void* u, void* y, int64_t ldo, void* yt, int64_t ldyt, int64_t M, int64_t N,
+                             int64_t K, hipStream_t stream) {
+  Q3_REQUIRE((dtype == Q3_BF16 || dtype == Q3_F16) && x && wg && wu && g && u && y && yt);
+  Q3_REQUIRE(M > 0 && N > 0 && K > 0 && M % 256 == 0 && N % 128 == 0 && K % 64 == 0 && M < (1ll << 31) &&
+             N < (1ll << 30) && K < (1ll << 31) && (M / 256) * (N / 128) < (1ll << 31));
+  Q3_REQUIRE(ldx % 8 == 0 && ldw % 8 == 0 && ldo % 8 == 0 && ldx >= K && ldw >= K && ldo >= N && al16(x) &&
+             al16(wg) && al16(wu) && al16(g) && al16(u) && al16(y));
+  Q3_REQUIRE(ldyt % 8 == 0 && ldyt >= M && al16(yt));
+  if (dtype == Q3_BF16) return launch_gate_up<BF16>(x, ldx, wg, wu, ldw, g, u, y, ldo, M, N, K, stream, yt, ldyt);
+  return launch_gate_up<F16>(x, ldx, wg, wu, ldw, g, u, y, ldo, M, N, K, stream, yt, ldyt);
 }
 
 int q3_gemm_nt_residual(int dtype, const void* A, int64_t lda, const void* B, int64_t ldb, const void* R,

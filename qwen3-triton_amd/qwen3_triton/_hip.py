@@ -55,6 +55,8 @@ SIGNATURES: dict[str, tuple] = {
     "q3_embedding_bwd": (_i32, [_i32, _p, _i32, _p, _p, _p, _i64, _i64, _i64, _p]),
     "q3_gemm_nt": (_i32, [_i32, _i32, _p, _i64, _p, _i64, _p, _i64, _i64, _i64, _i64, _f32, _i32, _p]),
     "q3_gemm_gate_up_swiglu": (_i32, [_i32, _p, _i64, _p, _p, _i64, _p, _p, _p, _i64, _i64, _i64, _i64, _p]),
+    "q3_gemm_gate_up_swiglu_t": (_i32, [_i32, _p, _i64, _p, _p, _i64, _p, _p, _p, _i64, _p, _i64, _i64, _i64, _i64,
+                                        _p]),
     "q3_gemm_nt_residual": (_i32, [_i32, _p, _i64, _p, _i64, _p, _i64, _p, _i64, _i64, _i64, _i64, _p]),
     "q3_gemm_swiglu_bwd": (_i32, [_i32, _p, _i64, _p, _i64, _p, _p, _i64, _p, _p, _i64, _p, _p, _i64, _i64, _i64,
                                   _i64, _p]),

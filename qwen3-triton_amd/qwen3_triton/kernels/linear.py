@@ -49,6 +49,13 @@ def gate_up_swiglu_into(x, wg, wu, g, u, y, m, n, k):
            g.data_ptr(), u.data_ptr(), y.data_ptr(), n, m, n, k, H.stream())
 
 
+def gate_up_swiglu_t_into(x, wg, wu, g, u, y, yt, m, n, k):
+    """``gate_up_swiglu_into`` that also writes yt = y^T [n, m] (the down projection's weight-gradient
+    operand) from the same epilogue."""
+    H.call("q3_gemm_gate_up_swiglu_t", H.code(x.dtype), x.data_ptr(), k, wg.data_ptr(), wu.data_ptr(), k,
+           g.data_ptr(), u.data_ptr(), y.data_ptr(), n, yt.data_ptr(), yt.stride(0), m, n, k, H.stream())
+
+
 def gemm_nt_residual_into(a, lda, bnk, ldb, res, out, m, n, k):
     """out[m, n] = res + a[m, k] . bnk[n, k]^T in one matrix-core launch (the GEMM output rounded, then
     the residual added and rounded again: bit-identical to the GEMM followed by the add kernel)."""

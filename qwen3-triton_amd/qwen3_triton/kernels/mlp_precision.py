@@ -11,7 +11,7 @@ buffer, so dX is a single GEMM over K = 2N and both weight gradients come from o
 import torch
 
 from . import _ops
-from .linear import (gate_up_fused_ok, gate_up_swiglu_into, gemm_nt_into, gemm_nt_residual_into, gemm_residual_ok,
+from .linear import (gate_up_fused_ok, gate_up_swiglu_into, gate_up_swiglu_t_into, gemm_nt_into, gemm_nt_residual_into, gemm_residual_ok,
                      linear, linear_residual, matmul, matmul_into, swiglu_bwd_gemm_into, swiglu_bwd_gemm_ok)
 
 
@@ -97,7 +97,14 @@ class _MLPBlock(torch.autograd.Function):
         m, k, n = x.numel() // x.shape[-1], x.shape[-1], wg.shape[0]
         h = wd.shape[0]
         flat = x.view(m, k)
-        g, u, y = _gate_up_forward(flat, wg, wu, m, n, k)
+        yt = None
+        if gate_up_fused_ok(flat, m, n, k):
+            # the epilogue also stores Y^T, the down weight-gradient operand of the backward
+            g, u, y = (torch.empty((m, n), device=x.device, dtype=x.dtype) for _ in range(3))
+            yt = torch.empty((n, m), device=x.device, dtype=x.dtype)
+            gate_up_swiglu_t_into(flat, wg, wu, g, u, y, yt, m, n, k)
+        else:
+            g, u, y = _gate_up_forward(flat, wg, wu, m, n, k)
         out = torch.empty((m, h), device=x.device, dtype=x.dtype)
         if res is None:
             gemm_nt_into(y, n, wd, n, out, m, h, n)
@@ -106,18 +113,24 @@ class _MLPBlock(torch.autograd.Function):
         else:
             gemm_nt_into(y, n, wd, n, out, m, h, n)
             out = _ops.add(res.view(m, h), out)
-        ctx.save_for_backward(x, wg, wu, wd, g, u, y)
+        ctx.save_for_backward(x, wg, wu, wd, g, u, y if yt is None else yt)
+        ctx.has_yt = yt is not None
         ctx.has_res = res is not None
         return out.view(*x.shape[:-1], h)
 
     @staticmethod
     def backward(ctx, dout):
-        x, wg, wu, wd, g, u, y = ctx.saved_tensors
+        x, wg, wu, wd, g, u, yy = ctx.saved_tensors
         m, k, n = x.numel() // x.shape[-1], x.shape[-1], wg.shape[0]
         h = wd.shape[0]
         dev, dt = x.device, x.dtype
         dof = dout.contiguous().view(m, h)
-        dwd = matmul(dof.t(), y)
+        if ctx.has_yt:  # dWd = dOut^T Y with Y^T stored by the forward epilogue
+            dwd = torch.empty((h, n), device=dev, dtype=dt)
+            doft = _ops.transpose_into(dof, torch.empty((h, m), device=dev, dtype=dt))
+            gemm_nt_into(doft, m, yy, m, dwd, h, n, m)
+        else:
+            dwd = matmul(dof.t(), yy)
         wdt = _ops.transpose_into(wd, torch.empty((n, h), device=dev, dtype=dt))
         dgu = torch.empty((m, 2 * n), device=dev, dtype=dt)
         dgut = torch.empty((2 * n, m), device=dev, dtype=dt)

@@ -151,6 +151,13 @@ def test_gate_up_swiglu_gemm(m, n, k, dtype):
     tol = 8e-3 if dtype == torch.bfloat16 else 1e-3
     assert max_rel(g[rows], eg) <= tol and max_rel(u[rows], eu) <= tol
     assert max_rel(y[rows], O.swiglu_reference(eg, eu, dtype=torch.float64)) <= 2 * tol
+    # the variant that also stores Y^T: G, U, Y unchanged bit for bit, Y^T exactly Y transposed
+    from qwen3_triton.kernels.linear import gate_up_swiglu_t_into
+    g3, u3, y3 = (torch.full((m, n), 7.0, device="cuda", dtype=dtype) for _ in range(3))
+    yt = torch.full((n, m + 8), 7.0, device="cuda", dtype=dtype)  # row pitch wider than M
+    gate_up_swiglu_t_into(x, wg, wu, g3, u3, y3, yt, m, n, k)
+    assert torch.equal(g3, g) and torch.equal(u3, u) and torch.equal(y3, y)
+    assert torch.equal(yt[:, :m], y.t()) and bool((yt[:, m:] == 7.0).all())
 
 
 @pytest.mark.parametrize("m,ns,k", [(256, (256,), 64), (512, (512, 256, 256), 128), (8192, (4096, 1024, 1024), 4096)])
