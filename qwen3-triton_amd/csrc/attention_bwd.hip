@@ -11,8 +11,8 @@
 // 48 keys per wave give every LDS fragment three MFMAs (the 32-key wave tile of attn_bwd_dkdv_v3 gives
 // two): 2/3 of the LDS traffic per MFMA.  (64 keys do not fit: K/V fragments + the S / dP tiles
 // exceed the 256 VGPRs beside the 256 AGPRs of the accumulators.)  The 4 heads' partial dK / dV fold through LDS in fixed
-// order at the end (deterministic, no atomics).  Causal balance: workgroup y handles key tile y and
-// then key tile NT - 1 - y, so every workgroup does the same amount of work.
+// order at the end (deterministic, no atomics).  Causal balance: one key tile per workgroup, the
+// tiles with the most queries first (a longest-first list schedule over the CUs).
 #include <type_traits>
 
 #include "common.h"
@@ -77,7 +77,12 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
     const float* __restrict__ LSE, const float* __restrict__ Delta, u16* __restrict__ dK, u16* __restrict__ dV,
     int Hq, int Hkv, int Lq, int Lk, int ntiles, float scale, float scale2) {
   __shared__ __attribute__((aligned(1024))) char lds[4 * kWaveLds];
-  const int bk = blockIdx.x, b = bk / Hkv, hk = bk % Hkv, ratio = Hq / Hkv, hpw = ratio / 4;
+  // One key tile per workgroup, launched in order of decreasing causal work: workgroup i takes key
+  // tile i / (B Hkv) of (batch, KV head) i % (B Hkv), so the dispatcher, which hands out workgroups in
+  // order as CUs free up, runs a longest-first list schedule (the tiles of one KV head are B Hkv
+  // workgroups apart: with B Hkv a multiple of 8 they share an XCD and its L2 copy of Q / dO).
+  const int nbk = (int)(gridDim.x / ntiles);
+  const int bk = (int)(blockIdx.x % nbk), b = bk / Hkv, hk = bk % Hkv, ratio = Hq / Hkv, hpw = ratio / 4;
   const int tid = threadIdx.x, lane = tid & 63, G = lane >> 4, r16 = lane & 15;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int off = Lk - Lq;
@@ -97,10 +102,8 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
 
   const int64_t kvbase = (int64_t)b * ksb + (int64_t)hk * ksh;
 
-#pragma nounroll
-  for (int pass = 0; pass < 2; ++pass) {
-    const int kt = pass == 0 ? (int)blockIdx.y : ntiles - 1 - (int)blockIdx.y;
-    if (pass == 1 && kt <= (int)blockIdx.y) break;  // the middle tile of an odd count runs once
+  {
+    const int kt = (int)(blockIdx.x / nbk);
     const int k0 = kt * kBN;
 
     // K / V B operands: lane (G, r16) holds key k0 + 16 c + r16, dims 32 ks + 8 G .. + 7
@@ -299,7 +302,6 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
     };
     fold(dk, dK, scale);
     fold(dv, dV, 1.f);
-    __syncthreads();  // the next pass reuses the LDS for its rings
   }
 }
 
@@ -313,7 +315,7 @@ int q3i_attn_bwd_dkdv_v4(int dtype, const void* q, int64_t qsb, int64_t qsh, int
                          hipStream_t s) {
   if ((Hq / Hkv) % 4 != 0) return Q3_ERR_INVALID;
   const int ntiles = (Lk + kBN - 1) / kBN;
-  dim3 g((unsigned)(B * Hkv), (unsigned)((ntiles + 1) / 2));
+  const dim3 g((unsigned)(B * Hkv * ntiles));
   if (dtype == Q3_BF16)
     attn_bwd_dkdv_v4<BF16><<<g, 256, 0, s>>>((const u16*)q, qsb, qsh, qss, (const u16*)k, (const u16*)v, ksb, ksh,
                                              kss, (const u16*)dout, lse, delta, (u16*)dk, (u16*)dv, Hq, Hkv, Lq, Lk,
