@@ -309,31 +309,39 @@ def init_params(cfg, *, seed=0, std=0.02, dtype=torch.float32):
     return p
 
 
-def decoder_layer_reference(x, p, pre, cfg, cos, sin, *, start=0, cache=None, dtype=torch.float32):
+def decoder_layer_reference(x, p, pre, cfg, cos, sin, *, start=0, cache=None, dtype=torch.float32,
+                            rounding=None):
     """One decoder layer, ``qwen3_triton/_model.py:60-91``.
 
     x [B,S,H]; cos/sin [B,S,D].  With ``cache`` (a dict holding fp K/V [B,Hk,L,D]) the new K/V are
     appended at ``start`` and attention runs over the whole prefix (``inference/model.py:114-119``).
+
+    ``rounding`` (e.g. ``torch.bfloat16``) rounds every op's output to that type while the math
+    stays in ``dtype``: the storage points of the reference's bf16 inference forward
+    (``inference/model.py:108-137``: each kernel computes in fp32 and stores bf16 -- the input norm,
+    the q/k/v projections, QK-norm + RoPE, attention, the o projection, the residual sum, the
+    post-attention norm, gate and up, SwiGLU, the down projection, the residual sum).
     """
     b, s, h = x.shape
     d, hq, hk, eps = cfg.head_dim, cfg.num_attention_heads, cfg.num_key_value_heads, cfg.rms_norm_eps
     W = lambda n: p[pre + n].to(dtype)  # noqa: E731
-    hn = rms_norm_reference(x, W("input_layernorm.weight"), eps, dtype=dtype)
-    q = (hn @ W("self_attn.q_proj.weight").T).view(b, s, hq, d)
-    k = (hn @ W("self_attn.k_proj.weight").T).view(b, s, hk, d)
-    v = (hn @ W("self_attn.v_proj.weight").T).view(b, s, hk, d)
+    R = (lambda t: t) if rounding is None else (lambda t: t.to(rounding).to(dtype))  # noqa: E731
+    hn = R(rms_norm_reference(x, W("input_layernorm.weight"), eps, dtype=dtype))
+    q = R(hn @ W("self_attn.q_proj.weight").T).view(b, s, hq, d)
+    k = R(hn @ W("self_attn.k_proj.weight").T).view(b, s, hk, d)
+    v = R(hn @ W("self_attn.v_proj.weight").T).view(b, s, hk, d)
     q, k = fused_qk_norm_rope_reference(q, k, W("self_attn.q_norm.weight"), W("self_attn.k_norm.weight"),
                                         cos, sin, eps, dtype=dtype)
-    q, k, v = q.transpose(1, 2), k.transpose(1, 2), v.transpose(1, 2)
+    q, k, v = R(q).transpose(1, 2), R(k).transpose(1, 2), v.transpose(1, 2)
     if cache is not None:
         cache["k"] = k if cache.get("k") is None else torch.cat([cache["k"], k], dim=2)
         cache["v"] = v if cache.get("v") is None else torch.cat([cache["v"], v], dim=2)
         k, v = cache["k"], cache["v"]
-    y = scaled_dot_product_attention_reference(q, k, v, scale=d ** -0.5, dtype=dtype)
-    x = x.to(dtype) + y.transpose(1, 2).reshape(b, s, hq * d) @ W("self_attn.o_proj.weight").T
-    hn = rms_norm_reference(x, W("post_attention_layernorm.weight"), eps, dtype=dtype)
-    m = swiglu_reference(hn @ W("mlp.gate_proj.weight").T, hn @ W("mlp.up_proj.weight").T, dtype=dtype)
-    return x + m @ W("mlp.down_proj.weight").T
+    y = R(scaled_dot_product_attention_reference(q, k, v, scale=d ** -0.5, dtype=dtype))
+    x = R(x.to(dtype) + R(y.transpose(1, 2).reshape(b, s, hq * d) @ W("self_attn.o_proj.weight").T))
+    hn = R(rms_norm_reference(x, W("post_attention_layernorm.weight"), eps, dtype=dtype))
+    m = R(swiglu_reference(hn @ W("mlp.gate_proj.weight").T, hn @ W("mlp.up_proj.weight").T, dtype=dtype))
+    return R(x + R(m @ W("mlp.down_proj.weight").T))
 
 
 def model_forward_reference(ids, p, cfg, *, labels=None, dtype=torch.float32, positions=None):

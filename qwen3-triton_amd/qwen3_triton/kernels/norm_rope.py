@@ -55,6 +55,8 @@ class _NormRoPEPair(torch.autograd.Function):
         q, k = q.contiguous(), k.contiguous()
         qw, kw = q_weight.contiguous().view(-1), k_weight.contiguous().view(-1)
         cos, sin = cos.contiguous(), sin.contiguous()
+        _check(q, qw, cos, sin, eps)   # dtype / device / shape rules of the single-tensor op, both tensors
+        _check(k, kw, cos, sin, eps)
         ctx.save_for_backward(q, k, qw, kw, cos, sin)
         ctx.eps = eps
         ctx.shapes = (q_weight.shape, k_weight.shape)

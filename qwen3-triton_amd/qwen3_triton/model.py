@@ -14,22 +14,22 @@ PRECISION_SWITCHES = ('xor_sum', 'lse_fma', 'native_delta', 'native_dq', 'sum_fm
 
 
 def _precision_items(precision_options):
-    """The five switches as an ordered tuple of (name, bool); all on when none are given."""
+    """The five switches as a tuple of (name, bool) in the caller's order; all on when none are given."""
     if precision_options is None:
         return tuple((name, True) for name in PRECISION_SWITCHES)
     given = dict(precision_options)
     if sorted(given) != sorted(PRECISION_SWITCHES) or not all(type(v) is bool for v in given.values()):
         raise ValueError(f'precision_options must give exactly the booleans {", ".join(PRECISION_SWITCHES)}')
-    return tuple((name, given[name]) for name in PRECISION_SWITCHES)
+    return tuple(given.items())
 
 
 def _optimization_options(options):
     """``OptimizationOptions`` from None (every switch off), an ``OptimizationOptions``, or any object
-    whose like-named attributes are read (missing ones off)."""
+    whose like-named attributes are taken as they are (missing ones off)."""
     if isinstance(options, OptimizationOptions):
         return options
     switches = [f.name for f in fields(OptimizationOptions) if f.name != 'precision_options']
-    return OptimizationOptions(**{name: bool(getattr(options, name, False)) for name in switches})
+    return OptimizationOptions(**{name: getattr(options, name, False) for name in switches})
 
 
 def _is_8b_shape(config):

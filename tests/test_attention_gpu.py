@@ -52,14 +52,22 @@ def test_attention_fwd_bwd_vs_oracle(b, hq, hk, s, d, dtype):
         assert max_rel(a, x) <= GRAD_TOL[dtype], f"d{n} max-rel {max_rel(a, x)}"
 
 
-@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16, torch.float32])
 @pytest.mark.parametrize("lq,lk", [(1, 1), (1, 300), (7, 129), (64, 1000), (129, 129)])
 def test_attention_query_suffix_offset(lq, lk, dtype):
-    """Prefill/chunked attention against a longer KV prefix (query i sees keys <= i + lk - lq)."""
-    q, k, v, _ = make(2, 8, 2, lq, lk, 128, dtype, seed=lq + lk)
-    o, lse = _ops.attention_fwd(q.cuda(), k.cuda(), v.cuda(), 128 ** -0.5)
+    """Prefill/chunked attention against a longer KV prefix (query i sees keys <= i + lk - lq):
+    forward, LSE and the backward (Hq/Hkv = 4, the grouped dK/dV kernel at head_dim 128)."""
+    print(f"attention suffix offset lq {lq} lk {lk} {dtype}", flush=True)
+    q, k, v, do = make(2, 8, 2, lq, lk, 128, dtype, seed=lq + lk)
+    qd, kd, vd, dod = q.cuda(), k.cuda(), v.cuda(), do.cuda()
+    o, lse = _ops.attention_fwd(qd, kd, vd, 128 ** -0.5)
     assert max_rel(o, O.scaled_dot_product_attention_reference(q, k, v)) <= FWD_TOL[dtype]
     assert (lse.cpu() - O.attention_lse_reference(q, k)).abs().max() <= 3e-3
+    grads = _ops.attention_bwd(qd, kd, vd, o, lse, dod, 128 ** -0.5)
+    e = O.scaled_dot_product_attention_backward_reference(q, k, v, do)
+    for a, x, n in zip(grads, e, "qkv"):
+        assert cosine(a, x) >= 0.999, f"d{n} cosine {cosine(a, x)}"
+        assert max_rel(a, x) <= GRAD_TOL[dtype], f"d{n} max-rel {max_rel(a, x)}"
 
 
 def test_reference_entry_points_agree():

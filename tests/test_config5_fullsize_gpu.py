@@ -1,0 +1,151 @@
+"""Config #5 at its real depth and length: the 36-layer Qwen3-8B of the decode benchmark.
+
+The model is built exactly as the benchmark builds it (``TritonQwen3Inference.random_init`` of the
+36-layer Qwen3-8B config, bf16 N(0, 0.02) weights from seed 4 on the device), with the benchmark's
+prompts (B1 x 2048 and B8 x 1024 tokens, uniform over the vocabulary, seed 4).
+
+1. Property checks of the benchmarked decode path (``inference/model.py:158-225``): the captured
+   one-step graph of ``DecodeSession`` replayed 32 times and ``CapturedGreedyRequest`` must give the
+   tokens of eager ``generate`` exactly, and the cache / device lengths must come out right.
+2. Oracle check: the prefill's last-position logits and the next teacher-forced decode steps'
+   logits against an fp32 host oracle (``oracle.decoder_layer_reference``, the math of
+   ``inference/model.py:102-142``) that streams one layer's weights from the device at a time, so
+   host memory holds one layer.  The oracle runs the whole prompt + forced tokens causally, which
+   equals the cached computation position by position.  Each row's logits must meet the bf16
+   forward gate; greedy picks are counted exact / decisive and printed.
+"""
+import pytest
+import torch
+
+import oracle as O
+from _util import max_rel
+
+from qwen3_triton.inference import CapturedGreedyRequest, DecodeSession, TritonQwen3Inference
+
+pytestmark = [pytest.mark.gpu, pytest.mark.timeout(1200)]
+
+LAYERS = 36
+ORACLE_CFG = O.OracleConfig(vocab_size=151936, hidden_size=4096, intermediate_size=12288,
+                            num_hidden_layers=LAYERS, num_attention_heads=32, num_key_value_heads=8, head_dim=128)
+
+
+def qwen3_8b_config(layers):
+    from transformers import Qwen3Config
+    return Qwen3Config(vocab_size=151936, hidden_size=4096, intermediate_size=12288, num_hidden_layers=layers,
+                       num_attention_heads=32, num_key_value_heads=8, head_dim=128, rope_theta=1e6,
+                       rms_norm_eps=1e-6, tie_word_embeddings=False, max_position_embeddings=40960,
+                       initializer_range=0.02)
+
+
+@pytest.fixture(scope="module")
+def model8b():
+    print("building the 36-layer Qwen3-8B (random bf16 weights, seed 4)", flush=True)
+    model = TritonQwen3Inference.random_init(qwen3_8b_config(LAYERS), seed=4, std=0.02, device="cuda")
+    yield model
+    del model
+    torch.cuda.empty_cache()
+
+
+def bench_prompt(batch, prompt):
+    gen = torch.Generator(device="cuda").manual_seed(4)
+    return torch.randint(0, 151936, (batch, prompt), device="cuda", generator=gen)
+
+
+@pytest.mark.parametrize("b,s", [(1, 2048), (8, 1024)])
+def test_decode_paths_agree_full_depth(model8b, b, s):
+    """DecodeSession (captured step replayed 32 times) == CapturedGreedyRequest == generate."""
+    new = 33
+    print(f"config #5 full depth B{b} S{s}: generate / DecodeSession / CapturedGreedyRequest x {new}", flush=True)
+    ids = bench_prompt(b, s)
+    eager = model8b.generate(ids, max_new_tokens=new, eos_token_id=[], pad_token_id=0)
+    assert eager.shape == (b, s + new)
+    sess = DecodeSession(model8b, b, s + new + 1)
+    sess.prefill(ids)
+    assert sess.cache.length == s
+    sess.capture()
+    for _ in range(new - 1):
+        sess.step()
+    torch.cuda.synchronize()
+    assert sess.cache.length == s + new - 1
+    assert int(sess.length.item()) == s + new - 1          # device-resident length advanced per replay
+    assert torch.equal(sess.tokens(), eager)
+    req = CapturedGreedyRequest(model8b, ids, max_new_tokens=new)
+    out = req(ids).clone()
+    assert int(req.length.item()) == s + new - 1
+    assert torch.equal(out, eager)
+    # a second call of the same request replays both graphs again from a clean cache
+    assert torch.equal(req(ids).clone(), eager)
+    del sess, req
+    torch.cuda.empty_cache()
+
+
+def _layer_params(layer):
+    return {n: t.detach().float().cpu() for n, t in layer.named_parameters()}
+
+
+def streamed_oracle_logits(model, ids, keep):
+    """Host forward of ``ids`` [R, L] through the model's own bf16 weights, one layer's weights on
+    the host at a time, twice in the same pass: in fp32 throughout, and in fp32 with every op's
+    output stored as bf16 (the reference's bf16 inference path, ``inference/model.py:108-137``).
+    Returns both runs' logits of the last ``keep`` positions, [R, keep, V] each."""
+    r, n = ids.shape
+    cfg = ORACLE_CFG
+    x = model.model.embed_tokens.weight[ids.cuda()].float().cpu()
+    xb = x.clone()
+    pos = torch.arange(n)[None, :].expand(r, n)
+    cos, sin = O.rotary_tables_reference(pos, O.rope_inv_freq(cfg.rope_theta, cfg.head_dim))
+    cosb, sinb = cos.bfloat16().float(), sin.bfloat16().float()
+    with torch.no_grad():
+        for layer in model.model.layers:
+            p = _layer_params(layer)
+            x = O.decoder_layer_reference(x, p, "", cfg, cos, sin)
+            xb = O.decoder_layer_reference(xb, p, "", cfg, cosb, sinb, rounding=torch.bfloat16)
+        w = model.model.norm.weight.float().cpu()
+        head = model.lm_head.weight.float().cpu()
+        x = O.rms_norm_reference(x[:, -keep:], w, cfg.rms_norm_eps)
+        xb = O.rms_norm_reference(xb[:, -keep:], w, cfg.rms_norm_eps).bfloat16().float()
+        return x @ head.T, xb @ head.T
+
+
+@pytest.mark.parametrize("b,s,rows", [(1, 2048, [0]), (8, 1024, [0, 7])])
+def test_logits_vs_streamed_oracle_full_depth(model8b, b, s, rows):
+    """Prefill last-row logits + 15 teacher-forced decode steps against the layer-streamed fp32
+    oracle, at the benchmark's batch and prompt length.  The decode steps are fed the GPU's own
+    greedy tokens, so both runs see the same context at every step."""
+    steps = 16
+    print(f"config #5 oracle B{b} S{s} rows {rows}: prefill + {steps - 1} forced steps", flush=True)
+    ids = bench_prompt(b, s)
+    toks = model8b.generate(ids, max_new_tokens=steps, eos_token_id=[], pad_token_id=0)
+    cache = model8b.new_cache(b, s + steps)
+    got = [model8b(ids, past_key_values=cache).logits[:, -1].float().cpu()]
+    for t in range(steps - 1):
+        got.append(model8b(toks[:, s + t:s + t + 1].contiguous(), past_key_values=cache).logits[:, -1].float().cpu())
+    got = torch.stack(got, dim=1)                                  # [B, steps, V]
+    assert cache.length == s + steps - 1
+    exp, exp_bf16 = streamed_oracle_logits(model8b, toks[rows, :s + steps - 1].cpu(), steps)
+    n_exact = n_decisive = 0
+    worst = worst_ref = 0.0
+    for i, r in enumerate(rows):
+        for t in range(steps):
+            e, a = exp[i, t], got[r, t]
+            rel, rel_ref = max_rel(a, e), max_rel(exp_bf16[i, t], e)
+            worst, worst_ref = max(worst, rel), max(worst_ref, rel_ref)
+            # 36 layers of bf16 storage put the reference's own bf16 path about 5 % (normwise) from
+            # fp32 at the logits, past the single-op 2e-2 gate; this path must be no further
+            # from fp32 than 1.25 x what the reference's bf16 storage points alone cost.
+            assert rel <= max(2e-2, 1.25 * rel_ref), \
+                f"B{b} row {r} step {t}: logits max-rel {rel:.3e} (bf16-storage reference {rel_ref:.3e})"
+            err = float((a.double() - e.double()).abs().max())
+            pick = int(toks[r, s + t])
+            assert pick == int(a.argmax()), "generate's token is the argmax of the same logits"
+            want = int(O.argmax_lowest_reference(e[None])[0])
+            top2 = e.topk(2).values
+            n_decisive += float(top2[0] - top2[1]) > 2 * err
+            n_exact += pick == want
+            assert pick == want or float(e[want] - e[pick]) <= 2 * err, \
+                f"B{b} row {r} step {t}: GPU picks {pick}, oracle {want} (err {err:.4f})"
+    total = len(rows) * steps
+    print(f"config #5 full depth B{b} S{s}: {n_exact}/{total} greedy tokens exact vs the fp32 oracle, "
+          f"{n_decisive} decisive (top-2 margin > 2 x max logit error); logits max-rel {worst:.3e} "
+          f"(the bf16-storage reference path: {worst_ref:.3e})", flush=True)
+    assert n_exact >= 0.75 * total

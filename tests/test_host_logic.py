@@ -51,6 +51,13 @@ def test_precision_model_option_validation():
         _precision_items(dict(xor_sum=1, lse_fma=True, native_delta=True, native_dq=True, sum_fma=True))
     o = _optimization_options(None)
     assert isinstance(o, OptimizationOptions) and not o.mlp_fusion and not o.linear_optimized
+    # the caller's order is kept (the reference stores ``tuple(precision_options.items())``)
+    order = dict(sum_fma=False, xor_sum=True, native_dq=True, lse_fma=False, native_delta=True)
+    assert _precision_items(order) == tuple(order.items())
+
+    class Foreign:        # attributes are taken as given, not coerced to bool
+        mlp_fusion = 1
+    assert _optimization_options(Foreign()).mlp_fusion == 1
 
 
 def test_architecture_rules():

@@ -237,3 +237,48 @@ def test_decode_session_replays_one_step_graph(b, s):
     torch.cuda.synchronize()
     assert sess.cache.length == s + n - 1
     assert torch.equal(sess.tokens(), eager)
+
+
+@pytest.mark.timeout(900)
+def test_decoder_layer_8b_benchmark_shape():
+    """Config #4's decoder layer exactly as the benchmark times it (B4 x S2048 = 8192 tokens, bf16
+    weights N(0, 0.02) and N(0, 1) input / upstream gradient from the device generator, seed 3):
+    output (bf16 gate) and every gradient (cosine >= 0.999) against the fp32 host oracle
+    (``_model.py:60-108``, ``components.py:18-54``).  At this size every GEMM runs its full-grid
+    plan (the residual, SwiGLU and SwiGLU-backward epilogues, the split-M remainder launch of the
+    Q/K/V weight gradient) and the weight gradients contract over K = 8192 tokens."""
+    oc = O.OracleConfig(vocab_size=16, hidden_size=4096, intermediate_size=12288, num_hidden_layers=1,
+                        num_attention_heads=32, num_key_value_heads=8, head_dim=128)
+    print("decoder layer B4 S2048 fwd+bwd vs the fp32 oracle (seed 3)", flush=True)
+    torch.manual_seed(3)
+    layer = DecoderLayer(hf_config(oc), OptimizationOptions()).to(device="cuda", dtype=torch.bfloat16)
+    gen = torch.Generator(device="cuda").manual_seed(3)
+    with torch.no_grad():
+        for name, p in layer.named_parameters():
+            if name.endswith("norm.weight"):
+                p.fill_(1.0)
+            else:
+                p.normal_(0.0, 0.02, generator=gen)
+    b, s = 4, 2048
+    x = torch.randn(b, s, 4096, device="cuda", dtype=torch.bfloat16, generator=gen)
+    dy = torch.randn(b, s, 4096, device="cuda", dtype=torch.bfloat16, generator=gen)
+    pos = torch.arange(s)[None].expand(b, s).contiguous()
+    cos, sin = O.rotary_tables_reference(pos, O.rope_inv_freq(1e6, 128), dtype=torch.bfloat16)
+    xd = x.clone().requires_grad_()
+    y = layer(xd, (cos.cuda(), sin.cuda()))
+    y.backward(dy)
+    torch.cuda.synchronize()
+    leaf = {"model.layers.0." + n: p.detach().float().cpu().requires_grad_() for n, p in layer.named_parameters()}
+    xr = x.float().cpu().requires_grad_()
+    yr = O.decoder_layer_reference(xr, leaf, "model.layers.0.", oc, cos.float(), sin.float())
+    yr.backward(dy.float().cpu())
+    rel = max_rel(y, yr)
+    cos_x = cosine(xd.grad, xr.grad)
+    worst = ("x", cos_x)
+    assert rel <= 2e-2, f"y max-rel {rel:.3e}"
+    assert cos_x >= 0.999, f"dx cosine {cos_x}"
+    for name, p in layer.named_parameters():
+        c = cosine(p.grad, leaf["model.layers.0." + name].grad)
+        worst = min(worst, (name, c), key=lambda t: t[1])
+        assert c >= 0.999, f"{name}: {c}"
+    print(f"B4 S2048 layer: y max-rel {rel:.3e}, worst gradient cosine {worst[1]:.6f} ({worst[0]})", flush=True)

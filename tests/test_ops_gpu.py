@@ -246,3 +246,23 @@ def test_embedding_out_of_range_raises():
     w = torch.randn(10, 8, device="cuda")
     with pytest.raises(ValueError):
         embedding(torch.tensor([[1, 10]], device="cuda"), w)
+
+
+def test_norm_rope_pair_validates_like_norm_rope():
+    """The Q/K pair op applies the single-tensor op's checks to both tensors: a weight or table in
+    another dtype than the activations, or a rotary table that requires grad, is rejected."""
+    from qwen3_triton.kernels.norm_rope import norm_rope_pair
+    q = torch.randn(1, 4, 8, 128, device="cuda", dtype=torch.bfloat16)
+    k = torch.randn(1, 4, 2, 128, device="cuda", dtype=torch.bfloat16)
+    w = torch.ones(128, device="cuda", dtype=torch.bfloat16)
+    cos = torch.ones(1, 4, 128, device="cuda", dtype=torch.bfloat16)
+    sin = torch.zeros(1, 4, 128, device="cuda", dtype=torch.bfloat16)
+    norm_rope_pair(q, k, w, w, cos, sin)
+    with pytest.raises(ValueError):
+        norm_rope_pair(q, k, w.float(), w, cos, sin)
+    with pytest.raises(ValueError):
+        norm_rope_pair(q, k, w, w.float(), cos, sin)
+    with pytest.raises(ValueError):
+        norm_rope_pair(q, k, w, w, cos.float(), sin.float())
+    with pytest.raises(ValueError):
+        norm_rope_pair(q, k, w, w, cos.clone().requires_grad_(), sin)

@@ -274,3 +274,22 @@ def test_cached_decode_matches_full_recomputation():
         e, _ = O.model_forward_reference(seq[:, :7 + t], p, cfg, dtype=D64)
         torch.testing.assert_close(flog[:, t], e[:, -1], rtol=1e-10, atol=1e-10)
         assert torch.equal(ftoks[:, t], O.argmax_lowest_reference(e[:, -1]))
+
+
+def test_decoder_layer_rounding_points():
+    """``rounding`` stores each op's output in that type: float32 storage is the unrounded layer bit
+    for bit; bf16 storage gives a bf16-representable output close to the fp32 one, and its error
+    grows when the stored activations are coarser (fp16 -> bf16)."""
+    cfg = O.OracleConfig(vocab_size=16, hidden_size=64, intermediate_size=96, num_hidden_layers=1,
+                         num_attention_heads=4, num_key_value_heads=2, head_dim=16)
+    p = O.init_params(cfg, seed=1, std=0.1)
+    gen = torch.Generator().manual_seed(2)
+    x = torch.randn(2, 9, 64, generator=gen)
+    cos, sin = O.rotary_tables_reference(torch.arange(9)[None].expand(2, 9), O.rope_inv_freq(1e6, 16))
+    y = O.decoder_layer_reference(x, p, "model.layers.0.", cfg, cos, sin)
+    assert torch.equal(O.decoder_layer_reference(x, p, "model.layers.0.", cfg, cos, sin, rounding=torch.float32), y)
+    yb = O.decoder_layer_reference(x, p, "model.layers.0.", cfg, cos, sin, rounding=torch.bfloat16)
+    yh = O.decoder_layer_reference(x, p, "model.layers.0.", cfg, cos, sin, rounding=torch.float16)
+    assert torch.equal(yb, yb.bfloat16().float())
+    eb, eh = float((yb - y).abs().max() / y.abs().max()), float((yh - y).abs().max() / y.abs().max())
+    assert 0 < eh < eb < 2e-2
