@@ -83,6 +83,16 @@ int q3_norm_rope_bwd(int dtype, const void* x, const void* w, const void* cos, c
 int q3_norm_rope_qk_fwd(int dtype, const void* q, const void* k, const void* wq, const void* wk, const void* cos,
                         const void* sin, void* yq, void* yk, int64_t tokens, int64_t hq, int64_t hk, int64_t d,
                         float eps, hipStream_t stream);
+/* Prefill form of q3_norm_rope_qk_fwd: q / k / v [B, S, h, d] (contiguous), yq [B, S, hq, d] as
+ * there; the normed + rotated keys and the unchanged values are written straight into the
+ * [B, hk, capacity, d] caches at positions start .. start + S - 1 (start + S <= capacity), so the
+ * whole Q/K-norm + RoPE + cache append of a prefill chunk is one launch.  Bit-identical to
+ * q3_norm_rope_qk_fwd followed by q3_kv_append.
+ * Replaces: inference/model.py:122-124 (norm_rope on q and k, kernels.append). */
+int q3_norm_rope_qk_cache_fwd(int dtype, const void* q, const void* k, const void* v, const void* wq, const void* wk,
+                              const void* cos, const void* sin, void* yq, void* cache_k, void* cache_v, int64_t B,
+                              int64_t S, int64_t hq, int64_t hk, int64_t d, int64_t capacity, int64_t start, float eps,
+                              hipStream_t stream);
 size_t q3_norm_rope_qk_bwd_workspace_bytes(int64_t tokens, int64_t hq, int64_t hk, int64_t d);
 int q3_norm_rope_qk_bwd(int dtype, const void* q, const void* k, const void* wq, const void* wk, const void* cos,
                         const void* sin, const void* dyq, const void* dyk, void* dxq, void* dxk, void* dw,

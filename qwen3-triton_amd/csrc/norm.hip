@@ -504,28 +504,50 @@ __global__ __launch_bounds__(kBlock) void norm_rope_bwd_kernel(const typename T:
 // norm_rope_bwd_kernel (bit-identical y and dx); each backward workgroup writes one partial row of
 // 2 D floats ([dW_q | dW_k], zeros in the other segment's half), reduced by one column sum.
 template <typename S> struct NrPair {
-  const S* x[2];
+  const S* x[3];
   const S* w[2];
   const S* dy[2];
-  S* y[2];  // forward output or input gradient
-  int64_t rows[2];
-  int heads[2];
-  int blocks[2];  // workgroups per segment
+  S* y[3];  // forward output or input gradient
+  int64_t rows[3];
+  int heads[3];
+  int blocks[3];  // workgroups per segment
+  // Prefill form of the forward (CACHE): segment 1's normed + rotated keys and segment 2's values
+  // (copied unchanged) go straight into the [B, heads, cap, D] caches at positions start + s of
+  // [B, seq] token rows, instead of a [tokens, heads, D] output.
+  int64_t cap, start, seq;
 };
 
-template <typename T, int TPR>
+template <typename T, int TPR, bool CACHE>
 __global__ __launch_bounds__(kBlock) void norm_rope_qk_fwd_kernel(NrPair<typename T::storage> p,
                                                                   const typename T::storage* __restrict__ cs,
                                                                   const typename T::storage* __restrict__ sn,
                                                                   float eps) {
   constexpr int V = T::vec, D = TPR * V, RPB = kBlock / TPR;
-  const int seg = (int)blockIdx.x >= p.blocks[0] ? 1 : 0;
-  const int blk = (int)blockIdx.x - (seg ? p.blocks[0] : 0), nblk = p.blocks[seg];
+  int seg = (int)blockIdx.x >= p.blocks[0] ? 1 : 0;
+  if (CACHE && (int)blockIdx.x >= p.blocks[0] + p.blocks[1]) seg = 2;
+  const int blk = (int)blockIdx.x - (seg == 0 ? 0 : seg == 1 ? p.blocks[0] : p.blocks[0] + p.blocks[1]);
+  const int nblk = p.blocks[seg];
   const typename T::storage* __restrict__ x = p.x[seg];
   typename T::storage* __restrict__ y = p.y[seg];
   const int64_t rows = p.rows[seg];
   const int heads = p.heads[seg];
   const int t = threadIdx.x % TPR, g = threadIdx.x / TPR;
+  // output offset of a [tokens, heads] row: row-major, or its cache slot (b, head, start + s)
+  auto out_off = [&](int64_t row) -> int64_t {
+    if (!CACHE || seg == 0) return row * D;
+    const int64_t tok = row / heads, h = row % heads, b = tok / p.seq, s = tok % p.seq;
+    return ((b * heads + h) * p.cap + p.start + s) * D;
+  };
+  if constexpr (CACHE) {
+    if (seg == 2) {  // values: copied into the cache unchanged
+      for (int64_t base = (int64_t)blk * RPB; base < rows; base += (int64_t)nblk * RPB) {
+        const int64_t row = base + g;
+        if (row < rows)
+          *reinterpret_cast<i32x4*>(y + out_off(row) + t * V) = *reinterpret_cast<const i32x4*>(x + row * D + t * V);
+      }
+      return;
+    }
+  }
   const float sign = (t < TPR / 2) ? -1.f : 1.f;
   const Vec<T> wv = load_vec<T>(p.w[seg] + t * V);
   for (int64_t base = (int64_t)blk * RPB; base < rows; base += (int64_t)nblk * RPB) {
@@ -549,7 +571,7 @@ __global__ __launch_bounds__(kBlock) void norm_rope_qk_fwd_kernel(NrPair<typenam
       const float np = partner<TPR>(n);
       o.v[e] = n * cv.v[e] + sign * np * sv.v[e];
     }
-    if (valid) store_vec<T>(y + row * D + t * V, o);
+    if (valid) store_vec<T>(y + out_off(row) + t * V, o);
   }
 }
 
@@ -813,14 +835,23 @@ int nr_qk_fwd_dispatch(const NrPair<typename T::storage>& p, const void* cs, con
   if (d % V != 0 || (d / 2) % V != 0 || (tpr != 8 && tpr != 16 && tpr != 32)) return Q3_ERR_INVALID;
   // each segment's grid as its single-tensor launch sizes it
   NrPair<S> q = p;
-  for (int i = 0; i < 2; ++i) {
+  const int nseg = p.cap > 0 ? 3 : 2;
+  for (int i = 0; i < nseg; ++i) {
     const int64_t g = (p.rows[i] + kBlock / tpr - 1) / (kBlock / tpr);
     q.blocks[i] = (int)(g > 256 * 16 ? 256 * 16 : g);
   }
-  const unsigned grid = (unsigned)(q.blocks[0] + q.blocks[1]);
-  if (tpr == 8) norm_rope_qk_fwd_kernel<T, 8><<<grid, kBlock, 0, s>>>(q, (const S*)cs, (const S*)sn, eps);
-  else if (tpr == 16) norm_rope_qk_fwd_kernel<T, 16><<<grid, kBlock, 0, s>>>(q, (const S*)cs, (const S*)sn, eps);
-  else norm_rope_qk_fwd_kernel<T, 32><<<grid, kBlock, 0, s>>>(q, (const S*)cs, (const S*)sn, eps);
+  const unsigned grid = (unsigned)(q.blocks[0] + q.blocks[1] + (nseg == 3 ? q.blocks[2] : 0));
+  const S* c = (const S*)cs;
+  const S* n = (const S*)sn;
+  if (nseg == 3) {
+    if (tpr == 8) norm_rope_qk_fwd_kernel<T, 8, true><<<grid, kBlock, 0, s>>>(q, c, n, eps);
+    else if (tpr == 16) norm_rope_qk_fwd_kernel<T, 16, true><<<grid, kBlock, 0, s>>>(q, c, n, eps);
+    else norm_rope_qk_fwd_kernel<T, 32, true><<<grid, kBlock, 0, s>>>(q, c, n, eps);
+  } else {
+    if (tpr == 8) norm_rope_qk_fwd_kernel<T, 8, false><<<grid, kBlock, 0, s>>>(q, c, n, eps);
+    else if (tpr == 16) norm_rope_qk_fwd_kernel<T, 16, false><<<grid, kBlock, 0, s>>>(q, c, n, eps);
+    else norm_rope_qk_fwd_kernel<T, 32, false><<<grid, kBlock, 0, s>>>(q, c, n, eps);
+  }
   return (int)hipGetLastError();
 }
 
@@ -840,6 +871,30 @@ int nr_qk_bwd_dispatch(const NrPair<typename T::storage>& p, const void* cs, con
   else norm_rope_qk_bwd_kernel<T, 32><<<(unsigned)nb, kBlock, 0, s>>>(q, (const S*)cs, (const S*)sn, part, eps);
   colsum<T>(part, (S*)dw, (int)nb, (int)(2 * d), s);
   return (int)hipGetLastError();
+}
+
+template <typename T>
+int nr_qk_cache_fwd_t(const void* q, const void* k, const void* v, const void* wq, const void* wk, const void* cs,
+                      const void* sn, void* yq, void* ck, void* cv, int64_t B, int64_t S_, int64_t hq, int64_t hk,
+                      int64_t d, int64_t cap, int64_t start, float eps, hipStream_t s) {
+  typedef typename T::storage S;
+  NrPair<S> p{};
+  p.x[0] = (const S*)q;
+  p.x[1] = (const S*)k;
+  p.x[2] = (const S*)v;
+  p.w[0] = (const S*)wq;
+  p.w[1] = (const S*)wk;
+  p.y[0] = (S*)yq;
+  p.y[1] = (S*)ck;
+  p.y[2] = (S*)cv;
+  p.rows[0] = B * S_ * hq;
+  p.rows[1] = p.rows[2] = B * S_ * hk;
+  p.heads[0] = (int)hq;
+  p.heads[1] = p.heads[2] = (int)hk;
+  p.cap = cap;
+  p.start = start;
+  p.seq = S_;
+  return nr_qk_fwd_dispatch<T>(p, cs, sn, d, eps, s);
 }
 
 template <typename T>
@@ -943,6 +998,19 @@ int q3_norm_rope_qk_fwd(int dtype, const void* q, const void* k, const void* wq,
   Q3_REQUIRE(dtype_ok(dtype) && q && k && wq && wk && cos && sin && yq && yk && tokens > 0 && hq > 0 && hk > 0 &&
              d > 0 && d % 2 == 0 && d <= 4096 && eps > 0.f && tokens * (hq + hk) < (1ll << 40));
   return Q3_DISPATCH(dtype, nr_qk_fwd_t, q, k, wq, wk, cos, sin, yq, yk, tokens, hq, hk, d, eps, stream);
+}
+
+int q3_norm_rope_qk_cache_fwd(int dtype, const void* q, const void* k, const void* v, const void* wq, const void* wk,
+                              const void* cos, const void* sin, void* yq, void* cache_k, void* cache_v, int64_t B,
+                              int64_t S, int64_t hq, int64_t hk, int64_t d, int64_t capacity, int64_t start, float eps,
+                              hipStream_t stream) {
+  Q3_REQUIRE(dtype_ok(dtype) && q && k && v && wq && wk && cos && sin && yq && cache_k && cache_v && B > 0 && S > 0 &&
+             hq > 0 && hk > 0 && d > 0 && d % 2 == 0 && d <= 4096 && eps > 0.f && start >= 0 && start + S <= capacity &&
+             B * S * (hq + hk) < (1ll << 40) && B * hk * capacity * d < (1ll << 40));
+  Q3_REQUIRE((((uintptr_t)q | (uintptr_t)k | (uintptr_t)v | (uintptr_t)yq | (uintptr_t)cache_k |
+               (uintptr_t)cache_v) & 15) == 0);
+  return Q3_DISPATCH(dtype, nr_qk_cache_fwd_t, q, k, v, wq, wk, cos, sin, yq, cache_k, cache_v, B, S, hq, hk, d,
+                     capacity, start, eps, stream);
 }
 
 size_t q3_norm_rope_qk_bwd_workspace_bytes(int64_t tokens, int64_t hq, int64_t hk, int64_t d) {

@@ -35,6 +35,8 @@ SIGNATURES: dict[str, tuple] = {
     "q3_norm_rope_bwd_workspace_bytes": (_sz, [_i64, _i64, _i64]),
     "q3_norm_rope_bwd": (_i32, [_i32, _p, _p, _p, _p, _p, _p, _p, _p, _i64, _i64, _i64, _f32, _p]),
     "q3_norm_rope_qk_fwd": (_i32, [_i32, _p, _p, _p, _p, _p, _p, _p, _p, _i64, _i64, _i64, _i64, _f32, _p]),
+    "q3_norm_rope_qk_cache_fwd": (_i32, [_i32, _p, _p, _p, _p, _p, _p, _p, _p, _p, _p, _i64, _i64, _i64, _i64, _i64,
+                                         _i64, _i64, _f32, _p]),
     "q3_norm_rope_qk_bwd_workspace_bytes": (_sz, [_i64, _i64, _i64, _i64]),
     "q3_norm_rope_qk_bwd": (_i32, [_i32, _p, _p, _p, _p, _p, _p, _p, _p, _p, _p, _p, _p, _i64, _i64, _i64, _i64,
                                     _f32, _p]),

@@ -212,9 +212,15 @@ class TritonQwen3Inference(nn.Module):
                 q = q.view(b, s, a.num_heads, d)
                 k = k.view(b, s, a.num_kv_heads, d)
                 v = v.view(b, s, a.num_kv_heads, d)
-                q = kernels.norm_rope(q, a.q_norm.weight, cos, sin, a.q_norm.eps)
-                k = kernels.norm_rope(k, a.k_norm.weight, cos, sin, a.k_norm.eps)
-                kernels.append(k, v, cache.keys[i], cache.values[i], start, start_dev)
+                if start_dev is None and a.q_norm.eps == a.k_norm.eps and _ops.norm_rope_qk_ok(q, k, d) and \
+                        all(t.is_contiguous() for t in (q, k, v)):
+                    # Q/K-norm + RoPE of both tensors and the K/V cache append in one launch
+                    q = _ops.norm_rope_qk_cache_fwd(q, k, v, a.q_norm.weight, a.k_norm.weight, cos, sin,
+                                                    cache.keys[i], cache.values[i], start, a.q_norm.eps)
+                else:
+                    q = kernels.norm_rope(q, a.q_norm.weight, cos, sin, a.q_norm.eps)
+                    k = kernels.norm_rope(k, a.k_norm.weight, cos, sin, a.k_norm.eps)
+                    kernels.append(k, v, cache.keys[i], cache.values[i], start, start_dev)
                 y = kernels.attention(q, cache.keys[i], cache.values[i], start, split_decode=self.split_decode,
                                       start_dev=start_dev).reshape(b, s, -1)
                 x = _residual_projection(x, y, a.o_proj.weight, self.gemv)

@@ -87,6 +87,18 @@ def norm_rope_qk_fwd(q, k, wq, wk, cos, sin, eps):
     return yq, yk
 
 
+def norm_rope_qk_cache_fwd(q, k, v, wq, wk, cos, sin, cache_k, cache_v, start, eps):
+    """Prefill chunk: q / k / v [B, S, h, d] contiguous; returns the normed + rotated q and writes the
+    normed + rotated k and the raw v into the [B, hk, capacity, d] caches at ``start``."""
+    b, s, hq, d = q.shape
+    hk = k.shape[2]
+    yq = torch.empty_like(q)
+    H.call("q3_norm_rope_qk_cache_fwd", H.code(q.dtype), q.data_ptr(), k.data_ptr(), v.data_ptr(), wq.data_ptr(),
+           wk.data_ptr(), cos.data_ptr(), sin.data_ptr(), yq.data_ptr(), cache_k.data_ptr(), cache_v.data_ptr(), b, s,
+           hq, hk, d, cache_k.shape[2], start, float(eps), H.stream())
+    return yq
+
+
 def norm_rope_qk_bwd(q, k, wq, wk, cos, sin, dyq, dyk, eps):
     d, hq, hk = q.shape[-1], q.shape[-2], k.shape[-2]
     tokens = q.numel() // (d * hq)

@@ -11,8 +11,11 @@ prompts (B1 x 2048 and B8 x 1024 tokens, uniform over the vocabulary, seed 4).
    logits against an fp32 host oracle (``oracle.decoder_layer_reference``, the math of
    ``inference/model.py:102-142``) that streams one layer's weights from the device at a time, so
    host memory holds one layer.  The oracle runs the whole prompt + forced tokens causally, which
-   equals the cached computation position by position.  Each row's logits must meet the bf16
-   forward gate; greedy picks are counted exact / decisive and printed.
+   equals the cached computation position by position.  The same pass runs the oracle a second
+   time with every op's output stored in bf16 (the reference's own bf16 inference path), which
+   measures how far bf16 storage alone moves 36 layers from fp32 (about 5 % normwise at the
+   logits); each row's logits must be no further from fp32 than 1.25 x that, or within the
+   single-op 2e-2 gate.  Greedy picks are counted exact / decisive and printed.
 """
 import pytest
 import torch

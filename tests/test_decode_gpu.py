@@ -168,3 +168,28 @@ def test_greedy_select_ties_pad_eos(dtype):
     assert nxt[:, 0].tolist() == [5, v - 1, 9, int(exp[3])]
     assert ids[:, 6].tolist() == nxt[:, 0].tolist()
     assert done.tolist() == [False, True, True, False]
+
+
+@pytest.mark.parametrize("b,s,start,cap", [(1, 2048, 0, 2304), (8, 64, 100, 200), (2, 7, 5, 12)])
+def test_norm_rope_qk_cache_matches_separate_launches(b, s, start, cap):
+    """The prefill launch (Q/K-norm + RoPE of q and k, k and v into the cache) is bit-identical to the
+    two QK-norm + RoPE launches followed by the cache append, and leaves other cache positions alone."""
+    from qwen3_triton.kernels import _ops
+    from qwen3_triton.inference import kernels
+    print(f"norm_rope_qk_cache B{b} S{s} start {start} cap {cap}", flush=True)
+    gen = seeded(b * 1000 + s)
+    r = lambda *sh: torch.randn(*sh, generator=gen).to(torch.bfloat16).cuda()  # noqa: E731
+    q, k, v = r(b, s, 32, 128), r(b, s, 8, 128), r(b, s, 8, 128)
+    qw, kw = r(128) * 0.1 + 1, r(128) * 0.1 + 1
+    pos = torch.arange(start, start + s)[None].expand(b, s)
+    cos, sin = O.rotary_tables_reference(pos, O.rope_inv_freq(1e6, 128), dtype=torch.bfloat16)
+    cos, sin = cos.cuda(), sin.cuda()
+    ck0, cv0 = r(b, 8, cap, 128), r(b, 8, cap, 128)
+    ck1, cv1 = ck0.clone(), cv0.clone()
+    yq = _ops.norm_rope_qk_cache_fwd(q, k, v, qw, kw, cos, sin, ck1, cv1, start, 1e-6)
+    eq = _ops.norm_rope_fwd(q, qw, cos, sin, 1e-6)
+    ek = _ops.norm_rope_fwd(k, kw, cos, sin, 1e-6)
+    kernels.append(ek, v, ck0, cv0, start)
+    torch.cuda.synchronize()
+    assert torch.equal(yq, eq)
+    assert torch.equal(ck1, ck0) and torch.equal(cv1, cv0)
