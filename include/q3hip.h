@@ -278,6 +278,16 @@ int q3_ce_finish(const float* m_part, const float* s_part, int nchunks, const fl
 int q3_ce_chunk_grad(int dtype, int out_dtype, const void* z, int64_t ld, int64_t n, int64_t col0, const int64_t* tgt,
                      const float* lse, const float* count, const float* up, void* dz, int64_t ldo, int64_t rows,
                      int64_t vocab, int64_t ignore_index, hipStream_t stream);
+/* q3_ce_chunk_grad for 16-bit logits with the transposed copy the weight gradient needs:
+ * dz[r, c] (row stride ldo, out type = dtype; dz may be z itself with ldo == ld) and
+ * dzt[c * lddzt + r] = dz[r, c] for the chunk's n columns (n and rows multiples of 8, 16-byte aligned
+ * buffers, strides multiples of 8).  The backward of the fused LM-head + CE when the forward stored
+ * the chunk's bf16 logits (q3_gemm_nt_ce_stats_store): dz comes from the stored logits, with no second
+ * logits GEMM.
+ * Replaces: kernels/loss.py:34-44,64-68 (_backward) on the reference's bf16 logits. */
+int q3_ce_chunk_grad_t(int dtype, const void* z, int64_t ld, int64_t n, int64_t col0, const int64_t* tgt,
+                       const float* lse, const float* count, const float* up, void* dz, int64_t ldo, void* dzt,
+                       int64_t lddzt, int64_t rows, int64_t vocab, int64_t ignore_index, hipStream_t stream);
 /* The logits GEMM and q3_ce_chunk_grad in one kernel: z = A . B^T (A [M, K] token rows, B [N, K] the
  * chunk's vocabulary rows starting at column col0; K % 64 == 0, 16-byte aligned K-contiguous rows) is
  * formed in fp32 on the matrix cores and only dz (dtype, row stride lddz) is written, with the same
@@ -301,6 +311,13 @@ int q3_gemm_nt_ce_grad(int dtype, const void* A, int64_t lda, const void* B, int
 int q3_gemm_nt_ce_stats(int dtype, const void* A, int64_t lda, const void* B, int64_t ldb, int64_t M, int64_t N,
                         int64_t K, int64_t col0, const int64_t* tgt, float* m_part, float* s_part, float* pick,
                         int64_t part0, int64_t ldp, hipStream_t stream);
+/* q3_gemm_nt_ce_stats that also stores the logits rounded to dtype, z[row * ldz + col] (ldz a multiple
+ * of 8, 16-byte aligned z), and forms the statistics from those rounded values -- the bf16 logits of
+ * the reference's lm_head output (_model.py:131-132), kept for the backward.
+ * Replaces: the logits matmul of _model.py:131-132 with kernels/loss.py:6-33,55-61 (_partials, _rows). */
+int q3_gemm_nt_ce_stats_store(int dtype, const void* A, int64_t lda, const void* B, int64_t ldb, int64_t M, int64_t N,
+                              int64_t K, int64_t col0, const int64_t* tgt, float* m_part, float* s_part, float* pick,
+                              int64_t part0, int64_t ldp, void* z, int64_t ldz, hipStream_t stream);
 
 /* ------------------------------------------------------------------ greedy decode
  * y[m, n] = sum_k x[m, k] * W[n, k] for m < M <= 16 (x rows at stride ldx, y rows at stride ldy),

@@ -239,6 +239,65 @@ int grad_t2(const void* z, int64_t ld, int64_t n, int64_t col0, const int64_t* t
   return (int)hipGetLastError();
 }
 
+// dz (in the input's 16-bit type) and its transpose for one logits chunk: a workgroup takes 64 rows x
+// 128 columns, computes dz with q3_ce_chunk_grad's expression, stores it row-major (16-byte stores; dz
+// may be the logits buffer itself: every element is read before it is written by the same thread) and
+// through an LDS tile (rows padded to 65 words: conflict-free row writes and column gathers) as
+// dzt[col][row] with 16-byte stores of 8 rows.
+template <typename T>
+__global__ __launch_bounds__(kThreads) void ce_grad_t_kernel(const u16* z, int64_t ld, int64_t n, int64_t col0,
+                                                             const int64_t* __restrict__ tgt,
+                                                             const float* __restrict__ lse,
+                                                             const float* __restrict__ count,
+                                                             const float* __restrict__ up, u16* dz, int64_t ldo,
+                                                             u16* __restrict__ dzt, int64_t lddzt, int64_t rows,
+                                                             int64_t vocab, int64_t ignore) {
+  constexpr int TR = 64, TC = 128, RP = TC + 2;
+  __shared__ __attribute__((aligned(16))) u16 tile[TR * RP];
+  const int64_t r0 = (int64_t)blockIdx.y * TR, c0 = (int64_t)blockIdx.x * TC;
+  const int tid = threadIdx.x, ch = tid & 15, rr = tid >> 4;
+  const int64_t col = c0 + 8 * ch;
+  const bool colok = col < n;
+  const float sc = (up ? *up : 1.f) / *count;
+  i32x4 zv[4];
+  int64_t tv[4];
+  float lv[4];
+#pragma unroll
+  for (int k = 0; k < 4; ++k) {  // every load first (clamped indices, masked below)
+    const int64_t row = min(r0 + rr + 16 * k, rows - 1);
+    zv[k] = *reinterpret_cast<const i32x4*>(z + row * ld + (colok ? col : 0));
+    tv[k] = tgt[row];
+    lv[k] = lse[row];
+  }
+#pragma unroll
+  for (int k = 0; k < 4; ++k) {
+    const int64_t row = r0 + rr + 16 * k;
+    const bool valid = tv[k] != ignore && tv[k] >= 0 && tv[k] < vocab;
+    const Vec<T> a = unpack_vec<T>(zv[k]);
+    Vec<T> o;
+#pragma unroll
+    for (int e = 0; e < 8; ++e)
+      o.v[e] = valid ? (__expf(a.v[e] - lv[k]) - ((col + e + col0 == tv[k]) ? 1.f : 0.f)) * sc : 0.f;
+    i32x4 pk;
+#pragma unroll
+    for (int w = 0; w < 4; ++w) pk[w] = (int)pack2<T>(o.v[2 * w], o.v[2 * w + 1]);
+    if (row < rows && colok) *reinterpret_cast<i32x4*>(dz + row * ldo + col) = pk;
+    uint32_t* tl = reinterpret_cast<uint32_t*>(tile + (rr + 16 * k) * RP + 8 * ch);
+#pragma unroll
+    for (int w = 0; w < 4; ++w) tl[w] = (uint32_t)pk[w];
+  }
+  __syncthreads();
+#pragma unroll
+  for (int k = 0; k < 4; ++k) {  // 8 lanes per output row: dzt[c0 + c][r0 + 8 q .. + 7]
+    const int idx = tid + kThreads * k, q = idx & 7, c = idx >> 3;
+    i32x4 v;
+#pragma unroll
+    for (int w = 0; w < 4; ++w)
+      v[w] = (int)((uint32_t)tile[(8 * q + 2 * w) * RP + c] | ((uint32_t)tile[(8 * q + 2 * w + 1) * RP + c] << 16));
+    if (c0 + c < n && r0 + 8 * q < rows) *reinterpret_cast<i32x4*>(dzt + (c0 + c) * lddzt + r0 + 8 * q) = v;
+  }
+}
+
 template <typename T>
 int grad_t(int out_dtype, const void* z, int64_t ld, int64_t n, int64_t col0, const int64_t* tgt, const float* lse,
            const float* count, const float* up, void* dz, int64_t ldo, int64_t rows, int64_t vocab, int64_t ignore,
@@ -278,6 +337,24 @@ int q3_ce_finish(const float* m_part, const float* s_part, int nchunks, const fl
   ce_finish_kernel<<<(unsigned)((rows + kFinRows - 1) / kFinRows), kThreads, 0, stream>>>(
       m_part, s_part, nchunks, pick, tgt, lse, loss_rows, bad, rows, vocab, ignore_index);
   ce_mean_kernel<<<1, kThreads, 0, stream>>>(loss_rows, tgt, rows, vocab, ignore_index, loss, count);
+  return (int)hipGetLastError();
+}
+
+int q3_ce_chunk_grad_t(int dtype, const void* z, int64_t ld, int64_t n, int64_t col0, const int64_t* tgt,
+                       const float* lse, const float* count, const float* up, void* dz, int64_t ldo, void* dzt,
+                       int64_t lddzt, int64_t rows, int64_t vocab, int64_t ignore_index, hipStream_t stream) {
+  Q3_REQUIRE((dtype == Q3_BF16 || dtype == Q3_F16) && z && tgt && lse && count && dz && dzt && n > 0 && rows > 0 &&
+             rows < (1ll << 31) && n % 8 == 0 && rows % 8 == 0 && ld >= n && ldo >= n && lddzt >= rows &&
+             ld % 8 == 0 && ldo % 8 == 0 && lddzt % 8 == 0 && (((uintptr_t)z | (uintptr_t)dz | (uintptr_t)dzt) & 15) == 0);
+  // dz may be z itself (in place), but no other overlap
+  Q3_REQUIRE(dz == z ? ldo == ld : true);
+  const dim3 g((unsigned)((n + 127) / 128), (unsigned)((rows + 63) / 64));
+  if (dtype == Q3_BF16)
+    ce_grad_t_kernel<BF16><<<g, kThreads, 0, stream>>>((const u16*)z, ld, n, col0, tgt, lse, count, up, (u16*)dz, ldo,
+                                                       (u16*)dzt, lddzt, rows, vocab, ignore_index);
+  else
+    ce_grad_t_kernel<F16><<<g, kThreads, 0, stream>>>((const u16*)z, ld, n, col0, tgt, lse, count, up, (u16*)dz, ldo,
+                                                      (u16*)dzt, lddzt, rows, vocab, ignore_index);
   return (int)hipGetLastError();
 }
 

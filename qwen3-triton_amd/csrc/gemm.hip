@@ -232,6 +232,10 @@ struct CeEpi {
   // EPI 3: when set, also Y^T [N, M] (row stride ldyt), the down projection's weight-gradient operand
   u16* yt;
   int64_t ldyt;
+  // EPI 2: when set, the logits rounded to the storage type are stored too (row stride ldzs), and the
+  // statistics are formed from those rounded values
+  u16* zs;
+  int64_t ldzs;
 };
 
 Q3_DEV void lse_merge(float& m, float& s, float m2, float s2) {
@@ -686,6 +690,41 @@ __global__ __launch_bounds__(WM * WN * 64) void gemm_nt_v4_kernel(const u16* __r
   }
   if constexpr (EPI == 2) {
     static_assert(TNW == 128, "one statistics partial per 128 columns");
+    if (ce.zs) {
+#pragma unroll
+      for (int i = 0; i < FM; ++i)
+#pragma unroll
+        for (int j = 0; j < FN; ++j)
+#pragma unroll
+          for (int v = 0; v < 4; ++v) acc[i][j][v] = to_f32<T>(from_f32<T>(acc[i][j][v]));
+      if constexpr (EVEN && O::vec == 8) {
+        if (vec_store == 2) {
+          constexpr auto NC = std::integral_constant<int, TNW>{};
+          __syncthreads();  // every wave is done with the operand ring
+#pragma unroll
+          for (int i = 0; i < FM; ++i)
+#pragma unroll
+            for (int j = 0; j < FN; ++j)
+              stage(NC, i, j, pack2<T>(acc[i][j][0], acc[i][j][1]), pack2<T>(acc[i][j][2], acc[i][j][3]));
+          flush(NC, ce.zs + (int64_t)(m0 + wm * TMW) * ce.ldzs + n0 + wn * TNW, ce.ldzs,
+                std::integral_constant<int, TMW>{});
+        }
+      }
+      if (!(EVEN && O::vec == 8 && vec_store == 2)) {
+#pragma unroll
+        for (int i = 0; i < FM; ++i) {
+          const int row = m0 + wm * TMW + i * 16 + (lane & 15);
+          if (row >= M) continue;
+#pragma unroll
+          for (int j = 0; j < FN; ++j)
+#pragma unroll
+            for (int v = 0; v < 4; ++v) {
+              const int col = n0 + wn * TNW + j * 16 + 4 * quarter + v;
+              if (col < N) ce.zs[(int64_t)row * ce.ldzs + col] = from_f32<T>(acc[i][j][v]);
+            }
+        }
+      }
+    }
     const int64_t part = ce.part0 + (n0 + wn * TNW) / 128;
 #pragma unroll
     for (int i = 0; i < FM; ++i) {
@@ -1021,6 +1060,20 @@ int q3_gemm_nt_ce_stats(int dtype, const void* A, int64_t lda, const void* B, in
   Q3_REQUIRE(M > 0 && N > 0 && K > 0 && M < (1ll << 31) && N < (1ll << 31) && K < (1ll << 31) && K % 64 == 0);
   Q3_REQUIRE(lda % 8 == 0 && ldb % 8 == 0 && lda >= K && ldb >= K && ldp >= M && part0 >= 0 && al16(A) && al16(B));
   const CeEpi ce{tgt, nullptr, nullptr, nullptr, col0, 0, 0, m_part, s_part, pick, part0, ldp};
+  if (dtype == Q3_BF16) return launch_ce_stats<BF16>(A, lda, B, ldb, M, N, K, ce, stream);
+  return launch_ce_stats<F16>(A, lda, B, ldb, M, N, K, ce, stream);
+}
+
+int q3_gemm_nt_ce_stats_store(int dtype, const void* A, int64_t lda, const void* B, int64_t ldb, int64_t M, int64_t N,
+                              int64_t K, int64_t col0, const int64_t* tgt, float* m_part, float* s_part, float* pick,
+                              int64_t part0, int64_t ldp, void* z, int64_t ldz, hipStream_t stream) {
+  Q3_REQUIRE((dtype == Q3_BF16 || dtype == Q3_F16) && A && B && tgt && m_part && s_part && pick && z);
+  Q3_REQUIRE(M > 0 && N > 0 && K > 0 && M < (1ll << 31) && N < (1ll << 31) && K < (1ll << 31) && K % 64 == 0);
+  Q3_REQUIRE(lda % 8 == 0 && ldb % 8 == 0 && lda >= K && ldb >= K && ldp >= M && part0 >= 0 && al16(A) && al16(B));
+  Q3_REQUIRE(ldz >= N && ldz % 8 == 0 && al16(z));
+  CeEpi ce{tgt, nullptr, nullptr, nullptr, col0, 0, 0, m_part, s_part, pick, part0, ldp};
+  ce.zs = (u16*)z;
+  ce.ldzs = ldz;
   if (dtype == Q3_BF16) return launch_ce_stats<BF16>(A, lda, B, ldb, M, N, K, ce, stream);
   return launch_ce_stats<F16>(A, lda, B, ldb, M, N, K, ce, stream);
 }

@@ -77,6 +77,10 @@ SIGNATURES: dict[str, tuple] = {
                                   _p, _i64, _i64, _p]),
     "q3_gemm_nt_ce_stats": (_i32, [_i32, _p, _i64, _p, _i64, _i64, _i64, _i64, _i64, _p, _p, _p, _p, _i64, _i64,
                                    _p]),
+    "q3_gemm_nt_ce_stats_store": (_i32, [_i32, _p, _i64, _p, _i64, _i64, _i64, _i64, _i64, _p, _p, _p, _p, _i64,
+                                         _i64, _p, _i64, _p]),
+    "q3_ce_chunk_grad_t": (_i32, [_i32, _p, _i64, _i64, _i64, _p, _p, _p, _p, _p, _i64, _p, _i64, _i64, _i64, _i64,
+                                  _p]),
     "q3_gemv": (_i32, [_i32, _p, _i64, _p, _p, _i64, _i64, _i64, _i64, _p]),
     "q3_decode_linear": (_i32, [_i32, _p, _i64, _i64, _i64, _p, _f32, _i32, _i32, _p, _p, _p, _p, _p, _i64, _p]),
     "q3_kv_append": (_i32, [_i32, _p, _p, _p, _p, _i64, _i64, _i64, _i64, _i64, _i64, _p, _p]),

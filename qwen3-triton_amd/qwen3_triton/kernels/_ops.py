@@ -349,6 +349,14 @@ class CEState:
                t, n, h, col0, tgt.data_ptr(), self.m.data_ptr(), self.s.data_ptr(), self.pick.data_ptr(), part0,
                self.rows, H.stream())
 
+    def gemm_stats_store(self, part0, x, w, col0, n, tgt, z):
+        """gemm_stats that also stores the logits in x's dtype into z[:, :n] (statistics from the stored,
+        rounded values)."""
+        t, h = x.shape
+        H.call("q3_gemm_nt_ce_stats_store", H.code(x.dtype), x.data_ptr(), x.stride(0), w[col0:].data_ptr(),
+               w.stride(0), t, n, h, col0, tgt.data_ptr(), self.m.data_ptr(), self.s.data_ptr(),
+               self.pick.data_ptr(), part0, self.rows, z.data_ptr(), z.stride(0), H.stream())
+
     def finish(self, tgt, vocab, ignore_index, check=True):
         capturing = torch.cuda.is_current_stream_capturing()
         bad = None if (capturing or not check) else torch.zeros((), device=tgt.device, dtype=torch.int32)
@@ -375,6 +383,13 @@ def ce_grad_transposed_ok(x, t, n, lddz, dz, dzt):
     """Whether q3_gemm_nt_ce_grad can write the transposed dz copy for this chunk."""
     return t % 256 == 0 and n % 256 == 0 and (t // 256) * (n // 256) >= 256 and lddz % 8 == 0 and \
         dz.data_ptr() % 16 == 0 and dzt.stride(0) % 8 == 0 and dzt.data_ptr() % 16 == 0
+
+
+def ce_grad_t(z, n, col0, tgt, lse, count, up, dz, dzt, vocab, ignore_index):
+    """dz[:, :n] (may be z itself) and dzt[:n, :] from stored 16-bit logits z[:, :n]."""
+    H.call("q3_ce_chunk_grad_t", H.code(z.dtype), z.data_ptr(), z.stride(0), n, col0, tgt.data_ptr(), lse.data_ptr(),
+           count.data_ptr(), 0 if up is None else up.data_ptr(), dz.data_ptr(), dz.stride(0), dzt.data_ptr(),
+           dzt.stride(0), tgt.numel(), vocab, int(ignore_index), H.stream())
 
 
 def ce_grad(z, ld, n, col0, tgt, lse, count, up, dz, ldo, vocab, ignore_index):

@@ -1,12 +1,15 @@
-"""Fused LM head + causal cross-entropy without materialising the full logits.
+"""Fused LM head + causal cross-entropy without materialising full fp32 logits.
 
 New in this build (the reference materialises [B,S,V] logits: ``qwen3_triton/_model.py:131-132``
 ``lm_head`` then ``kernels/loss.py:46-71``).  The vocabulary is processed in chunks of ``chunk``
 columns: each chunk's fp32 logits come from the matrix-core GEMM (h . W_c^T) into one reusable
 [T, chunk] buffer and are folded into per-row (max, sum-exp) partials plus the target logit; a
-final merge gives lse and the token-mean loss.  Backward recomputes each chunk's logits, turns them
-into dz = (softmax - onehot) * up / count (bf16), accumulates dH += dz . W_c in fp32 and writes
-dW_c = dz^T . h.  The same math as ``linear`` followed by ``causal_cross_entropy``.
+final merge gives lse and the token-mean loss.  On the matrix-core path the logits GEMM's epilogue also
+keeps each chunk's logits in the activation dtype (bf16: the reference's own lm_head output, whose
+[T, V] copy it materialises too), and the statistics are formed from those stored values; the backward
+turns them in place into dz = (softmax - onehot) * up / count plus dz^T, writes dW_c = dz_c^T . h per
+chunk and dX = dz . W in one GEMM.  Other shapes recompute each chunk's logits in the backward.  The
+same math as ``linear`` followed by ``causal_cross_entropy``.
 """
 import torch
 
@@ -46,15 +49,23 @@ class _LMHeadCE(torch.autograd.Function):
         tgt = _ops.ce_shift_labels(labels, ignore_index)
         chunk = min(chunk, v)
         nch = -(-v // chunk)
+        z = None
         if _mfma_ok(hidden, weight) and h % 64 == 0:
             # logits GEMM with the statistics epilogue: one partial per 128 logit columns, no fp32
-            # logits in memory
+            # logits in memory.  Where the shapes allow, the epilogue also keeps the logits in the
+            # activation dtype (the reference's bf16 lm_head output) for the backward, which then
+            # needs no second logits GEMM.
             groups = [-(-min(chunk, v - c * chunk) // 128) for c in range(nch)]
             st = _ops.CEState(b * s, sum(groups), hidden.device)
+            if (b * s) % 8 == 0 and chunk % 8 == 0:
+                z = torch.empty((b * s, -(-v // 64) * 64), device=hidden.device, dtype=hidden.dtype)
             part0 = 0
             for c in range(nch):
                 c0 = c * chunk
-                st.gemm_stats(part0, x, weight, c0, min(chunk, v - c0), tgt)
+                if z is not None:
+                    st.gemm_stats_store(part0, x, weight, c0, min(chunk, v - c0), tgt, z[:, c0:])
+                else:
+                    st.gemm_stats(part0, x, weight, c0, min(chunk, v - c0), tgt)
                 part0 += groups[c]
         else:
             st = _ops.CEState(b * s, nch, hidden.device)
@@ -67,6 +78,7 @@ class _LMHeadCE(torch.autograd.Function):
         loss = st.finish(tgt, v, ignore_index)
         ctx.save_for_backward(hidden, weight, tgt, st.lse, st.count)
         ctx.ignore, ctx.chunk = ignore_index, chunk
+        ctx.z = z
         return loss.clone()
 
     @staticmethod
@@ -78,6 +90,24 @@ class _LMHeadCE(torch.autograd.Function):
         up = dy.float().contiguous()
         dw = torch.empty_like(weight)
         mfma = _mfma_ok(x, weight) and t % 8 == 0
+        z, ctx.z = ctx.z, None   # consumed: dz overwrites the stored logits in place
+        if z is not None:
+            # dz of every chunk from the stored logits, in place, and its transpose (the dW operand);
+            # dW_c = dz_c^T . x per chunk, dX = dz . W in one GEMM over the whole vocabulary.
+            vp = z.shape[1]
+            if vp > v:
+                z[:, v:].zero_()
+            wt = _ops.transpose_last2(weight, pad_to=64)  # [H, Vp]
+            xt = _ops.transpose_last2(x)                  # [H, T]
+            dzt = torch.empty((chunk, t), device=x.device, dtype=x.dtype)
+            for c in range(-(-v // chunk)):
+                c0 = c * chunk
+                n = min(chunk, v - c0)
+                _ops.ce_grad_t(z[:, c0:], n, c0, tgt, lse, count, up, z[:, c0:], dzt, v, ctx.ignore)
+                gemm_nt_into(dzt, t, xt, t, dw[c0:c0 + n], n, h, t)
+            dx = torch.empty((t, h), device=x.device, dtype=x.dtype)
+            gemm_nt_into(z, vp, wt, vp, dx, t, h, vp)
+            return dx.view(b, s, h), dw, None, None, None
         if mfma and h % 64 == 0:
             # Every chunk's dz lands in one [T, Vp] buffer (Vp = V rounded up to 64, zero pad) written
             # by the logits GEMM's CE-gradient epilogue; dW_c = dz_c^T . x per chunk, and dX = dz . W

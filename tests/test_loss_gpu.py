@@ -76,7 +76,8 @@ def test_lm_head_ce_config_shape_sampled_rows():
     xd, wd, yd = x.cuda().requires_grad_(), w.cuda().requires_grad_(), y.cuda()
     loss = lm_head_cross_entropy(xd, wd, yd)
     dx, dw = torch.autograd.grad(loss, (xd, wd))
-    # per-row pieces from the same kernels
+    # per-row pieces from the unfused kernels on the same bf16 logits (the fused path keeps the logits
+    # in bf16, the reference's lm_head output dtype, and forms its statistics from them)
     tgt = _ops.ce_shift_labels(yd, -100)
     st = _ops.CEState(b * s, 10, "cuda")
     zbuf = torch.empty(b * s, 16384, device="cuda")
@@ -84,7 +85,8 @@ def test_lm_head_ce_config_shape_sampled_rows():
     for c in range(10):
         n = min(16384, v - c * 16384)
         _chunk_logits(xf, wd.detach(), c * 16384, n, zbuf)
-        st.stats(c, zbuf, 16384, n, c * 16384, tgt)
+        zb = zbuf.to(torch.bfloat16)
+        st.stats(c, zb, 16384, n, c * 16384, tgt)
     st.finish(tgt, v, -100)
     assert abs(float(st.loss) - float(loss)) <= 1e-6 * abs(float(loss))
     rows = torch.randperm(b * s, generator=gen)[:24]
@@ -94,7 +96,9 @@ def test_lm_head_ce_config_shape_sampled_rows():
     tg = tgt.cpu()[rows]
     assert (st.lse.cpu()[rows].double() - lse).abs().max() < 2e-3
     valid = tg != -100
-    el = torch.where(valid, lse - z.gather(1, tg.clamp_min(0)[:, None])[:, 0], torch.zeros_like(lse))
+    # the target logit as the bf16 logits hold it (the reference's lm_head output is bf16 as well)
+    zt = z.gather(1, tg.clamp_min(0)[:, None])[:, 0].to(torch.bfloat16).double()
+    el = torch.where(valid, lse - zt, torch.zeros_like(lse))
     assert (st.loss_rows.cpu()[rows].double() - el).abs().max() < 2e-3
     count = float((tgt != -100).sum())
     p = torch.softmax(z, -1)
@@ -179,3 +183,74 @@ def test_fused_ce_stats_gemm_matches_two_step(t, h, v, chunk):
     valid = (tgt != -100).cpu()
     assert max_rel(fused.lse.cpu()[valid], ref.lse.cpu()[valid].double()) < 1e-6
     assert abs(float(loss_f) - float(loss_r)) <= 1e-6 * abs(float(loss_r))
+
+
+@pytest.mark.parametrize("t,h,v,chunk", [(512, 256, 5000, 2048), (1024, 512, 9000, 4096), (256, 64, 8576, 4096)])
+def test_fused_ce_stats_store_matches_rounded_two_step(t, h, v, chunk):
+    """The statistics GEMM that also stores the logits: the stored chunk is the fp32 GEMM logits rounded
+    to bf16 bit for bit (full and ragged tiles), and lse / loss equal the statistics of those rounded
+    logits to fp32 rounding of the merge order."""
+    print(f"fused ce stats store t={t} h={h} v={v} chunk={chunk}", flush=True)
+    gen = seeded(t + v + 1)
+    x = randn(t, h, gen=gen, dtype=torch.bfloat16).cuda()
+    w = (randn(v, h, gen=gen) * 0.05).to(torch.bfloat16).cuda()
+    tgt = torch.randint(0, v, (t,), generator=gen)
+    tgt[::9] = -100
+    tgt = tgt.cuda()
+    nch = -(-v // chunk)
+    groups = [-(-min(chunk, v - c * chunk) // 128) for c in range(nch)]
+    fused = _ops.CEState(t, sum(groups), x.device)
+    vp = -(-v // 64) * 64
+    zs = torch.full((t, vp), 3.0, device="cuda", dtype=torch.bfloat16)
+    part0 = 0
+    for c in range(nch):
+        fused.gemm_stats_store(part0, x, w, c * chunk, min(chunk, v - c * chunk), tgt, zs[:, c * chunk:])
+        part0 += groups[c]
+    loss_f = fused.finish(tgt, v, -100).clone()
+    ref = _ops.CEState(t, nch, x.device)
+    z = torch.empty(t, chunk, device="cuda", dtype=torch.float32)
+    for c in range(nch):
+        n = min(chunk, v - c * chunk)
+        _chunk_logits(x, w, c * chunk, n, z)
+        zb = z.to(torch.bfloat16)
+        assert torch.equal(zs[:, c * chunk:c * chunk + n], zb[:, :n])
+        ref.stats(c, zb, chunk, n, c * chunk, tgt)
+    assert torch.all(zs[:, v:].float() == 3.0)                  # nothing past the vocabulary written
+    loss_r = ref.finish(tgt, v, -100).clone()
+    valid = (tgt != -100).cpu()
+    assert max_rel(fused.lse.cpu()[valid], ref.lse.cpu()[valid].double()) < 1e-6
+    assert abs(float(loss_f) - float(loss_r)) <= 1e-6 * abs(float(loss_r))
+
+
+@pytest.mark.parametrize("t,n,col0,inplace", [(512, 1000, 3000, False), (8192, 16384, 0, True),
+                                              (64, 4480, 147456, True), (24, 136, 8, False)])
+def test_ce_grad_transposed_matches_chunk_grad(t, n, col0, inplace):
+    """dz from stored bf16 logits with its transpose (q3_ce_chunk_grad_t) equals q3_ce_chunk_grad on the
+    same logits bit for bit, in place or not, with ignored and in-chunk targets; dzt = dz^T."""
+    print(f"ce grad t t={t} n={n} col0={col0} inplace={inplace}", flush=True)
+    gen = seeded(t + n + col0)
+    v = col0 + n + 9
+    ld = n + 24
+    z = (randn(t, ld, gen=gen) * 3).to(torch.bfloat16).cuda()
+    tgt = torch.randint(0, v, (t,), generator=gen)
+    tgt[::7] = -100
+    tgt[1::5] = col0 + torch.randint(0, n, (len(tgt[1::5]),), generator=gen)
+    tgt = tgt.cuda()
+    lse = (randn(t, gen=gen) + 6.0).cuda()
+    count = torch.tensor([float((tgt != -100).sum())], device="cuda")
+    up = torch.tensor([1.25], device="cuda")
+    ref = torch.empty(t, n, device="cuda", dtype=torch.bfloat16)
+    _ops.ce_grad(z, ld, n, col0, tgt, lse, count, up, ref, n, v, -100)
+    dzt = torch.full((n, t + 8), 5.0, device="cuda", dtype=torch.bfloat16)
+    if inplace:
+        zc = z.clone()
+        _ops.ce_grad_t(zc, n, col0, tgt, lse, count, up, zc, dzt, v, -100)
+        dz = zc
+        assert torch.equal(zc[:, n:], z[:, n:])                    # columns past n untouched
+    else:
+        dz = torch.full((t, ld), 7.0, device="cuda", dtype=torch.bfloat16)
+        _ops.ce_grad_t(z, n, col0, tgt, lse, count, up, dz, dzt, v, -100)
+        assert torch.all(dz[:, n:].float() == 7.0)
+    assert torch.equal(dz[:, :n], ref)
+    assert torch.equal(dzt[:, :t], ref.t())
+    assert torch.all(dzt[:, t:].float() == 5.0)
