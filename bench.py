@@ -33,7 +33,7 @@ PEAK_HBM_GBS = 8000.0       # MI355X HBM3E
 # device copy read 1 GiB): every GEMM dispatch of one step (13: the Q/K/V weight gradient runs as two)
 # summed and divided by the step's 12 GEMM calls.  Re-measure with those two passes (rocprofv3 --pmc
 # FETCH_SIZE / WRITE_SIZE -- python bench.py --pmc-probe) when the GEMM kernels change.
-GEMM_TRAFFIC_BYTES_PER_LAUNCH = 1221.6e6 + 204.5e6
+GEMM_TRAFFIC_BYTES_PER_LAUNCH = 1238.6e6 + 204.6e6
 
 
 def qwen3_8b_config(layers):
