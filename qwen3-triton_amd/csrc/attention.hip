@@ -262,7 +262,8 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2, 2))
 // step hand over P in exactly the key order of a 16-byte chunk of the permuted V^T copy
 // (positions 0-3, 8-11, 4-7, 12-15 of every 16-block): P is the B operand of P.V as it comes out
 // of the exponentials.  Row statistics need one max over the 4 lanes of a query (gfx950
-// permlane16/32 swaps); the row sums stay per lane until the end.
+// permlane16/32 swaps); the row sums come from the matrix cores (a block of ones times P, beside
+// P.V), so the VALU forms no sums.
 // Online softmax with a lazy rescale: the running max m (raw score units) moves only when a block
 // max exceeds it by more than 8 / scale2 (a factor 2^8 in p), so O is rarely rescaled; p <= 2^8
 // is exact in fp32 and in the bf16/fp16 P operand range.
@@ -369,7 +370,12 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
   for (int dt = 0; dt < 8; ++dt)
 #pragma unroll
     for (int u = 0; u < 2; ++u) oacc[dt][u] = f32x4{0.f, 0.f, 0.f, 0.f};
-  float m[2] = {-INFINITY, -INFINITY}, l[2] = {0.f, 0.f}, alpha[2] = {1.f, 1.f};
+  // Row sums on the matrix cores: a block of ones as the A operand gives lsum[u] = sum over keys of P,
+  // every element of the quad equal (the P that P.V uses, rescaled with O like a 129th column).
+  const uint32_t one2 = pack2<T>(1.f, 1.f);
+  const i32x4 ones = i32x4{(int)one2, (int)one2, (int)one2, (int)one2};
+  f32x4 lsum[2] = {f32x4{0.f, 0.f, 0.f, 0.f}, f32x4{0.f, 0.f, 0.f, 0.f}};
+  float m[2] = {-INFINITY, -INFINITY}, alpha[2] = {1.f, 1.f};
   bool pend = false;
   const float thr = 8.f / scale2;
 
@@ -395,6 +401,10 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
 #pragma unroll
         for (int u = 0; u < 2; ++u) oacc[dt][u] = mma16<T>(as_frag(a), as_frag(P[u][kc]), oacc[dt][u]);
       }
+#pragma unroll
+    for (int kc = 0; kc < 2; ++kc)
+#pragma unroll
+      for (int u = 0; u < 2; ++u) lsum[u] = mma16<T>(as_frag(ones), as_frag(P[u][kc]), lsum[u]);
   };
   auto rescale = [&]() {
     if (pend) {
@@ -404,6 +414,10 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
         for (int u = 0; u < 2; ++u)
 #pragma unroll
           for (int i = 0; i < 4; ++i) oacc[dt][u][i] *= alpha[u];
+#pragma unroll
+      for (int u = 0; u < 2; ++u)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) lsum[u][i] *= alpha[u];
     }
   };
   // row max of S(j) for query tile u, then (after both) the lazy-rescale decision
@@ -423,20 +437,14 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
       need[u] = bm[u] > m[u] + thr;
       const float mn = need[u] ? bm[u] : m[u];
       alpha[u] = __builtin_amdgcn_exp2f((m[u] - mn) * scale2);
-      l[u] *= alpha[u];
       m[u] = mn;
       ms[u] = mn == -INFINITY ? 0.f : mn * scale2;
     }
     pend = __any(need[0] || need[1]);
   };
-  auto expo = [&](int u, int kt) {  // p = exp2(s * scale2 - m * scale2), summed per lane
-    float ps = 0.f;
+  auto expo = [&](int u, int kt) {  // p = exp2(s * scale2 - m * scale2)
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      S[kt][u][i] = __builtin_amdgcn_exp2f(__builtin_fmaf(S[kt][u][i], scale2, -ms[u]));
-      ps += S[kt][u][i];
-    }
-    l[u] += ps;
+    for (int i = 0; i < 4; ++i) S[kt][u][i] = __builtin_amdgcn_exp2f(__builtin_fmaf(S[kt][u][i], scale2, -ms[u]));
   };
   auto pack = [&]() {
 #pragma unroll
@@ -513,6 +521,7 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
 #pragma unroll
             for (int u = 0; u < 2; ++u)
               oacc[2 * st + dd][u] = mma16<T>(as_frag(F[2 * dd + kc]), as_frag(P[u][kc]), oacc[2 * st + dd][u]);
+        lsum[st >> 1] = mma16<T>(as_frag(ones), as_frag(P[st >> 1][st & 1]), lsum[st >> 1]);
       } else {
         const int ks = st - 4;
 #pragma unroll
@@ -573,7 +582,7 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
   // O^T accumulator: lane holds O[q0 + 16u + r16][16 dt + 4G + i]
 #pragma unroll
   for (int u = 0; u < 2; ++u) {
-    const float lt = xsum4(l[u]);
+    const float lt = lsum[u][0];
     const int qi = q0 + 16 * u + r16;
     if (qi < Lq) {
       const float inv = 1.f / lt;
