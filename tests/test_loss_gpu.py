@@ -254,3 +254,19 @@ def test_ce_grad_transposed_matches_chunk_grad(t, n, col0, inplace):
     assert torch.equal(dz[:, :n], ref)
     assert torch.equal(dzt[:, :t], ref.t())
     assert torch.all(dzt[:, t:].float() == 5.0)
+
+
+def test_lm_head_ce_second_backward_recomputes():
+    """The stored bf16 logits are consumed (turned into dz in place) by the first backward; a second
+    backward through a retained graph recomputes the logits instead, and both give the same gradients
+    to the bf16 gate (their logits differ by one bf16 rounding)."""
+    gen = seeded(77)
+    x = randn(2, 256, 256, gen=gen, dtype=torch.bfloat16).cuda().requires_grad_()
+    w = randn(4096, 256, gen=gen, dtype=torch.bfloat16, scale=0.05).cuda().requires_grad_()
+    y = labels_for(2, 256, 4096, gen).cuda()
+    loss = lm_head_cross_entropy(x, w, y, chunk=1024)
+    g1 = torch.autograd.grad(loss, (x, w), retain_graph=True)
+    g2 = torch.autograd.grad(loss, (x, w))
+    for a, b in zip(g1, g2):
+        assert cosine(a, b) >= 0.9999
+        assert max_rel(a, b) <= 2e-2
