@@ -441,6 +441,7 @@ __global__ __launch_bounds__(WM * WN * 64) void gemm_nt_v4_kernel(const u16* __r
   // NC = columns of the staged tile (TNW, or TNW / 2 for one gate/up output)
   [[maybe_unused]] auto stage = [&](auto nc_c, int i, int jc, uint32_t lo, uint32_t hi) {
     constexpr int NC = decltype(nc_c)::value, CH = NC / 8;
+    static_assert(CH == 8 || CH == 16, "the staging swizzle needs 8 or 16 16-byte chunks per row");
     const int r = i * 16 + (lane & 15);
     const int c = (jc * 16 + 4 * quarter) >> 3;  // logical 16-byte chunk
     const int sw = CH == 16 ? (r & 15) : ((r >> 1) & 7);
@@ -448,6 +449,7 @@ __global__ __launch_bounds__(WM * WN * 64) void gemm_nt_v4_kernel(const u16* __r
   };
   [[maybe_unused]] auto flush = [&](auto nc_c, typename O::storage* dst, int64_t ld, auto nr_c) {
     constexpr int NC = decltype(nc_c)::value, CH = NC / 8, RPI = 64 / CH;  // rows per instruction
+    static_assert(CH == 8 || CH == 16, "the staging swizzle needs 8 or 16 16-byte chunks per row");
     constexpr int NR = decltype(nr_c)::value;
     __builtin_amdgcn_s_waitcnt((15) | (7 << 4) | (0 << 8) | (3 << 14));  // this wave's staging writes
     __builtin_amdgcn_wave_barrier();
