@@ -146,9 +146,12 @@ __global__ __launch_bounds__(kBlock) void rmsnorm_bwd_kernel(const typename T::s
     for (int j = 0; j < MAXV; ++j) {
       const int vi = j * TPR + t;
       const int64_t off = rc * h + (int64_t)(vi < nvec ? vi : 0) * V;
-      xr[j] = *reinterpret_cast<const i32x4*>(x + off);
+      // x (the forward pass's input) and dres were written long before this launch: streamed past
+      // the caches.  dy was just produced by the preceding launch and may still be cache-resident.
+      // [32768, 4096] bf16 on MI355X: 161 -> 143 us (62 -> 70 % of HBM bandwidth); [8192, 4096]: level.
+      xr[j] = ld_nt(x + off);
       gr[j] = *reinterpret_cast<const i32x4*>(dy + off);
-      if constexpr (RES) rr[j] = *reinterpret_cast<const i32x4*>(dres + off);
+      if constexpr (RES) rr[j] = ld_nt(dres + off);
     }
     float ss = 0.f, dot = 0.f;
 #pragma unroll
