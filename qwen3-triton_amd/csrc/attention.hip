@@ -43,7 +43,6 @@ Q3_DEV f32x16 zero16() {
   return z;
 }
 Q3_DEV i32x4 ld16(const u16* p) { return *reinterpret_cast<const i32x4*>(p); }
-Q3_DEV void st16(u16* p, i32x4 v) { *reinterpret_cast<i32x4*>(p) = v; }
 Q3_DEV bf16x8_t as_frag(i32x4 v) { return __builtin_bit_cast(bf16x8_t, v); }
 
 // Pack 8 accumulator values (v0..v0+7 of one 32x32 tile) into a B-operand fragment.
@@ -277,12 +276,6 @@ Q3_DEV float xmax4(float x) {  // max over lanes {l, l^16, l^32, l^48}
   x = __builtin_fmaxf(__uint_as_float(a[0]), __uint_as_float(a[1]));
   auto c = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
   return __builtin_fmaxf(__uint_as_float(c[0]), __uint_as_float(c[1]));
-}
-Q3_DEV float xsum4(float x) {  // sum over lanes {l, l^16, l^32, l^48}
-  auto a = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
-  x = __uint_as_float(a[0]) + __uint_as_float(a[1]);
-  auto c = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
-  return __uint_as_float(c[0]) + __uint_as_float(c[1]);
 }
 // LDS swizzles (16-byte chunk index XOR): K rows (16 chunks) by rows {0-7, 16-23} / {8-15, 24-31}
 // of each 32-row group, V^T rows (8 chunks) by row pair.

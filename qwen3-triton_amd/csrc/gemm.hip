@@ -411,7 +411,7 @@ __global__ __launch_bounds__(WM * WN * 64) void gemm_nt_v4_kernel(const u16* __r
           __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // MFMA
         }
       } else {
-                __builtin_amdgcn_sched_group_barrier(0x008, FM * FN * 3 / 8, 0);
+        __builtin_amdgcn_sched_group_barrier(0x008, FM * FN * 3 / 8, 0);
 #pragma unroll
         for (int q = 0; q < FM + FN; ++q) {
           __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
