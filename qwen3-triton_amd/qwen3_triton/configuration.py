@@ -27,4 +27,4 @@ def options_for_variant(name):
         return OptimizationOptions()
     if name in fields:
         return replace(OptimizationOptions(), **{fields[name]: False})
-    raise ValueError('Unknown variant: ' + str(name))
+    raise ValueError('Unknown Triton variant: ' + str(name))

@@ -19,6 +19,8 @@ class _Embedding(torch.autograd.Function):
             raise TypeError('Integer IDs and floating point weight required')
         if not ids.is_contiguous() or not weight.is_contiguous() or weight.ndim != 2 or ids.numel() < 1:
             raise ValueError('Contiguous nonempty IDs and matrix weight required')
+        if min(weight.shape) < 1:
+            raise ValueError('Nonempty vocabulary and hidden dimension required')
         capturing = torch.cuda.is_current_stream_capturing()
         bad = None if capturing else torch.zeros((), dtype=torch.int32, device=ids.device)
         y = _ops.embedding_fwd(ids, weight, bad)

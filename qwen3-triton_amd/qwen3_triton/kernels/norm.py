@@ -9,18 +9,22 @@ import torch
 from . import _ops
 
 
+def _validate(x, weight, eps, max_h):
+    if not x.is_cuda or x.device != weight.device or x.dtype != weight.dtype:
+        raise ValueError('Same-device/dtype ROCm input and weight required; no fallback')
+    if x.dtype not in (torch.float32, torch.bfloat16, torch.float16):
+        raise TypeError('Floating point required')
+    if weight.ndim != 1 or not x.is_contiguous() or not weight.is_contiguous() or \
+            x.shape[-1] != weight.numel() or x.numel() < 1:
+        raise ValueError('Contiguous [...,H] input and [H] weight required')
+    if weight.numel() > max_h or eps <= 0:
+        raise ValueError(f'Supported H<={max_h} and positive epsilon required')
+
+
 class _RMSNorm(torch.autograd.Function):
     @staticmethod
     def forward(ctx, x, weight, eps, optimized):
-        if not x.is_cuda or x.device != weight.device or x.dtype != weight.dtype:
-            raise ValueError('Same-device/dtype ROCm input and weight required; no fallback')
-        if x.dtype not in (torch.float32, torch.bfloat16, torch.float16):
-            raise TypeError('Floating point required')
-        if weight.ndim != 1 or not x.is_contiguous() or not weight.is_contiguous() or \
-                x.shape[-1] != weight.numel() or x.numel() < 1:
-            raise ValueError('Contiguous [...,H] input and [H] weight required')
-        if eps <= 0:
-            raise ValueError('Positive epsilon required')
+        _validate(x, weight, eps, 8192)
         ctx.save_for_backward(x, weight)
         ctx.eps = eps
         return _ops.rmsnorm_fwd(x, weight, eps)
@@ -45,8 +49,10 @@ class _RMSNormFork(torch.autograd.Function):
 
     @staticmethod
     def forward(ctx, x, weight, eps):
-        y = _RMSNorm.forward(ctx, x, weight, eps, False)
-        return x.view_as(x), y
+        _validate(x, weight, eps, 16384)   # the widest row the backward kernels take
+        ctx.save_for_backward(x, weight)
+        ctx.eps = eps
+        return x.view_as(x), _ops.rmsnorm_fwd(x, weight, eps)
 
     @staticmethod
     def backward(ctx, dres, dy):

@@ -18,10 +18,8 @@ def _check(x, w, cos, sin, eps):
     if not x.is_cuda or any(t.device != x.device or t.dtype != x.dtype or not t.is_contiguous()
                             for t in (x, w, cos, sin)):
         raise ValueError('Matching contiguous ROCm tensors required')
-    if x.dtype not in (torch.float32, torch.bfloat16, torch.float16):
-        raise TypeError('Floating point required')
-    if x.shape[-1] % 2 or x.numel() < 1 or eps <= 0:
-        raise ValueError('Even nonempty D and positive epsilon required')
+    if x.dtype not in (torch.float32, torch.bfloat16, torch.float16) or x.shape[-1] % 2 or x.numel() < 1 or eps <= 0:
+        raise ValueError('Floating point, even nonempty D and positive epsilon required')
     if cos.requires_grad or sin.requires_grad:
         raise ValueError('Fixed rotary buffers only')
 

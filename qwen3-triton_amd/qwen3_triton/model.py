@@ -19,7 +19,7 @@ def _precision_items(precision_options):
         return tuple((name, True) for name in PRECISION_SWITCHES)
     given = dict(precision_options)
     if sorted(given) != sorted(PRECISION_SWITCHES) or not all(type(v) is bool for v in given.values()):
-        raise ValueError(f'precision_options must give exactly the booleans {", ".join(PRECISION_SWITCHES)}')
+        raise ValueError('Explicit five boolean precision options required')
     return tuple(given.items())
 
 

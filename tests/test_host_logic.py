@@ -39,13 +39,21 @@ def test_reference_api_modules_and_defaults():
     assert attention_precision.f32(128 ** -0.5) != 128 ** -0.5
 
 
+def test_unknown_variant_message():
+    """``configuration.py:21``: an unknown preset name raises with the reference's message."""
+    import pytest
+    from qwen3_triton.configuration import options_for_variant
+    with pytest.raises(ValueError, match='Unknown Triton variant: nope'):
+        options_for_variant('nope')
+
+
 def test_precision_model_option_validation():
     from qwen3_triton.model import _optimization_options, _precision_items
     from qwen3_triton.configuration import OptimizationOptions
     import pytest
     assert dict(_precision_items(None)) == dict(xor_sum=True, lse_fma=True, native_delta=True, native_dq=True,
                                                 sum_fma=True)
-    with pytest.raises(ValueError):
+    with pytest.raises(ValueError, match='Explicit five boolean precision options required'):
         _precision_items(dict(xor_sum=True))
     with pytest.raises(ValueError):
         _precision_items(dict(xor_sum=1, lse_fma=True, native_delta=True, native_dq=True, sum_fma=True))

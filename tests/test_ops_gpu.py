@@ -266,3 +266,26 @@ def test_norm_rope_pair_validates_like_norm_rope():
         norm_rope_pair(q, k, w, w, cos.float(), sin.float())
     with pytest.raises(ValueError):
         norm_rope_pair(q, k, w, w, cos.clone().requires_grad_(), sin)
+
+
+@pytest.mark.gpu
+def test_module_validation_matches_reference():
+    """Argument checks that raise before any launch, as ``kernels/norm.py:47``, ``embedding.py:59``
+    and ``norm_rope.py:57`` raise them."""
+    from qwen3_triton.kernels.embedding import embedding
+    x = torch.randn(2, 8200, device="cuda", dtype=torch.bfloat16)
+    with pytest.raises(ValueError, match="H<=8192"):
+        rms_norm(x, torch.ones(8200, device="cuda", dtype=torch.bfloat16))
+    with pytest.raises(ValueError, match="positive epsilon"):
+        rms_norm(x[:, :64].contiguous(), torch.ones(64, device="cuda", dtype=torch.bfloat16), 0.0)
+    ids = torch.zeros(4, dtype=torch.int64, device="cuda")
+    with pytest.raises(ValueError, match="Nonempty vocabulary"):
+        embedding(ids, torch.empty(0, 8, device="cuda", dtype=torch.bfloat16))
+    q = torch.zeros(1, 2, 2, 8, device="cuda", dtype=torch.int32)
+    cs = torch.zeros(1, 2, 8, device="cuda", dtype=torch.int32)
+    with pytest.raises(ValueError, match="Floating point, even nonempty D"):
+        norm_rope(q, torch.zeros(8, device="cuda", dtype=torch.int32), cs, cs, 1e-6)
+    qo = torch.randn(1, 2, 2, 7, device="cuda", dtype=torch.bfloat16)
+    co = torch.randn(1, 2, 7, device="cuda", dtype=torch.bfloat16)
+    with pytest.raises(ValueError, match="Floating point, even nonempty D"):
+        norm_rope(qo, torch.ones(7, device="cuda", dtype=torch.bfloat16), co, co, 1e-6)
