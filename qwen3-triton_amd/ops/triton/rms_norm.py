@@ -13,6 +13,8 @@ def _validate(x, weight):
         raise TypeError("x and weight must have the same dtype")
     if x.shape[-1] != weight.numel():
         raise ValueError("weight length must equal x.shape[-1]")
+    if x.shape[-1] > 65536:
+        raise ValueError("hidden dimension is too large for this first kernel")
 
 
 class _RMSNormFunction(torch.autograd.Function):

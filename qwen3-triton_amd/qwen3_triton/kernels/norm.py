@@ -49,7 +49,7 @@ class _RMSNormFork(torch.autograd.Function):
 
     @staticmethod
     def forward(ctx, x, weight, eps):
-        _validate(x, weight, eps, 16384)   # the widest row the backward kernels take
+        _validate(x, weight, eps, 1 << 20)   # the widest row the kernels take
         ctx.save_for_backward(x, weight)
         ctx.eps = eps
         return x.view_as(x), _ops.rmsnorm_fwd(x, weight, eps)

@@ -289,3 +289,25 @@ def test_module_validation_matches_reference():
     co = torch.randn(1, 2, 7, device="cuda", dtype=torch.bfloat16)
     with pytest.raises(ValueError, match="Floating point, even nonempty D"):
         norm_rope(qo, torch.ones(7, device="cuda", dtype=torch.bfloat16), co, co, 1e-6)
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
+@pytest.mark.parametrize("shape", [(3, 4096), (2, 20000)])
+def test_rms_norm_triton_op(shape, dtype):
+    """``ops/triton/rms_norm.py:118-138``: forward and backward against the oracle, including rows wider
+    than the vector path (the scalar kernels); wider than 65536 is rejected as the reference rejects it."""
+    print(f"rms_norm_triton {shape} {dtype}", flush=True)
+    gen = seeded(5)
+    h = shape[-1]
+    x = randn(*shape, gen=gen, dtype=dtype)
+    w = randn(h, gen=gen, dtype=dtype, scale=0.1, shift=1.0)
+    dy = randn(*shape, gen=gen, dtype=dtype)
+    xd, wd = x.cuda().requires_grad_(), w.cuda().requires_grad_()
+    y = rms_norm_triton(xd, wd, 1e-6)
+    dx, dw = _grads(y, (xd, wd), dy.cuda())
+    check(y, O.rms_norm_reference(x, w, 1e-6), dtype, "y")
+    ex, ew = O.rms_norm_backward_reference(x, w, dy, 1e-6)
+    check(dx, ex, dtype, "dx")
+    check(dw, ew, dtype, "dw")
+    with pytest.raises(ValueError, match="too large"):
+        rms_norm_triton(torch.ones(1, 65537, device="cuda", dtype=dtype), torch.ones(65537, device="cuda", dtype=dtype))
