@@ -9,6 +9,8 @@ from qwen3_triton.kernels import _ops
 
 
 def _validate(q, k, v, is_causal):
+    """The checks of ``ops/triton/attention.py:151-178``, in order; then the shared dtype this build
+    needs (the reference's kernel would fail to compile a mixed-dtype dot product)."""
     if not all(t.is_cuda for t in (q, k, v)):
         raise ValueError("attention_triton requires ROCm tensors")
     if not (q.ndim == k.ndim == v.ndim == 4):
@@ -16,15 +18,17 @@ def _validate(q, k, v, is_causal):
     batch, q_heads, q_len, head_dim = q.shape
     k_batch, kv_heads, k_len, k_dim = k.shape
     if (k_batch, k_len, k_dim) != (batch, q_len, head_dim):
-        raise ValueError("q/k sequence and head_dim shapes must match")
+        raise ValueError("first kernel requires q/k sequence and head_dim shapes to match")
     if v.shape != (batch, kv_heads, q_len, head_dim):
         raise ValueError("v must have shape [batch, kv_heads, seq_len, head_dim]")
     if q_heads % kv_heads != 0:
         raise ValueError("q_heads must be divisible by kv_heads for GQA")
     if not is_causal:
-        raise NotImplementedError("only causal attention is supported")
-    if head_dim <= 0 or head_dim % 2 != 0 or head_dim > 256:
-        raise ValueError("head_dim must be a positive even number <= 256")
+        raise NotImplementedError("first attention kernel only supports causal attention")
+    if head_dim <= 0 or head_dim % 2 != 0:
+        raise ValueError("head_dim must be a positive even number")
+    if head_dim > 256:
+        raise ValueError("first attention kernel supports head_dim <= 256")
     if q.dtype != k.dtype or q.dtype != v.dtype:
         raise TypeError("q, k, v must share a dtype")
 

@@ -4,23 +4,28 @@ import torch
 from qwen3_triton.kernels import _ops
 
 
-def _check(x, cos, sin):
+def _check(x, cos, sin, what):
     if not x.is_cuda or not cos.is_cuda or not sin.is_cuda:
-        raise ValueError("rope requires ROCm tensors")
+        raise ValueError("rope_triton requires ROCm tensors")
     if x.ndim != 4 or cos.ndim != 3 or sin.shape != cos.shape:
-        raise ValueError("expected x=[batch,heads,seq,head_dim] and cos/sin=[batch,seq,head_dim]")
+        raise ValueError(f"expected {what}=[batch,heads,seq,head_dim] and cos/sin=[batch,seq,head_dim]")
     b, _, s, d = x.shape
     if cos.shape != (b, s, d):
-        raise ValueError("cos/sin shape must match x batch, sequence, and head_dim")
+        raise ValueError(f"cos/sin shape must match {what} batch, sequence, and head_dim")
     if d % 2:
         raise ValueError("head_dim must be even")
-    if cos.dtype != x.dtype or sin.dtype != x.dtype:
-        raise TypeError("cos/sin must have the dtype of x")
+    if d > 65536:
+        raise ValueError("head_dim is too large for this first kernel")
 
 
 def _one(x, cos, sin, backward):
-    _check(x, cos, sin)
-    return _ops.rope_apply(x.contiguous(), cos.contiguous(), sin.contiguous(), layout=1, backward=backward)
+    """Rotated x in x's dtype.  Tables of another dtype are taken as the reference's kernel takes them
+    (every operand widened to fp32, the result stored in x's dtype): the op then runs in fp32."""
+    _check(x, cos, sin, "grad" if backward else "x")
+    if cos.dtype == x.dtype and sin.dtype == x.dtype:
+        return _ops.rope_apply(x.contiguous(), cos.contiguous(), sin.contiguous(), layout=1, backward=backward)
+    f32 = lambda t: _ops.cast(t.contiguous(), torch.float32)
+    return _ops.cast(_ops.rope_apply(f32(x), f32(cos), f32(sin), layout=1, backward=backward), x.dtype)
 
 
 class _RoPEFunction(torch.autograd.Function):

@@ -280,3 +280,39 @@ def test_gemm_nt_residual(m, n, k, dtype):
     rows = torch.arange(0, m, max(1, m // 64))
     ref64 = r[rows].cpu().double() + a[rows].cpu().double() @ w.cpu().double().t()
     assert max_rel(out[rows], ref64) <= (1.6e-2 if dtype == torch.bfloat16 else 2e-3)
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+def test_gate_up_swiglu_triton_op(dtype):
+    """``ops/triton/gate_up_swiglu.py:274-288``: a strided [B, S, K] input (taken as a contiguous copy, as
+    the reference takes it) gives the module path's output and gradients bit for bit, and matches the
+    fp64 SwiGLU of the fp64 products; the reference's argument errors are raised."""
+    import oracle as O
+    from ops.triton.gate_up_swiglu import gate_up_swiglu_triton
+    from qwen3_triton.kernels.mlp_precision import gate_up_swiglu
+    print(f"gate_up_swiglu_triton {dtype}", flush=True)
+    gen = seeded(41)
+    b, s, k, n = 2, 128, 256, 384
+    xs = randn(b, k, s, gen=gen, dtype=dtype).cuda().transpose(1, 2)        # [B, S, K], not contiguous
+    wg = randn(n, k, gen=gen, dtype=dtype, scale=0.05).cuda()
+    wu = randn(n, k, gen=gen, dtype=dtype, scale=0.05).cuda()
+    dy = randn(b, s, n, gen=gen, dtype=dtype).cuda()
+    x1 = xs.detach().requires_grad_()
+    w1 = [w.detach().requires_grad_() for w in (wg, wu)]
+    y1 = gate_up_swiglu_triton(x1, *w1)
+    y1.backward(dy)
+    x2 = xs.detach().contiguous().requires_grad_()
+    w2 = [w.detach().requires_grad_() for w in (wg, wu)]
+    y2 = gate_up_swiglu(x2, *w2)
+    y2.backward(dy)
+    assert torch.equal(y1, y2) and torch.equal(x1.grad, x2.grad)
+    assert all(torch.equal(a.grad, c.grad) for a, c in zip(w1, w2))
+    xr = xs.detach().cpu().double().reshape(-1, k)
+    e = O.swiglu_reference(xr @ wg.cpu().double().t(), xr @ wu.cpu().double().t(), dtype=torch.float64)
+    assert max_rel(y1.reshape(-1, n), e) <= (2e-2 if dtype == torch.bfloat16 else 3e-3)
+    with pytest.raises(ValueError, match="K dimensions"):
+        gate_up_swiglu_triton(xs, wg[:, :128], wu[:, :128])
+    with pytest.raises(TypeError, match="same dtype"):
+        gate_up_swiglu_triton(xs, wg.float(), wu.float())
+    with pytest.raises(ValueError, match="matching weights"):
+        gate_up_swiglu_triton(xs, wg, wu[:-1])

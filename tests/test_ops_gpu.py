@@ -114,6 +114,22 @@ def test_norm_rope_fwd_bwd(b, s, hq, hk, d, dtype):
     # the single-tensor module API (kernels/norm_rope.py) agrees with the pair API
     y1 = norm_rope(dev[0].detach(), dev[2].detach(), c.cuda(), sn.cuda(), 1e-6)
     assert torch.equal(y1, yq.detach())
+    # fp32 weights and tables beside 16-bit activations (the reference reads every operand as fp32)
+    if dtype != torch.float32:
+        c32, s32 = randn(b, s, d, gen=gen, dtype=torch.float32), randn(b, s, d, gen=gen, dtype=torch.float32)
+        w32 = [randn(d, gen=gen, dtype=torch.float32, scale=0.1, shift=1.0) for _ in range(2)]
+        dm = [q.cuda().requires_grad_(), k.cuda().requires_grad_()] + [w.cuda().requires_grad_() for w in w32]
+        yq, yk = fused_qk_norm_rope_triton(*dm, c32.cuda(), s32.cuda(), 1e-6)
+        assert yq.dtype == dtype and yk.dtype == dtype
+        grads = _grads((yq, yk), dm, (gq.cuda(), gk.cuda()))
+        assert grads[0].dtype == dtype and grads[2].dtype == torch.float32
+        eq, ek = O.fused_qk_norm_rope_reference(q.float(), k.float(), *w32, c32, s32, 1e-6)
+        check(yq, eq, dtype, "yq[mixed]")
+        check(yk, ek, dtype, "yk[mixed]")
+        e = O.fused_qk_norm_rope_backward_reference(q.float(), k.float(), *w32, c32, s32, gq.float(), gk.float(),
+                                                    1e-6)
+        for a, x, n in zip(grads, e, ("dq", "dk", "dqw", "dkw")):
+            check(a, x, dtype, n + "[mixed]")
 
 
 @pytest.mark.parametrize("dtype", DTYPES)
@@ -138,6 +154,18 @@ def test_rope_both_layouts(b, s, h, d, dtype):
     check(yq, e, dtype, "yq[BHSD]")
     (dxh,) = _grads(yq, (xh,), gy.transpose(1, 2).contiguous().cuda())
     check(dxh, eg, dtype, "dx[BHSD]")
+    # fp32 tables beside 16-bit activations, as the reference's kernel accepts them
+    if dtype != torch.float32:
+        c32 = randn(b, s, d, gen=gen, dtype=torch.float32)
+        s32 = randn(b, s, d, gen=gen, dtype=torch.float32)
+        xm = x.transpose(1, 2).contiguous().cuda().requires_grad_()
+        ym, _ = apply_rope_triton(xm, xm.detach(), c32.cuda(), s32.cuda())
+        assert ym.dtype == dtype
+        em, _ = O.apply_rope_reference(x.transpose(1, 2).float(), x.transpose(1, 2).float(), c32, s32)
+        check(ym, em, dtype, "yq[fp32 tables]")
+        (dxm,) = _grads(ym, (xm,), gy.transpose(1, 2).contiguous().cuda())
+        egm, _ = O.apply_rope_backward_reference(gy.transpose(1, 2).float(), gy.transpose(1, 2).float(), c32, s32)
+        check(dxm, egm, dtype, "dx[fp32 tables]")
 
 
 @pytest.mark.parametrize("dtype", DTYPES)
