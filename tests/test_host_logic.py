@@ -37,6 +37,13 @@ def test_reference_api_modules_and_defaults():
         dict(lse_fma=False, native_delta=False, native_dq=False, sum_fma=False, xor_sum=True)
     assert attention_precision.f32(0.1) == 0.10000000149011612
     assert attention_precision.f32(128 ** -0.5) != 128 ** -0.5
+    # the reference-order replay modules: importable, and their gates closed (callers keep their route)
+    from qwen3_triton.inference import accumulation
+    from qwen3_triton.kernels import hf_reduction
+    assert accumulation.strategy(1, 4096, 4096) is None
+    assert accumulation.linear(torch.zeros(1, 8), torch.zeros(8, 8)) is None
+    assert accumulation.short_norm(torch.zeros(1, 4096), torch.zeros(4096), 1e-6) is None
+    assert hf_reduction.supports_hf_reduction(torch.zeros(16, 128)) is False
 
 
 def test_unknown_variant_message():
