@@ -126,14 +126,17 @@ class TritonQwen3Inference(nn.Module):
         return model.load_hf_state_dict(state)
 
     @classmethod
-    def from_pretrained(cls, path, *, device='cuda', **kw):
+    def from_pretrained(cls, path, *, device='cuda', gemv=True, split_decode=False, sliced_decode=False,
+                        prefill_tiling=False, reference_accumulation=False):
         """A local Qwen3 safetensors checkpoint (``inference/model.py:68-88``): ``config.json``, an
         optional ``generation_config.json``, and ``model.safetensors`` or the shards named by
         ``model.safetensors.index.json``.  Tensors are read shard by shard straight onto ``device``;
         nothing is downloaded."""
         from transformers import AutoConfig
         path = Path(path).resolve()
-        model = cls(AutoConfig.from_pretrained(path, local_files_only=True), **kw)
+        model = cls(AutoConfig.from_pretrained(path, local_files_only=True), gemv=gemv, split_decode=split_decode,
+                    sliced_decode=sliced_decode, prefill_tiling=prefill_tiling,
+                    reference_accumulation=reference_accumulation)
         if (path / 'generation_config.json').is_file():
             from transformers import GenerationConfig
             model.generation_config = GenerationConfig.from_pretrained(path, local_files_only=True)
