@@ -692,6 +692,12 @@ __global__ __launch_bounds__(WM * WN * 64) void gemm_nt_v4_kernel(const u16* __r
   }
   if constexpr (EPI == 2) {
     static_assert(TNW == 128, "one statistics partial per 128 columns");
+    // With the logits stored: round them; full tiles stage each 16-row group of this wave's block in
+    // LDS right before that group's statistics (so a group's accumulators die before the next group's
+    // temporaries are live) and flush the block at the end; other tiles store each group's logits
+    // directly, also beside its statistics.
+    [[maybe_unused]] constexpr auto NC = std::integral_constant<int, TNW>{};
+    bool staged = false;
     if (ce.zs) {
 #pragma unroll
       for (int i = 0; i < FM; ++i)
@@ -701,50 +707,45 @@ __global__ __launch_bounds__(WM * WN * 64) void gemm_nt_v4_kernel(const u16* __r
           for (int v = 0; v < 4; ++v) acc[i][j][v] = to_f32<T>(from_f32<T>(acc[i][j][v]));
       if constexpr (EVEN && O::vec == 8) {
         if (vec_store == 2) {
-          constexpr auto NC = std::integral_constant<int, TNW>{};
           __syncthreads();  // every wave is done with the operand ring
-#pragma unroll
-          for (int i = 0; i < FM; ++i)
-#pragma unroll
-            for (int j = 0; j < FN; ++j)
-              stage(NC, i, j, pack2<T>(acc[i][j][0], acc[i][j][1]), pack2<T>(acc[i][j][2], acc[i][j][3]));
-          flush(NC, ce.zs + (int64_t)(m0 + wm * TMW) * ce.ldzs + n0 + wn * TNW, ce.ldzs,
-                std::integral_constant<int, TMW>{});
-        }
-      }
-      if (!(EVEN && O::vec == 8 && vec_store == 2)) {
-#pragma unroll
-        for (int i = 0; i < FM; ++i) {
-          const int row = m0 + wm * TMW + i * 16 + (lane & 15);
-          if (row >= M) continue;
-#pragma unroll
-          for (int j = 0; j < FN; ++j)
-#pragma unroll
-            for (int v = 0; v < 4; ++v) {
-              const int col = n0 + wn * TNW + j * 16 + 4 * quarter + v;
-              if (col < N) ce.zs[(int64_t)row * ce.ldzs + col] = from_f32<T>(acc[i][j][v]);
-            }
+          staged = true;    // each row group is staged beside its statistics below
         }
       }
     }
     const int64_t part = ce.part0 + (n0 + wn * TNW) / 128;
 #pragma unroll
     for (int i = 0; i < FM; ++i) {
+      if constexpr (EVEN && O::vec == 8) {
+        if (staged) {
+#pragma unroll
+          for (int j = 0; j < FN; ++j)
+            stage(NC, i, j, pack2<T>(acc[i][j][0], acc[i][j][1]), pack2<T>(acc[i][j][2], acc[i][j][3]));
+        }
+      }
       const int row = m0 + wm * TMW + i * 16 + (lane & 15);
+      if (ce.zs && !staged && row < M) {
+#pragma unroll
+        for (int j = 0; j < FN; ++j)
+#pragma unroll
+          for (int v = 0; v < 4; ++v) {
+            const int col = n0 + wn * TNW + j * 16 + 4 * quarter + v;
+            if (col < N) ce.zs[(int64_t)row * ce.ldzs + col] = from_f32<T>(acc[i][j][v]);
+          }
+      }
       const int64_t t = row < M ? ce.tgt[row] - ce.col0 : -1;  // target column within this chunk
       float mx = -INFINITY;
 #pragma unroll
       for (int j = 0; j < FN; ++j)
 #pragma unroll
         for (int v = 0; v < 4; ++v)
-          if (n0 + wn * TNW + j * 16 + 4 * quarter + v < N) mx = fmaxf(mx, acc[i][j][v]);
+          if (EVEN || n0 + wn * TNW + j * 16 + 4 * quarter + v < N) mx = fmaxf(mx, acc[i][j][v]);
       float sm = 0.f;
 #pragma unroll
       for (int j = 0; j < FN; ++j)
 #pragma unroll
         for (int v = 0; v < 4; ++v) {
           const int col = n0 + wn * TNW + j * 16 + 4 * quarter + v;
-          if (col < N) {
+          if (EVEN || col < N) {
             sm += mx == -INFINITY ? 0.f : __expf(acc[i][j][v] - mx);
             if (col == t) ce.pick[row] = acc[i][j][v];
           }
@@ -757,6 +758,11 @@ __global__ __launch_bounds__(WM * WN * 64) void gemm_nt_v4_kernel(const u16* __r
         ce.m_part[part * ce.ldp + row] = mx;
         ce.s_part[part * ce.ldp + row] = sm;
       }
+    }
+    if constexpr (EVEN && O::vec == 8) {
+      if (staged)
+        flush(NC, ce.zs + (int64_t)(m0 + wm * TMW) * ce.ldzs + n0 + wn * TNW, ce.ldzs,
+              std::integral_constant<int, TMW>{});
     }
     return;
   }
