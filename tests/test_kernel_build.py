@@ -48,3 +48,51 @@ def test_dkdv_accumulators_never_move(tmp_path):
         scratch = int(re.search(r"; ScratchSize: (\d+)", text).group(1))
         assert scratch == 0, f"{name}: {scratch} bytes of scratch"
 
+
+
+BUNDLER = "/opt/rocm/llvm/bin/clang-offload-bundler"
+OBJCOPY = "/opt/rocm/llvm/bin/llvm-objcopy"
+READELF = "/opt/rocm/llvm/bin/llvm-readelf"
+
+
+def _kernel_metadata(obj, tmp_path):
+    """[(kernel name, {field: int})] from the gfx950 code object embedded in one built object file."""
+    stem = os.path.basename(obj)[:-2]
+    fat, co = tmp_path / f"{stem}.fatbin", tmp_path / f"{stem}.co"
+    sections = subprocess.run([READELF, "-S", obj], check=True, capture_output=True, text=True, timeout=120).stdout
+    if ".hip_fatbin" not in sections:  # host-only object (the C ABI glue)
+        return []
+    subprocess.run([OBJCOPY, f"--dump-section=.hip_fatbin={fat}", obj, str(tmp_path / f"{stem}.copy.o")],
+                   check=True, capture_output=True, timeout=120)
+    subprocess.run([BUNDLER, "--type=o", "--targets=hipv4-amdgcn-amd-amdhsa--gfx950", f"--input={fat}",
+                    f"--output={co}", "--unbundle"], check=True, capture_output=True, timeout=120)
+    notes = subprocess.run([READELF, "--notes", str(co)], check=True, capture_output=True, text=True,
+                           timeout=120).stdout
+    out = []
+    for block in re.split(r"\n\s+- \.", notes)[1:]:
+        name = re.search(r"\.name:\s+(\S+)", "." + block)
+        if not name:
+            continue
+        fields = {k: int(v) for k, v in re.findall(r"\.(private_segment_fixed_size|vgpr_spill_count|"
+                                                    r"sgpr_spill_count):\s+(\d+)", "." + block)}
+        out.append((name.group(1), fields))
+    return out
+
+
+@pytest.mark.skipif(not all(os.path.exists(t) for t in (BUNDLER, OBJCOPY, READELF)), reason="ROCm LLVM tools missing")
+def test_no_kernel_spills_to_scratch(tmp_path):
+    """No kernel of the built library spills registers or uses scratch memory: a spill in a hot loop or
+    epilogue is a silent slowdown (the CE-statistics epilogue once spilled 55 VGPRs).  Reads the kernel
+    descriptors of the objects the Makefile built (skipped when nothing is built)."""
+    build = os.path.join(PKG, "build")
+    objs = sorted(os.path.join(build, f) for f in os.listdir(build)) if os.path.isdir(build) else []
+    objs = [o for o in objs if o.endswith(".o")]
+    if not objs:
+        pytest.skip("library not built")
+    kernels = 0
+    for obj in objs:
+        for name, f in _kernel_metadata(obj, tmp_path):
+            kernels += 1
+            assert f.get("vgpr_spill_count", 0) == 0 and f.get("sgpr_spill_count", 0) == 0, (obj, name, f)
+            assert f.get("private_segment_fixed_size", 0) == 0, (obj, name, f)
+    assert kernels > 50, kernels
