@@ -170,8 +170,9 @@ int q3_gemm_nt(int in_dtype, int out_dtype, const void* A, int64_t lda, const vo
 /* Projection plus residual in one matrix-core GEMM: C = R + A B^T for A [M, K], B [N, K] (K-contiguous
  * rows) and the residual R [M, N] (row stride ldr); the GEMM output is rounded to dtype and then
  * added to R in fp32 and rounded again, so C is bit-identical to q3_gemm_nt followed by q3_add.
- * C may alias R.  M % 256 == 0, N % 256 == 0, K % 64 == 0, (M / 256) (N / 256) >= 256 (the full-tile
- * grid), strides % 8 == 0, pointers 16-byte aligned.
+ * C may alias R.  M % 128 == 0, N % 128 == 0, K % 64 == 0 (256 x 256 tiles when M and N are multiples of
+ * 256 and that grid has at least 256 tiles, else 128 x 128, as q3_gemm_nt plans them), strides % 8 == 0,
+ * pointers 16-byte aligned.
  * Replaces: _model.py:60-108 / components.py (x = x + self_attn(...), x = x + mlp(...): the o_proj /
  * down_proj kernels/linear.py launch followed by kernels/residual.py:13-30). */
 int q3_gemm_nt_residual(int dtype, const void* A, int64_t lda, const void* B, int64_t ldb, const void* R,
@@ -211,9 +212,10 @@ int q3_gemm_swiglu_bwd(int dtype, const void* dy, int64_t lddy, const void* wt, 
 /* Several projections of one input in one matrix-core launch: for A [M, K] and nseg (1..3) weights
  * Bs[s] [Ns[s], K] (common row stride ldb), writes Cs[s] = A Bs[s]^T ([M, Ns[s]] at row stride
  * ldcs[s]), fp32 accumulation, one rounding, bit-identical to nseg separate q3_gemm_nt calls with
- * the same tile plan.  M % 256 == 0, every Ns[s] % 256 == 0, K % 64 == 0, ldcs[s] % 8 == 0,
- * pointers 16-byte aligned.  The K and V projections of Qwen3-8B (N = 1024) alone fill only half
- * of the 256 CUs with 256 x 256 tiles; side by side with Q they share one well-filled grid.
+ * the same tile plan.  M % 128 == 0, every Ns[s] % 128 == 0, K % 64 == 0, ldcs[s] % 8 == 0,
+ * pointers 16-byte aligned; 256 x 256 tiles when M and every Ns[s] are multiples of 256 and that grid
+ * has at least 256 tiles, else 128 x 128.  The K and V projections of Qwen3-8B (N = 1024) alone fill
+ * only part of the 256 CUs; side by side with Q they share one well-filled grid.
  * Replaces: components.py:19-21 / _model.py (q_proj, k_proj, v_proj: three kernels/linear.py
  * launches on the same input). */
 int q3_gemm_nt_multi(int dtype, const void* A, int64_t lda, int nseg, const void* const* Bs, int64_t ldb,

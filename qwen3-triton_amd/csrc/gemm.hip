@@ -632,7 +632,8 @@ __global__ __launch_bounds__(WM * WN * 64) void gemm_nt_v4_kernel(const u16* __r
 #pragma unroll
         for (int q = 0; q < TMW / RPI; ++q) {
           const int r = q * RPI + lane / CH;
-          const Vec<O> a = unpack_vec<O>(*reinterpret_cast<const i32x4*>(wl + r * (TNW * 2) + ((c ^ (r & 15)) << 4)));
+          const int sw = CH == 16 ? (r & 15) : ((r >> 1) & 7);  // the staging swizzle
+          const Vec<O> a = unpack_vec<O>(*reinterpret_cast<const i32x4*>(wl + r * (TNW * 2) + ((c ^ sw) << 4)));
           const Vec<O> b = unpack_vec<O>(rv[q]);
           i32x4 o;
 #pragma unroll
@@ -882,6 +883,13 @@ int launch_swiglu_bwd(const void* A, int64_t lda, const void* B, int64_t ldb, in
 
 // Q/K/V-style GEMM: one A, up to 3 weights side by side as the B rows, one output per weight
 // (256 x 256 tiles of full tiles only).
+int64_t tiles_of(int64_t M, int64_t N, int64_t bm, int64_t bn) { return ((M + bm - 1) / bm) * ((N + bn - 1) / bn); }
+bool all_n_multiple(const int64_t* Ns, int nseg, int64_t q) {
+  for (int i = 0; i < nseg; ++i)
+    if (Ns[i] % q != 0) return false;
+  return true;
+}
+
 template <typename T>
 int launch_multi(const void* A, int64_t lda, int nseg, const void* const* Bs, int64_t ldb, void* const* Cs,
                  const int64_t* Ns, const int64_t* ldcs, int64_t M, int64_t K, hipStream_t s) {
@@ -895,7 +903,11 @@ int launch_multi(const void* A, int64_t lda, int nseg, const void* const* Bs, in
     n += Ns[i];
   }
   e.nseg = nseg;
-  return launch_v4<T, T, 256, 256, 4, 2, 2, true, 64, 4>(A, lda, Bs[0], ldb, Cs[0], ldcs[0], M, n, K, 1.f, 0, s, e);
+  // The tile plan of the plain GEMM: 256 x 256 when that grid gives every CU a workgroup, else 128 x 128
+  // (the same per-element k order either way: every output equals its single-weight GEMM bit for bit).
+  if (M % 256 == 0 && n % 256 == 0 && tiles_of(M, n, 256, 256) >= 256 && all_n_multiple(Ns, nseg, 256))
+    return launch_v4<T, T, 256, 256, 4, 2, 2, true, 64, 4>(A, lda, Bs[0], ldb, Cs[0], ldcs[0], M, n, K, 1.f, 0, s, e);
+  return launch_v4<T, T, 128, 128, 4, 2, 2, true, 64, 4>(A, lda, Bs[0], ldb, Cs[0], ldcs[0], M, n, K, 1.f, 0, s, e);
 }
 
 // ---------------------------------------------------------------- strided SIMT fallback
@@ -942,7 +954,6 @@ __global__ __launch_bounds__(kThreads) void gemm_generic_kernel(const typename T
 
 constexpr int kBM = 256, kBN = 128, kBK = 64;
 
-int64_t tiles_of(int64_t M, int64_t N, int64_t bm, int64_t bn) { return ((M + bm - 1) / bm) * ((N + bn - 1) / bn); }
 
 template <typename T, typename O>
 int launch_nt(const void* A, int64_t lda, const void* B, int64_t ldb, void* C, int64_t ldc, int64_t M, int64_t N,
@@ -1117,16 +1128,21 @@ int q3_gemm_gate_up_swiglu_t(int dtype, const void* x, int64_t ldx, const void* 
 int q3_gemm_nt_residual(int dtype, const void* A, int64_t lda, const void* B, int64_t ldb, const void* R,
                         int64_t ldr, void* C, int64_t ldc, int64_t M, int64_t N, int64_t K, hipStream_t stream) {
   Q3_REQUIRE((dtype == Q3_BF16 || dtype == Q3_F16) && A && B && R && C);
-  Q3_REQUIRE(M > 0 && N > 0 && K > 0 && M % 256 == 0 && N % 256 == 0 && K % 64 == 0 && M < (1ll << 31) &&
-             N < (1ll << 31) && K < (1ll << 31) && (M / 256) * (N / 256) >= 256 && (M / 256) * (N / 256) < (1ll << 31));
+  Q3_REQUIRE(M > 0 && N > 0 && K > 0 && M % 128 == 0 && N % 128 == 0 && K % 64 == 0 && M < (1ll << 31) &&
+             N < (1ll << 31) && K < (1ll << 31) && (M / 128) * (N / 128) < (1ll << 31));
   Q3_REQUIRE(lda % 8 == 0 && ldb % 8 == 0 && ldr % 8 == 0 && ldc % 8 == 0 && lda >= K && ldb >= K && ldr >= N &&
              ldc >= N && al16(A) && al16(B) && al16(R) && al16(C));
   CeEpi e{};
   e.res = (const u16*)R;
   e.ldres = ldr;
-  if (dtype == Q3_BF16)
-    return launch_v4<BF16, BF16, 256, 256, 4, 2, 2, true>(A, lda, B, ldb, C, ldc, M, N, K, 1.f, 0, stream, e);
-  return launch_v4<F16, F16, 256, 256, 4, 2, 2, true>(A, lda, B, ldb, C, ldc, M, N, K, 1.f, 0, stream, e);
+  // The plain GEMM's tile plan: 256 x 256 when that grid gives every CU a workgroup, else 128 x 128.
+  const bool big = M % 256 == 0 && N % 256 == 0 && tiles_of(M, N, 256, 256) >= 256;
+  if (dtype == Q3_BF16) {
+    if (big) return launch_v4<BF16, BF16, 256, 256, 4, 2, 2, true>(A, lda, B, ldb, C, ldc, M, N, K, 1.f, 0, stream, e);
+    return launch_v4<BF16, BF16, 128, 128, 4, 2, 2, true>(A, lda, B, ldb, C, ldc, M, N, K, 1.f, 0, stream, e);
+  }
+  if (big) return launch_v4<F16, F16, 256, 256, 4, 2, 2, true>(A, lda, B, ldb, C, ldc, M, N, K, 1.f, 0, stream, e);
+  return launch_v4<F16, F16, 128, 128, 4, 2, 2, true>(A, lda, B, ldb, C, ldc, M, N, K, 1.f, 0, stream, e);
 }
 
 int q3_gemm_swiglu_bwd(int dtype, const void* dy, int64_t lddy, const void* wt, int64_t ldw, const void* g,
@@ -1156,15 +1172,15 @@ int q3_gemm_nt_multi(int dtype, const void* A, int64_t lda, int nseg, const void
                      void* const* Cs, const int64_t* Ns, const int64_t* ldcs, int64_t M, int64_t K,
                      hipStream_t stream) {
   Q3_REQUIRE((dtype == Q3_BF16 || dtype == Q3_F16) && A && Bs && Cs && Ns && ldcs && nseg >= 1 && nseg <= 3);
-  Q3_REQUIRE(M > 0 && K > 0 && M % 256 == 0 && K % 64 == 0 && M < (1ll << 31) && K < (1ll << 31));
+  Q3_REQUIRE(M > 0 && K > 0 && M % 128 == 0 && K % 64 == 0 && M < (1ll << 31) && K < (1ll << 31));
   Q3_REQUIRE(lda % 8 == 0 && ldb % 8 == 0 && lda >= K && ldb >= K && al16(A));
   int64_t n = 0;
   for (int i = 0; i < nseg; ++i) {
-    Q3_REQUIRE(Bs[i] && Cs[i] && Ns[i] > 0 && Ns[i] % 256 == 0 && ldcs[i] >= Ns[i] && ldcs[i] % 8 == 0 &&
+    Q3_REQUIRE(Bs[i] && Cs[i] && Ns[i] > 0 && Ns[i] % 128 == 0 && ldcs[i] >= Ns[i] && ldcs[i] % 8 == 0 &&
                al16(Bs[i]) && al16(Cs[i]));
     n += Ns[i];
   }
-  Q3_REQUIRE(n < (1ll << 31) && (M / 256) * (n / 256) < (1ll << 31));
+  Q3_REQUIRE(n < (1ll << 31) && (M / 128) * (n / 128) < (1ll << 31));
   if (dtype == Q3_BF16) return launch_multi<BF16>(A, lda, nseg, Bs, ldb, Cs, Ns, ldcs, M, K, stream);
   return launch_multi<F16>(A, lda, nseg, Bs, ldb, Cs, Ns, ldcs, M, K, stream);
 }

@@ -64,9 +64,8 @@ def gemm_nt_residual_into(a, lda, bnk, ldb, res, out, m, n, k):
 
 
 def gemm_residual_ok(dtype, m, n, k):
-    """The fused residual epilogue serves 16-bit full-tile grids that cover the 256 CUs."""
-    return dtype in (torch.bfloat16, torch.float16) and m % 256 == 0 and n % 256 == 0 and k % 64 == 0 and \
-        (m // 256) * (n // 256) >= 256
+    """The fused residual epilogue serves 16-bit data in full 128 x 128 (or 256 x 256) tiles."""
+    return dtype in (torch.bfloat16, torch.float16) and m % 128 == 0 and n % 128 == 0 and k % 64 == 0
 
 
 def swiglu_bwd_gemm_into(dy, wt, g, u, dg, du, dgt, dut, m, n, k):
@@ -96,10 +95,9 @@ def gemm_nt_multi_into(a, weights, outs, m, k):
 
 
 def gemm_multi_ok(x, m, k, weights):
-    """The one-launch path needs 16-bit data, full 256 x 256 tiles and a grid of at least 256 tiles."""
-    ntot = sum(w.shape[0] for w in weights)
-    return x.dtype in (torch.bfloat16, torch.float16) and len(weights) <= 3 and m % 256 == 0 and k % 64 == 0 and \
-        all(w.shape[0] % 256 == 0 for w in weights) and (m // 256) * (ntot // 256) >= 256
+    """The one-launch path needs 16-bit data and full 128 x 128 (or 256 x 256) tiles."""
+    return x.dtype in (torch.bfloat16, torch.float16) and len(weights) <= 3 and m % 128 == 0 and k % 64 == 0 and \
+        all(w.shape[0] % 128 == 0 for w in weights)
 
 
 def gate_up_fused_ok(x, m, n, k):

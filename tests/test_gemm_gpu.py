@@ -164,7 +164,8 @@ def test_gate_up_swiglu_gemm(m, n, k, dtype):
     assert torch.equal(yt[:, :m], y.t()) and bool((yt[:, m:] == 7.0).all())
 
 
-@pytest.mark.parametrize("m,ns,k", [(256, (256,), 64), (512, (512, 256, 256), 128), (8192, (4096, 1024, 1024), 4096)])
+@pytest.mark.parametrize("m,ns,k", [(256, (256,), 64), (512, (512, 256, 256), 128), (8192, (4096, 1024, 1024), 4096),
+                                    (2048, (4096, 1024, 1024), 4096), (384, (128, 256), 64)])
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
 def test_gemm_nt_multi(m, ns, k, dtype):
     """One launch over up to 3 weights (the q/k/v projections): every output equals its own q3_gemm_nt
@@ -256,7 +257,8 @@ def test_mlp_block_matches_composition(b, s, h, i, dtype):
         assert cosine(a, e) >= 0.999
 
 
-@pytest.mark.parametrize("m,n,k", [(4096, 4096, 256), (8192, 4096, 4096)])
+@pytest.mark.parametrize("m,n,k", [(4096, 4096, 256), (8192, 4096, 4096), (2048, 4096, 4096), (2048, 4096, 12288),
+                                   (256, 384, 128), (384, 128, 64)])
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
 def test_gemm_nt_residual(m, n, k, dtype):
     """q3_gemm_nt_residual: bit-equal to q3_gemm_nt followed by q3_add (in place on the residual too),
