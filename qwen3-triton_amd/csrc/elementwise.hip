@@ -397,6 +397,38 @@ __global__ __launch_bounds__(kBlock) void transpose2d16_kernel(const u16* __rest
   }
 }
 
+// 16-bit transpose of full 128 x 128 tiles through LDS: rows go in as 256-byte row segments and come
+// out as 256-byte row segments of y (the register-block kernel above moves 128-byte segments).  LDS
+// row r keeps its 16-byte chunk c at physical chunk c ^ ((r >> 3) & 15): the row writes and the
+// column gathers (16 lanes on rows 8 apart) both hit 16 different chunks.
+__global__ __launch_bounds__(kBlock) void transpose2d16_lds_kernel(const u16* __restrict__ x, int64_t ldx,
+                                                                   u16* __restrict__ y, int64_t ldy) {
+  __shared__ __attribute__((aligned(16))) u16 tile[128 * 128];
+  const int t = threadIdx.x, ch = t & 15, rr = t >> 4;
+  const int64_t r0 = (int64_t)blockIdx.y * 128, c0 = (int64_t)blockIdx.x * 128;
+  i32x4 v[8];
+#pragma unroll
+  for (int p = 0; p < 8; ++p) v[p] = *reinterpret_cast<const i32x4*>(x + (r0 + 16 * p + rr) * ldx + c0 + 8 * ch);
+#pragma unroll
+  for (int p = 0; p < 8; ++p) {
+    const int r = 16 * p + rr;
+    *reinterpret_cast<i32x4*>(tile + r * 128 + 8 * (ch ^ ((r >> 3) & 15))) = v[p];
+  }
+  __syncthreads();
+#pragma unroll
+  for (int p = 0; p < 8; ++p) {  // output row oc (a tile column), rows 8 ch .. 8 ch + 7 of the tile
+    const int oc = 16 * p + rr, pc = (oc >> 3), off = oc & 7;
+    uint32_t w[4];
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      const int ra = 8 * ch + 2 * e, rb = ra + 1;  // (ra >> 3) & 15 == ch for both rows
+      const uint32_t a = tile[ra * 128 + 8 * (pc ^ ch) + off], b = tile[rb * 128 + 8 * (pc ^ ch) + off];
+      w[e] = a | (b << 16);
+    }
+    *reinterpret_cast<i32x4*>(y + (c0 + oc) * ldy + r0 + 8 * ch) = i32x4{(int)w[0], (int)w[1], (int)w[2], (int)w[3]};
+  }
+}
+
 template <typename S>
 __global__ __launch_bounds__(kBlock) void transpose2d_scalar_kernel(const S* __restrict__ x, int64_t ldx,
                                                                     S* __restrict__ y, int64_t ldy, int64_t rows,
@@ -621,6 +653,12 @@ int q3_transpose2d(int dtype, const void* x, int64_t ldx, void* y, int64_t ldy, 
                    hipStream_t stream) {
   Q3_REQUIRE(dtype_ok(dtype) && x && y && rows > 0 && cols > 0 && ldx >= cols && ldy >= rows &&
              (rows + 63) / 64 < 65536);
+  if (dtype != Q3_F32 && cols % 128 == 0 && rows % 128 == 0 && ldx % 8 == 0 && ldy % 8 == 0 &&
+      aligned16<u16>(x) && aligned16<u16>(y)) {
+    dim3 g((unsigned)(cols / 128), (unsigned)(rows / 128));
+    transpose2d16_lds_kernel<<<g, kBlock, 0, stream>>>((const u16*)x, ldx, (u16*)y, ldy);
+    return (int)hipGetLastError();
+  }
   if (dtype != Q3_F32 && cols % 8 == 0 && rows % 8 == 0 && ldx % 8 == 0 && ldy % 8 == 0 && aligned16<u16>(x) &&
       aligned16<u16>(y)) {
     dim3 g16((unsigned)((cols + 255) / 256), (unsigned)((rows + 63) / 64));

@@ -217,7 +217,7 @@ def test_residual_cast_fill_transpose(dtype):
 
 
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
-@pytest.mark.parametrize("r,c", [(64, 256), (8192, 1024), (72, 40), (37, 50)])
+@pytest.mark.parametrize("r,c", [(64, 256), (8192, 1024), (384, 128), (72, 40), (37, 50)])
 def test_strided_data_movement(r, c, dtype):
     """q3_transpose2d into a column block of a wider matrix writes nothing else; q3_copy2d and the
     row-strided SwiGLU backward match their contiguous forms bit for bit."""
