@@ -402,10 +402,13 @@ __global__ __launch_bounds__(kBlock) void transpose2d16_kernel(const u16* __rest
 // row r keeps its 16-byte chunk c at physical chunk c ^ ((r >> 3) & 15): the row writes and the
 // column gathers (16 lanes on rows 8 apart) both hit 16 different chunks.
 __global__ __launch_bounds__(kBlock) void transpose2d16_lds_kernel(const u16* __restrict__ x, int64_t ldx,
-                                                                   u16* __restrict__ y, int64_t ldy) {
+                                                                   u16* __restrict__ y, int64_t ldy, int64_t bsx,
+                                                                   int64_t bsy) {
   __shared__ __attribute__((aligned(16))) u16 tile[128 * 128];
   const int t = threadIdx.x, ch = t & 15, rr = t >> 4;
   const int64_t r0 = (int64_t)blockIdx.y * 128, c0 = (int64_t)blockIdx.x * 128;
+  x += (int64_t)blockIdx.z * bsx;  // batch z: x [rows, cols] at z bsx, y [cols, ldy] at z bsy
+  y += (int64_t)blockIdx.z * bsy;
   i32x4 v[8];
 #pragma unroll
   for (int p = 0; p < 8; ++p) v[p] = *reinterpret_cast<const i32x4*>(x + (r0 + 16 * p + rr) * ldx + c0 + 8 * ch);
@@ -656,7 +659,7 @@ int q3_transpose2d(int dtype, const void* x, int64_t ldx, void* y, int64_t ldy, 
   if (dtype != Q3_F32 && cols % 128 == 0 && rows % 128 == 0 && ldx % 8 == 0 && ldy % 8 == 0 &&
       aligned16<u16>(x) && aligned16<u16>(y)) {
     dim3 g((unsigned)(cols / 128), (unsigned)(rows / 128));
-    transpose2d16_lds_kernel<<<g, kBlock, 0, stream>>>((const u16*)x, ldx, (u16*)y, ldy);
+    transpose2d16_lds_kernel<<<g, kBlock, 0, stream>>>((const u16*)x, ldx, (u16*)y, ldy, 0, 0);
     return (int)hipGetLastError();
   }
   if (dtype != Q3_F32 && cols % 8 == 0 && rows % 8 == 0 && ldx % 8 == 0 && ldy % 8 == 0 && aligned16<u16>(x) &&
@@ -700,6 +703,12 @@ int q3_transpose(int dtype, const void* x, void* y, int64_t batch, int64_t rows,
                  hipStream_t stream) {
   Q3_REQUIRE(dtype_ok(dtype) && x && y && batch > 0 && rows > 0 && cols > 0 && batch < 65536 && ldy >= rows);
   Q3_REQUIRE((ldy + 63) / 64 < 65536);
+  if (dtype != Q3_F32 && ldy == rows && rows % 128 == 0 && cols % 128 == 0 && aligned16<u16>(x) &&
+      aligned16<u16>(y)) {  // no padding rows to zero: whole 128 x 128 tiles through LDS
+    dim3 g((unsigned)(cols / 128), (unsigned)(rows / 128), (unsigned)batch);
+    transpose2d16_lds_kernel<<<g, kBlock, 0, stream>>>((const u16*)x, cols, (u16*)y, ldy, rows * cols, cols * ldy);
+    return (int)hipGetLastError();
+  }
   if (dtype != Q3_F32 && cols % 8 == 0 && ldy % 8 == 0 && aligned16<u16>(x) && aligned16<u16>(y)) {
     dim3 g16((unsigned)((cols + 255) / 256), (unsigned)((ldy + 63) / 64), (unsigned)batch);
     transpose16_kernel<<<g16, kBlock, 0, stream>>>((const u16*)x, (u16*)y, rows, cols, ldy);

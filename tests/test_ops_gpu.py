@@ -239,7 +239,7 @@ def test_strided_data_movement(r, c, dtype):
 
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
 @pytest.mark.parametrize("batch,r,c,pad", [(1, 8192, 4096, 1), (2, 67, 136, 8), (1, 70, 264, 64), (3, 5, 8, 16),
-                                           (1, 2048, 1024, 8), (2, 67, 130, 1)])
+                                           (1, 2048, 1024, 8), (2, 67, 130, 1), (3, 256, 384, 1), (2, 128, 256, 64)])
 def test_transpose_shapes(batch, r, c, pad, dtype):
     """Bit-exact layout change, vector (cols % 8 == 0, padded ld % 8 == 0) and scalar paths; the pad
     columns are zero."""
