@@ -171,12 +171,24 @@ int q3_gemm_nt(int in_dtype, int out_dtype, const void* A, int64_t lda, const vo
  * rows) and the residual R [M, N] (row stride ldr); the GEMM output is rounded to dtype and then
  * added to R in fp32 and rounded again, so C is bit-identical to q3_gemm_nt followed by q3_add.
  * C may alias R.  M % 128 == 0, N % 128 == 0, K % 64 == 0 (256 x 256 tiles when M and N are multiples of
- * 256 and that grid has at least 256 tiles, else 128 x 128, as q3_gemm_nt plans them), strides % 8 == 0,
+ * 256 and that grid has at least 192 tiles, else 128 x 128, as q3_gemm_nt plans them), strides % 8 == 0,
  * pointers 16-byte aligned.
  * Replaces: _model.py:60-108 / components.py (x = x + self_attn(...), x = x + mlp(...): the o_proj /
  * down_proj kernels/linear.py launch followed by kernels/residual.py:13-30). */
 int q3_gemm_nt_residual(int dtype, const void* A, int64_t lda, const void* B, int64_t ldb, const void* R,
                         int64_t ldr, void* C, int64_t ldc, int64_t M, int64_t N, int64_t K, hipStream_t stream);
+/* q3_gemm_nt_residual with a caller workspace of q3_gemm_nt_residual_workspace_bytes(M, N, K) bytes
+ * (16-byte aligned).  When that size is nonzero -- M, N multiples of 256 whose 256 x 256 grid has 96 to 128
+ * tiles, i.e. would occupy at most half of the CUs, and K % 128 == 0 with K / 2 >= 4096, e.g. the
+ * 2048-token prefill's down projection -- the GEMM runs as two K halves on 256 x 256 tiles into
+ * fp32 partials in the workspace, and one pass forms C = R + (P0 + P1) with the same two roundings
+ * (the product rounded, then the residual added and rounded): within the rounding of the unsplit
+ * launch, not bit-identical to it.  With a null workspace, or a zero size, it is q3_gemm_nt_residual.
+ * Replaces: the same reference launches as q3_gemm_nt_residual. */
+size_t q3_gemm_nt_residual_workspace_bytes(int64_t M, int64_t N, int64_t K);
+int q3_gemm_nt_residual_ws(int dtype, const void* A, int64_t lda, const void* B, int64_t ldb, const void* R,
+                           int64_t ldr, void* C, int64_t ldc, int64_t M, int64_t N, int64_t K, void* workspace,
+                           size_t workspace_bytes, hipStream_t stream);
 /* Gate/up projections with the SwiGLU epilogue in one matrix-core GEMM: for x [M, K] and weights
  * wg, wu [N, K] (K-contiguous rows, row stride ldw), stores G = x wg^T, U = x wu^T (each rounded to
  * dtype) and Y = silu(G) * U computed from the rounded G and U (the same expression as
@@ -214,7 +226,7 @@ int q3_gemm_swiglu_bwd(int dtype, const void* dy, int64_t lddy, const void* wt, 
  * ldcs[s]), fp32 accumulation, one rounding, bit-identical to nseg separate q3_gemm_nt calls with
  * the same tile plan.  M % 128 == 0, every Ns[s] % 128 == 0, K % 64 == 0, ldcs[s] % 8 == 0,
  * pointers 16-byte aligned; 256 x 256 tiles when M and every Ns[s] are multiples of 256 and that grid
- * has at least 256 tiles, else 128 x 128.  The K and V projections of Qwen3-8B (N = 1024) alone fill
+ * has at least 192 tiles, else 128 x 128.  The K and V projections of Qwen3-8B (N = 1024) alone fill
  * only part of the 256 CUs; side by side with Q they share one well-filled grid.
  * Replaces: components.py:19-21 / _model.py (q_proj, k_proj, v_proj: three kernels/linear.py
  * launches on the same input). */

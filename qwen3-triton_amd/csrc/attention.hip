@@ -282,11 +282,11 @@ Q3_DEV float xmax4(float x) {  // max over lanes {l, l^16, l^32, l^48}
 Q3_DEV int kswz3(int r) { return (r & 7) | (((r >> 4) & 1) << 3); }
 Q3_DEV int vswz3(int r) { return (r >> 1) & 7; }
 
-template <typename T, int GH>
-__global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) void attn_fwd_v3(
+template <typename T, int GH, int NW>
+__global__ __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(2, 2))) void attn_fwd_v3(
     const u16* __restrict__ Q, Lay ql, const u16* __restrict__ K, Lay kl, const u16* __restrict__ Vt,
     u16* __restrict__ O, float* __restrict__ LSE, int Hq, int Hkv, int Lq, int Lk, int ldvt, float scale2) {
-  constexpr int D = 128, BN = 64, NW = 8, QT = 32 * (NW / GH);
+  constexpr int D = 128, BN = 64, QT = 32 * (NW / GH);
   constexpr int KST = BN * D * 2, VST = D * BN * 2;
   __shared__ __attribute__((aligned(1024))) char lds[2 * KST + 2 * VST];
   char* const kring = lds;
@@ -1579,14 +1579,26 @@ __global__ __launch_bounds__(kThreads) void seq_major_vec_kernel(const u16* __re
 // ============================================================================ host dispatch
 bool dtype_ok(int dt) { return dt == Q3_F32 || dt == Q3_F16 || dt == Q3_BF16; }
 
+template <typename T, int GH, int NW>
+int fwd_v3_launch(const void* q, Lay ql, const void* k, Lay kl, const void* vt, void* o, float* lse, int B, int Hq,
+                  int Hkv, int Lq, int Lk, int ldvt, float scale, hipStream_t s) {
+  constexpr int QT = 32 * (NW / GH);
+  dim3 grid((unsigned)(B * Hq / GH), (unsigned)((Lq + QT - 1) / QT));
+  attn_fwd_v3<T, GH, NW><<<grid, NW * 64, 0, s>>>((const u16*)q, ql, (const u16*)k, kl, (const u16*)vt, (u16*)o,
+                                                  lse, Hq, Hkv, Lq, Lk, ldvt, scale * kLog2e);
+  return (int)hipGetLastError();
+}
+
+// 8-wave workgroups (every K/V tile feeds 256 query rows) when the grid has at least two of them per
+// CU; otherwise 4-wave workgroups of half the query rows, two per CU: the longest (last) query tiles
+// of a causal grid bound the launch, and halving their rows halves their time.
 template <typename T, int GH>
 int fwd_v3(const void* q, Lay ql, const void* k, Lay kl, const void* vt, void* o, float* lse, int B, int Hq, int Hkv,
            int Lq, int Lk, int ldvt, float scale, hipStream_t s) {
-  constexpr int QT = 32 * (8 / GH);
-  dim3 grid((unsigned)(B * Hq / GH), (unsigned)((Lq + QT - 1) / QT));
-  attn_fwd_v3<T, GH><<<grid, 512, 0, s>>>((const u16*)q, ql, (const u16*)k, kl, (const u16*)vt, (u16*)o, lse, Hq,
-                                          Hkv, Lq, Lk, ldvt, scale * kLog2e);
-  return (int)hipGetLastError();
+  constexpr int QT8 = 32 * (8 / GH);
+  if (GH <= 4 && (int64_t)(B * Hq / GH) * ((Lq + QT8 - 1) / QT8) < 512)
+    return fwd_v3_launch<T, GH, 4>(q, ql, k, kl, vt, o, lse, B, Hq, Hkv, Lq, Lk, ldvt, scale, s);
+  return fwd_v3_launch<T, GH, 8>(q, ql, k, kl, vt, o, lse, B, Hq, Hkv, Lq, Lk, ldvt, scale, s);
 }
 
 template <typename T, int D>

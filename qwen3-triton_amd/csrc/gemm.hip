@@ -229,6 +229,9 @@ struct CeEpi {
   // EPI 0 (16-bit output, full 256 x 256 tiles): when set, C = res + the GEMM output (row stride ldres)
   const u16* res;
   int64_t ldres;
+  // EPI 0 over a grid of gridDim.y K splits: split y multiplies the y-th K / gridDim.y slice and stores
+  // its partial product at C + y * split_ld
+  int64_t split_ld;
   // EPI 3: when set, also Y^T [N, M] (row stride ldyt), the down projection's weight-gradient operand
   u16* yt;
   int64_t ldyt;
@@ -265,6 +268,14 @@ __global__ __launch_bounds__(WM * WN * 64) void gemm_nt_v4_kernel(const u16* __r
   int tm, tn;
   tile_coords(blockIdx.x, (M + BM - 1) / BM, (N + BN - 1) / BN, tm, tn);
   const int m0 = tm * BM, n0 = tn * BN;
+  if constexpr (EPI == 0) {
+    if (gridDim.y > 1) {  // K split: this workgroup's slice of K and its own partial output
+      K /= (int)gridDim.y;
+      A += (int64_t)blockIdx.y * K;
+      B += (int64_t)blockIdx.y * K;
+      C += (int64_t)blockIdx.y * ce.split_ld;
+    }
+  }
   if constexpr (EPI == 4) {  // this tile's weight and output, shifted so column n0 addresses them
     int sg = 0;
     while (sg + 1 < ce.nseg && n0 >= ce.seg_n0[sg + 1]) ++sg;
@@ -827,13 +838,13 @@ __global__ __launch_bounds__(WM * WN * 64) void gemm_nt_v4_kernel(const u16* __r
 
 template <typename T, typename O, int BM, int BN, int WM, int WN, int ST, bool EVEN, int BK = 64, int EPI = 0>
 int launch_v4(const void* A, int64_t lda, const void* B, int64_t ldb, void* C, int64_t ldc, int64_t M, int64_t N,
-              int64_t K, float alpha, int acc, hipStream_t s, CeEpi ce = CeEpi{}) {
+              int64_t K, float alpha, int acc, hipStream_t s, CeEpi ce = CeEpi{}, int splits = 1) {
   const int64_t tiles = ((M + BM - 1) / BM) * ((N + BN - 1) / BN);
   static_assert(BM * BN * 2 <= ST * (BM + BN) * BK * 2, "the LDS epilogue reuses the operand ring");
   // 2: 16-byte row stores (the LDS epilogue), 1: 8-byte (16-bit) / 16-byte (fp32) stores, 0: scalar
   const int vec = (ldc % 8 == 0 && ((uintptr_t)C & 15) == 0) ? 2
                   : ((ldc % 4 == 0) && (((uintptr_t)C & (O::vec == 4 ? 15 : 7)) == 0)) ? 1 : 0;
-  gemm_nt_v4_kernel<T, O, BM, BN, WM, WN, BK, ST, EVEN, EPI><<<(unsigned)tiles, WM * WN * 64, 0, s>>>(
+  gemm_nt_v4_kernel<T, O, BM, BN, WM, WN, BK, ST, EVEN, EPI><<<dim3((unsigned)tiles, (unsigned)splits), WM * WN * 64, 0, s>>>(
       (const u16*)A, (const u16*)B, (typename O::storage*)C, (int)M, (int)N, (int)K, lda, ldb, ldc, alpha, acc, vec,
       ce);
   return (int)hipGetLastError();
@@ -884,6 +895,10 @@ int launch_swiglu_bwd(const void* A, int64_t lda, const void* B, int64_t ldb, in
 // Q/K/V-style GEMM: one A, up to 3 weights side by side as the B rows, one output per weight
 // (256 x 256 tiles of full tiles only).
 int64_t tiles_of(int64_t M, int64_t N, int64_t bm, int64_t bn) { return ((M + bm - 1) / bm) * ((N + bn - 1) / bn); }
+// 256 x 256 tiles when their grid occupies at least three quarters of the 256 CUs, else 128 x 128 (two
+// workgroups per CU).  Measured on MI355X: 2048 x 6144 x 4096 (192 tiles) 92.6 us against 108.0 us on
+// 768 tiles of 128 x 128 (1.5 rounds); at 128 or 144 tiles of 256 x 256, 128 x 128 is faster.
+bool tiles_256(int64_t M, int64_t N) { return tiles_of(M, N, 256, 256) >= 192; }
 bool all_n_multiple(const int64_t* Ns, int nseg, int64_t q) {
   for (int i = 0; i < nseg; ++i)
     if (Ns[i] % q != 0) return false;
@@ -903,9 +918,9 @@ int launch_multi(const void* A, int64_t lda, int nseg, const void* const* Bs, in
     n += Ns[i];
   }
   e.nseg = nseg;
-  // The tile plan of the plain GEMM: 256 x 256 when that grid gives every CU a workgroup, else 128 x 128
-  // (the same per-element k order either way: every output equals its single-weight GEMM bit for bit).
-  if (M % 256 == 0 && n % 256 == 0 && tiles_of(M, n, 256, 256) >= 256 && all_n_multiple(Ns, nseg, 256))
+  // The tile plan of the plain GEMM (the same per-element k order either way: every output equals its
+  // single-weight GEMM bit for bit).
+  if (M % 256 == 0 && n % 256 == 0 && tiles_256(M, n) && all_n_multiple(Ns, nseg, 256))
     return launch_v4<T, T, 256, 256, 4, 2, 2, true, 64, 4>(A, lda, Bs[0], ldb, Cs[0], ldcs[0], M, n, K, 1.f, 0, s, e);
   return launch_v4<T, T, 128, 128, 4, 2, 2, true, 64, 4>(A, lda, Bs[0], ldb, Cs[0], ldcs[0], M, n, K, 1.f, 0, s, e);
 }
@@ -959,8 +974,8 @@ template <typename T, typename O>
 int launch_nt(const void* A, int64_t lda, const void* B, int64_t ldb, void* C, int64_t ldc, int64_t M, int64_t N,
               int64_t K, float alpha, int acc, hipStream_t s) {
   if (K % 64 == 0) {
-    // 256 x 256 tiles when they still give every CU (256) a workgroup, else 128 x 128 (measured on
-    // MI355X for the Qwen3-8B projection shapes: below 256 tiles of 256 x 256, 128 x 128 beats both
+    // 256 x 256 tiles when they fill at least three quarters of the CUs, else 128 x 128 (measured on
+    // MI355X for the Qwen3-8B projection shapes: at 128 tiles of 256 x 256, 128 x 128 beats both
     // 256 x 256 and 256 x 128, e.g. 2048 x 4096 x 12288 in 190 us against 250 / 203 us).
     const int64_t t256 = tiles_of(M, N, 256, 256), nN = (N + 255) / 256;
     // A last round of 256 x 256 tiles that would leave at least half of the CUs idle (e.g. the
@@ -976,7 +991,7 @@ int launch_nt(const void* A, int64_t lda, const void* B, int64_t ldb, void* C, i
                                static_cast<typename O::storage*>(C) + m1 * ldc, ldc, M - m1, N, K, alpha, acc, s);
       }
     }
-    if (t256 >= 256) {
+    if (tiles_256(M, N)) {
       if (M % 256 == 0 && N % 256 == 0)
         return launch_v4<T, O, 256, 256, 4, 2, 2, true>(A, lda, B, ldb, C, ldc, M, N, K, alpha, acc, s);
       return launch_v4<T, O, 256, 256, 4, 2, 2, false>(A, lda, B, ldb, C, ldc, M, N, K, alpha, acc, s);
@@ -1023,6 +1038,56 @@ int generic_out(int out, const void* A, int64_t sam, int64_t sak, const void* B,
 
 bool dtype_ok(int dt) { return dt == Q3_F32 || dt == Q3_F16 || dt == Q3_BF16; }
 bool al16(const void* p) { return ((uintptr_t)p & 15) == 0; }
+
+
+// Residual GEMM as two K splits (at least kSplitKMin of K each): 256 x 256 tiles whose grid alone would
+// occupy at most half of the 256 CUs (and so runs as 128 x 128 tiles otherwise) doubled along K.
+// Measured on MI355X at M = 2048, N = 4096: K = 12288 161 + 16 us (the combining pass) against 207 us on
+// 128 x 128 tiles; K = 4096 65 + 16 against 69 us, hence the minimum.
+constexpr int64_t kSplitKMin = 4096;
+int residual_splits(int64_t M, int64_t N, int64_t K) {
+  if (M % 256 != 0 || N % 256 != 0 || K % 128 != 0 || K / 2 < kSplitKMin) return 1;
+  const int64_t t = tiles_of(M, N, 256, 256);
+  return t >= 96 && t <= 128 ? 2 : 1;
+}
+
+// C = R + (P0 + P1) from the two fp32 partial products (P1 at P0 + split_ld, row stride N) with the
+// roundings of the unsplit residual GEMM: the product rounded to T, added to R in fp32, rounded again.
+template <typename T>
+__global__ __launch_bounds__(256) void split_residual_kernel(const float* __restrict__ P, int64_t split_ld,
+                                                             const u16* __restrict__ R, int64_t ldr,
+                                                             u16* __restrict__ C, int64_t ldc, int64_t M, int64_t N) {
+  const int64_t cols = N / 8, i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (i >= M * cols) return;
+  const int64_t r = i / cols, c = (i - r * cols) * 8;
+  const float* p = P + r * N + c;
+  const f32x4 a0 = *reinterpret_cast<const f32x4*>(p), a1 = *reinterpret_cast<const f32x4*>(p + 4);
+  const f32x4 b0 = *reinterpret_cast<const f32x4*>(p + split_ld), b1 = *reinterpret_cast<const f32x4*>(p + split_ld + 4);
+  const i32x4 rv = *reinterpret_cast<const i32x4*>(R + r * ldr + c);
+  i32x4 o;
+#pragma unroll
+  for (int w = 0; w < 4; ++w) {
+    const float s0 = w < 2 ? a0[2 * w] + b0[2 * w] : a1[2 * w - 4] + b1[2 * w - 4];
+    const float s1 = w < 2 ? a0[2 * w + 1] + b0[2 * w + 1] : a1[2 * w - 3] + b1[2 * w - 3];
+    const u16 lo = from_f32<T>(to_f32<T>(from_f32<T>(s0)) + to_f32<T>((u16)(rv[w] & 0xffff)));
+    const u16 hi = from_f32<T>(to_f32<T>(from_f32<T>(s1)) + to_f32<T>((u16)((uint32_t)rv[w] >> 16)));
+    o[w] = (int)((uint32_t)lo | ((uint32_t)hi << 16));
+  }
+  *reinterpret_cast<i32x4*>(C + r * ldc + c) = o;
+}
+
+template <typename T>
+int launch_split_residual(const void* A, int64_t lda, const void* B, int64_t ldb, const void* R, int64_t ldr,
+                          void* C, int64_t ldc, int64_t M, int64_t N, int64_t K, float* P, hipStream_t s) {
+  CeEpi e{};
+  e.split_ld = M * N;
+  int rc = launch_v4<T, F32, 256, 256, 4, 2, 2, true>(A, lda, B, ldb, P, N, M, N, K, 1.f, 0, s, e, 2);
+  if (rc != 0) return rc;
+  const int64_t n8 = M * N / 8;
+  split_residual_kernel<T><<<(unsigned)((n8 + 255) / 256), 256, 0, s>>>(P, M * N, (const u16*)R, ldr, (u16*)C, ldc,
+                                                                        M, N);
+  return (int)hipGetLastError();
+}
 
 }  // namespace
 
@@ -1125,24 +1190,41 @@ int q3_gemm_gate_up_swiglu_t(int dtype, const void* x, int64_t ldx, const void* 
   return launch_gate_up<F16>(x, ldx, wg, wu, ldw, g, u, y, ldo, M, N, K, stream, yt, ldyt);
 }
 
-int q3_gemm_nt_residual(int dtype, const void* A, int64_t lda, const void* B, int64_t ldb, const void* R,
-                        int64_t ldr, void* C, int64_t ldc, int64_t M, int64_t N, int64_t K, hipStream_t stream) {
+size_t q3_gemm_nt_residual_workspace_bytes(int64_t M, int64_t N, int64_t K) {
+  return M > 0 && N > 0 && residual_splits(M, N, K) > 1 ? (size_t)(2 * M * N) * sizeof(float) : 0;
+}
+
+int q3_gemm_nt_residual_ws(int dtype, const void* A, int64_t lda, const void* B, int64_t ldb, const void* R,
+                           int64_t ldr, void* C, int64_t ldc, int64_t M, int64_t N, int64_t K, void* workspace,
+                           size_t workspace_bytes, hipStream_t stream) {
   Q3_REQUIRE((dtype == Q3_BF16 || dtype == Q3_F16) && A && B && R && C);
   Q3_REQUIRE(M > 0 && N > 0 && K > 0 && M % 128 == 0 && N % 128 == 0 && K % 64 == 0 && M < (1ll << 31) &&
              N < (1ll << 31) && K < (1ll << 31) && (M / 128) * (N / 128) < (1ll << 31));
   Q3_REQUIRE(lda % 8 == 0 && ldb % 8 == 0 && ldr % 8 == 0 && ldc % 8 == 0 && lda >= K && ldb >= K && ldr >= N &&
              ldc >= N && al16(A) && al16(B) && al16(R) && al16(C));
+  const size_t need = q3_gemm_nt_residual_workspace_bytes(M, N, K);
+  if (need > 0 && workspace) {
+    Q3_REQUIRE(workspace_bytes >= need && al16(workspace));
+    if (dtype == Q3_BF16)
+      return launch_split_residual<BF16>(A, lda, B, ldb, R, ldr, C, ldc, M, N, K, (float*)workspace, stream);
+    return launch_split_residual<F16>(A, lda, B, ldb, R, ldr, C, ldc, M, N, K, (float*)workspace, stream);
+  }
   CeEpi e{};
   e.res = (const u16*)R;
   e.ldres = ldr;
-  // The plain GEMM's tile plan: 256 x 256 when that grid gives every CU a workgroup, else 128 x 128.
-  const bool big = M % 256 == 0 && N % 256 == 0 && tiles_of(M, N, 256, 256) >= 256;
+  // The plain GEMM's tile plan.
+  const bool big = M % 256 == 0 && N % 256 == 0 && tiles_256(M, N);
   if (dtype == Q3_BF16) {
     if (big) return launch_v4<BF16, BF16, 256, 256, 4, 2, 2, true>(A, lda, B, ldb, C, ldc, M, N, K, 1.f, 0, stream, e);
     return launch_v4<BF16, BF16, 128, 128, 4, 2, 2, true>(A, lda, B, ldb, C, ldc, M, N, K, 1.f, 0, stream, e);
   }
   if (big) return launch_v4<F16, F16, 256, 256, 4, 2, 2, true>(A, lda, B, ldb, C, ldc, M, N, K, 1.f, 0, stream, e);
   return launch_v4<F16, F16, 128, 128, 4, 2, 2, true>(A, lda, B, ldb, C, ldc, M, N, K, 1.f, 0, stream, e);
+}
+
+int q3_gemm_nt_residual(int dtype, const void* A, int64_t lda, const void* B, int64_t ldb, const void* R,
+                        int64_t ldr, void* C, int64_t ldc, int64_t M, int64_t N, int64_t K, hipStream_t stream) {
+  return q3_gemm_nt_residual_ws(dtype, A, lda, B, ldb, R, ldr, C, ldc, M, N, K, nullptr, 0, stream);
 }
 
 int q3_gemm_swiglu_bwd(int dtype, const void* dy, int64_t lddy, const void* wt, int64_t ldw, const void* g,

@@ -57,10 +57,15 @@ def gate_up_swiglu_t_into(x, wg, wu, g, u, y, yt, m, n, k):
 
 
 def gemm_nt_residual_into(a, lda, bnk, ldb, res, out, m, n, k):
-    """out[m, n] = res + a[m, k] . bnk[n, k]^T in one matrix-core launch (the GEMM output rounded, then
-    the residual added and rounded again: bit-identical to the GEMM followed by the add kernel)."""
-    H.call("q3_gemm_nt_residual", H.code(a.dtype), a.data_ptr(), lda, bnk.data_ptr(), ldb, res.data_ptr(),
-           res.stride(0), out.data_ptr(), out.stride(0), m, n, k, H.stream())
+    """out[m, n] = res + a[m, k] . bnk[n, k]^T (the GEMM output rounded, then the residual added and
+    rounded again).  One matrix-core launch, bit-identical to the GEMM followed by the add kernel;
+    shapes whose 256 x 256 grid would leave half of the CUs idle and whose K is long (the 2048-token
+    prefill's down projection) run as two K halves into an fp32 workspace and one combining pass instead."""
+    ws_bytes = H.query("q3_gemm_nt_residual_workspace_bytes", m, n, k)
+    ws = H.workspace(ws_bytes, a.device) if ws_bytes else None
+    H.call("q3_gemm_nt_residual_ws", H.code(a.dtype), a.data_ptr(), lda, bnk.data_ptr(), ldb, res.data_ptr(),
+           res.stride(0), out.data_ptr(), out.stride(0), m, n, k, None if ws is None else ws.data_ptr(),
+           ws_bytes, H.stream())
 
 
 def gemm_residual_ok(dtype, m, n, k):

@@ -106,9 +106,10 @@ def test_attention_invariants_full_shape():
     assert torch.equal(o[:, :, 0], v.repeat_interleave(4, 1)[:, :, 0])
 
 
-@pytest.mark.parametrize("b,s", [(4, 2048), (1, 8192)])
+@pytest.mark.parametrize("b,s", [(4, 2048), (1, 8192), (1, 2048)])
 def test_attention_benchmark_shapes_vs_sdpa_fp32(b, s):
-    """Config #3 shapes against torch SDPA in fp32 on the GPU (a library routine as the checker)."""
+    """Config #3 shapes against torch SDPA in fp32 on the GPU (a library routine as the checker); B1 S2048
+    (the 2048-token prefill) runs the forward's 4-wave workgroups, the other two its 8-wave ones."""
     print(f"attention full {b}x{s}", flush=True)
     gen = seeded(2)
     q = randn(b, 32, s, 128, gen=gen, dtype=torch.bfloat16).cuda()

@@ -20,7 +20,7 @@ def ref(a, b):
                                    (513, 687, 688), (2048, 1024, 4096), (64, 151936 // 16, 256), (1000, 3000, 128),
                                    (8192, 4096, 4096), (4096, 12288, 640), (8192, 1024, 192), (333, 4100, 4160),
                                    (4353, 4100, 1024), (2050, 4000, 512), (6144, 4096, 256),
-                                   (5000, 4096, 128),
+                                   (5000, 4096, 128), (3072, 4096, 256), (3000, 4000, 192),
                                    (4096, 12288, 8192), (6144, 4096, 8192)])
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
 def test_gemm_nt_shapes(m, n, k, dtype):
@@ -262,7 +262,10 @@ def test_mlp_block_matches_composition(b, s, h, i, dtype):
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
 def test_gemm_nt_residual(m, n, k, dtype):
     """q3_gemm_nt_residual: bit-equal to q3_gemm_nt followed by q3_add (in place on the residual too),
-    and within one rounding of the fp64 sum."""
+    and within one rounding of the fp64 sum.  Shapes with a workspace plan (two K halves) give, through
+    q3_gemm_nt_residual_ws, exactly R + (P0 + P1) rounded like the unsplit path, P0 / P1 the fp32
+    products of the K halves; without the workspace they stay bit-equal to the GEMM + add."""
+    from qwen3_triton import _hip as H
     from qwen3_triton.kernels import _ops
     from qwen3_triton.kernels.linear import gemm_nt_residual_into
     print(f"gemm_nt_residual {m}x{n}x{k} {dtype}", flush=True)
@@ -275,7 +278,21 @@ def test_gemm_nt_residual(m, n, k, dtype):
     y = torch.empty_like(out)
     gemm_nt_into(a, k, w, k, y, m, n, k)
     e = _ops.add(r, y)
-    assert torch.equal(out, e)
+    split = H.query("q3_gemm_nt_residual_workspace_bytes", m, n, k) > 0
+    assert split == (m == 2048 and n == 4096 and k >= 8192)
+    if split:
+        p = [torch.empty(m, n, device="cuda", dtype=torch.float32) for _ in range(2)]
+        gemm_nt_into(a, k, w, k, p[0], m, n, k // 2)
+        gemm_nt_into(a[:, k // 2:], k, w[:, k // 2:], k, p[1], m, n, k // 2)
+        es = ((p[0] + p[1]).to(dtype).float() + r.float()).to(dtype)
+        assert torch.equal(out, es)
+        plain = torch.empty_like(out)
+        H.call("q3_gemm_nt_residual", H.code(dtype), a.data_ptr(), k, w.data_ptr(), k, r.data_ptr(), n,
+               plain.data_ptr(), n, m, n, k, H.stream())
+        assert torch.equal(plain, e)
+        e = es
+    else:
+        assert torch.equal(out, e)
     r2 = r.clone()
     gemm_nt_residual_into(a, k, w, k, r2, r2, m, n, k)   # C aliasing R
     assert torch.equal(r2, e)
