@@ -193,8 +193,8 @@ int q3_gemm_nt_residual_ws(int dtype, const void* A, int64_t lda, const void* B,
  * wg, wu [N, K] (K-contiguous rows, row stride ldw), stores G = x wg^T, U = x wu^T (each rounded to
  * dtype) and Y = silu(G) * U computed from the rounded G and U (the same expression as
  * q3_swiglu_fwd on the stored G, U), all [M, N] at row stride ldo.  One launch reads x and both
- * weights once per tile.  M % 256 == 0, N % 128 == 0, K % 64 == 0, ldo % 8 == 0; every pointer
- * 16-byte aligned.
+ * weights once per tile.  g and u may both be null (inference: Y only, the same values).  M % 256 == 0,
+ * N % 128 == 0, K % 64 == 0, ldo % 8 == 0; every pointer 16-byte aligned.
  * Replaces: kernels/mlp_precision.py:16-33 / kernels/mlp.py:14-33 (_gate_up: both K loops and the
  * G, U, Y stores in one kernel), ops/triton/gate_up_swiglu.py:178-288. */
 int q3_gemm_gate_up_swiglu(int dtype, const void* x, int64_t ldx, const void* wg, const void* wu, int64_t ldw,

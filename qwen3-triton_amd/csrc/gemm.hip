@@ -481,7 +481,7 @@ __global__ __launch_bounds__(WM * WN * 64) void gemm_nt_v4_kernel(const u16* __r
     __syncthreads();  // every wave is done with the operand ring
     const int64_t o0 = (int64_t)(m0 + wm * TMW) * ldc + (n0 + wn * TNW) / 2;
 #pragma unroll
-    for (int out = 0; out < 3; ++out) {
+    for (int out = ce.g_out ? 0 : 2; out < 3; ++out) {  // G and U only when stored (training)
 #pragma unroll
       for (int i = 0; i < FM; ++i)
 #pragma unroll
@@ -1168,7 +1168,7 @@ int q3_gemm_nt_ce_stats_store(int dtype, const void* A, int64_t lda, const void*
 int q3_gemm_gate_up_swiglu(int dtype, const void* x, int64_t ldx, const void* wg, const void* wu, int64_t ldw,
                            void* g, void* u, void* y, int64_t ldo, int64_t M, int64_t N, int64_t K,
                            hipStream_t stream) {
-  Q3_REQUIRE((dtype == Q3_BF16 || dtype == Q3_F16) && x && wg && wu && g && u && y);
+  Q3_REQUIRE((dtype == Q3_BF16 || dtype == Q3_F16) && x && wg && wu && !g == !u && y);
   Q3_REQUIRE(M > 0 && N > 0 && K > 0 && M % 256 == 0 && N % 128 == 0 && K % 64 == 0 && M < (1ll << 31) &&
              N < (1ll << 30) && K < (1ll << 31) && (M / 256) * (N / 128) < (1ll << 31));
   Q3_REQUIRE(ldx % 8 == 0 && ldw % 8 == 0 && ldo % 8 == 0 && ldx >= K && ldw >= K && ldo >= N && al16(x) &&

@@ -44,9 +44,11 @@ def gemm_nt_into(a, lda, bnk, ldb, out, m, n, k, *, alpha=1.0, accumulate=False)
 
 def gate_up_swiglu_into(x, wg, wu, g, u, y, m, n, k):
     """g = x wg^T, u = x wu^T, y = silu(g) * u in one matrix-core GEMM (M % 256 == 0, N % 128 == 0,
-    K % 64 == 0; contiguous [M, K] x and [N, K] weights, contiguous [M, N] outputs)."""
+    K % 64 == 0; contiguous [M, K] x and [N, K] weights, contiguous [M, N] outputs); g and u None:
+    y only."""
     H.call("q3_gemm_gate_up_swiglu", H.code(x.dtype), x.data_ptr(), k, wg.data_ptr(), wu.data_ptr(), k,
-           g.data_ptr(), u.data_ptr(), y.data_ptr(), n, m, n, k, H.stream())
+           None if g is None else g.data_ptr(), None if u is None else u.data_ptr(), y.data_ptr(), n, m, n, k,
+           H.stream())
 
 
 def gate_up_swiglu_t_into(x, wg, wu, g, u, y, yt, m, n, k):

@@ -15,17 +15,34 @@ from .linear import (gate_up_fused_ok, gate_up_swiglu_into, gate_up_swiglu_t_int
                      linear, linear_residual, matmul, matmul_into, swiglu_bwd_gemm_into, swiglu_bwd_gemm_ok)
 
 
+def _check(x, wg, wu):
+    if not x.is_cuda or x.ndim < 2 or wg.ndim != 2 or wg.shape != wu.shape or x.shape[-1] != wg.shape[1]:
+        raise ValueError('Expected ROCm X[...,K] and matching [N,K] gate/up weights')
+    if x.dtype not in (torch.float32, torch.bfloat16, torch.float16) or \
+            any(t.device != x.device or t.dtype != x.dtype or not t.is_contiguous() for t in (x, wg, wu)):
+        raise ValueError('Matching contiguous floating point ROCm inputs required')
+    m, k, n = x.numel() // x.shape[-1], x.shape[-1], wg.shape[0]
+    if min(m, k, n) < 1:
+        raise ValueError('Nonempty inputs required')
+    return m, k, n
+
+
+def _gate_up_y(x, wg, wu):
+    """Y alone (no autograd: nothing is saved, so the fused GEMM skips the G and U stores)."""
+    m, k, n = _check(x, wg, wu)
+    flat = x.view(m, k)
+    if gate_up_fused_ok(x, m, n, k):
+        y = torch.empty((m, n), device=x.device, dtype=x.dtype)
+        gate_up_swiglu_into(flat, wg, wu, None, None, y, m, n, k)
+    else:
+        y = _ops.swiglu_fwd(matmul(flat, wg.t()), matmul(flat, wu.t()))
+    return y.view(*x.shape[:-1], n)
+
+
 class _GateUp(torch.autograd.Function):
     @staticmethod
     def forward(ctx, x, wg, wu, optimized):
-        if not x.is_cuda or x.ndim < 2 or wg.ndim != 2 or wg.shape != wu.shape or x.shape[-1] != wg.shape[1]:
-            raise ValueError('Expected ROCm X[...,K] and matching [N,K] gate/up weights')
-        if x.dtype not in (torch.float32, torch.bfloat16, torch.float16) or \
-                any(t.device != x.device or t.dtype != x.dtype or not t.is_contiguous() for t in (x, wg, wu)):
-            raise ValueError('Matching contiguous floating point ROCm inputs required')
-        m, k, n = x.numel() // x.shape[-1], x.shape[-1], wg.shape[0]
-        if min(m, k, n) < 1:
-            raise ValueError('Nonempty inputs required')
+        m, k, n = _check(x, wg, wu)
         flat = x.view(m, k)
         if gate_up_fused_ok(x, m, n, k):
             # one GEMM over both weights; the SwiGLU runs in its epilogue
@@ -71,7 +88,10 @@ class _GateUp(torch.autograd.Function):
 
 
 def gate_up_swiglu(x, gate_weight, up_weight, *, optimized=False):
-    """``kernels/mlp_precision.py:65``."""
+    """``kernels/mlp_precision.py:65``.  Without autograd (inference, or no input needing a gradient)
+    only Y is formed: the same values, without the G and U the backward would need."""
+    if not (torch.is_grad_enabled() and any(t.requires_grad for t in (x, gate_weight, up_weight))):
+        return _gate_up_y(x, gate_weight, up_weight)
     return _GateUp.apply(x, gate_weight, up_weight, optimized)
 
 

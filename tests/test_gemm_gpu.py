@@ -162,6 +162,13 @@ def test_gate_up_swiglu_gemm(m, n, k, dtype):
     gate_up_swiglu_t_into(x, wg, wu, g3, u3, y3, yt, m, n, k)
     assert torch.equal(g3, g) and torch.equal(u3, u) and torch.equal(y3, y)
     assert torch.equal(yt[:, :m], y.t()) and bool((yt[:, m:] == 7.0).all())
+    # Y alone (null G / U: inference): the same Y bit for bit, and the op without autograd gives it too
+    y4 = torch.full((m, n), 7.0, device="cuda", dtype=dtype)
+    gate_up_swiglu_into(x, wg, wu, None, None, y4, m, n, k)
+    assert torch.equal(y4, y)
+    from qwen3_triton.kernels.mlp_precision import gate_up_swiglu
+    with torch.no_grad():
+        assert torch.equal(gate_up_swiglu(x, wg, wu), y)
 
 
 @pytest.mark.parametrize("m,ns,k", [(256, (256,), 64), (512, (512, 256, 256), 128), (8192, (4096, 1024, 1024), 4096),
