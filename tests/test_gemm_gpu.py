@@ -166,6 +166,8 @@ def test_gate_up_swiglu_gemm(m, n, k, dtype):
     y4 = torch.full((m, n), 7.0, device="cuda", dtype=dtype)
     gate_up_swiglu_into(x, wg, wu, None, None, y4, m, n, k)
     assert torch.equal(y4, y)
+    with pytest.raises(RuntimeError):   # G and U are stored together or not at all
+        gate_up_swiglu_into(x, wg, wu, g3, None, y4, m, n, k)
     from qwen3_triton.kernels.mlp_precision import gate_up_swiglu
     with torch.no_grad():
         assert torch.equal(gate_up_swiglu(x, wg, wu), y)
@@ -297,6 +299,11 @@ def test_gemm_nt_residual(m, n, k, dtype):
         H.call("q3_gemm_nt_residual", H.code(dtype), a.data_ptr(), k, w.data_ptr(), k, r.data_ptr(), n,
                plain.data_ptr(), n, m, n, k, H.stream())
         assert torch.equal(plain, e)
+        need = H.query("q3_gemm_nt_residual_workspace_bytes", m, n, k)
+        short = torch.empty(need, dtype=torch.uint8, device="cuda")
+        with pytest.raises(RuntimeError):   # a workspace below the stated size is refused before any launch
+            H.call("q3_gemm_nt_residual_ws", H.code(dtype), a.data_ptr(), k, w.data_ptr(), k, r.data_ptr(), n,
+                   plain.data_ptr(), n, m, n, k, short.data_ptr(), need - 16, H.stream())
         e = es
     else:
         assert torch.equal(out, e)
