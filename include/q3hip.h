@@ -189,6 +189,17 @@ size_t q3_gemm_nt_residual_workspace_bytes(int64_t M, int64_t N, int64_t K);
 int q3_gemm_nt_residual_ws(int dtype, const void* A, int64_t lda, const void* B, int64_t ldb, const void* R,
                            int64_t ldr, void* C, int64_t ldc, int64_t M, int64_t N, int64_t K, void* workspace,
                            size_t workspace_bytes, hipStream_t stream);
+/* q3_gemm_nt_residual_ws that also writes Y = RMSNorm(C) with weight norm_w [N] and eps (the norm of the
+ * next block's input: Y = C rsqrt(mean(C^2) + eps) norm_w from the rounded C, q3_rmsnorm_fwd's
+ * expression, row stride ldy), N <= 8192.  On the two-K-halves plan the combining pass forms both
+ * (one row per workgroup: C is never re-read); otherwise the residual GEMM runs, then
+ * q3_rmsnorm_fwd (contiguous C and Y required there).
+ * Replaces: the o_proj / down_proj launch + residual add of components.py / _model.py followed by
+ * the next RMSNorm (kernels/norm.py:39-66, inference/kernels.py:176). */
+int q3_gemm_nt_residual_norm_ws(int dtype, const void* A, int64_t lda, const void* B, int64_t ldb, const void* R,
+                                int64_t ldr, void* C, int64_t ldc, const void* norm_w, float eps, void* Y,
+                                int64_t ldy, int64_t M, int64_t N, int64_t K, void* workspace,
+                                size_t workspace_bytes, hipStream_t stream);
 /* Gate/up projections with the SwiGLU epilogue in one matrix-core GEMM: for x [M, K] and weights
  * wg, wu [N, K] (K-contiguous rows, row stride ldw), stores G = x wg^T, U = x wu^T (each rounded to
  * dtype) and Y = silu(G) * U computed from the rounded G and U (the same expression as

@@ -1076,13 +1076,78 @@ __global__ __launch_bounds__(256) void split_residual_kernel(const float* __rest
   *reinterpret_cast<i32x4*>(C + r * ldc + c) = o;
 }
 
+// split_residual_kernel's C for one row per 512-thread workgroup, and also Y = C rsqrt(mean(C^2) + eps) w
+// (the following RMSNorm, from the rounded C: q3_rmsnorm_fwd's expression, one rounding).
+template <typename T>
+__global__ __launch_bounds__(512) void split_residual_norm_kernel(const float* __restrict__ P, int64_t split_ld,
+                                                                  const u16* __restrict__ R, int64_t ldr,
+                                                                  u16* __restrict__ C, int64_t ldc,
+                                                                  const u16* __restrict__ w, float eps,
+                                                                  u16* __restrict__ Y, int64_t ldy, int N) {
+  constexpr int kMaxG = 2;  // 8-column groups per thread: N <= 8192
+  __shared__ float red[8];
+  const int64_t r = blockIdx.x;
+  const int tid = threadIdx.x;
+  float c[kMaxG][8];
+  float ss = 0.f;
+#pragma unroll
+  for (int gi = 0; gi < kMaxG; ++gi) {
+    const int col = (gi * 512 + tid) * 8;
+    if (col < N) {
+      const float* p = P + r * N + col;
+      const f32x4 a0 = *reinterpret_cast<const f32x4*>(p), a1 = *reinterpret_cast<const f32x4*>(p + 4);
+      const f32x4 b0 = *reinterpret_cast<const f32x4*>(p + split_ld);
+      const f32x4 b1 = *reinterpret_cast<const f32x4*>(p + split_ld + 4);
+      const i32x4 rv = *reinterpret_cast<const i32x4*>(R + r * ldr + col);
+      i32x4 o;
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        const float sum = e < 4 ? a0[e] + b0[e] : a1[e - 4] + b1[e - 4];
+        const u16 rr = (u16)(((uint32_t)rv[e >> 1] >> (16 * (e & 1))) & 0xffffu);
+        c[gi][e] = to_f32<T>(from_f32<T>(to_f32<T>(from_f32<T>(sum)) + to_f32<T>(rr)));
+        ss += c[gi][e] * c[gi][e];
+      }
+#pragma unroll
+      for (int q = 0; q < 4; ++q) o[q] = (int)pack2<T>(c[gi][2 * q], c[gi][2 * q + 1]);
+      *reinterpret_cast<i32x4*>(C + r * ldc + col) = o;
+    }
+  }
+  ss = group_sum<64>(ss);
+  if ((tid & 63) == 0) red[tid >> 6] = ss;
+  __syncthreads();
+  float tot = 0.f;
+#pragma unroll
+  for (int i = 0; i < 8; ++i) tot += red[i];
+  const float inv = rsqrtf(tot * (1.f / (float)N) + eps);
+#pragma unroll
+  for (int gi = 0; gi < kMaxG; ++gi) {
+    const int col = (gi * 512 + tid) * 8;
+    if (col < N) {
+      const i32x4 wv = *reinterpret_cast<const i32x4*>(w + col);
+      i32x4 o;
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        const float w0 = to_f32<T>((u16)((uint32_t)wv[q] & 0xffffu)), w1 = to_f32<T>((u16)((uint32_t)wv[q] >> 16));
+        o[q] = (int)pack2<T>(c[gi][2 * q] * inv * w0, c[gi][2 * q + 1] * inv * w1);
+      }
+      *reinterpret_cast<i32x4*>(Y + r * ldy + col) = o;
+    }
+  }
+}
+
 template <typename T>
 int launch_split_residual(const void* A, int64_t lda, const void* B, int64_t ldb, const void* R, int64_t ldr,
-                          void* C, int64_t ldc, int64_t M, int64_t N, int64_t K, float* P, hipStream_t s) {
+                          void* C, int64_t ldc, int64_t M, int64_t N, int64_t K, float* P, hipStream_t s,
+                          const void* nw = nullptr, float eps = 0.f, void* Y = nullptr, int64_t ldy = 0) {
   CeEpi e{};
   e.split_ld = M * N;
   int rc = launch_v4<T, F32, 256, 256, 4, 2, 2, true>(A, lda, B, ldb, P, N, M, N, K, 1.f, 0, s, e, 2);
   if (rc != 0) return rc;
+  if (Y) {
+    split_residual_norm_kernel<T><<<(unsigned)M, 512, 0, s>>>(P, M * N, (const u16*)R, ldr, (u16*)C, ldc,
+                                                              (const u16*)nw, eps, (u16*)Y, ldy, (int)N);
+    return (int)hipGetLastError();
+  }
   const int64_t n8 = M * N / 8;
   split_residual_kernel<T><<<(unsigned)((n8 + 255) / 256), 256, 0, s>>>(P, M * N, (const u16*)R, ldr, (u16*)C, ldc,
                                                                         M, N);
@@ -1225,6 +1290,29 @@ int q3_gemm_nt_residual_ws(int dtype, const void* A, int64_t lda, const void* B,
 int q3_gemm_nt_residual(int dtype, const void* A, int64_t lda, const void* B, int64_t ldb, const void* R,
                         int64_t ldr, void* C, int64_t ldc, int64_t M, int64_t N, int64_t K, hipStream_t stream) {
   return q3_gemm_nt_residual_ws(dtype, A, lda, B, ldb, R, ldr, C, ldc, M, N, K, nullptr, 0, stream);
+}
+
+int q3_gemm_nt_residual_norm_ws(int dtype, const void* A, int64_t lda, const void* B, int64_t ldb, const void* R,
+                                int64_t ldr, void* C, int64_t ldc, const void* norm_w, float eps, void* Y,
+                                int64_t ldy, int64_t M, int64_t N, int64_t K, void* workspace,
+                                size_t workspace_bytes, hipStream_t stream) {
+  Q3_REQUIRE(norm_w && Y && eps > 0.f && N <= 8192 && ldy % 8 == 0 && ldy >= N && al16(norm_w) && al16(Y));
+  const size_t need = q3_gemm_nt_residual_workspace_bytes(M, N, K);
+  if (need == 0 || !workspace) {  // the residual GEMM, then the norm as its own pass
+    const int rc = q3_gemm_nt_residual_ws(dtype, A, lda, B, ldb, R, ldr, C, ldc, M, N, K, nullptr, 0, stream);
+    if (rc != 0) return rc;
+    Q3_REQUIRE(ldc == N && ldy == N);
+    return q3_rmsnorm_fwd(dtype, C, norm_w, Y, M, N, eps, stream);
+  }
+  Q3_REQUIRE((dtype == Q3_BF16 || dtype == Q3_F16) && A && B && R && C && workspace_bytes >= need &&
+             al16(workspace));
+  Q3_REQUIRE(lda % 8 == 0 && ldb % 8 == 0 && ldr % 8 == 0 && ldc % 8 == 0 && lda >= K && ldb >= K && ldr >= N &&
+             ldc >= N && al16(A) && al16(B) && al16(R) && al16(C));
+  if (dtype == Q3_BF16)
+    return launch_split_residual<BF16>(A, lda, B, ldb, R, ldr, C, ldc, M, N, K, (float*)workspace, stream, norm_w,
+                                       eps, Y, ldy);
+  return launch_split_residual<F16>(A, lda, B, ldb, R, ldr, C, ldc, M, N, K, (float*)workspace, stream, norm_w, eps,
+                                    Y, ldy);
 }
 
 int q3_gemm_swiglu_bwd(int dtype, const void* dy, int64_t lddy, const void* wt, int64_t ldw, const void* g,

@@ -62,6 +62,8 @@ SIGNATURES: dict[str, tuple] = {
     "q3_gemm_nt_residual": (_i32, [_i32, _p, _i64, _p, _i64, _p, _i64, _p, _i64, _i64, _i64, _i64, _p]),
     "q3_gemm_nt_residual_workspace_bytes": (_sz, [_i64, _i64, _i64]),
     "q3_gemm_nt_residual_ws": (_i32, [_i32, _p, _i64, _p, _i64, _p, _i64, _p, _i64, _i64, _i64, _i64, _p, _sz, _p]),
+    "q3_gemm_nt_residual_norm_ws": (_i32, [_i32, _p, _i64, _p, _i64, _p, _i64, _p, _i64, _p, _f32, _p, _i64, _i64,
+                                            _i64, _i64, _p, _sz, _p]),
     "q3_gemm_swiglu_bwd": (_i32, [_i32, _p, _i64, _p, _i64, _p, _p, _i64, _p, _p, _i64, _p, _p, _i64, _i64, _i64,
                                   _i64, _p]),
     "q3_gemm_nt_multi": (_i32, [_i32, _p, _i64, _i32, _p, _i64, _p, _p, _p, _i64, _i64, _p]),

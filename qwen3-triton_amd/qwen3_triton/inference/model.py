@@ -14,7 +14,8 @@ from ..configuration import OptimizationOptions
 from ..kernels import _ops
 from ..kernels.activation import swiglu
 from ..kernels.embedding import embedding
-from ..kernels.linear import gemm_multi_ok, gemm_nt_multi_into, gemm_nt_residual_into, gemm_residual_ok
+from ..kernels.linear import (gemm_multi_ok, gemm_nt_multi_into, gemm_nt_residual_into, gemm_nt_residual_norm_into,
+                              gemm_residual_ok)
 from ..kernels.mlp_precision import gate_up_swiglu
 from ..kernels.residual import residual_add
 from . import kernels
@@ -31,14 +32,24 @@ def _projections(h, weights, gemv):
     return [kernels.linear(h, w, gemv=gemv) for w in weights]
 
 
-def _residual_projection(x, y, weight, gemv):
-    """x + y W^T, the residual sum in the projection GEMM's epilogue where the shapes allow it."""
+def _residual_projection(x, y, weight, gemv, norm=None):
+    """x + y W^T, the residual sum in the projection GEMM's epilogue where the shapes allow it.  With
+    ``norm`` (an RMSNorm module: the next block's input norm) also returns rms_norm of that sum, formed
+    by the GEMM's combining pass where it has one."""
     m, k, n = y.numel() // y.shape[-1], y.shape[-1], weight.shape[0]
     if gemm_residual_ok(y.dtype, m, n, k) and y.is_contiguous() and x.is_contiguous() and weight.is_contiguous():
         out = torch.empty_like(x)
+        if norm is not None and n <= 8192 and norm.weight.is_contiguous() and norm.weight.dtype == x.dtype:
+            h = torch.empty_like(x)
+            gemm_nt_residual_norm_into(y.view(m, k), k, weight, k, x.view(m, n), out.view(m, n), norm.weight,
+                                       norm.eps, h.view(m, n), m, n, k)
+            return out, h
         gemm_nt_residual_into(y.view(m, k), k, weight, k, x.view(m, n), out.view(m, n), m, n, k)
+    else:
+        out = residual_add(x, kernels.linear(y, weight, gemv=gemv))
+    if norm is None:
         return out
-    return residual_add(x, kernels.linear(y, weight, gemv=gemv))
+    return out, kernels.rms_norm(out, norm.weight, norm.eps)
 
 
 @dataclass
@@ -183,7 +194,9 @@ class TritonQwen3Inference(nn.Module):
             x = embedding(input_ids, self.model.embed_tokens.weight)
             cos, sin = self.model.rotary_emb(pos, torch.bfloat16)
             fused = self.gemv and kernels.decode_linear_ok(x, self.lm_head.weight)
-            for i, layer in enumerate(self.model.layers):
+            layers = self.model.layers
+            h = None  # the next layer's normed input when the previous down projection formed it
+            for i, layer in enumerate(layers):
                 a = layer.self_attn
                 d = a.head_dim
                 if fused:  # decode step: norms, residual adds and SwiGLU ride in the projections
@@ -210,7 +223,8 @@ class TritonQwen3Inference(nn.Module):
                                               eps=layer.post_attention_layernorm.eps)
                     x = kernels.decode_linear(y, [m.down_proj.weight], mode=1, res=x)
                     continue
-                h = kernels.rms_norm(x, layer.input_layernorm.weight, layer.input_layernorm.eps)
+                if h is None:
+                    h = kernels.rms_norm(x, layer.input_layernorm.weight, layer.input_layernorm.eps)
                 q, k, v = _projections(h, [a.q_proj.weight, a.k_proj.weight, a.v_proj.weight], self.gemv)
                 q = q.view(b, s, a.num_heads, d)
                 k = k.view(b, s, a.num_kv_heads, d)
@@ -234,7 +248,11 @@ class TritonQwen3Inference(nn.Module):
                                kernels.linear(h, m.up_proj.weight, gemv=True))
                 else:
                     y = gate_up_swiglu(h, m.gate_proj.weight, m.up_proj.weight, optimized=True)
-                x = _residual_projection(x, y, m.down_proj.weight, self.gemv)
+                if i + 1 < len(layers):  # the next layer's input norm rides with this residual sum
+                    x, h = _residual_projection(x, y, m.down_proj.weight, self.gemv,
+                                                layers[i + 1].input_layernorm)
+                else:
+                    x, h = _residual_projection(x, y, m.down_proj.weight, self.gemv), None
             if logits_to_keep:
                 x = x[:, -logits_to_keep:, :].contiguous()
             if fused:

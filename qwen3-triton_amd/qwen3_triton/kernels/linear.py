@@ -70,6 +70,17 @@ def gemm_nt_residual_into(a, lda, bnk, ldb, res, out, m, n, k):
            ws_bytes, H.stream())
 
 
+def gemm_nt_residual_norm_into(a, lda, bnk, ldb, res, out, norm_w, eps, y, m, n, k):
+    """``gemm_nt_residual_into`` that also writes y = rms_norm(out, norm_w, eps) (the next block's
+    normed input; N <= 8192): in the same combining pass on the two-K-halves plan, else a separate
+    norm launch."""
+    ws_bytes = H.query("q3_gemm_nt_residual_workspace_bytes", m, n, k)
+    ws = H.workspace(ws_bytes, a.device) if ws_bytes else None
+    H.call("q3_gemm_nt_residual_norm_ws", H.code(a.dtype), a.data_ptr(), lda, bnk.data_ptr(), ldb, res.data_ptr(),
+           res.stride(0), out.data_ptr(), out.stride(0), norm_w.data_ptr(), float(eps), y.data_ptr(), y.stride(0),
+           m, n, k, None if ws is None else ws.data_ptr(), ws_bytes, H.stream())
+
+
 def gemm_residual_ok(dtype, m, n, k):
     """The fused residual epilogue serves 16-bit data in full 128 x 128 (or 256 x 256) tiles."""
     return dtype in (torch.bfloat16, torch.float16) and m % 128 == 0 and n % 128 == 0 and k % 64 == 0

@@ -310,6 +310,15 @@ def test_gemm_nt_residual(m, n, k, dtype):
     r2 = r.clone()
     gemm_nt_residual_into(a, k, w, k, r2, r2, m, n, k)   # C aliasing R
     assert torch.equal(r2, e)
+    # with the next RMSNorm: the same C, and Y = rms_norm(C) (the fused pass sums the squares in its
+    # own order: a last-bit difference in 1 / rms may move a few elements by one rounding step)
+    from qwen3_triton.kernels.linear import gemm_nt_residual_norm_into
+    nw = randn(n, gen=gen, dtype=dtype).cuda()
+    c3, y3 = torch.empty_like(out), torch.empty_like(out)
+    gemm_nt_residual_norm_into(a, k, w, k, r, c3, nw, 1e-6, y3, m, n, k)
+    assert torch.equal(c3, e)
+    yr = _ops.rmsnorm_fwd(c3, nw, 1e-6)
+    assert (y3 != yr).float().mean().item() < 0.01 and max_rel(y3, yr) <= (8e-3 if dtype == torch.bfloat16 else 1e-3)
     rows = torch.arange(0, m, max(1, m // 64))
     ref64 = r[rows].cpu().double() + a[rows].cpu().double() @ w.cpu().double().t()
     assert max_rel(out[rows], ref64) <= (1.6e-2 if dtype == torch.bfloat16 else 2e-3)
